@@ -1,0 +1,215 @@
+/*
+ * lightx2v_hip.h -- C ABI of the MI355X (gfx950) quantized-linear backend.
+ *
+ * This is the drop-in boundary a `lightx2v-hip` crate binds to implement the
+ * lightx2v-rs `Backend` trait's linear path (crates/lightx2v-core/src/
+ * backend.rs:145-212).  Every entry point names the trait method it replaces.
+ * Plain pointers and sizes only; no torch, no C++ types.
+ *
+ * Conventions
+ *  - Every function returns an int status (LX2V_OK == 0).  On failure the
+ *    thread-local message from lx2v_hip_last_error() says why.  The trait's
+ *    methods are infallible and panic on misuse; a binding maps a non-zero
+ *    status to `panic!` with that message, except lx2v_hip_create's
+ *    LX2V_ERR_NO_DEVICE, which maps to `try_new() -> None` (the CLI's
+ *    `skip:` path, crates/lightx2v-cli/src/main.rs:199-236).
+ *  - Host-facing data is f32, as the trait's (backend.rs:9-11).  Device
+ *    buffers hold f32 or bf16 activations (the backend's own precision):
+ *    upload/download/write convert at the boundary.
+ *  - One context = one device + one HIP stream.  Every op is stream-ordered
+ *    and asynchronous except download (blocking) and the create/free calls.
+ *    A context is used by one thread at a time (the reference CPU backend is
+ *    !Send, crates/lightx2v-cpu/src/lib.rs:107-124).
+ *  - Weights are copied into HBM during the weight_* call in the reference's
+ *    packed byte layouts; the caller keeps ownership of host memory
+ *    (backend.rs:178-188; crates/lightx2v-cpu/src/lib.rs:249-284).
+ */
+#ifndef LIGHTX2V_HIP_H
+#define LIGHTX2V_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LX2V_HIP_ABI_VERSION 1
+
+typedef struct lx2v_hip_ctx lx2v_hip_ctx;
+typedef struct lx2v_hip_buf lx2v_hip_buf;
+typedef struct lx2v_hip_weight lx2v_hip_weight;
+
+/* status codes */
+enum {
+    LX2V_OK = 0,
+    LX2V_ERR_NO_DEVICE = 1,   /* no usable gfx950 device: the `skip:` path  */
+    LX2V_ERR_BAD_SHAPE = 2,   /* sizes/offsets out of range or inconsistent */
+    LX2V_ERR_ALIAS = 3,       /* output overlaps an input (backend.rs:13-14) */
+    LX2V_ERR_HIP = 4,         /* a HIP runtime call failed                  */
+    LX2V_ERR_BAD_ARG = 5,     /* null handle, unknown enum value            */
+    LX2V_ERR_OOM = 6,         /* device allocation failed                   */
+    LX2V_ERR_UNSUPPORTED = 7  /* valid request this build does not serve    */
+};
+
+/* Act (backend.rs:38-43) */
+enum { LX2V_ACT_NONE = 0, LX2V_ACT_GELU_TANH = 1 };
+
+/* device activation dtypes */
+enum { LX2V_DTYPE_F32 = 0, LX2V_DTYPE_BF16 = 1 };
+
+/* weight formats (quant.rs:134-140 plus the native f32 matrix) */
+enum { LX2V_WFMT_F32 = 0, LX2V_WFMT_Q8 = 1, LX2V_WFMT_Q4 = 2, LX2V_WFMT_FP8 = 3 };
+
+/* How linear contracts an FP8 weight (no reference counterpart: the
+ * reference has no activation quantization, backend.rs:9-11).
+ *  FP8_ACT_E4M3: per-token dynamic e4m3 activations, fp8 MFMA (default);
+ *  FP8_ACT_BF16: bf16 activations, weights dequantized to bf16, bf16 MFMA. */
+enum { LX2V_FP8_ACT_E4M3 = 0, LX2V_FP8_ACT_BF16 = 1 };
+
+/* ---- errors / context --------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *lx2v_hip_last_error(void);
+
+/* Number of visible HIP devices (0 on a host without a GPU; never fails). */
+int lx2v_hip_device_count(int *count);
+
+/* WgpuBackend::try_new (crates/lightx2v-wgpu/src/lib.rs:282-287): create a
+ * context on `device`.  LX2V_ERR_NO_DEVICE when no usable gfx950 device. */
+int lx2v_hip_create(int device, lx2v_hip_ctx **out);
+int lx2v_hip_destroy(lx2v_hip_ctx *ctx);
+
+/* Backend::name (backend.rs:158): "hip:<device name> (gfx950)". */
+int lx2v_hip_name(const lx2v_hip_ctx *ctx, char *out, size_t cap);
+
+/* dtype of buffers created by lx2v_hip_alloc / lx2v_hip_upload from now on
+ * (default LX2V_DTYPE_F32). */
+int lx2v_hip_set_act_dtype(lx2v_hip_ctx *ctx, int dtype);
+/* LX2V_FP8_ACT_* used by lx2v_hip_linear for FP8 weights. */
+int lx2v_hip_set_fp8_act(lx2v_hip_ctx *ctx, int mode);
+
+/* ---- buffers (backend.rs:160-177) -------------------------------------- */
+
+/* Backend::alloc (backend.rs:161-162): zero-filled, `len` elements. */
+int lx2v_hip_alloc(lx2v_hip_ctx *ctx, size_t len, lx2v_hip_buf **out);
+int lx2v_hip_alloc_dtype(lx2v_hip_ctx *ctx, size_t len, int dtype, lx2v_hip_buf **out);
+/* Backend::upload (backend.rs:163). */
+int lx2v_hip_upload(lx2v_hip_ctx *ctx, const float *data, size_t len, lx2v_hip_buf **out);
+/* Backend::write (backend.rs:171-172): overwrite the first `len` elements. */
+int lx2v_hip_write(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, const float *data, size_t len);
+/* Backend::download (backend.rs:173-174): blocking; `len` == buffer length. */
+int lx2v_hip_download(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, float *out, size_t len);
+/* Backend::buf_len (backend.rs:175). */
+int lx2v_hip_buf_len(const lx2v_hip_buf *buf, size_t *len);
+int lx2v_hip_buf_dtype(const lx2v_hip_buf *buf, int *dtype);
+/* Backend::copy (backend.rs:176-177): dst[dst_off..][..len] = src[src_off..][..len]. */
+int lx2v_hip_copy(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t src_off,
+                  lx2v_hip_buf *dst, size_t dst_off, size_t len);
+/* Drop of the trait's Buf. */
+int lx2v_hip_buf_free(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf);
+
+/* ---- weights (backend.rs:178-188) -------------------------------------- */
+
+/* Backend::weight (backend.rs:178): native f32 [rows, cols] row-major. */
+int lx2v_hip_weight_f32(lx2v_hip_ctx *ctx, const float *data, size_t rows, size_t cols,
+                        lx2v_hip_weight **out);
+/* Backend::weight_q8 (backend.rs:179-182) over quant.rs:142-151's Q8:
+ * q int8 [rows, cols], scales f32 [rows, cols/group]. */
+int lx2v_hip_weight_q8(lx2v_hip_ctx *ctx, const int8_t *q, const float *scales,
+                       size_t rows, size_t cols, size_t group, lx2v_hip_weight **out);
+/* Backend::weight_q4 (backend.rs:183-185) over quant.rs:207-220's Q4:
+ * codes 0..15, one per byte (packed == 0, the Q4 struct's `q`) or two per
+ * byte with element 2i in the low nibble (packed == 1, Q4::packed,
+ * quant.rs:305-311); scales and zeros f32 [rows, cols/group];
+ * dequantized value (code - zero) * scale (quant.rs:294-303). */
+int lx2v_hip_weight_q4(lx2v_hip_ctx *ctx, const uint8_t *codes, int packed,
+                       const float *scales, const float *zeros, size_t rows,
+                       size_t cols, size_t group, lx2v_hip_weight **out);
+/* Backend::weight_fp8 (backend.rs:186-188) over quant.rs:364-373's Fp8E4M3:
+ * e4m3 codes [rows, cols], scales f32 [rows, cols/group] (group == cols is
+ * the per-output-channel case).  Codes with exponent field 0 and a non-zero
+ * mantissa (reference value m * 2^-12 * s, at most 3.9e-6 * the group's
+ * absmax) are stored as signed zero so the fp8 MFMA, which decodes OCP
+ * e4m3fn, sees the reference value of every other code exactly; the count
+ * is reported by lx2v_hip_weight_info. */
+int lx2v_hip_weight_fp8(lx2v_hip_ctx *ctx, const uint8_t *q, const float *scales,
+                        size_t rows, size_t cols, size_t group, lx2v_hip_weight **out);
+/* Drop of the trait's Weight. */
+int lx2v_hip_weight_free(lx2v_hip_ctx *ctx, lx2v_hip_weight *w);
+
+typedef struct {
+    int fmt;            /* LX2V_WFMT_* */
+    size_t rows, cols, group;
+    size_t device_bytes;
+    size_t canonicalized; /* FP8 exponent-0 codes stored as zero */
+} lx2v_hip_weight_info_t;
+int lx2v_hip_weight_info(const lx2v_hip_weight *w, lx2v_hip_weight_info_t *info);
+
+/* Test hook, no trait counterpart: the weight as the device decodes it
+ * (the decode the GEMMs use), f32 [rows, cols] into host memory.  For every
+ * format this equals the reference's dequantize() bit for bit
+ * (quant.rs:180-186, 294-303, 449-455); for FP8 the reference decode of
+ * the codes as passed in (exponent-0 codes included). */
+int lx2v_hip_weight_dequantize(lx2v_hip_ctx *ctx, const lx2v_hip_weight *w, float *out,
+                               size_t len);
+
+/* ---- device-side quantizers (reference runs these on the host) ---------- */
+
+/* Q8::quantize (quant.rs:154-178) of the f32 matrix in `src` (f32 buffer),
+ * group given explicitly (the reference uses 128 when it divides cols). */
+int lx2v_hip_quantize_q8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
+                         size_t cols, size_t group, lx2v_hip_weight **out);
+/* Symmetric 4-bit in the Q4 layout: s = absmax/7, q = clamp(round(v/s),-8,7),
+ * code = q + 8, zero = 8 (the HQQ path of quant.rs:226-292 stays on host). */
+int lx2v_hip_quantize_q4_sym(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
+                             size_t cols, size_t group, lx2v_hip_weight **out);
+/* Fp8E4M3::quantize (quant.rs:423-447) with the canonical encoder:
+ * quant.rs:376-406 for |v/s| >= 2^-6, 0x08 (2^-6) for 2^-7 < |v/s| < 2^-6,
+ * signed zero below; never emits an exponent-0 or NaN code. */
+int lx2v_hip_quantize_fp8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
+                          size_t cols, size_t group, lx2v_hip_weight **out);
+
+/* Synthetic data for benchmarks (Rng::normal, rng.rs:39-54, drawn per element
+ * index on the device; values agree with the host Rng to libm ulps):
+ * buf[i] = normal(seed)[i] * std. */
+int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std);
+
+/* ---- the op (backend.rs:198-212) ----------------------------------------- */
+
+/* Backend::linear: y[y_row + i, :] = act(x[x_row + i, :] . W^T + b) for
+ * i < rows; x has row stride w.cols, y row stride w.rows, bias (nullable)
+ * has w.rows elements.  y must not overlap x or bias (LX2V_ERR_ALIAS). */
+int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                    const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act,
+                    lx2v_hip_buf *y, size_t y_row);
+
+/* Test hook: the per-token e4m3 activation quantization linear applies to
+ * x rows [x_row, x_row + rows) of width cols (FP8_ACT_E4M3), copied to host:
+ * q [rows, cols] codes, s [rows] scales. */
+int lx2v_hip_act_quant(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                       size_t cols, uint8_t *q, float *s);
+
+/* ---- sync / profiling (backend.rs:189-196) -------------------------------- */
+
+/* Backend::sync (backend.rs:189-190). */
+int lx2v_hip_sync(lx2v_hip_ctx *ctx);
+/* Per-kernel timing with HIP events on the context stream.  Off by default;
+ * LIGHTX2V_PROFILE=1 (any value but 0) at create time or this call turns it
+ * on (the reference's switch, crates/lightx2v-cpu/src/lib.rs:27-34). */
+int lx2v_hip_profile_enable(lx2v_hip_ctx *ctx, int on);
+/* Backend::profile_report (backend.rs:192-195): table of kernel, calls,
+ * total ms, mean us, share.  Synchronises.  Writes "" when nothing was
+ * recorded.  Truncates to cap-1 bytes. */
+int lx2v_hip_profile_report(lx2v_hip_ctx *ctx, char *out, size_t cap);
+/* Backend::profile_reset (backend.rs:196). */
+int lx2v_hip_profile_reset(lx2v_hip_ctx *ctx);
+/* Machine-readable form of one row of the report: calls and total
+ * milliseconds of kernel `name` (0, 0 if never recorded).  Synchronises. */
+int lx2v_hip_profile_kernel(lx2v_hip_ctx *ctx, const char *name, uint64_t *calls,
+                            double *total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

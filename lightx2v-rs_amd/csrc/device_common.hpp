@@ -1,0 +1,141 @@
+// device_common.hpp -- device-side helpers shared by every gfx950 kernel of
+// the quantized-linear backend: vector types, the e4m3 / bf16 codecs the
+// GEMMs and the dequant kernel share, buffer-resource loads and the GELU
+// epilogue.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lx2v {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- bf16 ------------------------------------------------------------------
+
+// f32 -> bf16 bits, round to nearest even, NaN kept quiet (bit-exact with the
+// host rule used at upload/download).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7FFFu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+    return __uint_as_float(h << 16);
+}
+
+// Two f32 -> packed bf16 pair (low half = a), RNE via the gfx950 conversion.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    f32x2_t v = {a, b};
+    bf16x2_t r = __builtin_convertvector(v, bf16x2_t);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// ---- e4m3 ------------------------------------------------------------------
+
+// quant.rs:409-420 bit for bit: exponent field 0 decodes m * 2^-12 (the
+// reference's value, not OCP's m * 2^-9), e=15/m=7 is +NaN (0x7FC00000).
+__device__ __forceinline__ float e4m3_ref_decode(uint32_t c) {
+    uint32_t e = (c >> 3) & 15u, m = c & 7u;
+    float mag;
+    if (e == 0) {
+        mag = (float)m * 0x1p-12f;
+    } else if (e == 15u && m == 7u) {
+        return __uint_as_float(0x7FC00000u);
+    } else {
+        mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    }
+    return (c & 0x80u) ? -mag : mag;
+}
+
+// OCP e4m3fn decode (what the fp8 MFMA sees): subnormals m * 2^-9.
+__device__ __forceinline__ float e4m3_ocp_decode(uint32_t c) {
+    uint32_t e = (c >> 3) & 15u, m = c & 7u;
+    float mag;
+    if (e == 0) {
+        mag = (float)m * 0x1p-9f;
+    } else if (e == 15u && m == 7u) {
+        return __uint_as_float(0x7FC00000u);
+    } else {
+        mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    }
+    return (c & 0x80u) ? -mag : mag;
+}
+
+// OCP e4m3fn encode, round to nearest even, |v| <= 448 (callers clamp).
+__device__ __forceinline__ uint32_t e4m3_ocp_encode(float v) {
+    uint32_t b = __float_as_uint(v);
+    uint32_t sign = (b >> 24) & 0x80u;
+    uint32_t ab = b & 0x7FFFFFFFu;
+    if (ab > 0x7F800000u) return 0x7Fu;
+    float a = __uint_as_float(ab);
+    if (a >= 0x1p-6f) {
+        ab += 0x7FFFFu + ((ab >> 20) & 1u);
+        int e8 = (int)(ab >> 23) - 120;
+        uint32_t m = (ab >> 20) & 7u;
+        if (e8 > 15 || (e8 == 15 && m == 7u)) return sign | 0x7Eu;
+        return sign | ((uint32_t)e8 << 3) | m;
+    }
+    return sign | (uint32_t)__builtin_rintf(a * 512.0f);
+}
+
+// Canonical weight encoder (see lx2v_hip_quantize_fp8): quant.rs:376-406 for
+// |v| >= 2^-6 -- where floor(log2|v|) is the exact binade exponent whatever
+// way a libm log2f rounds, so it is taken from the bits -- 0x08 for
+// 2^-7 < |v| < 2^-6, signed zero below.
+__device__ __forceinline__ uint32_t e4m3_canon_encode(float v) {
+    uint32_t b = __float_as_uint(v);
+    uint32_t sign = (b >> 24) & 0x80u;
+    float a = __builtin_fabsf(v);
+    if (!(a < 464.0f)) return sign | 0x7Eu;  // inf, NaN, >= 464 (quant.rs:382-385)
+    if (a < 0x1p-6f) return a > 0x1p-7f ? (sign | 0x08u) : sign;
+    int e = (int)((__float_as_uint(a) >> 23) & 0xFFu) - 127;  // exact floor(log2 a)
+    if (e > 8) return sign | 0x7Eu;
+    uint32_t exp = (uint32_t)(e + 7);
+    float p = __uint_as_float((uint32_t)(e + 127) << 23);
+    float t = (a / p - 1.0f) * 8.0f;
+    uint32_t mant = (uint32_t)__builtin_roundf(t);  // half away from zero, t in [0, 8]
+    if (mant >= 8u) {
+        if (exp >= 15u) return sign | 0x7Eu;
+        return sign | ((exp + 1u) << 3);
+    }
+    return sign | (exp << 3) | mant;
+}
+
+// ---- GELU (crates/lightx2v-cpu/src/lib.rs:151-153) --------------------------
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float c = 0.7978845608028654f;  // sqrt(2/pi) rounded to f32
+    return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+
+// ---- buffer resources ----------------------------------------------------------
+
+// A raw buffer descriptor: loads at byte offsets >= num_bytes return zero,
+// which is how the GEMMs zero-fill ragged M/N edges without branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t num_bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)num_bytes,
+                                             0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buffer_load_x4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ uint32_t buffer_load_x1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+// Offset that is always out of range (reads as zero).
+constexpr uint32_t kOob = 0x80000000u;
+
+}  // namespace lx2v

@@ -1,0 +1,338 @@
+// k_misc.hip -- the small kernels around the GEMMs: dtype conversion,
+// synthetic fill, weight dequantization (the bit-exact decode check),
+// per-token e4m3 activation quantization, and the device-side weight
+// quantizers (quant.rs:154-178, 423-447 and the symmetric Q4 layout).
+//
+// Built with -ffp-contract=off: the quantizers and the dequant must round
+// exactly like the reference's separate f32 multiply / divide / add.
+#include "device_common.hpp"
+#include "runtime.hpp"
+
+namespace lx2v {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+inline unsigned grid_for(size_t n, int per_block) {
+    size_t g = (n + per_block - 1) / per_block;
+    return (unsigned)(g > 0x7FFFFFFF ? 0x7FFFFFFF : (g == 0 ? 1 : g));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// ---- conversion ----------------------------------------------------------------
+
+__global__ void k_convert(const void *src, int sd, void *dst, int dd, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float v = sd == LX2V_DTYPE_BF16 ? bf16_bits_to_f32(((const uint16_t *)src)[i])
+                                        : ((const float *)src)[i];
+        if (dd == LX2V_DTYPE_BF16)
+            ((uint16_t *)dst)[i] = f32_to_bf16_bits(v);
+        else
+            ((float *)dst)[i] = v;
+    }
+}
+
+// ---- Rng::normal per element (rng.rs:39-54) --------------------------------------
+
+__device__ __forceinline__ uint64_t splitmix(uint64_t seed, uint64_t draw) {
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull * (draw + 2);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float u01(uint64_t z) {
+    return (float)(z >> 40) / 16777216.0f;
+}
+
+__global__ void k_fill_normal(void *dst, int dtype, size_t n, uint64_t seed, float std) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        uint64_t pair = i >> 1;
+        float u1 = fmaxf(u01(splitmix(seed, 2 * pair)), 1e-7f);
+        float u2 = u01(splitmix(seed, 2 * pair + 1));
+        float r = sqrtf(-2.0f * logf(u1));
+        float t = 6.2831854820251465f * u2;
+        float v = ((i & 1) ? r * sinf(t) : r * cosf(t)) * std;
+        if (dtype == LX2V_DTYPE_BF16)
+            ((uint16_t *)dst)[i] = f32_to_bf16_bits(v);
+        else
+            ((float *)dst)[i] = v;
+    }
+}
+
+// ---- dequantization (quant.rs:180-186, 294-303, 449-455) ----------------------
+
+__global__ void k_dequant(int fmt, const void *codes, const float *scales, const float *zeros,
+                          size_t group, size_t n, float *out) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float v;
+        if (fmt == LX2V_WFMT_F32) {
+            v = ((const float *)codes)[i];
+        } else if (fmt == LX2V_WFMT_Q8) {
+            v = (float)((const int8_t *)codes)[i] * scales[i / group];
+        } else if (fmt == LX2V_WFMT_Q4) {
+            uint32_t byte = ((const uint8_t *)codes)[i >> 1];
+            uint32_t c = (byte >> (4 * (i & 1))) & 15u;
+            size_t g = i / group;
+            v = ((float)c - zeros[g]) * scales[g];
+        } else {
+            v = e4m3_ref_decode(((const uint8_t *)codes)[i]) * scales[i / group];
+        }
+        out[i] = v;
+    }
+}
+
+// ---- per-token e4m3 activation quantization ---------------------------------------
+//
+// One workgroup per row.  amax = max|x|; inv = 448/amax, s = amax/448 (both
+// correctly rounded divisions; amax <= 2^-64 -> 1, 1); q = e4m3(clamp(x*inv,
+// -448, 448)) rounded to nearest even.  Rows up to kRegChunks*16*256 wide
+// stay in registers between the two passes.
+
+constexpr int kRegChunks = 4;  // 16-element chunks per thread kept in registers
+
+template <int DT>
+__device__ __forceinline__ void load16(const void *row, size_t c, float v[16]) {
+    if (DT == LX2V_DTYPE_BF16) {
+        const u32x4 *p = (const u32x4 *)((const uint16_t *)row + c * 16);
+        u32x4 a = p[0], b = p[1];
+        uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+        }
+    } else {
+        const f32x4 *p = (const f32x4 *)((const float *)row + c * 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            f32x4 a = p[j];
+            v[4 * j] = a.x;
+            v[4 * j + 1] = a.y;
+            v[4 * j + 2] = a.z;
+            v[4 * j + 3] = a.w;
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t quant4(const float *v, float inv) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float t = fminf(fmaxf(v[j] * inv, -448.0f), 448.0f);
+        r |= e4m3_ocp_encode(t) << (8 * j);
+    }
+    return r;
+}
+
+__device__ float block_max(float v, float *red) {
+    v = wave_max(v);
+    int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kThreads / 64; i++) r = fmaxf(r, red[i]);
+    return r;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_act_quant16(const void *x, size_t cols, uint8_t *q,
+                                                          float *scale) {
+    __shared__ float red[kThreads / 64];
+    const size_t row = blockIdx.x;
+    const void *xr = (const char *)x + row * cols * (DT == LX2V_DTYPE_BF16 ? 2 : 4);
+    const size_t nchunks = cols / 16;
+    float v[kRegChunks][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRegChunks; j++) {
+        size_t c = threadIdx.x + (size_t)j * kThreads;
+        if (c < nchunks) {
+            load16<DT>(xr, c, v[j]);
+#pragma unroll
+            for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(v[j][e]));
+        }
+    }
+    amax = block_max(amax, red);
+    float inv = 1.0f, s = 1.0f;
+    if (amax > 0x1p-64f) {
+        inv = 448.0f / amax;
+        s = amax / 448.0f;
+    }
+    u32x4 *qr = (u32x4 *)(q + row * cols);
+#pragma unroll
+    for (int j = 0; j < kRegChunks; j++) {
+        size_t c = threadIdx.x + (size_t)j * kThreads;
+        if (c < nchunks) {
+            u32x4 o;
+            o.x = quant4(&v[j][0], inv);
+            o.y = quant4(&v[j][4], inv);
+            o.z = quant4(&v[j][8], inv);
+            o.w = quant4(&v[j][12], inv);
+            qr[c] = o;
+        }
+    }
+    if (threadIdx.x == 0) scale[row] = s;
+}
+
+// Any width: two passes over the row from memory.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_act_quant_any(const void *x, size_t cols, uint8_t *q,
+                                                            float *scale) {
+    __shared__ float red[kThreads / 64];
+    const size_t row = blockIdx.x;
+    auto ld = [&](size_t c) -> float {
+        if (DT == LX2V_DTYPE_BF16) return bf16_bits_to_f32(((const uint16_t *)x)[row * cols + c]);
+        return ((const float *)x)[row * cols + c];
+    };
+    float amax = 0.0f;
+    for (size_t c = threadIdx.x; c < cols; c += kThreads) amax = fmaxf(amax, fabsf(ld(c)));
+    amax = block_max(amax, red);
+    float inv = 1.0f, s = 1.0f;
+    if (amax > 0x1p-64f) {
+        inv = 448.0f / amax;
+        s = amax / 448.0f;
+    }
+    for (size_t c = threadIdx.x; c < cols; c += kThreads) {
+        float t = fminf(fmaxf(ld(c) * inv, -448.0f), 448.0f);
+        q[row * cols + c] = (uint8_t)e4m3_ocp_encode(t);
+    }
+    if (threadIdx.x == 0) scale[row] = s;
+}
+
+// ---- weight quantizers: one wave per group -------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void k_quantize_q8(const float *src, size_t ngroups,
+                                                          size_t group, int8_t *q, float *scales) {
+    size_t g = blockIdx.x * (size_t)(kThreads / 64) + (threadIdx.x >> 6);
+    int lane = threadIdx.x & 63;
+    if (g >= ngroups) return;
+    const float *w = src + g * group;
+    float amax = 0.0f;
+    for (size_t i = lane; i < group; i += 64) amax = fmaxf(amax, fabsf(w[i]));
+    amax = wave_max(amax);
+    float s = amax > 0.0f ? amax / 127.0f : 1.0f;  // quant.rs:165
+    for (size_t i = lane; i < group; i += 64) {
+        float r = __builtin_roundf(w[i] / s);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);  // finite inputs: clamp == f32::clamp
+        q[g * group + i] = (int8_t)(int)r;
+    }
+    if (lane == 0) scales[g] = s;
+}
+
+__global__ __launch_bounds__(kThreads) void k_quantize_q4_sym(const float *src, size_t ngroups,
+                                                              size_t group, uint8_t *packed,
+                                                              float *scales, float *zeros) {
+    size_t g = blockIdx.x * (size_t)(kThreads / 64) + (threadIdx.x >> 6);
+    int lane = threadIdx.x & 63;
+    if (g >= ngroups) return;
+    const float *w = src + g * group;
+    float amax = 0.0f;
+    for (size_t i = lane; i < group; i += 64) amax = fmaxf(amax, fabsf(w[i]));
+    amax = wave_max(amax);
+    float s = amax > 0.0f ? amax / 7.0f : 1.0f;
+    for (size_t p = lane; p < group / 2; p += 64) {
+        float r0 = fminf(fmaxf(__builtin_roundf(w[2 * p] / s), -8.0f), 7.0f);
+        float r1 = fminf(fmaxf(__builtin_roundf(w[2 * p + 1] / s), -8.0f), 7.0f);
+        uint32_t c0 = (uint32_t)((int)r0 + 8), c1 = (uint32_t)((int)r1 + 8);
+        packed[(g * group) / 2 + p] = (uint8_t)(c0 | (c1 << 4));
+    }
+    if (lane == 0) {
+        scales[g] = s;
+        zeros[g] = 8.0f;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_quantize_fp8(const float *src, size_t ngroups,
+                                                           size_t group, uint8_t *q,
+                                                           float *scales) {
+    size_t g = blockIdx.x * (size_t)(kThreads / 64) + (threadIdx.x >> 6);
+    int lane = threadIdx.x & 63;
+    if (g >= ngroups) return;
+    const float *w = src + g * group;
+    float amax = 0.0f;
+    for (size_t i = lane; i < group; i += 64) amax = fmaxf(amax, fabsf(w[i]));
+    amax = wave_max(amax);
+    float s = amax > 0.0f ? amax / 448.0f : 1.0f;  // quant.rs:434
+    for (size_t i = lane; i < group; i += 64) q[g * group + i] = (uint8_t)e4m3_canon_encode(w[i] / s);
+    if (lane == 0) scales[g] = s;
+}
+
+}  // namespace
+
+void launch_convert(hipStream_t s, const void *src, int sd, void *dst, int dd, size_t n) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_convert, dim3(grid_for(n, kThreads * 4)), dim3(kThreads), 0, s, src, sd, dst,
+                       dd, n);
+}
+
+void launch_fill_normal(hipStream_t s, void *dst, int dtype, size_t n, uint64_t seed, float std) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_fill_normal, dim3(grid_for(n, kThreads * 4)), dim3(kThreads), 0, s, dst,
+                       dtype, n, seed, std);
+}
+
+void launch_dequant(hipStream_t s, const lx2v_hip_weight *w, const uint8_t *fp8_codes, float *out) {
+    size_t n = w->rows * w->cols;
+    if (n == 0) return;
+    const void *codes = w->fmt == LX2V_WFMT_FP8 ? (const void *)fp8_codes : w->codes;
+    hipLaunchKernelGGL(k_dequant, dim3(grid_for(n, kThreads * 4)), dim3(kThreads), 0, s, w->fmt,
+                       codes, w->scales, w->zeros, w->group ? w->group : 1, n, out);
+}
+
+void launch_act_quant(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols,
+                      uint8_t *q, float *scale) {
+    if (rows == 0) return;
+    bool fast = cols % 16 == 0 && cols <= (size_t)kRegChunks * 16 * kThreads;
+    if (dtype == LX2V_DTYPE_BF16) {
+        if (fast)
+            hipLaunchKernelGGL(k_act_quant16<LX2V_DTYPE_BF16>, dim3(rows), dim3(kThreads), 0, s, x,
+                               cols, q, scale);
+        else
+            hipLaunchKernelGGL(k_act_quant_any<LX2V_DTYPE_BF16>, dim3(rows), dim3(kThreads), 0, s, x,
+                               cols, q, scale);
+    } else {
+        if (fast)
+            hipLaunchKernelGGL(k_act_quant16<LX2V_DTYPE_F32>, dim3(rows), dim3(kThreads), 0, s, x,
+                               cols, q, scale);
+        else
+            hipLaunchKernelGGL(k_act_quant_any<LX2V_DTYPE_F32>, dim3(rows), dim3(kThreads), 0, s, x,
+                               cols, q, scale);
+    }
+}
+
+void launch_quantize_q8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,
+                        int8_t *q, float *scales) {
+    size_t ng = rows * cols / group;
+    if (ng == 0) return;
+    hipLaunchKernelGGL(k_quantize_q8, dim3(grid_for(ng, kThreads / 64)), dim3(kThreads), 0, s, src, ng,
+                       group, q, scales);
+}
+
+void launch_quantize_q4_sym(hipStream_t s, const float *src, size_t rows, size_t cols,
+                            size_t group, uint8_t *packed, float *scales, float *zeros) {
+    size_t ng = rows * cols / group;
+    if (ng == 0) return;
+    hipLaunchKernelGGL(k_quantize_q4_sym, dim3(grid_for(ng, kThreads / 64)), dim3(kThreads), 0, s, src,
+                       ng, group, packed, scales, zeros);
+}
+
+void launch_quantize_fp8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,
+                         uint8_t *q, float *scales) {
+    size_t ng = rows * cols / group;
+    if (ng == 0) return;
+    hipLaunchKernelGGL(k_quantize_fp8, dim3(grid_for(ng, kThreads / 64)), dim3(kThreads), 0, s, src,
+                       ng, group, q, scales);
+}
+
+}  // namespace lx2v

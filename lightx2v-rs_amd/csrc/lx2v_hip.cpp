@@ -1,0 +1,869 @@
+// lx2v_hip.cpp -- the C ABI of include/lightx2v_hip.h: context, buffers,
+// weights, the linear dispatch and the per-kernel profiler.  Each entry point
+// cites the Backend trait method it implements (crates/lightx2v-core/src/
+// backend.rs).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "runtime.hpp"
+
+using namespace lx2v;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(e == hipErrorOutOfMemory ? LX2V_ERR_OOM : LX2V_ERR_HIP, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+#define HIP_TRY(call, what)                     \
+    do {                                        \
+        hipError_t e_ = (call);                 \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+#define NEED(p, name) \
+    if (!(p)) return fail(LX2V_ERR_BAD_ARG, "%s is null", name)
+
+int ok() {
+    g_err.clear();
+    return LX2V_OK;
+}
+
+bool valid_dtype(int d) { return d == LX2V_DTYPE_F32 || d == LX2V_DTYPE_BF16; }
+
+// Device-side staging owned by the context for boundary conversions.
+struct Stage {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+int ensure(lx2v_hip_ctx *ctx, void **ptr, size_t *have, size_t need, const char *what) {
+    if (*have >= need) return LX2V_OK;
+    if (*ptr) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream), what);
+        HIP_TRY(hipFree(*ptr), what);
+        *ptr = nullptr;
+        *have = 0;
+    }
+    size_t sz = std::max<size_t>(need, 1 << 20);
+    HIP_TRY(hipMalloc(ptr, sz), what);
+    *have = sz;
+    return LX2V_OK;
+}
+
+// Byte ranges [a, a+na) and [b, b+nb) overlap.
+bool overlap(const void *a, size_t na, const void *b, size_t nb) {
+    uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return na && nb && x < y + nb && y < x + na;
+}
+
+int set_dev(const lx2v_hip_ctx *ctx) {
+    HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    return LX2V_OK;
+}
+
+// Context-owned staging buffer (one per context, grown on demand).
+struct CtxExtra {
+    Stage stage;
+};
+
+}  // namespace
+
+// Staging lives beside the context's workspace; stored in a side table keyed
+// by context so runtime.hpp stays free of it.
+#include <unordered_map>
+static std::unordered_map<const lx2v_hip_ctx *, CtxExtra> &extras() {
+    static std::unordered_map<const lx2v_hip_ctx *, CtxExtra> m;
+    return m;
+}
+
+namespace lx2v {
+
+void prof_begin(lx2v_hip_ctx *ctx, const char *name, hipEvent_t *a, hipEvent_t *b) {
+    auto &p = ctx->prof;
+    for (hipEvent_t *e : {a, b}) {
+        if (!p.pool.empty()) {
+            *e = p.pool.back();
+            p.pool.pop_back();
+        } else if (hipEventCreate(e) != hipSuccess) {
+            *e = nullptr;
+        }
+    }
+    if (*a) (void)hipEventRecord(*a, ctx->stream);
+    p.pending.push_back({name, *a, *b});
+}
+
+void prof_end(lx2v_hip_ctx *ctx, hipEvent_t b) {
+    if (b) (void)hipEventRecord(b, ctx->stream);
+}
+
+}  // namespace lx2v
+
+namespace {
+
+void prof_harvest(lx2v_hip_ctx *ctx) {
+    auto &p = ctx->prof;
+    if (p.pending.empty()) return;
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto &e : p.pending) {
+        float ms = 0.0f;
+        if (e.a && e.b && hipEventElapsedTime(&ms, e.a, e.b) == hipSuccess) {
+            auto &s = p.stats[e.name];
+            s.first += 1;
+            s.second += ms;
+        }
+        if (e.a) p.pool.push_back(e.a);
+        if (e.b) p.pool.push_back(e.b);
+    }
+    p.pending.clear();
+}
+
+template <class F>
+int run(lx2v_hip_ctx *ctx, const char *name, F &&fn) {
+    hipError_t e = timed(ctx, name, fn);
+    if (ctx->prof.on && ctx->prof.pending.size() > 8192) prof_harvest(ctx);
+    if (e != hipSuccess) return hip_fail(e, name);
+    return LX2V_OK;
+}
+
+int stage_for(lx2v_hip_ctx *ctx, size_t bytes, void **out) {
+    auto &st = extras()[ctx].stage;
+    int rc = ensure(ctx, &st.ptr, &st.bytes, bytes, "staging alloc");
+    if (rc) return rc;
+    *out = st.ptr;
+    return LX2V_OK;
+}
+
+int alloc_buf(lx2v_hip_ctx *ctx, size_t len, int dtype, lx2v_hip_buf **out) {
+    auto *b = new lx2v_hip_buf;
+    b->len = len;
+    b->dtype = dtype;
+    hipError_t e = hipMalloc(&b->ptr, std::max<size_t>(b->bytes(), 4));
+    if (e != hipSuccess) {
+        delete b;
+        return hip_fail(e, "hipMalloc(buffer)");
+    }
+    e = hipMemsetAsync(b->ptr, 0, std::max<size_t>(b->bytes(), 4), ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(b->ptr);
+        delete b;
+        return hip_fail(e, "hipMemsetAsync(buffer)");
+    }
+    *out = b;
+    return LX2V_OK;
+}
+
+// host f32 -> device buffer elements [off, off+len)
+int write_range(lx2v_hip_ctx *ctx, lx2v_hip_buf *b, size_t off, const float *data, size_t len) {
+    if (!len) return LX2V_OK;
+    if (b->dtype == LX2V_DTYPE_F32) {
+        HIP_TRY(hipMemcpyAsync((float *)b->ptr + off, data, len * 4, hipMemcpyHostToDevice, ctx->stream),
+                "hipMemcpyAsync(write)");
+        return LX2V_OK;
+    }
+    void *st;
+    int rc = stage_for(ctx, len * 4, &st);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(st, data, len * 4, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(write)");
+    return run(ctx, "convert", [&] {
+        launch_convert(ctx->stream, st, LX2V_DTYPE_F32, (uint16_t *)b->ptr + off, LX2V_DTYPE_BF16, len);
+    });
+}
+
+template <class T>
+int upload_raw(T **dst, const void *src, size_t bytes, hipStream_t s, const char *what) {
+    hipError_t e = hipMalloc((void **)dst, std::max<size_t>(bytes, 4));
+    if (e != hipSuccess) return hip_fail(e, what);
+    if (bytes) {
+        e = hipMemcpyAsync(*dst, src, bytes, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return hip_fail(e, what);
+    }
+    return LX2V_OK;
+}
+
+void free_weight(lx2v_hip_weight *w) {
+    if (!w) return;
+    if (w->codes) (void)hipFree(w->codes);
+    if (w->scales) (void)hipFree(w->scales);
+    if (w->zeros) (void)hipFree(w->zeros);
+    if (w->raw_e4m3) (void)hipFree(w->raw_e4m3);
+    delete w;
+}
+
+int check_quant_shape(size_t rows, size_t cols, size_t group) {
+    if (!rows || !cols) return fail(LX2V_ERR_BAD_SHAPE, "empty weight %zux%zu", rows, cols);
+    if (!group || cols % group)
+        return fail(LX2V_ERR_BAD_SHAPE, "group %zu does not divide cols %zu", group, cols);
+    return LX2V_OK;
+}
+
+}  // namespace
+
+// ============================================================================
+extern "C" {
+
+const char *lx2v_hip_last_error(void) { return g_err.c_str(); }
+
+int lx2v_hip_device_count(int *count) {
+    NEED(count, "count");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return ok();
+}
+
+int lx2v_hip_create(int device, lx2v_hip_ctx **out) {
+    NEED(out, "out");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(LX2V_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= n)
+        return fail(LX2V_ERR_NO_DEVICE, "device %d out of range (%d visible)", device, n);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(LX2V_ERR_NO_DEVICE, "device %d is %s, this build targets gfx950", device,
+                    prop.gcnArchName);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    auto *ctx = new lx2v_hip_ctx;
+    ctx->device = device;
+    ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    ctx->name = std::string("hip:") + prop.name + " (" + prop.gcnArchName + ")";
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_fail(e, "hipStreamCreate");
+    }
+    const char *pv = getenv("LIGHTX2V_PROFILE");
+    ctx->prof.on = pv && strcmp(pv, "0") != 0;
+    extras()[ctx];
+    *out = ctx;
+    return ok();
+}
+
+int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
+    if (!ctx) return ok();
+    set_dev(ctx);
+    (void)hipStreamSynchronize(ctx->stream);
+    prof_harvest(ctx);
+    for (auto e : ctx->prof.pool) (void)hipEventDestroy(e);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    auto &x = extras()[ctx];
+    if (x.stage.ptr) (void)hipFree(x.stage.ptr);
+    extras().erase(ctx);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return ok();
+}
+
+int lx2v_hip_name(const lx2v_hip_ctx *ctx, char *out, size_t cap) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (!cap) return fail(LX2V_ERR_BAD_ARG, "cap is 0");
+    snprintf(out, cap, "%s", ctx->name.c_str());
+    return ok();
+}
+
+int lx2v_hip_set_act_dtype(lx2v_hip_ctx *ctx, int dtype) {
+    NEED(ctx, "ctx");
+    if (!valid_dtype(dtype)) return fail(LX2V_ERR_BAD_ARG, "unknown dtype %d", dtype);
+    ctx->act_dtype = dtype;
+    return ok();
+}
+
+int lx2v_hip_set_fp8_act(lx2v_hip_ctx *ctx, int mode) {
+    NEED(ctx, "ctx");
+    if (mode != LX2V_FP8_ACT_E4M3 && mode != LX2V_FP8_ACT_BF16)
+        return fail(LX2V_ERR_BAD_ARG, "unknown fp8 activation mode %d", mode);
+    ctx->fp8_act = mode;
+    return ok();
+}
+
+// ---- buffers -------------------------------------------------------------------
+
+int lx2v_hip_alloc_dtype(lx2v_hip_ctx *ctx, size_t len, int dtype, lx2v_hip_buf **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (!valid_dtype(dtype)) return fail(LX2V_ERR_BAD_ARG, "unknown dtype %d", dtype);
+    if (int rc = set_dev(ctx)) return rc;
+    if (int rc = alloc_buf(ctx, len, dtype, out)) return rc;
+    return ok();
+}
+
+int lx2v_hip_alloc(lx2v_hip_ctx *ctx, size_t len, lx2v_hip_buf **out) {
+    NEED(ctx, "ctx");
+    return lx2v_hip_alloc_dtype(ctx, len, ctx->act_dtype, out);
+}
+
+int lx2v_hip_upload(lx2v_hip_ctx *ctx, const float *data, size_t len, lx2v_hip_buf **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (len) NEED(data, "data");
+    if (int rc = set_dev(ctx)) return rc;
+    lx2v_hip_buf *b = nullptr;
+    if (int rc = alloc_buf(ctx, len, ctx->act_dtype, &b)) return rc;
+    if (int rc = write_range(ctx, b, 0, data, len)) {
+        (void)hipFree(b->ptr);
+        delete b;
+        return rc;
+    }
+    *out = b;
+    return ok();
+}
+
+int lx2v_hip_write(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, const float *data, size_t len) {
+    NEED(ctx, "ctx");
+    NEED(buf, "buf");
+    if (len) NEED(data, "data");
+    if (len > buf->len) return fail(LX2V_ERR_BAD_SHAPE, "write of %zu elements into a buffer of %zu", len, buf->len);
+    if (int rc = set_dev(ctx)) return rc;
+    if (int rc = write_range(ctx, buf, 0, data, len)) return rc;
+    return ok();
+}
+
+int lx2v_hip_download(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, float *out, size_t len) {
+    NEED(ctx, "ctx");
+    NEED(buf, "buf");
+    if (len != buf->len) return fail(LX2V_ERR_BAD_SHAPE, "download of %zu elements from a buffer of %zu", len, buf->len);
+    if (len) NEED(out, "out");
+    if (int rc = set_dev(ctx)) return rc;
+    if (len) {
+        const void *src = buf->ptr;
+        if (buf->dtype == LX2V_DTYPE_BF16) {
+            void *st;
+            if (int rc = stage_for(ctx, len * 4, &st)) return rc;
+            if (int rc = run(ctx, "convert", [&] {
+                    launch_convert(ctx->stream, buf->ptr, LX2V_DTYPE_BF16, st, LX2V_DTYPE_F32, len);
+                }))
+                return rc;
+            src = st;
+        }
+        HIP_TRY(hipMemcpyAsync(out, src, len * 4, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(download)");
+    }
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(download)");
+    return ok();
+}
+
+int lx2v_hip_buf_len(const lx2v_hip_buf *buf, size_t *len) {
+    NEED(buf, "buf");
+    NEED(len, "len");
+    *len = buf->len;
+    return ok();
+}
+
+int lx2v_hip_buf_dtype(const lx2v_hip_buf *buf, int *dtype) {
+    NEED(buf, "buf");
+    NEED(dtype, "dtype");
+    *dtype = buf->dtype;
+    return ok();
+}
+
+int lx2v_hip_copy(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t src_off, lx2v_hip_buf *dst,
+                  size_t dst_off, size_t len) {
+    NEED(ctx, "ctx");
+    NEED(src, "src");
+    NEED(dst, "dst");
+    if (src_off > src->len || len > src->len - src_off || dst_off > dst->len || len > dst->len - dst_off)
+        return fail(LX2V_ERR_BAD_SHAPE, "copy [%zu,+%zu) -> [%zu,+%zu) out of range (%zu, %zu)", src_off, len,
+                    dst_off, len, src->len, dst->len);
+    if (!len) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    const char *s = (const char *)src->ptr + src_off * src->elem_bytes();
+    char *d = (char *)dst->ptr + dst_off * dst->elem_bytes();
+    if (src->dtype == dst->dtype) {
+        HIP_TRY(hipMemcpyAsync(d, s, len * src->elem_bytes(), hipMemcpyDeviceToDevice, ctx->stream),
+                "hipMemcpyAsync(copy)");
+        return ok();
+    }
+    if (int rc = run(ctx, "convert", [&] { launch_convert(ctx->stream, s, src->dtype, d, dst->dtype, len); }))
+        return rc;
+    return ok();
+}
+
+int lx2v_hip_buf_free(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf) {
+    NEED(ctx, "ctx");
+    if (!buf) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(free)");
+    (void)hipFree(buf->ptr);
+    delete buf;
+    return ok();
+}
+
+// ---- weights ---------------------------------------------------------------------
+
+int lx2v_hip_weight_f32(lx2v_hip_ctx *ctx, const float *data, size_t rows, size_t cols,
+                        lx2v_hip_weight **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    NEED(data, "data");
+    if (!rows || !cols) return fail(LX2V_ERR_BAD_SHAPE, "empty weight %zux%zu", rows, cols);
+    if (int rc = set_dev(ctx)) return rc;
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_F32;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = cols;
+    int rc = upload_raw((float **)&w->codes, data, rows * cols * 4, ctx->stream, "weight_f32");
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    w->device_bytes = rows * cols * 4;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload");
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_weight_q8(lx2v_hip_ctx *ctx, const int8_t *q, const float *scales, size_t rows,
+                       size_t cols, size_t group, lx2v_hip_weight **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    NEED(q, "q");
+    NEED(scales, "scales");
+    if (int rc = check_quant_shape(rows, cols, group)) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_Q8;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = group;
+    size_t n = rows * cols, ns = n / group;
+    int rc = upload_raw((int8_t **)&w->codes, q, n, ctx->stream, "weight_q8");
+    if (!rc) rc = upload_raw(&w->scales, scales, ns * 4, ctx->stream, "weight_q8 scales");
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    w->device_bytes = n + ns * 4;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload");
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_weight_q4(lx2v_hip_ctx *ctx, const uint8_t *codes, int packed, const float *scales,
+                       const float *zeros, size_t rows, size_t cols, size_t group,
+                       lx2v_hip_weight **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    NEED(codes, "codes");
+    NEED(scales, "scales");
+    NEED(zeros, "zeros");
+    if (int rc = check_quant_shape(rows, cols, group)) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    size_t n = rows * cols, np = (n + 1) / 2, ns = n / group;
+    std::vector<uint8_t> pk;
+    const uint8_t *src = codes;
+    if (!packed) {  // Q4::packed (quant.rs:305-311)
+        pk.resize(np);
+        for (size_t i = 0; i < n; i += 2) {
+            uint8_t lo = codes[i], hi = i + 1 < n ? codes[i + 1] : 0;
+            if (lo > 15 || hi > 15)
+                return fail(LX2V_ERR_BAD_ARG, "q4 code %u at %zu is not in 0..15", lo > 15 ? lo : hi,
+                            lo > 15 ? i : i + 1);
+            pk[i / 2] = (uint8_t)(lo | (hi << 4));
+        }
+        src = pk.data();
+    }
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_Q4;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = group;
+    int rc = upload_raw((uint8_t **)&w->codes, src, np, ctx->stream, "weight_q4");
+    if (!rc) rc = upload_raw(&w->scales, scales, ns * 4, ctx->stream, "weight_q4 scales");
+    if (!rc) rc = upload_raw(&w->zeros, zeros, ns * 4, ctx->stream, "weight_q4 zeros");
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    w->device_bytes = np + 2 * ns * 4;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload");  // pk must outlive the copy
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_weight_fp8(lx2v_hip_ctx *ctx, const uint8_t *q, const float *scales, size_t rows,
+                        size_t cols, size_t group, lx2v_hip_weight **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    NEED(q, "q");
+    NEED(scales, "scales");
+    if (int rc = check_quant_shape(rows, cols, group)) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    size_t n = rows * cols, ns = n / group;
+    // Exponent-0, non-zero-mantissa codes: the reference decodes m * 2^-12
+    // (quant.rs:413-414), the MFMA would decode m * 2^-9; store signed zero.
+    std::vector<uint8_t> canon;
+    size_t changed = 0;
+    for (size_t i = 0; i < n; i++)
+        if ((q[i] & 0x78) == 0 && (q[i] & 7) != 0) {
+            if (canon.empty()) canon.assign(q, q + n);
+            canon[i] = q[i] & 0x80;
+            changed++;
+        }
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_FP8;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = group;
+    w->canonicalized = changed;
+    int rc = upload_raw((uint8_t **)&w->codes, changed ? canon.data() : q, n, ctx->stream, "weight_fp8");
+    if (!rc && changed) rc = upload_raw(&w->raw_e4m3, q, n, ctx->stream, "weight_fp8 raw");
+    if (!rc) rc = upload_raw(&w->scales, scales, ns * 4, ctx->stream, "weight_fp8 scales");
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    w->device_bytes = n + ns * 4;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload");
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_weight_free(lx2v_hip_ctx *ctx, lx2v_hip_weight *w) {
+    NEED(ctx, "ctx");
+    if (!w) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(weight_free)");
+    free_weight(w);
+    return ok();
+}
+
+int lx2v_hip_weight_info(const lx2v_hip_weight *w, lx2v_hip_weight_info_t *info) {
+    NEED(w, "weight");
+    NEED(info, "info");
+    info->fmt = w->fmt;
+    info->rows = w->rows;
+    info->cols = w->cols;
+    info->group = w->group;
+    info->device_bytes = w->device_bytes;
+    info->canonicalized = w->canonicalized;
+    return ok();
+}
+
+int lx2v_hip_weight_dequantize(lx2v_hip_ctx *ctx, const lx2v_hip_weight *w, float *out, size_t len) {
+    NEED(ctx, "ctx");
+    NEED(w, "weight");
+    NEED(out, "out");
+    size_t n = w->rows * w->cols;
+    if (len != n) return fail(LX2V_ERR_BAD_SHAPE, "dequantize into %zu elements, weight has %zu", len, n);
+    if (int rc = set_dev(ctx)) return rc;
+    void *st;
+    if (int rc = stage_for(ctx, n * 4, &st)) return rc;
+    const uint8_t *fp8 = w->raw_e4m3 ? w->raw_e4m3 : (const uint8_t *)w->codes;
+    if (int rc = run(ctx, "dequant", [&] { launch_dequant(ctx->stream, w, fp8, (float *)st); })) return rc;
+    HIP_TRY(hipMemcpyAsync(out, st, n * 4, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(dequant)");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(dequant)");
+    return ok();
+}
+
+// ---- device quantizers -------------------------------------------------------------
+
+static int quant_src_check(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows, size_t cols,
+                           size_t group) {
+    NEED(ctx, "ctx");
+    NEED(src, "src");
+    if (src->dtype != LX2V_DTYPE_F32) return fail(LX2V_ERR_BAD_ARG, "quantizer source must be an f32 buffer");
+    if (int rc = check_quant_shape(rows, cols, group)) return rc;
+    if (rows * cols > src->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "source has %zu elements, %zux%zu needs %zu", src->len, rows, cols,
+                    rows * cols);
+    return set_dev(ctx);
+}
+
+int lx2v_hip_quantize_q8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows, size_t cols,
+                         size_t group, lx2v_hip_weight **out) {
+    NEED(out, "out");
+    if (int rc = quant_src_check(ctx, src, rows, cols, group)) return rc;
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_Q8;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = group;
+    size_t n = rows * cols, ns = n / group;
+    hipError_t e = hipMalloc(&w->codes, n);
+    if (e == hipSuccess) e = hipMalloc((void **)&w->scales, ns * 4);
+    if (e != hipSuccess) {
+        free_weight(w);
+        return hip_fail(e, "quantize_q8 alloc");
+    }
+    w->device_bytes = n + ns * 4;
+    int rc = run(ctx, "quantize_q8", [&] {
+        launch_quantize_q8(ctx->stream, (const float *)src->ptr, rows, cols, group, (int8_t *)w->codes, w->scales);
+    });
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_quantize_q4_sym(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows, size_t cols,
+                             size_t group, lx2v_hip_weight **out) {
+    NEED(out, "out");
+    if (int rc = quant_src_check(ctx, src, rows, cols, group)) return rc;
+    if (group % 2) return fail(LX2V_ERR_BAD_SHAPE, "q4 group %zu must be even", group);
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_Q4;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = group;
+    size_t n = rows * cols, ns = n / group;
+    hipError_t e = hipMalloc(&w->codes, n / 2);
+    if (e == hipSuccess) e = hipMalloc((void **)&w->scales, ns * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&w->zeros, ns * 4);
+    if (e != hipSuccess) {
+        free_weight(w);
+        return hip_fail(e, "quantize_q4 alloc");
+    }
+    w->device_bytes = n / 2 + 2 * ns * 4;
+    int rc = run(ctx, "quantize_q4", [&] {
+        launch_quantize_q4_sym(ctx->stream, (const float *)src->ptr, rows, cols, group, (uint8_t *)w->codes,
+                               w->scales, w->zeros);
+    });
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_quantize_fp8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows, size_t cols,
+                          size_t group, lx2v_hip_weight **out) {
+    NEED(out, "out");
+    if (int rc = quant_src_check(ctx, src, rows, cols, group)) return rc;
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_FP8;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = group;
+    size_t n = rows * cols, ns = n / group;
+    hipError_t e = hipMalloc(&w->codes, n);
+    if (e == hipSuccess) e = hipMalloc((void **)&w->scales, ns * 4);
+    if (e != hipSuccess) {
+        free_weight(w);
+        return hip_fail(e, "quantize_fp8 alloc");
+    }
+    w->device_bytes = n + ns * 4;
+    int rc = run(ctx, "quantize_fp8", [&] {
+        launch_quantize_fp8(ctx->stream, (const float *)src->ptr, rows, cols, group, (uint8_t *)w->codes,
+                            w->scales);
+    });
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std) {
+    NEED(ctx, "ctx");
+    NEED(buf, "buf");
+    if (int rc = set_dev(ctx)) return rc;
+    if (int rc = run(ctx, "fill_normal", [&] {
+            launch_fill_normal(ctx->stream, buf->ptr, buf->dtype, buf->len, seed, std);
+        }))
+        return rc;
+    return ok();
+}
+
+// ---- linear ----------------------------------------------------------------------
+
+static int act_quant_into_ws(lx2v_hip_ctx *ctx, const void *x, int dtype, size_t rows, size_t cols,
+                             uint8_t **q, float **s) {
+    size_t qbytes = (rows * cols + 255) & ~(size_t)255;
+    if (int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, qbytes + rows * 4, "workspace alloc")) return rc;
+    *q = (uint8_t *)ctx->ws;
+    *s = (float *)((uint8_t *)ctx->ws + qbytes);
+    return run(ctx, "act_quant_e4m3", [&] { launch_act_quant(ctx->stream, x, dtype, rows, cols, *q, *s); });
+}
+
+int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                    const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y,
+                    size_t y_row) {
+    NEED(ctx, "ctx");
+    NEED(x, "x");
+    NEED(w, "weight");
+    NEED(y, "y");
+    if (act != LX2V_ACT_NONE && act != LX2V_ACT_GELU_TANH) return fail(LX2V_ERR_BAD_ARG, "unknown act %d", act);
+    const size_t N = w->rows, K = w->cols;
+    if (x_row + rows < x_row || (x_row + rows) * K > x->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "x has %zu elements, rows [%zu,+%zu) x %zu need %zu", x->len, x_row, rows,
+                    K, (x_row + rows) * K);
+    if (y_row + rows < y_row || (y_row + rows) * N > y->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "y has %zu elements, rows [%zu,+%zu) x %zu need %zu", y->len, y_row, rows,
+                    N, (y_row + rows) * N);
+    if (bias && bias->len < N) return fail(LX2V_ERR_BAD_SHAPE, "bias has %zu elements, weight has %zu rows", bias->len, N);
+    const char *xp = (const char *)x->ptr + x_row * K * x->elem_bytes();
+    char *yp = (char *)y->ptr + y_row * N * y->elem_bytes();
+    if (overlap(yp, rows * N * y->elem_bytes(), xp, rows * K * x->elem_bytes()))
+        return fail(LX2V_ERR_ALIAS, "linear output overlaps its input");
+    if (bias && overlap(yp, rows * N * y->elem_bytes(), bias->ptr, N * bias->elem_bytes()))
+        return fail(LX2V_ERR_ALIAS, "linear output overlaps its bias");
+    if (!rows) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+
+    // The epilogue reads an f32 bias.
+    const float *bp = nullptr;
+    if (bias) {
+        if (bias->dtype == LX2V_DTYPE_F32) {
+            bp = (const float *)bias->ptr;
+        } else {
+            void *st;
+            if (int rc = stage_for(ctx, N * 4, &st)) return rc;
+            if (int rc = run(ctx, "convert", [&] {
+                    launch_convert(ctx->stream, bias->ptr, LX2V_DTYPE_BF16, st, LX2V_DTYPE_F32, N);
+                }))
+                return rc;
+            bp = (const float *)st;
+        }
+    }
+
+    if (w->fmt == LX2V_WFMT_FP8 && ctx->fp8_act == LX2V_FP8_ACT_E4M3) {
+        uint8_t *q;
+        float *s;
+        if (int rc = act_quant_into_ws(ctx, xp, x->dtype, rows, K, &q, &s)) return rc;
+        if (w->group == K && gemm_fp8_supported(rows, N, K)) {
+            if (int rc = run(ctx, "gemm_fp8_e4m3", [&] {
+                    launch_gemm_fp8(ctx->stream, ctx->num_cu, q, s, (const uint8_t *)w->codes, w->scales, bp, act,
+                                    yp, y->dtype, rows, N, K);
+                }))
+                return rc;
+        } else {
+            if (int rc = run(ctx, "gemm_generic", [&] {
+                    launch_gemm_generic(ctx->stream, q, A_E4M3, s, w, bp, act, yp, y->dtype, rows);
+                }))
+                return rc;
+        }
+        return ok();
+    }
+    if (w->fmt != LX2V_WFMT_F32 && gemm_w16_supported(w)) {
+        const char *name = w->fmt == LX2V_WFMT_Q8 ? "gemm_w16_q8" : w->fmt == LX2V_WFMT_Q4 ? "gemm_w16_q4" : "gemm_w16_fp8";
+        if (int rc = run(ctx, name, [&] {
+                launch_gemm_w16(ctx->stream, ctx->num_cu, xp, x->dtype, w, bp, act, yp, y->dtype, rows);
+            }))
+            return rc;
+        return ok();
+    }
+    if ((rows + 15) / 16 > 65535) return fail(LX2V_ERR_UNSUPPORTED, "rows %zu too many for the generic kernel", rows);
+    int amode = x->dtype == LX2V_DTYPE_BF16 ? A_BF16 : A_F32;
+    if (int rc = run(ctx, "gemm_generic", [&] {
+            launch_gemm_generic(ctx->stream, xp, amode, nullptr, w, bp, act, yp, y->dtype, rows);
+        }))
+        return rc;
+    return ok();
+}
+
+int lx2v_hip_act_quant(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows, size_t cols,
+                       uint8_t *q, float *s) {
+    NEED(ctx, "ctx");
+    NEED(x, "x");
+    if (rows) {
+        NEED(q, "q");
+        NEED(s, "s");
+    }
+    if ((x_row + rows) * cols > x->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "x has %zu elements, rows [%zu,+%zu) x %zu", x->len, x_row, rows, cols);
+    if (!rows || !cols) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    uint8_t *dq;
+    float *ds;
+    const char *xp = (const char *)x->ptr + x_row * cols * x->elem_bytes();
+    if (int rc = act_quant_into_ws(ctx, xp, x->dtype, rows, cols, &dq, &ds)) return rc;
+    HIP_TRY(hipMemcpyAsync(q, dq, rows * cols, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(act_quant)");
+    HIP_TRY(hipMemcpyAsync(s, ds, rows * 4, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(act_quant)");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(act_quant)");
+    return ok();
+}
+
+// ---- sync / profile ----------------------------------------------------------------
+
+int lx2v_hip_sync(lx2v_hip_ctx *ctx) {
+    NEED(ctx, "ctx");
+    if (int rc = set_dev(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return ok();
+}
+
+int lx2v_hip_profile_enable(lx2v_hip_ctx *ctx, int on) {
+    NEED(ctx, "ctx");
+    if (!on) prof_harvest(ctx);
+    ctx->prof.on = on != 0;
+    return ok();
+}
+
+int lx2v_hip_profile_report(lx2v_hip_ctx *ctx, char *out, size_t cap) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (!cap) return fail(LX2V_ERR_BAD_ARG, "cap is 0");
+    if (int rc = set_dev(ctx)) return rc;
+    prof_harvest(ctx);
+    std::string s;
+    if (!ctx->prof.stats.empty()) {
+        std::vector<std::pair<std::string, std::pair<uint64_t, double>>> rows(ctx->prof.stats.begin(),
+                                                                              ctx->prof.stats.end());
+        std::sort(rows.begin(), rows.end(), [](auto &a, auto &b) { return a.second.second > b.second.second; });
+        double total = 0;
+        for (auto &r : rows) total += r.second.second;
+        char line[256];
+        s += "hip profile (HIP events per kernel on the context stream):\n";
+        s += "kernel              calls      total_ms   mean_us   share\n";
+        for (auto &r : rows) {
+            snprintf(line, sizeof line, "%-18s %8llu %12.3f %9.1f %6.1f%%\n", r.first.c_str(),
+                     (unsigned long long)r.second.first, r.second.second, r.second.second * 1e3 / r.second.first,
+                     total > 0 ? r.second.second / total * 100.0 : 0.0);
+            s += line;
+        }
+        snprintf(line, sizeof line, "profile total: %.3f ms\n", total);
+        s += line;
+    }
+    snprintf(out, cap, "%s", s.c_str());
+    return ok();
+}
+
+int lx2v_hip_profile_reset(lx2v_hip_ctx *ctx) {
+    NEED(ctx, "ctx");
+    prof_harvest(ctx);
+    ctx->prof.stats.clear();
+    return ok();
+}
+
+int lx2v_hip_profile_kernel(lx2v_hip_ctx *ctx, const char *name, uint64_t *calls, double *total_ms) {
+    NEED(ctx, "ctx");
+    NEED(name, "name");
+    NEED(calls, "calls");
+    NEED(total_ms, "total_ms");
+    if (int rc = set_dev(ctx)) return rc;
+    prof_harvest(ctx);
+    auto it = ctx->prof.stats.find(name);
+    *calls = it == ctx->prof.stats.end() ? 0 : it->second.first;
+    *total_ms = it == ctx->prof.stats.end() ? 0.0 : it->second.second;
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,129 @@
+// runtime.hpp -- host-side objects behind the C ABI (context, buffers,
+// weights) and the launchers each kernel translation unit exports.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/lightx2v_hip.h"
+
+struct lx2v_hip_buf {
+    void *ptr = nullptr;
+    size_t len = 0;    // elements
+    int dtype = LX2V_DTYPE_F32;
+    size_t elem_bytes() const { return dtype == LX2V_DTYPE_BF16 ? 2 : 4; }
+    size_t bytes() const { return len * elem_bytes(); }
+};
+
+struct lx2v_hip_weight {
+    int fmt = LX2V_WFMT_F32;
+    size_t rows = 0, cols = 0, group = 0;
+    void *codes = nullptr;    // f32 [rows*cols] | i8 [rows*cols] | packed u8 [rows*cols/2] | e4m3 [rows*cols]
+    float *scales = nullptr;  // [rows * cols/group]
+    float *zeros = nullptr;   // Q4 only
+    uint8_t *raw_e4m3 = nullptr;  // FP8: codes exactly as passed in (for the dequant hook), only
+                                  // kept when canonicalization changed a code
+    size_t device_bytes = 0;
+    size_t canonicalized = 0;
+};
+
+namespace lx2v {
+
+// Per-kernel timing (Backend::profile_report).
+struct Profiler {
+    bool on = false;
+    struct Pending {
+        std::string name;
+        hipEvent_t a, b;
+    };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> pool;
+    std::map<std::string, std::pair<uint64_t, double>> stats;  // calls, total ms
+};
+
+}  // namespace lx2v
+
+struct lx2v_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+    int act_dtype = LX2V_DTYPE_F32;
+    int fp8_act = LX2V_FP8_ACT_E4M3;
+    int num_cu = 256;
+    // Workspace: per-token e4m3 activations + row scales (grown on demand).
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    lx2v::Profiler prof;
+};
+
+namespace lx2v {
+
+// Records `name` around the kernels `fn` enqueues when profiling is on.
+template <class F>
+hipError_t timed(lx2v_hip_ctx *ctx, const char *name, F &&fn);
+
+void prof_begin(lx2v_hip_ctx *ctx, const char *name, hipEvent_t *a, hipEvent_t *b);
+void prof_end(lx2v_hip_ctx *ctx, hipEvent_t b);
+
+template <class F>
+hipError_t timed(lx2v_hip_ctx *ctx, const char *name, F &&fn) {
+    if (!ctx->prof.on) {
+        fn();
+        return hipGetLastError();
+    }
+    hipEvent_t a = nullptr, b = nullptr;
+    prof_begin(ctx, name, &a, &b);
+    fn();
+    hipError_t e = hipGetLastError();
+    prof_end(ctx, b);
+    return e;
+}
+
+// ---- launchers (k_misc.hip) -------------------------------------------------
+void launch_convert(hipStream_t s, const void *src, int src_dtype, void *dst, int dst_dtype,
+                    size_t n);
+void launch_f32_to_bf16(hipStream_t s, const float *src, uint16_t *dst, size_t n);
+void launch_fill_normal(hipStream_t s, void *dst, int dtype, size_t n, uint64_t seed, float std);
+void launch_dequant(hipStream_t s, const lx2v_hip_weight *w, const uint8_t *fp8_codes, float *out);
+void launch_fp8_canon_count(hipStream_t s, uint8_t *codes, size_t n, unsigned long long *count);
+void launch_q4_pack(hipStream_t s, const uint8_t *codes, size_t n, uint8_t *packed);
+void launch_act_quant(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols,
+                      uint8_t *q, float *scale);
+void launch_quantize_q8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,
+                        int8_t *q, float *scales);
+void launch_quantize_q4_sym(hipStream_t s, const float *src, size_t rows, size_t cols,
+                            size_t group, uint8_t *packed, float *scales, float *zeros);
+void launch_quantize_fp8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,
+                         uint8_t *q, float *scales);
+
+// ---- GEMM launchers -----------------------------------------------------------
+// Y[m, n] = act(sum_k A[m,k] B[n,k] * scales + bias[n]); A/Y already offset to
+// the first row.  Return false when the shape is not served by that kernel.
+
+// Activation operand of the generic GEMM.
+enum AMode { A_F32 = 0, A_BF16 = 1, A_E4M3 = 2 };
+
+// k_gemm_generic.hip: any shape, any weight format (the correctness path
+// for ragged / tiny shapes).
+void launch_gemm_generic(hipStream_t s, const void *a, int amode, const float *a_scale,
+                         const lx2v_hip_weight *w, const float *bias, int act, void *y,
+                         int y_dtype, size_t M);
+
+// k_gemm_fp8.hip: fp8 MFMA, per-output-channel weight scale (group == K).
+bool gemm_fp8_supported(size_t M, size_t N, size_t K);
+void launch_gemm_fp8(hipStream_t s, int num_cu, const uint8_t *a, const float *a_scale,
+                     const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
+                     int y_dtype, size_t M, size_t N, size_t K);
+
+// k_gemm_w16.hip: bf16 MFMA with the weight dequantized to bf16 in the
+// tile loader (Q8, Q4, FP8 with any group that is a multiple of 32).
+bool gemm_w16_supported(const lx2v_hip_weight *w);
+void launch_gemm_w16(hipStream_t s, int num_cu, const void *x, int x_dtype,
+                     const lx2v_hip_weight *w, const float *bias, int act, void *y, int y_dtype,
+                     size_t M);
+
+}  // namespace lx2v

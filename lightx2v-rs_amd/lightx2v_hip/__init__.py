@@ -1,0 +1,343 @@
+"""Python binding of the gfx950 quantized-linear backend (liblightx2v_hip.so).
+
+``HipBackend`` mirrors the lightx2v-rs ``Backend`` trait's linear path
+(crates/lightx2v-core/src/backend.rs:145-212) method for method, over the C
+ABI declared in include/lightx2v_hip.h, the same surface a ``lightx2v-hip``
+Rust crate binds.  Misuse raises ``HipError`` (the trait panics);
+``HipBackend.try_new`` returns None when no gfx950 device answers, like
+``WgpuBackend::try_new`` (crates/lightx2v-wgpu/src/lib.rs:282-287).
+
+There is no fallback: if the shared library is missing, importing this module
+raises, and every op runs the library's HIP kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblightx2v_hip.so")
+
+OK, ERR_NO_DEVICE, ERR_BAD_SHAPE, ERR_ALIAS, ERR_HIP, ERR_BAD_ARG, ERR_OOM, ERR_UNSUPPORTED = range(8)
+ACT_NONE, ACT_GELU_TANH = 0, 1
+DTYPE_F32, DTYPE_BF16 = 0, 1
+WFMT_F32, WFMT_Q8, WFMT_Q4, WFMT_FP8 = 0, 1, 2, 3
+FP8_ACT_E4M3, FP8_ACT_BF16 = 0, 1
+
+# Every entry point include/lightx2v_hip.h declares (checked by the tests).
+EXPORTS = [
+    "lx2v_hip_last_error", "lx2v_hip_device_count", "lx2v_hip_create", "lx2v_hip_destroy",
+    "lx2v_hip_name", "lx2v_hip_set_act_dtype", "lx2v_hip_set_fp8_act", "lx2v_hip_alloc",
+    "lx2v_hip_alloc_dtype", "lx2v_hip_upload", "lx2v_hip_write", "lx2v_hip_download",
+    "lx2v_hip_buf_len", "lx2v_hip_buf_dtype", "lx2v_hip_copy", "lx2v_hip_buf_free",
+    "lx2v_hip_weight_f32", "lx2v_hip_weight_q8", "lx2v_hip_weight_q4", "lx2v_hip_weight_fp8",
+    "lx2v_hip_weight_free", "lx2v_hip_weight_info", "lx2v_hip_weight_dequantize",
+    "lx2v_hip_quantize_q8", "lx2v_hip_quantize_q4_sym", "lx2v_hip_quantize_fp8",
+    "lx2v_hip_fill_normal", "lx2v_hip_linear", "lx2v_hip_act_quant", "lx2v_hip_sync",
+    "lx2v_hip_profile_enable", "lx2v_hip_profile_report", "lx2v_hip_profile_reset",
+    "lx2v_hip_profile_kernel",
+]
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"lightx2v-hip status {status}: {msg}")
+        self.status = status
+
+
+class _WeightInfo(ctypes.Structure):
+    _fields_ = [("fmt", ctypes.c_int), ("rows", ctypes.c_size_t), ("cols", ctypes.c_size_t),
+                ("group", ctypes.c_size_t), ("device_bytes", ctypes.c_size_t),
+                ("canonicalized", ctypes.c_size_t)]
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built (run __graft_entry__.build() or make -C lightx2v-rs_amd)")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, sz, ip = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+    pp = ctypes.POINTER(ctypes.c_void_p)
+    sig = {
+        "lx2v_hip_last_error": (ctypes.c_char_p, []),
+        "lx2v_hip_device_count": (ip, [ctypes.POINTER(ctypes.c_int)]),
+        "lx2v_hip_create": (ip, [ip, pp]),
+        "lx2v_hip_destroy": (ip, [vp]),
+        "lx2v_hip_name": (ip, [vp, ctypes.c_char_p, sz]),
+        "lx2v_hip_set_act_dtype": (ip, [vp, ip]),
+        "lx2v_hip_set_fp8_act": (ip, [vp, ip]),
+        "lx2v_hip_alloc": (ip, [vp, sz, pp]),
+        "lx2v_hip_alloc_dtype": (ip, [vp, sz, ip, pp]),
+        "lx2v_hip_upload": (ip, [vp, vp, sz, pp]),
+        "lx2v_hip_write": (ip, [vp, vp, vp, sz]),
+        "lx2v_hip_download": (ip, [vp, vp, vp, sz]),
+        "lx2v_hip_buf_len": (ip, [vp, ctypes.POINTER(ctypes.c_size_t)]),
+        "lx2v_hip_buf_dtype": (ip, [vp, ctypes.POINTER(ctypes.c_int)]),
+        "lx2v_hip_copy": (ip, [vp, vp, sz, vp, sz, sz]),
+        "lx2v_hip_buf_free": (ip, [vp, vp]),
+        "lx2v_hip_weight_f32": (ip, [vp, vp, sz, sz, pp]),
+        "lx2v_hip_weight_q8": (ip, [vp, vp, vp, sz, sz, sz, pp]),
+        "lx2v_hip_weight_q4": (ip, [vp, vp, ip, vp, vp, sz, sz, sz, pp]),
+        "lx2v_hip_weight_fp8": (ip, [vp, vp, vp, sz, sz, sz, pp]),
+        "lx2v_hip_weight_free": (ip, [vp, vp]),
+        "lx2v_hip_weight_info": (ip, [vp, ctypes.POINTER(_WeightInfo)]),
+        "lx2v_hip_weight_dequantize": (ip, [vp, vp, vp, sz]),
+        "lx2v_hip_quantize_q8": (ip, [vp, vp, sz, sz, sz, pp]),
+        "lx2v_hip_quantize_q4_sym": (ip, [vp, vp, sz, sz, sz, pp]),
+        "lx2v_hip_quantize_fp8": (ip, [vp, vp, sz, sz, sz, pp]),
+        "lx2v_hip_fill_normal": (ip, [vp, vp, ctypes.c_uint64, ctypes.c_float]),
+        "lx2v_hip_linear": (ip, [vp, vp, sz, sz, vp, vp, ip, vp, sz]),
+        "lx2v_hip_act_quant": (ip, [vp, vp, sz, sz, sz, vp, vp]),
+        "lx2v_hip_sync": (ip, [vp]),
+        "lx2v_hip_profile_enable": (ip, [vp, ip]),
+        "lx2v_hip_profile_report": (ip, [vp, ctypes.c_char_p, sz]),
+        "lx2v_hip_profile_reset": (ip, [vp]),
+        "lx2v_hip_profile_kernel": (ip, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64),
+                                         ctypes.POINTER(ctypes.c_double)]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    return L
+
+
+lib = _load()
+
+
+def _check(rc: int):
+    if rc != OK:
+        raise HipError(rc, lib.lx2v_hip_last_error().decode())
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    _check(lib.lx2v_hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+class Buf:
+    """The trait's ``Buf``: a flat device buffer of activations."""
+
+    def __init__(self, be: "HipBackend", h: int):
+        self._be, self.h = be, h
+
+    def __len__(self) -> int:
+        n = ctypes.c_size_t(0)
+        _check(lib.lx2v_hip_buf_len(self.h, ctypes.byref(n)))
+        return n.value
+
+    @property
+    def dtype(self) -> int:
+        d = ctypes.c_int(0)
+        _check(lib.lx2v_hip_buf_dtype(self.h, ctypes.byref(d)))
+        return d.value
+
+    def free(self):
+        if self.h and self._be.ctx:
+            lib.lx2v_hip_buf_free(self._be.ctx, self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Weight:
+    """The trait's ``Weight``: a quantized (or f32) matrix resident in HBM."""
+
+    def __init__(self, be: "HipBackend", h: int):
+        self._be, self.h = be, h
+
+    def info(self) -> dict:
+        i = _WeightInfo()
+        _check(lib.lx2v_hip_weight_info(self.h, ctypes.byref(i)))
+        return {f: getattr(i, f) for f, _ in _WeightInfo._fields_}
+
+    def free(self):
+        if self.h and self._be.ctx:
+            lib.lx2v_hip_weight_free(self._be.ctx, self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HipBackend:
+    """lightx2v-rs ``Backend`` (linear path) on one gfx950 device."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_create(device, ctypes.byref(h)))
+        self.ctx = h.value
+
+    @classmethod
+    def try_new(cls, device: int = 0) -> Optional["HipBackend"]:
+        try:
+            return cls(device)
+        except HipError as e:
+            if e.status == ERR_NO_DEVICE:
+                return None
+            raise
+
+    def close(self):
+        if self.ctx:
+            lib.lx2v_hip_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- backend.rs:158-196 ----
+    def name(self) -> str:
+        b = ctypes.create_string_buffer(256)
+        _check(lib.lx2v_hip_name(self.ctx, b, 256))
+        return b.value.decode()
+
+    def set_act_dtype(self, dtype: int):
+        _check(lib.lx2v_hip_set_act_dtype(self.ctx, dtype))
+
+    def set_fp8_act(self, mode: int):
+        _check(lib.lx2v_hip_set_fp8_act(self.ctx, mode))
+
+    def _out(self):
+        return ctypes.c_void_p()
+
+    def alloc(self, n: int, dtype: Optional[int] = None) -> Buf:
+        h = ctypes.c_void_p()
+        if dtype is None:
+            _check(lib.lx2v_hip_alloc(self.ctx, n, ctypes.byref(h)))
+        else:
+            _check(lib.lx2v_hip_alloc_dtype(self.ctx, n, dtype, ctypes.byref(h)))
+        return Buf(self, h.value)
+
+    def upload(self, data) -> Buf:
+        a = np.ascontiguousarray(data, np.float32).ravel()
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_upload(self.ctx, _ptr(a), a.size, ctypes.byref(h)))
+        return Buf(self, h.value)
+
+    def write(self, buf: Buf, data):
+        a = np.ascontiguousarray(data, np.float32).ravel()
+        _check(lib.lx2v_hip_write(self.ctx, buf.h, _ptr(a), a.size))
+
+    def download(self, buf: Buf) -> np.ndarray:
+        out = np.empty(len(buf), np.float32)
+        _check(lib.lx2v_hip_download(self.ctx, buf.h, _ptr(out), out.size))
+        return out
+
+    def buf_len(self, buf: Buf) -> int:
+        return len(buf)
+
+    def copy(self, src: Buf, src_off: int, dst: Buf, dst_off: int, n: int):
+        _check(lib.lx2v_hip_copy(self.ctx, src.h, src_off, dst.h, dst_off, n))
+
+    def weight(self, data, rows: int, cols: int) -> Weight:
+        a = np.ascontiguousarray(data, np.float32).ravel()
+        if a.size != rows * cols:
+            raise HipError(ERR_BAD_SHAPE, f"weight has {a.size} elements, {rows}x{cols} expected")
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_weight_f32(self.ctx, _ptr(a), rows, cols, ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def weight_q8(self, q, scales, rows: int, cols: int, group: int) -> Weight:
+        qa = np.ascontiguousarray(q, np.int8).ravel()
+        sa = np.ascontiguousarray(scales, np.float32).ravel()
+        if qa.size != rows * cols or sa.size != rows * cols // group:
+            raise HipError(ERR_BAD_SHAPE, "q8 codes/scales do not match the shape")
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_weight_q8(self.ctx, _ptr(qa), _ptr(sa), rows, cols, group, ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def weight_q4(self, codes, scales, zeros, rows: int, cols: int, group: int,
+                  packed: bool = False) -> Weight:
+        ca = np.ascontiguousarray(codes, np.uint8).ravel()
+        sa = np.ascontiguousarray(scales, np.float32).ravel()
+        za = np.ascontiguousarray(zeros, np.float32).ravel()
+        need = (rows * cols + 1) // 2 if packed else rows * cols
+        if ca.size != need or sa.size != rows * cols // group or za.size != sa.size:
+            raise HipError(ERR_BAD_SHAPE, "q4 codes/scales/zeros do not match the shape")
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_weight_q4(self.ctx, _ptr(ca), int(packed), _ptr(sa), _ptr(za), rows, cols,
+                                      group, ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def weight_fp8(self, q, scales, rows: int, cols: int, group: int) -> Weight:
+        qa = np.ascontiguousarray(q, np.uint8).ravel()
+        sa = np.ascontiguousarray(scales, np.float32).ravel()
+        if qa.size != rows * cols or sa.size != rows * cols // group:
+            raise HipError(ERR_BAD_SHAPE, "fp8 codes/scales do not match the shape")
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_weight_fp8(self.ctx, _ptr(qa), _ptr(sa), rows, cols, group, ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def dequantize(self, w: Weight) -> np.ndarray:
+        i = w.info()
+        out = np.empty(i["rows"] * i["cols"], np.float32)
+        _check(lib.lx2v_hip_weight_dequantize(self.ctx, w.h, _ptr(out), out.size))
+        return out.reshape(i["rows"], i["cols"])
+
+    def quantize_q8(self, src: Buf, rows: int, cols: int, group: int) -> Weight:
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_quantize_q8(self.ctx, src.h, rows, cols, group, ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def quantize_q4_sym(self, src: Buf, rows: int, cols: int, group: int) -> Weight:
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_quantize_q4_sym(self.ctx, src.h, rows, cols, group, ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def quantize_fp8(self, src: Buf, rows: int, cols: int, group: int) -> Weight:
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_quantize_fp8(self.ctx, src.h, rows, cols, group, ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def fill_normal(self, buf: Buf, seed: int, std: float):
+        _check(lib.lx2v_hip_fill_normal(self.ctx, buf.h, ctypes.c_uint64(seed), ctypes.c_float(std)))
+
+    def linear(self, x: Buf, x_row: int, rows: int, w: Weight, bias: Optional[Buf], act: int,
+               y: Buf, y_row: int):
+        _check(lib.lx2v_hip_linear(self.ctx, x.h, x_row, rows, w.h, bias.h if bias else None, act, y.h,
+                                   y_row))
+
+    def act_quant(self, x: Buf, x_row: int, rows: int, cols: int):
+        q = np.empty((rows, cols), np.uint8)
+        s = np.empty(rows, np.float32)
+        _check(lib.lx2v_hip_act_quant(self.ctx, x.h, x_row, rows, cols, _ptr(q), _ptr(s)))
+        return q, s
+
+    def sync(self):
+        _check(lib.lx2v_hip_sync(self.ctx))
+
+    def profile_enable(self, on: bool = True):
+        _check(lib.lx2v_hip_profile_enable(self.ctx, int(on)))
+
+    def profile_report(self) -> Optional[str]:
+        b = ctypes.create_string_buffer(1 << 16)
+        _check(lib.lx2v_hip_profile_report(self.ctx, b, 1 << 16))
+        s = b.value.decode()
+        return s or None
+
+    def profile_reset(self):
+        _check(lib.lx2v_hip_profile_reset(self.ctx))
+
+    def profile_kernel(self, name: str):
+        c = ctypes.c_uint64(0)
+        t = ctypes.c_double(0.0)
+        _check(lib.lx2v_hip_profile_kernel(self.ctx, name.encode(), ctypes.byref(c), ctypes.byref(t)))
+        return c.value, t.value

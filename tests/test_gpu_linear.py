@@ -1,0 +1,257 @@
+"""Backend::linear (crates/lightx2v-core/src/backend.rs:198-212) on the gfx950
+kernels against the CPU oracle (crates/lightx2v-cpu/src/lib.rs:296-326).
+
+Tolerances (rel-L2 over the output, max-abs as a fraction of max|y|):
+  * against the oracle applied to the same rounded operands the device
+    contracts (per-token e4m3 activations for FP8; bf16 activations and
+    bf16-rounded dequantized weights for the bf16-MFMA path):
+    rel-L2 <= 1e-5, max-abs <= 1e-4 * max|y|  (only the summation order and
+    where the scales are applied differ);
+  * against the plain f32 oracle on the unrounded activations: FP8 (e4m3
+    activations, 3 mantissa bits) rel-L2 <= 4e-2 (measured ~2.6e-2);
+    bf16 paths rel-L2 <= 5e-3 (measured ~2.3e-3);
+  * bf16 outputs add one bf16 rounding: rel-L2 <= 4e-3 against the oracle.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import lightx2v_hip as H
+import oracle as O
+from helpers import (assert_close, fp8_weight, normal, oracle_w16, oracle_w8a8, q4_sym_weight,
+                     q8_weight, u32)
+
+pytestmark = pytest.mark.gpu
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "quant_kats.json")))
+
+TIGHT = (1e-5, 1e-4)
+
+
+def run_linear(be, x, w, bias, act, y_dtype=H.DTYPE_F32, x_dtype=H.DTYPE_F32, x_row=0, y_row=0,
+               rows=None):
+    M, K = x.shape
+    n = w.info()["rows"]
+    rows = M - x_row if rows is None else rows
+    be.set_act_dtype(x_dtype)
+    try:
+        xb = be.upload(x)
+        bb = be.upload(bias) if bias is not None else None
+    finally:
+        be.set_act_dtype(H.DTYPE_F32)
+    yb = be.alloc((y_row + rows) * n, y_dtype)
+    be.linear(xb, x_row, rows, w, bb, act, yb, y_row)
+    return be.download(yb).reshape(y_row + rows, n)[y_row:]
+
+
+def test_check_linear_f32_weight(be):
+    """check.rs:74-103's hand case, tol 1e-6 (wgpu measured 0.0)."""
+    g = GOLD["check_linear"]
+    w = be.weight(np.array(g["w"], np.float32), g["n"], g["k"])
+    y = run_linear(be, np.array(g["x"], np.float32).reshape(g["rows"], g["k"]), w,
+                   np.array(g["b"], np.float32), H.ACT_NONE)
+    assert np.max(np.abs(y.ravel() - np.array(g["want"]))) <= g["tolerance"]
+
+
+# ---- FP8 per-output-channel: per-token e4m3 activations, fp8 MFMA ----------------------
+
+FP8_SHAPES = [(64, 256, 192), (77, 272, 130), (300, 1536, 1536), (1, 128, 64), (257, 384, 513),
+              (520, 1024, 640)]
+
+
+@pytest.mark.parametrize("M,K,N", FP8_SHAPES)
+def test_fp8_channel_vs_oracle(be, M, K, N):
+    x = normal(1001 + M, M * K).reshape(M, K)
+    _, q, s = fp8_weight(1002 + N, N, K, K)
+    b = normal(1003, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, K)
+    y = run_linear(be, x, w, b, H.ACT_NONE)
+    assert_close(y, oracle_w8a8(x, q, s, K, b, 0), *TIGHT, what="fp8 vs oracle(same e4m3 acts)")
+    wd = O.fp8_dequantize(q, s, N, K, K)
+    assert_close(y, O.linear(x, wd, b, 0, nthreads=8), 4e-2, 0.3, what="fp8 vs f32 oracle")
+
+
+@pytest.mark.parametrize("act", [H.ACT_NONE, H.ACT_GELU_TANH])
+@pytest.mark.parametrize("ydt", [H.DTYPE_F32, H.DTYPE_BF16])
+@pytest.mark.parametrize("xdt", [H.DTYPE_F32, H.DTYPE_BF16])
+def test_fp8_epilogue_dtypes_offsets(be, act, ydt, xdt):
+    M, K, N = 200, 512, 384
+    x = normal(5, M * K).reshape(M, K)
+    xs = x if xdt == H.DTYPE_F32 else O.bf16_round(x)
+    _, q, s = fp8_weight(6, N, K, K)
+    b = normal(7, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, K)
+    y = run_linear(be, x, w, b, act, y_dtype=ydt, x_dtype=xdt, x_row=13, y_row=7, rows=150)
+    want = oracle_w8a8(xs[13:163], q, s, K, b, act)
+    if ydt == H.DTYPE_F32:
+        assert_close(y, want, *TIGHT, what="fp8 epilogue")
+    else:
+        assert_close(y, want, 4e-3, 8e-3, what="fp8 epilogue bf16 out")
+
+
+def test_fp8_no_bias(be):
+    M, K, N = 96, 640, 320
+    x = normal(8, M * K).reshape(M, K)
+    _, q, s = fp8_weight(9, N, K, K)
+    w = be.weight_fp8(q, s, N, K, K)
+    y = run_linear(be, x, w, None, H.ACT_NONE)
+    assert_close(y, oracle_w8a8(x, q, s, K, None, 0), *TIGHT, what="fp8 no bias")
+
+
+def test_fp8_reference_quantizer_codes(be):
+    """Weights from the reference's own encoder (quant.rs:376-406, exponent-0
+    and NaN codes included): exponent-0 codes are stored as zero, so the
+    result equals the oracle with those weights zeroed; NaN codes give NaN
+    columns in both."""
+    M, K, N = 64, 512, 256
+    x = normal(10, M * K).reshape(M, K)
+    wf = normal(11, N * K, 0.02).reshape(N, K)
+    q, s = O.fp8_quantize(wf, N, K, K, False)
+    w = be.weight_fp8(q, s, N, K, K)
+    n_e0 = int(np.sum(((q & 0x78) == 0) & ((q & 7) != 0)))
+    assert w.info()["canonicalized"] == n_e0
+    qc = np.where(((q & 0x78) == 0) & ((q & 7) != 0), q & 0x80, q).astype(np.uint8)
+    y = run_linear(be, x, w, None, H.ACT_NONE)
+    want = oracle_w8a8(x, qc, s, K, None, 0)
+    nan_cols = np.any((q & 0x7F) == 0x7F, axis=1)
+    assert np.array_equal(np.isnan(y).any(0), nan_cols)
+    ok = ~nan_cols
+    assert_close(y[:, ok], want[:, ok], *TIGHT, what="fp8 reference-encoder codes")
+
+
+def test_fp8_grouped_paths(be):
+    """Group-128 FP8 (the reference default, quant.rs:21): e4m3 activations
+    and the bf16-activation mode."""
+    M, K, N = 130, 512, 200
+    x = normal(12, M * K).reshape(M, K)
+    _, q, s = fp8_weight(13, N, K, 128)
+    b = normal(14, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, 128)
+    y = run_linear(be, x, w, b, H.ACT_NONE)
+    assert_close(y, oracle_w8a8(x, q, s, 128, b, 0), *TIGHT, what="fp8 g128 e4m3 acts")
+    be.set_fp8_act(H.FP8_ACT_BF16)
+    try:
+        y2 = run_linear(be, x, w, b, H.ACT_NONE)
+    finally:
+        be.set_fp8_act(H.FP8_ACT_E4M3)
+    wd = O.fp8_dequantize(q, s, N, K, 128)
+    assert_close(y2, oracle_w16(x, wd, b, 0), *TIGHT, what="fp8 g128 bf16 acts")
+    assert_close(y2, O.linear(x, wd, b, 0), 5e-3, 0.05, what="fp8 g128 bf16 acts vs f32 oracle")
+
+
+# ---- Q8 / Q4: bf16 MFMA with in-loader dequantization ----------------------------------
+
+@pytest.mark.parametrize("M,K,N,group", [(64, 256, 192, 32), (77, 288, 130, 32), (300, 1536, 1000, 128),
+                                         (129, 512, 256, 512), (256, 1536, 896, 32)])
+@pytest.mark.parametrize("xdt", [H.DTYPE_F32, H.DTYPE_BF16])
+def test_q8_vs_oracle(be, M, K, N, group, xdt):
+    x = normal(20 + M, M * K).reshape(M, K)
+    _, q, s = q8_weight(21 + N, N, K, group)
+    b = normal(22, N, 0.01)
+    w = be.weight_q8(q, s, N, K, group)
+    y = run_linear(be, x, w, b, H.ACT_GELU_TANH, x_dtype=xdt)
+    wd = O.q8_dequantize(q, s, N, K, group)
+    assert_close(y, oracle_w16(x, wd, b, 1), *TIGHT, what="q8 vs oracle(bf16 operands)")
+    assert_close(y, O.linear(x, wd, b, 1, nthreads=8), 5e-3, 0.05, what="q8 vs f32 oracle")
+
+
+@pytest.mark.parametrize("M,K,N,group,hqq", [(64, 256, 192, 32, None), (77, 320, 130, 32, None),
+                                             (300, 1536, 512, 64, True), (200, 512, 384, 64, False),
+                                             (129, 896, 256, 128, None)])
+def test_q4_vs_oracle(be, M, K, N, group, hqq):
+    x = normal(30 + M, M * K).reshape(M, K)
+    if hqq is None:
+        _, c, s, z = q4_sym_weight(31 + N, N, K, group)
+    else:
+        wf = normal(31 + N, N * K, 0.02).reshape(N, K)
+        c, s, z = O.q4_quantize(wf, N, K, group, hqq)
+    b = normal(32, N, 0.01)
+    w = be.weight_q4(O.q4_pack(c), s, z, N, K, group, packed=True)
+    y = run_linear(be, x, w, b, H.ACT_NONE)
+    wd = O.q4_dequantize(c, s, z, N, K, group)
+    assert_close(y, oracle_w16(x, wd, b, 0), *TIGHT, what="q4 vs oracle(bf16 operands)")
+    assert_close(y, O.linear(x, wd, b, 0, nthreads=8), 5e-3, 0.05, what="q4 vs f32 oracle")
+
+
+# ---- shapes the MFMA kernels do not tile: the generic kernel ----------------------------
+
+@pytest.mark.parametrize("fmt", ["f32", "q8", "q4", "fp8"])
+def test_odd_shapes_generic(be, fmt):
+    M, K, N = 9, 100, 7
+    x = normal(40, M * K).reshape(M, K)
+    b = normal(41, N, 0.01)
+    if fmt == "f32":
+        wf = normal(42, N * K, 0.1).reshape(N, K)
+        w = be.weight(wf, N, K)
+        y = run_linear(be, x, w, b, H.ACT_GELU_TANH)
+        assert_close(y, O.linear(x, wf, b, 1), 1e-6, 1e-5, what="f32 weight generic")
+    elif fmt == "q8":
+        _, q, s = q8_weight(42, N, K, 20)
+        w = be.weight_q8(q, s, N, K, 20)
+        y = run_linear(be, x, w, b, H.ACT_NONE)
+        assert_close(y, O.linear(x, O.q8_dequantize(q, s, N, K, 20), b, 0), 1e-6, 1e-5, what="q8 generic")
+    elif fmt == "q4":
+        wf = normal(42, N * K, 0.02).reshape(N, K)
+        c, s, z = O.q4_quantize(wf, N, K, 50, True)
+        w = be.weight_q4(c, s, z, N, K, 50)
+        y = run_linear(be, x, w, b, H.ACT_NONE)
+        assert_close(y, O.linear(x, O.q4_dequantize(c, s, z, N, K, 50), b, 0), 1e-6, 1e-5, what="q4 generic")
+    else:
+        _, q, s = fp8_weight(42, N, K, K)
+        w = be.weight_fp8(q, s, N, K, K)
+        y = run_linear(be, x, w, b, H.ACT_NONE)
+        assert_close(y, oracle_w8a8(x, q, s, K, b, 0), 1e-5, 1e-4, what="fp8 generic")
+
+
+# ---- boundary errors ----------------------------------------------------------------------
+
+def test_alias_and_shape_errors(be):
+    K, N = 64, 64
+    _, q, s = fp8_weight(50, N, K, K)
+    w = be.weight_fp8(q, s, N, K, K)
+    x = be.upload(normal(51, 4 * K))
+    with pytest.raises(H.HipError) as e:
+        be.linear(x, 0, 2, w, None, H.ACT_NONE, x, 1)  # y rows [1,3) overlap x rows [0,2)
+    assert e.value.status == H.ERR_ALIAS
+    be.linear(x, 0, 2, w, None, H.ACT_NONE, x, 2)  # disjoint rows of one buffer: allowed
+    with pytest.raises(H.HipError) as e:
+        be.linear(x, 0, 4, w, None, H.ACT_NONE, x, 0)
+    assert e.value.status == H.ERR_ALIAS
+    y = be.alloc(4 * N)
+    with pytest.raises(H.HipError) as e:
+        be.linear(x, 1, 4, w, None, H.ACT_NONE, y, 0)
+    assert e.value.status == H.ERR_BAD_SHAPE
+    be.linear(x, 0, 0, w, None, H.ACT_NONE, y, 0)  # zero rows: no-op
+
+
+def test_profile_report_names_kernels(be):
+    M, K, N = 64, 256, 128
+    _, q, s = fp8_weight(60, N, K, K)
+    w = be.weight_fp8(q, s, N, K, K)
+    be.profile_reset()
+    be.profile_enable(True)
+    try:
+        run_linear(be, normal(61, M * K).reshape(M, K), w, None, H.ACT_NONE)
+        rep = be.profile_report()
+        calls, ms = be.profile_kernel("gemm_fp8_e4m3")
+    finally:
+        be.profile_enable(False)
+    assert rep and "gemm_fp8_e4m3" in rep and "act_quant_e4m3" in rep
+    assert calls == 1 and ms > 0
+
+
+def test_cpp_check_harness(be):
+    """The C++ consumer of the boundary (`lightx2v check --backend hip`):
+    exact quantized-linear checks and bit-exact dequant through the C ABI."""
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "lightx2v-rs_amd", "bin",
+                       "lx2v_hip_check")
+    if not os.path.exists(exe):
+        pytest.fail("lightx2v-rs_amd/bin/lx2v_hip_check is not built")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "5 checks, 5 passed, 0 failed" in r.stdout
