@@ -118,6 +118,50 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
 }
 
+// The GEMM epilogues' GELU: 0.5 x (1 + tanh(u)) == x / (1 + e^(-2u)) with
+// u = sqrt(2/pi) (x + 0.044715 x^3), on the hardware exp2 and reciprocal
+// (a few ulp; the oracle's own 1 + tanhf(u) loses more than that to
+// cancellation for u < 0).  Limits: x -> -inf gives -0, x -> +inf gives x.
+__device__ __forceinline__ float gelu_tanh_fast(float x) {
+    const float c = 0.7978845608028654f;
+    float u = c * (x + 0.044715f * x * x * x);
+    float e = __builtin_amdgcn_exp2f(u * -2.8853900817779268f);  // -2 log2(e)
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// ---- workgroup -> output tile ------------------------------------------------------
+
+// Map a linear workgroup id to an output tile (tm, tn) so that the
+// workgroups one XCD runs (ids congruent mod 8 go to the same XCD) form a
+// compact block of tiles: bands of up to 4 tile-rows walked column by
+// column, so an XCD's L2 holds the few A row-panels and B column-panels
+// its workgroups share.
+__device__ __forceinline__ void xcd_tile(int bid, int nb, int tiles_m, int tiles_n, int *tm, int *tn) {
+    const int per = nb / 8, rem = nb % 8;
+    const int x = bid % 8, j = bid / 8;
+    const int id = x * per + (x < rem ? x : rem) + j;
+    const int G = tiles_m < 4 ? tiles_m : 4;
+    const int group = id / (G * tiles_n);
+    const int first = group * G;
+    const int gsz = (tiles_m - first) < G ? (tiles_m - first) : G;
+    const int in = id - first * tiles_n;
+    *tm = first + in % gsz;
+    *tn = in / gsz;
+}
+
+// ---- epilogue stores ----------------------------------------------------------------
+
+// Four consecutive outputs y[0..3] (16-byte aligned for f32, 8 for bf16).
+__device__ __forceinline__ void store4(float *y, float a, float b, float c, float d) {
+    *(f32x4 *)y = (f32x4){a, b, c, d};
+}
+__device__ __forceinline__ void store4(uint16_t *y, float a, float b, float c, float d) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    *(u32x2_t *)y = (u32x2_t){pack_bf16x2(a, b), pack_bf16x2(c, d)};
+}
+__device__ __forceinline__ void store1(float *y, float v) { *y = v; }
+__device__ __forceinline__ void store1(uint16_t *y, float v) { *y = f32_to_bf16_bits(v); }
+
 // ---- buffer resources ----------------------------------------------------------
 
 // A raw buffer descriptor: loads at byte offsets >= num_bytes return zero,

@@ -10,8 +10,10 @@
 // chunk in registers exactly as the reference's dequantize() (q*s,
 // (c-z)*s, e4m3(c)*s in f32), rounds to bf16 and writes the K-major tile to
 // LDS; activations (f32 or bf16) are rounded to bf16 on the same path.
-// Tile shape, swizzle and XCD mapping follow k_gemm_fp8.hip with a 64-
-// element K stage (128 bytes of bf16 per row).
+// Tile shape, swizzle, XCD mapping, the two-register-stage pipeline and the
+// operand roles (weights = MFMA A operand, so the epilogue writes four
+// consecutive channels per lane) follow k_gemm_fp8.hip, with a 64-element K
+// stage (128 bytes of bf16 per row).
 #include "device_common.hpp"
 #include "runtime.hpp"
 
@@ -24,30 +26,6 @@ constexpr int ROWB = BK * 2;  // bytes per LDS tile row (bf16)
 
 __device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t c) {
     return row * ROWB + ((c ^ ((row >> 1) & 7u)) << 4);
-}
-
-__device__ __forceinline__ void tile_of(int bid, int nb, int tiles_m, int tiles_n, int *tm, int *tn) {
-    const int per = nb / 8, rem = nb % 8;
-    const int x = bid % 8, j = bid / 8;
-    const int id = x * per + (x < rem ? x : rem) + j;
-    const int G = tiles_m < 4 ? tiles_m : 4;
-    const int group = id / (G * tiles_n);
-    const int first = group * G;
-    const int gsz = (tiles_m - first) < G ? (tiles_m - first) : G;
-    const int in = id - first * tiles_n;
-    *tm = first + in % gsz;
-    *tn = in / gsz;
-}
-
-template <typename TY>
-__device__ __forceinline__ void store_y(TY *y, size_t idx, float v);
-template <>
-__device__ __forceinline__ void store_y<float>(float *y, size_t idx, float v) {
-    y[idx] = v;
-}
-template <>
-__device__ __forceinline__ void store_y<uint16_t>(uint16_t *y, size_t idx, float v) {
-    y[idx] = f32_to_bf16_bits(v);
 }
 
 // Source chunks per weight row per K stage, and K elements per source chunk.
@@ -124,12 +102,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm_w16(const void *__restrict__ X,
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int XB = XT == LX2V_DTYPE_BF16 ? 2 : 4;    // bytes per activation
     constexpr int XLD = XT == LX2V_DTYPE_BF16 ? 1 : 2;   // 16B loads per LDS chunk
-    constexpr int ACH = BM * 8 / 256;                     // LDS chunks of A per thread
+    constexpr int ACH = BM * 8 / 256;                     // LDS chunks of X per thread
     constexpr int CPR = WTraits<WF>::kChunksPerRow;
     constexpr int KPC = WTraits<WF>::kPerChunk;
     constexpr int BCH = BN * CPR / 256;                   // weight source chunks per thread
-    constexpr int WB_NUM = WF == LX2V_WFMT_Q4 ? 1 : 1;
-    constexpr int WB_DEN = WF == LX2V_WFMT_Q4 ? 2 : 1;    // code bytes per element = NUM/DEN
+    constexpr uint32_t WB_DEN = WF == LX2V_WFMT_Q4 ? 2 : 1;  // code bytes per element = 1/DEN
     static_assert(BCH >= 1, "tile too small for the weight loader");
     constexpr int STAGE = (BM + BN) * ROWB;
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
@@ -137,24 +114,22 @@ __global__ __launch_bounds__(256, 1) void k_gemm_w16(const void *__restrict__ X,
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid >> 1, wn = wid & 1;
     int tm, tn;
-    tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int KG = K / group;  // scale columns
+    const int KT = (K + BK - 1) / BK;
 
     const auto rx = make_rsrc((const uint8_t *)X + (size_t)m0 * K * XB, (uint32_t)(M - m0) * (uint32_t)K * XB);
-    const uint32_t wrow_bytes = (uint32_t)K * WB_NUM / WB_DEN;
+    const uint32_t wrow_bytes = (uint32_t)K / WB_DEN;
     const auto rw = make_rsrc(Wc + (size_t)n0 * wrow_bytes, (uint32_t)(N - n0) * wrow_bytes);
 
-    // A chunk coordinates: LDS chunk c of row r holds K elements [8c, 8c+8).
-    uint32_t a_goff[ACH], a_loff[ACH], a_kc[ACH];
-#pragma unroll
-    for (int j = 0; j < ACH; j++) {
-        uint32_t id = j * 256 + tid, row = id >> 3, c = id & 7;
-        a_goff[j] = (row * (uint32_t)K + c * 8) * XB;
-        a_loff[j] = lds_off(row, c);
-        a_kc[j] = c * 8;
-    }
-    // Weight source chunk coordinates.
+    // X chunk j of this thread: tile row j * 32 + tid / 8, LDS chunk tid % 8
+    // (K elements [8c, 8c+8) of the stage); one LDS offset up to j * 32 rows.
+    const uint32_t crow = (uint32_t)tid >> 3, cc = (uint32_t)tid & 7u;
+    const uint32_t x_goff = (crow * (uint32_t)K + cc * 8) * XB;
+    const uint32_t x_gstep = 32u * (uint32_t)K * XB;
+    const uint32_t x_loff = lds_off(crow, cc);
+    // Weight source chunks.
     uint32_t w_goff[BCH], w_row[BCH], w_sc[BCH], w_srow[BCH];
 #pragma unroll
     for (int j = 0; j < BCH; j++) {
@@ -166,64 +141,62 @@ __global__ __launch_bounds__(256, 1) void k_gemm_w16(const void *__restrict__ X,
         w_srow[j] = (n < (uint32_t)N ? n : (uint32_t)N - 1) * (uint32_t)KG;
     }
 
-    u32x4 ra[ACH][XLD], rw_[BCH];
-    float wsc[BCH], wze[BCH];
-    auto gload = [&](int k0) {
+    struct Regs {
+        u32x4 x[ACH][XLD];
+        u32x4 w[BCH];
+        float sc[BCH], ze[BCH];
+    };
+    // Stage `kt` into registers; stages past the end load zeros.
+    auto gload = [&](Regs &r, int kt) {
+        const uint32_t k0 = (uint32_t)kt * BK;
+        const bool xin = kt < KT && k0 + cc * 8 < (uint32_t)K;
 #pragma unroll
-        for (int j = 0; j < ACH; j++) {
-            bool kin = (uint32_t)k0 + a_kc[j] < (uint32_t)K;
+        for (int j = 0; j < ACH; j++)
 #pragma unroll
             for (int h = 0; h < XLD; h++)
-                ra[j][h] = buffer_load_x4(rx, kin ? a_goff[j] + (uint32_t)k0 * XB + h * 16 : kOob);
-        }
+                r.x[j][h] = buffer_load_x4(rx, xin ? x_goff + j * x_gstep + k0 * XB + h * 16 : kOob);
 #pragma unroll
         for (int j = 0; j < BCH; j++) {
-            uint32_t kk = (uint32_t)k0 + w_sc[j] * KPC;
-            bool kin = kk < (uint32_t)K;
-            rw_[j] = buffer_load_x4(rw, kin ? w_goff[j] + (uint32_t)k0 * WB_NUM / WB_DEN : kOob);
+            uint32_t kk = k0 + w_sc[j] * KPC;
+            bool kin = kt < KT && kk < (uint32_t)K;
+            r.w[j] = buffer_load_x4(rw, kin ? w_goff[j] + k0 / WB_DEN : kOob);
             uint32_t g = w_srow[j] + (kin ? kk : 0) / (uint32_t)group;
-            wsc[j] = Ws[g];
-            if (WF == LX2V_WFMT_Q4) wze[j] = Wz[g];
+            r.sc[j] = Ws[g];
+            if (WF == LX2V_WFMT_Q4) r.ze[j] = Wz[g];
         }
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](const Regs &r, int buf) {
         uint8_t *s = smem + buf * STAGE;
 #pragma unroll
         for (int j = 0; j < ACH; j++) {
             u32x4 o;
             if (XT == LX2V_DTYPE_BF16) {
-                o = ra[j][0];
+                o = r.x[j][0];
             } else {
-                f32x4 lo = __builtin_bit_cast(f32x4, ra[j][0]);
-                f32x4 hi = __builtin_bit_cast(f32x4, ra[j][1]);
+                f32x4 lo = __builtin_bit_cast(f32x4, r.x[j][0]);
+                f32x4 hi = __builtin_bit_cast(f32x4, r.x[j][1]);
                 o.x = pack_bf16x2(lo.x, lo.y);
                 o.y = pack_bf16x2(lo.z, lo.w);
                 o.z = pack_bf16x2(hi.x, hi.y);
                 o.w = pack_bf16x2(hi.z, hi.w);
             }
-            *(u32x4 *)(s + a_loff[j]) = o;
+            *(u32x4 *)(s + x_loff + j * 32 * ROWB) = o;
         }
         uint8_t *sb = s + BM * ROWB;
 #pragma unroll
         for (int j = 0; j < BCH; j++)
-            dequant_store<WF>(sb, w_row[j], w_sc[j], rw_[j], wsc[j], WF == LX2V_WFMT_Q4 ? wze[j] : 0.0f);
+            dequant_store<WF>(sb, w_row[j], w_sc[j], r.w[j], r.sc[j], WF == LX2V_WFMT_Q4 ? r.ze[j] : 0.0f);
     };
 
-    f32x16 acc[TM][TN];
+    f32x16 acc[TN][TM];
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+    for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = (f32x16){};
+        for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
 
     const uint32_t frow = lane & 31, fhalf = lane >> 5;
-    const int KT = (K + BK - 1) / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload((kt + 1) * BK);
-        const uint8_t *s = smem + cur * STAGE;
+    auto compute = [&](int buf) {
+        const uint8_t *s = smem + buf * STAGE;
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             bf16x8 af[TM], bfr[TN];
@@ -234,37 +207,74 @@ __global__ __launch_bounds__(256, 1) void k_gemm_w16(const void *__restrict__ X,
 #pragma unroll
             for (int j = 0; j < TN; j++)
                 bfr[j] = __builtin_bit_cast(
-                    bf16x8, *(const u32x4 *)(s + BM * ROWB + lds_off(wn * WN + j * 32 + frow, c)));
+                    bf16x8, *(const u32x4 *)(s + lds_off(BM + wn * WN + j * 32 + frow, c)));
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+            for (int j = 0; j < TN; j++)
 #pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < TM; i++)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[j][i], 0, 0, 0);
         }
-        if (kt + 1 < KT) sstore(cur ^ 1);
+    };
+
+    // Same pipeline as k_gemm_fp8: LDS buffer 0 holds stage kt, r1 stage
+    // kt + 1, r0 stage kt + 2 on entry; the scheduling barriers pin the
+    // load issue points.
+    Regs r0, r1;
+    gload(r0, 0);
+    gload(r1, 1);
+    sstore(r0, 0);
+    __syncthreads();
+    gload(r0, 2);
+    for (int kt = 0; kt < KT; kt += 2) {
+        compute(0);
+        sstore(r1, 1);
         __syncthreads();
+        gload(r1, kt + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(1);
+        sstore(r0, 0);
+        __syncthreads();
+        gload(r0, kt + 4);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
-    float bn[TN];
-    int ncol[TN];
+    // Epilogue: D[n][m] blocks, four consecutive channels per register group.
+    const bool vec = (N & 3) == 0;
+    int mrow[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++) mrow[i] = m0 + wm * WM + i * 32 + (lane & 31);
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-        int n = n0 + wn * WN + j * 32 + (lane & 31);
-        ncol[j] = n;
-        bn[j] = (n < N && bias) ? bias[n] : 0.0f;
-    }
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
+        for (int g = 0; g < 4; g++) {
+            const int nb = n0 + wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+            if (nb >= N) continue;
+            const bool full = vec && nb + 3 < N;
+            float b4[4];
+            if (full) {
+                f32x4 u = bias ? *(const f32x4 *)(bias + nb) : (f32x4){};
+                b4[0] = u.x, b4[1] = u.y, b4[2] = u.z, b4[3] = u.w;
+            } else {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (m >= M) continue;
+                for (int q = 0; q < 4; q++) b4[q] = (nb + q < N && bias) ? bias[nb + q] : 0.0f;
+            }
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                if (ncol[j] >= N) continue;
-                float v = acc[i][j][r] + bn[j];
-                if (act == LX2V_ACT_GELU_TANH) v = gelu_tanh(v);
-                store_y<TY>(Y, (size_t)m * N + ncol[j], v);
+            for (int i = 0; i < TM; i++) {
+                if (mrow[i] >= M) continue;
+                float v[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    v[q] = acc[j][i][4 * g + q] + b4[q];
+                    if (act == LX2V_ACT_GELU_TANH) v[q] = gelu_tanh_fast(v[q]);
+                }
+                TY *yp = Y + (size_t)mrow[i] * N + nb;
+                if (full) {
+                    store4(yp, v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        if (nb + q < N) store1(yp + q, v[q]);
+                }
             }
         }
     }
@@ -321,10 +331,10 @@ void launch_gemm_w16(hipStream_t s, int num_cu, const void *x, int x_dtype, cons
     struct Cfg {
         int bm, bn;
     };
-    const Cfg cfgs[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+    const Cfg cfgs[] = {{256, 128}, {128, 256}, {128, 128}};
     double best = -1.0;
     int pick = 0;
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 3; i++) {
         size_t tiles = ((M + cfgs[i].bm - 1) / cfgs[i].bm) * ((N + cfgs[i].bn - 1) / cfgs[i].bn);
         size_t waves = (tiles + num_cu - 1) / num_cu;
         double eff = (double)M * N / ((double)waves * num_cu * cfgs[i].bm * cfgs[i].bn);
@@ -335,9 +345,8 @@ void launch_gemm_w16(hipStream_t s, int num_cu, const void *x, int x_dtype, cons
     }
     int m = (int)M;
     switch (pick) {
-        case 0: launch_tile<256, 256>(s, x, x_dtype, w, bias, act, y, y_dtype, m); break;
-        case 1: launch_tile<256, 128>(s, x, x_dtype, w, bias, act, y, y_dtype, m); break;
-        case 2: launch_tile<128, 256>(s, x, x_dtype, w, bias, act, y, y_dtype, m); break;
+        case 0: launch_tile<256, 128>(s, x, x_dtype, w, bias, act, y, y_dtype, m); break;
+        case 1: launch_tile<128, 256>(s, x, x_dtype, w, bias, act, y, y_dtype, m); break;
         default: launch_tile<128, 128>(s, x, x_dtype, w, bias, act, y, y_dtype, m); break;
     }
 }

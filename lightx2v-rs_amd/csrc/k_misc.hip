@@ -93,45 +93,98 @@ __global__ void k_dequant(int fmt, const void *codes, const float *scales, const
 
 // ---- per-token e4m3 activation quantization ---------------------------------------
 //
-// One workgroup per row.  amax = max|x|; inv = 448/amax, s = amax/448 (both
+// One wave per row.  amax = max|x|; inv = 448/amax, s = amax/448 (both
 // correctly rounded divisions; amax <= 2^-64 -> 1, 1); q = e4m3(clamp(x*inv,
-// -448, 448)) rounded to nearest even.  Rows up to kRegChunks*16*256 wide
-// stay in registers between the two passes.
-
-constexpr int kRegChunks = 4;  // 16-element chunks per thread kept in registers
+// -448, 448)) rounded to nearest even.  Lane l owns the 8-element chunks
+// l, l + 64, ... of its row and keeps them in registers between the max and
+// the quantization, so the row is read from HBM once.
 
 template <int DT>
-__device__ __forceinline__ void load16(const void *row, size_t c, float v[16]) {
+__device__ __forceinline__ void unpack8(const u32x4 *raw, float v[8]) {
     if (DT == LX2V_DTYPE_BF16) {
-        const u32x4 *p = (const u32x4 *)((const uint16_t *)row + c * 16);
-        u32x4 a = p[0], b = p[1];
-        uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const u32x4 a = raw[0];
+        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < 4; j++) {
             v[2 * j] = __uint_as_float(w[j] << 16);
             v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
         }
     } else {
-        const f32x4 *p = (const f32x4 *)((const float *)row + c * 16);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            f32x4 a = p[j];
-            v[4 * j] = a.x;
-            v[4 * j + 1] = a.y;
-            v[4 * j + 2] = a.z;
-            v[4 * j + 3] = a.w;
+        for (int h = 0; h < 2; h++) {
+            f32x4 a = __builtin_bit_cast(f32x4, raw[h]);
+            v[4 * h] = a.x, v[4 * h + 1] = a.y, v[4 * h + 2] = a.z, v[4 * h + 3] = a.w;
         }
     }
 }
 
+// Four clamped, scaled values -> four e4m3 codes (byte j = element j) with
+// the hardware pack conversion, round to nearest even.  An exhaustive sweep
+// of every f32 in [-448, 448] on gfx950 found it bit-identical to
+// e4m3_ocp_encode, the rule the oracle restates.
 __device__ __forceinline__ uint32_t quant4(const float *v, float inv) {
-    uint32_t r = 0;
+    float t[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        float t = fminf(fmaxf(v[j] * inv, -448.0f), 448.0f);
-        r |= e4m3_ocp_encode(t) << (8 * j);
+    for (int j = 0; j < 4; j++) t[j] = fminf(fmaxf(v[j] * inv, -448.0f), 448.0f);
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[1], 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(t[2], t[3], r, true);
+    return (uint32_t)r;
+}
+
+// W waves share a row (W = 1, 2 or 4; the workgroup holds 4 / W rows); T =
+// chunks of 8 per lane, 64 * W * T * 8 >= cols, cols % 8 == 0.  Wave part p
+// of a row owns chunks lane + 64 (p + W t).
+template <int DT, int T, int W>
+__global__ __launch_bounds__(kThreads) void k_act_quant_rows(const void *x, size_t rows, size_t cols,
+                                                             uint8_t *q, float *scale) {
+    constexpr int R = DT == LX2V_DTYPE_BF16 ? 1 : 2;  // 16-byte loads per chunk
+    __shared__ float red[kThreads / 64];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, part = wv % W;
+    const size_t row = blockIdx.x * (size_t)(kThreads / 64 / W) + wv / W;
+    const bool live = row < rows;
+    const int nch = (int)(cols / 8);
+    const u32x4 *xr = (const u32x4 *)((const char *)x + (live ? row : 0) * cols * (DT == LX2V_DTYPE_BF16 ? 2 : 4));
+    u32x4 raw[T][R];
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const int c = lane + 64 * (part + W * t);
+#pragma unroll
+        for (int h = 0; h < R; h++) raw[t][h] = (live && c < nch) ? xr[(size_t)c * R + h] : (u32x4){};
     }
-    return r;
+    float amax = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        float v[8];
+        unpack8<DT>(raw[t], v);
+#pragma unroll
+        for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    }
+    amax = wave_max(amax);
+    if (W > 1) {
+        if (lane == 0) red[wv] = amax;
+        __syncthreads();
+        const int first = wv - part;
+#pragma unroll
+        for (int p = 0; p < W; p++) amax = fmaxf(amax, red[first + p]);
+    }
+    if (!live) return;
+    float inv = 1.0f, s = 1.0f;
+    if (amax > 0x1p-64f) {
+        inv = 448.0f / amax;
+        s = amax / 448.0f;
+    }
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    u32x2_t *qr = (u32x2_t *)(q + row * cols);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const int c = lane + 64 * (part + W * t);
+        if (c < nch) {
+            float v[8];
+            unpack8<DT>(raw[t], v);
+            qr[c] = (u32x2_t){quant4(&v[0], inv), quant4(&v[4], inv)};
+        }
+    }
+    if (lane == 0 && part == 0) scale[row] = s;
 }
 
 __device__ float block_max(float v, float *red) {
@@ -143,46 +196,6 @@ __device__ float block_max(float v, float *red) {
 #pragma unroll
     for (int i = 1; i < kThreads / 64; i++) r = fmaxf(r, red[i]);
     return r;
-}
-
-template <int DT>
-__global__ __launch_bounds__(kThreads) void k_act_quant16(const void *x, size_t cols, uint8_t *q,
-                                                          float *scale) {
-    __shared__ float red[kThreads / 64];
-    const size_t row = blockIdx.x;
-    const void *xr = (const char *)x + row * cols * (DT == LX2V_DTYPE_BF16 ? 2 : 4);
-    const size_t nchunks = cols / 16;
-    float v[kRegChunks][16];
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kRegChunks; j++) {
-        size_t c = threadIdx.x + (size_t)j * kThreads;
-        if (c < nchunks) {
-            load16<DT>(xr, c, v[j]);
-#pragma unroll
-            for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(v[j][e]));
-        }
-    }
-    amax = block_max(amax, red);
-    float inv = 1.0f, s = 1.0f;
-    if (amax > 0x1p-64f) {
-        inv = 448.0f / amax;
-        s = amax / 448.0f;
-    }
-    u32x4 *qr = (u32x4 *)(q + row * cols);
-#pragma unroll
-    for (int j = 0; j < kRegChunks; j++) {
-        size_t c = threadIdx.x + (size_t)j * kThreads;
-        if (c < nchunks) {
-            u32x4 o;
-            o.x = quant4(&v[j][0], inv);
-            o.y = quant4(&v[j][4], inv);
-            o.z = quant4(&v[j][8], inv);
-            o.w = quant4(&v[j][12], inv);
-            qr[c] = o;
-        }
-    }
-    if (threadIdx.x == 0) scale[row] = s;
 }
 
 // Any width: two passes over the row from memory.
@@ -290,25 +303,43 @@ void launch_dequant(hipStream_t s, const lx2v_hip_weight *w, const uint8_t *fp8_
                        codes, w->scales, w->zeros, w->group ? w->group : 1, n, out);
 }
 
+template <int DT>
+void act_quant_rows(hipStream_t s, const void *x, size_t rows, size_t cols, uint8_t *q, float *scale) {
+    const size_t per = (cols / 8 + 63) / 64;  // chunks per lane with one wave per row
+    const dim3 block(kThreads);
+    auto grid = [&](int w) { return dim3((unsigned)((rows + (kThreads / 64 / w) - 1) / (kThreads / 64 / w))); };
+    if (per <= 2)
+        hipLaunchKernelGGL((k_act_quant_rows<DT, 2, 1>), grid(1), block, 0, s, x, rows, cols, q, scale);
+    else if (per <= 4)
+        hipLaunchKernelGGL((k_act_quant_rows<DT, 4, 1>), grid(1), block, 0, s, x, rows, cols, q, scale);
+    else if (per <= 8)
+        hipLaunchKernelGGL((k_act_quant_rows<DT, 4, 2>), grid(2), block, 0, s, x, rows, cols, q, scale);
+    else if (per <= 16)
+        hipLaunchKernelGGL((k_act_quant_rows<DT, 4, 4>), grid(4), block, 0, s, x, rows, cols, q, scale);
+    else
+        hipLaunchKernelGGL((k_act_quant_rows<DT, 8, 4>), grid(4), block, 0, s, x, rows, cols, q, scale);
+}
+
 void launch_act_quant(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols,
                       uint8_t *q, float *scale) {
     if (rows == 0) return;
-    bool fast = cols % 16 == 0 && cols <= (size_t)kRegChunks * 16 * kThreads;
-    if (dtype == LX2V_DTYPE_BF16) {
-        if (fast)
-            hipLaunchKernelGGL(k_act_quant16<LX2V_DTYPE_BF16>, dim3(rows), dim3(kThreads), 0, s, x,
-                               cols, q, scale);
+    // Rows kept in registers: up to 8 chunks of 8 per lane over 4 waves
+    // (16384 elements); wider or ragged rows take the two-pass kernel.
+    const size_t per = (cols / 8 + 63) / 64;
+    const bool fast = cols % 8 == 0 && per <= 32u;
+    if (fast) {
+        if (dtype == LX2V_DTYPE_BF16)
+            act_quant_rows<LX2V_DTYPE_BF16>(s, x, rows, cols, q, scale);
         else
-            hipLaunchKernelGGL(k_act_quant_any<LX2V_DTYPE_BF16>, dim3(rows), dim3(kThreads), 0, s, x,
-                               cols, q, scale);
-    } else {
-        if (fast)
-            hipLaunchKernelGGL(k_act_quant16<LX2V_DTYPE_F32>, dim3(rows), dim3(kThreads), 0, s, x,
-                               cols, q, scale);
-        else
-            hipLaunchKernelGGL(k_act_quant_any<LX2V_DTYPE_F32>, dim3(rows), dim3(kThreads), 0, s, x,
-                               cols, q, scale);
+            act_quant_rows<LX2V_DTYPE_F32>(s, x, rows, cols, q, scale);
+        return;
     }
+    if (dtype == LX2V_DTYPE_BF16)
+        hipLaunchKernelGGL(k_act_quant_any<LX2V_DTYPE_BF16>, dim3(rows), dim3(kThreads), 0, s, x, cols,
+                           q, scale);
+    else
+        hipLaunchKernelGGL(k_act_quant_any<LX2V_DTYPE_F32>, dim3(rows), dim3(kThreads), 0, s, x, cols, q,
+                           scale);
 }
 
 void launch_quantize_q8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,

@@ -755,6 +755,8 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
                 }))
                 return rc;
         } else {
+            if ((rows + 15) / 16 > 65535)
+                return fail(LX2V_ERR_UNSUPPORTED, "rows %zu too many for the generic kernel", rows);
             if (int rc = run(ctx, "gemm_generic", [&] {
                     launch_gemm_generic(ctx->stream, q, A_E4M3, s, w, bp, act, yp, y->dtype, rows);
                 }))
@@ -762,7 +764,8 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
         }
         return ok();
     }
-    if (w->fmt != LX2V_WFMT_F32 && gemm_w16_supported(w)) {
+    // The tile loaders address X with 32-bit buffer offsets.
+    if (w->fmt != LX2V_WFMT_F32 && gemm_w16_supported(w) && rows * K * x->elem_bytes() < (1ull << 31)) {
         const char *name = w->fmt == LX2V_WFMT_Q8 ? "gemm_w16_q8" : w->fmt == LX2V_WFMT_Q4 ? "gemm_w16_q4" : "gemm_w16_fp8";
         if (int rc = run(ctx, name, [&] {
                 launch_gemm_w16(ctx->stream, ctx->num_cu, xp, x->dtype, w, bp, act, yp, y->dtype, rows);

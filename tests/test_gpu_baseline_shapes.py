@@ -17,7 +17,7 @@ import pytest
 
 import lightx2v_hip as H
 import oracle as O
-from helpers import assert_close, normal, oracle_w16, oracle_w8a8, u32
+from helpers import FP8_TIGHT, W16_TIGHT, assert_close, normal, oracle_w16, oracle_w8a8, u32
 
 pytestmark = pytest.mark.gpu
 
@@ -101,7 +101,7 @@ def test_cfg1_fp8_sampled_rows(be):
     y = _run(be, x, w, b)
     assert np.all(np.isfinite(y))
     xs = x[SAMPLE]
-    assert_close(y[SAMPLE], oracle_w8a8(xs, q, s, K, b, 0), 1e-5, 1e-4, what="cfg1 vs oracle(e4m3 acts)")
+    assert_close(y[SAMPLE], oracle_w8a8(xs, q, s, K, b, 0), *FP8_TIGHT, what="cfg1 vs oracle(e4m3 acts)")
     assert_close(y[SAMPLE], O.linear(xs, O.fp8_dequantize(q, s, N, K, K), b, 0, nthreads=8), 4e-2, 0.3,
                  what="cfg1 vs f32 oracle")
 
@@ -132,7 +132,7 @@ def test_cfg3_q4_sampled_rows(be, heavy):
     w = be.weight_q4(O.q4_pack(c), s, z, N, K, g, packed=True)
     y = _run(be, x, w, b, x_dtype=H.DTYPE_BF16)
     wd = O.q4_dequantize(c, s, z, N, K, g)
-    assert_close(y[SAMPLE], oracle_w16(x[SAMPLE], wd, b, 0), 1e-5, 1e-4, what="cfg3 vs oracle(bf16 operands)")
+    assert_close(y[SAMPLE], oracle_w16(x[SAMPLE], wd, b, 0), *W16_TIGHT, what="cfg3 vs oracle(bf16 operands)")
     assert_close(y[SAMPLE], O.linear(x[SAMPLE], wd, b, 0, nthreads=8), 5e-3, 0.05, what="cfg3 vs f32 oracle")
 
 
@@ -148,4 +148,4 @@ def test_cfg5_wan22_5b_fp8(be, rows, K, N):
     w = be.weight_fp8(q, s, N, K, K)
     y = _run(be, x, w, b, x_dtype=H.DTYPE_BF16)
     sample = SAMPLE[SAMPLE < rows][:48]
-    assert_close(y[sample], oracle_w8a8(x[sample], q, s, K, b, 0), 1e-5, 1e-4, what="cfg5 vs oracle(e4m3 acts)")
+    assert_close(y[sample], oracle_w8a8(x[sample], q, s, K, b, 0), *FP8_TIGHT, what="cfg5 vs oracle(e4m3 acts)")

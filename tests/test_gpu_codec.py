@@ -101,7 +101,7 @@ def test_quantize_fp8_matches_oracle(be, group):
 # ---- per-token e4m3 activation quantization ---------------------------------------------
 
 @pytest.mark.parametrize("dtype", [H.DTYPE_F32, H.DTYPE_BF16])
-@pytest.mark.parametrize("cols", [1536, 8960, 100, 16400])
+@pytest.mark.parametrize("cols", [512, 1536, 3072, 5120, 8960, 16384, 100, 16400])
 def test_act_quant_bit_exact(be, dtype, cols):
     rows = 37
     x = normal(cols, rows * cols).reshape(rows, cols)
@@ -121,6 +121,28 @@ def test_act_quant_bit_exact(be, dtype, cols):
     # row offset
     q2, s2 = be.act_quant(xb, 5, 3, cols)
     assert np.array_equal(q2, qw[5:8]) and np.array_equal(u32(s2), u32(sw[5:8]))
+
+
+def test_act_quant_rounding_edges(be):
+    """Rows whose absmax is 448 quantize with inv == 1 exactly, so every
+    element reaches the e4m3 rounding unchanged: all midpoints between
+    adjacent codes (ties to even, subnormal ties at (k + 1/2) 2^-9), their
+    float neighbours, and values past 448 that saturate."""
+    vals = O.e4m3_decode_ocp(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)  # 0 .. 448
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    up = np.nextafter(mids, np.float32(np.inf))
+    dn = np.nextafter(mids, np.float32(0))
+    edge = np.concatenate([mids, up, dn, [447.99997, 448.0, 2 ** -10, 2 ** -9, 3 * 2 ** -10]]).astype(np.float32)
+    cols = 512
+    row = np.zeros(cols, np.float32)
+    row[: edge.size] = edge
+    row[0] = 448.0
+    x = np.stack([row, -row, row[::-1].copy()])
+    xb = be.upload(x)
+    q, s = be.act_quant(xb, 0, 3, cols)
+    qw, sw = O.act_quant_e4m3(x)
+    assert np.all(s == 1.0) and np.array_equal(u32(s), u32(sw))
+    assert np.array_equal(q, qw)
 
 
 # ---- buffers, synthetic fill --------------------------------------------------------------
