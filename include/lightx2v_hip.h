@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define LX2V_HIP_ABI_VERSION 1
+#define LX2V_HIP_ABI_VERSION 2
 
 typedef struct lx2v_hip_ctx lx2v_hip_ctx;
 typedef struct lx2v_hip_buf lx2v_hip_buf;
@@ -55,8 +55,10 @@ enum {
 /* Act (backend.rs:38-43) */
 enum { LX2V_ACT_NONE = 0, LX2V_ACT_GELU_TANH = 1 };
 
-/* device activation dtypes */
-enum { LX2V_DTYPE_F32 = 0, LX2V_DTYPE_BF16 = 1 };
+/* device activation dtypes.  E4M3 buffers hold per-token quantized
+ * activations (e4m3 codes [rows, cols] plus one f32 scale per row, value =
+ * code * scale) and are made only by lx2v_hip_alloc_e4m3. */
+enum { LX2V_DTYPE_F32 = 0, LX2V_DTYPE_BF16 = 1, LX2V_DTYPE_E4M3 = 2 };
 
 /* weight formats (quant.rs:134-140 plus the native f32 matrix) */
 enum { LX2V_WFMT_F32 = 0, LX2V_WFMT_Q8 = 1, LX2V_WFMT_Q4 = 2, LX2V_WFMT_FP8 = 3 };
@@ -175,11 +177,28 @@ int lx2v_hip_quantize_fp8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t row
  * buf[i] = normal(seed)[i] * std. */
 int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std);
 
+/* ---- pre-quantized activations (no reference counterpart) ----------------
+ * The reference keeps activations f32 (backend.rs:9-11); these let a
+ * producer hand linear e4m3 activations directly, so an FP8 linear runs
+ * only its GEMM (the per-token quantization linear otherwise performs on
+ * its input is done once, here). */
+
+/* A [rows, cols] E4M3 activation buffer (len = rows * cols). */
+int lx2v_hip_alloc_e4m3(lx2v_hip_ctx *ctx, size_t rows, size_t cols, lx2v_hip_buf **out);
+/* xq rows [0, rows) = per-token e4m3 quantization (the rule linear applies
+ * to FP8 weights: s = absmax / 448, code = RNE e4m3 of clamp(x * 448 /
+ * absmax)) of x rows [x_row, x_row + rows); x is F32 or BF16 with xq's
+ * cols per row, rows <= xq's rows. */
+int lx2v_hip_quantize_act(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                          lx2v_hip_buf *xq);
+
 /* ---- the op (backend.rs:198-212) ----------------------------------------- */
 
 /* Backend::linear: y[y_row + i, :] = act(x[x_row + i, :] . W^T + b) for
  * i < rows; x has row stride w.cols, y row stride w.rows, bias (nullable)
- * has w.rows elements.  y must not overlap x or bias (LX2V_ERR_ALIAS). */
+ * has w.rows elements.  y must not overlap x or bias (LX2V_ERR_ALIAS).
+ * An E4M3 x (its cols == w.cols) needs an FP8 weight and skips the
+ * activation quantization; y is F32 or BF16. */
 int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
                     const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act,
                     lx2v_hip_buf *y, size_t y_row);
@@ -189,6 +208,21 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
  * q [rows, cols] codes, s [rows] scales. */
 int lx2v_hip_act_quant(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
                        size_t cols, uint8_t *q, float *s);
+
+/* ---- HIP graphs (no reference counterpart: the wgpu backend batches
+ * dispatches into command encoders instead, crates/lightx2v-wgpu/src/
+ * lib.rs:441-505) ------------------------------------------------------------
+ * Capture a fixed sequence of linear / quantize_act / copy calls on the
+ * context stream once and replay it with one launch.  Between begin and end
+ * only those calls are allowed (anything that allocates, frees, transfers
+ * host memory or synchronises fails with LX2V_ERR_UNSUPPORTED); run the
+ * sequence once eagerly first so workspaces are already large enough.
+ * Replays read and write the buffers captured, at their current contents. */
+typedef struct lx2v_hip_graph lx2v_hip_graph;
+int lx2v_hip_graph_begin(lx2v_hip_ctx *ctx);
+int lx2v_hip_graph_end(lx2v_hip_ctx *ctx, lx2v_hip_graph **out);
+int lx2v_hip_graph_launch(lx2v_hip_ctx *ctx, const lx2v_hip_graph *g);
+int lx2v_hip_graph_free(lx2v_hip_ctx *ctx, lx2v_hip_graph *g);
 
 /* ---- sync / profiling (backend.rs:189-196) -------------------------------- */
 
@@ -204,6 +238,12 @@ int lx2v_hip_profile_enable(lx2v_hip_ctx *ctx, int on);
 int lx2v_hip_profile_report(lx2v_hip_ctx *ctx, char *out, size_t cap);
 /* Backend::profile_reset (backend.rs:196). */
 int lx2v_hip_profile_reset(lx2v_hip_ctx *ctx);
+/* Time a region of the context stream with HIP events, whatever the
+ * per-kernel switch says: begin != 0 records the start, begin == 0 the end,
+ * and the elapsed time joins the report as row `name` (one call per
+ * begin/end pair).  Regions do not nest per name.  No reference counterpart
+ * (the reference times ops on the host, crates/lightx2v-cpu/src/lib.rs:27-105). */
+int lx2v_hip_profile_region(lx2v_hip_ctx *ctx, const char *name, int begin);
 /* Machine-readable form of one row of the report: calls and total
  * milliseconds of kernel `name` (0, 0 if never recorded).  Synchronises. */
 int lx2v_hip_profile_kernel(lx2v_hip_ctx *ctx, const char *name, uint64_t *calls,

@@ -39,6 +39,12 @@ __global__ void k_convert(const void *src, int sd, void *dst, int dd, size_t n) 
     }
 }
 
+__global__ void k_decode_e4m3_rows(const uint8_t *q, const float *scale, size_t cols, size_t n, float *out) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        out[i] = e4m3_ocp_decode(q[i]) * scale[i / cols];
+}
+
 // ---- Rng::normal per element (rng.rs:39-54) --------------------------------------
 
 __device__ __forceinline__ uint64_t splitmix(uint64_t seed, uint64_t draw) {
@@ -287,6 +293,14 @@ void launch_convert(hipStream_t s, const void *src, int sd, void *dst, int dd, s
     if (n == 0) return;
     hipLaunchKernelGGL(k_convert, dim3(grid_for(n, kThreads * 4)), dim3(kThreads), 0, s, src, sd, dst,
                        dd, n);
+}
+
+void launch_decode_e4m3_rows(hipStream_t s, const uint8_t *q, const float *scale, size_t rows, size_t cols,
+                             float *out) {
+    const size_t n = rows * cols;
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_decode_e4m3_rows, dim3(grid_for(n, kThreads * 4)), dim3(kThreads), 0, s, q, scale, cols,
+                       n, out);
 }
 
 void launch_fill_normal(hipStream_t s, void *dst, int dtype, size_t n, uint64_t seed, float std) {

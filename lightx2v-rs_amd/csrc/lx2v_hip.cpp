@@ -59,6 +59,9 @@ struct Stage {
 
 int ensure(lx2v_hip_ctx *ctx, void **ptr, size_t *have, size_t need, const char *what) {
     if (*have >= need) return LX2V_OK;
+    if (ctx->capturing)
+        return fail(LX2V_ERR_UNSUPPORTED, "%s: would grow a workspace during graph capture (run the sequence "
+                    "once before capturing)", what);
     if (*ptr) {
         HIP_TRY(hipStreamSynchronize(ctx->stream), what);
         HIP_TRY(hipFree(*ptr), what);
@@ -79,6 +82,13 @@ bool overlap(const void *a, size_t na, const void *b, size_t nb) {
 
 int set_dev(const lx2v_hip_ctx *ctx) {
     HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    return LX2V_OK;
+}
+
+// Calls that allocate, free, move host data or synchronise cannot be
+// recorded into a graph.
+int not_capturing(const lx2v_hip_ctx *ctx, const char *what) {
+    if (ctx->capturing) return fail(LX2V_ERR_UNSUPPORTED, "%s is not allowed during graph capture", what);
     return LX2V_OK;
 }
 
@@ -140,6 +150,11 @@ void prof_harvest(lx2v_hip_ctx *ctx) {
 
 template <class F>
 int run(lx2v_hip_ctx *ctx, const char *name, F &&fn) {
+    if (ctx->capturing) {  // no per-kernel events inside a graph
+        fn();
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? LX2V_OK : hip_fail(e, name);
+    }
     hipError_t e = timed(ctx, name, fn);
     if (ctx->prof.on && ctx->prof.pending.size() > 8192) prof_harvest(ctx);
     if (e != hipSuccess) return hip_fail(e, name);
@@ -265,9 +280,16 @@ int lx2v_hip_create(int device, lx2v_hip_ctx **out) {
 int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
     if (!ctx) return ok();
     set_dev(ctx);
+    if (ctx->capturing) {  // abandon an unfinished capture
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(ctx->stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        ctx->capturing = false;
+    }
     (void)hipStreamSynchronize(ctx->stream);
     prof_harvest(ctx);
     for (auto e : ctx->prof.pool) (void)hipEventDestroy(e);
+    for (auto &r : ctx->prof.open_regions) (void)hipEventDestroy(r.second);
     if (ctx->ws) (void)hipFree(ctx->ws);
     auto &x = extras()[ctx];
     if (x.stage.ptr) (void)hipFree(x.stage.ptr);
@@ -287,6 +309,7 @@ int lx2v_hip_name(const lx2v_hip_ctx *ctx, char *out, size_t cap) {
 
 int lx2v_hip_set_act_dtype(lx2v_hip_ctx *ctx, int dtype) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "set_act_dtype")) return rc;
     if (!valid_dtype(dtype)) return fail(LX2V_ERR_BAD_ARG, "unknown dtype %d", dtype);
     ctx->act_dtype = dtype;
     return ok();
@@ -294,6 +317,7 @@ int lx2v_hip_set_act_dtype(lx2v_hip_ctx *ctx, int dtype) {
 
 int lx2v_hip_set_fp8_act(lx2v_hip_ctx *ctx, int mode) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "set_fp8_act")) return rc;
     if (mode != LX2V_FP8_ACT_E4M3 && mode != LX2V_FP8_ACT_BF16)
         return fail(LX2V_ERR_BAD_ARG, "unknown fp8 activation mode %d", mode);
     ctx->fp8_act = mode;
@@ -305,7 +329,8 @@ int lx2v_hip_set_fp8_act(lx2v_hip_ctx *ctx, int mode) {
 int lx2v_hip_alloc_dtype(lx2v_hip_ctx *ctx, size_t len, int dtype, lx2v_hip_buf **out) {
     NEED(ctx, "ctx");
     NEED(out, "out");
-    if (!valid_dtype(dtype)) return fail(LX2V_ERR_BAD_ARG, "unknown dtype %d", dtype);
+    if (!valid_dtype(dtype)) return fail(LX2V_ERR_BAD_ARG, "unknown dtype %d (E4M3 buffers come from lx2v_hip_alloc_e4m3)", dtype);
+    if (int rc = not_capturing(ctx, "alloc")) return rc;
     if (int rc = set_dev(ctx)) return rc;
     if (int rc = alloc_buf(ctx, len, dtype, out)) return rc;
     return ok();
@@ -320,6 +345,7 @@ int lx2v_hip_upload(lx2v_hip_ctx *ctx, const float *data, size_t len, lx2v_hip_b
     NEED(ctx, "ctx");
     NEED(out, "out");
     if (len) NEED(data, "data");
+    if (int rc = not_capturing(ctx, "upload")) return rc;
     if (int rc = set_dev(ctx)) return rc;
     lx2v_hip_buf *b = nullptr;
     if (int rc = alloc_buf(ctx, len, ctx->act_dtype, &b)) return rc;
@@ -336,7 +362,9 @@ int lx2v_hip_write(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, const float *data, size
     NEED(ctx, "ctx");
     NEED(buf, "buf");
     if (len) NEED(data, "data");
+    if (buf->dtype == LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "write into an E4M3 buffer (use lx2v_hip_quantize_act)");
     if (len > buf->len) return fail(LX2V_ERR_BAD_SHAPE, "write of %zu elements into a buffer of %zu", len, buf->len);
+    if (int rc = not_capturing(ctx, "write")) return rc;
     if (int rc = set_dev(ctx)) return rc;
     if (int rc = write_range(ctx, buf, 0, data, len)) return rc;
     return ok();
@@ -347,10 +375,20 @@ int lx2v_hip_download(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, float *out, si
     NEED(buf, "buf");
     if (len != buf->len) return fail(LX2V_ERR_BAD_SHAPE, "download of %zu elements from a buffer of %zu", len, buf->len);
     if (len) NEED(out, "out");
+    if (int rc = not_capturing(ctx, "download")) return rc;
     if (int rc = set_dev(ctx)) return rc;
     if (len) {
         const void *src = buf->ptr;
-        if (buf->dtype == LX2V_DTYPE_BF16) {
+        if (buf->dtype == LX2V_DTYPE_E4M3) {  // the values the codes stand for: code * row scale
+            void *st;
+            if (int rc = stage_for(ctx, len * 4, &st)) return rc;
+            if (int rc = run(ctx, "convert", [&] {
+                    launch_decode_e4m3_rows(ctx->stream, (const uint8_t *)buf->ptr, buf->scales, buf->rows, buf->cols,
+                                            (float *)st);
+                }))
+                return rc;
+            src = st;
+        } else if (buf->dtype == LX2V_DTYPE_BF16) {
             void *st;
             if (int rc = stage_for(ctx, len * 4, &st)) return rc;
             if (int rc = run(ctx, "convert", [&] {
@@ -387,6 +425,8 @@ int lx2v_hip_copy(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t src_off, lx
     if (src_off > src->len || len > src->len - src_off || dst_off > dst->len || len > dst->len - dst_off)
         return fail(LX2V_ERR_BAD_SHAPE, "copy [%zu,+%zu) -> [%zu,+%zu) out of range (%zu, %zu)", src_off, len,
                     dst_off, len, src->len, dst->len);
+    if (src->dtype == LX2V_DTYPE_E4M3 || dst->dtype == LX2V_DTYPE_E4M3)
+        return fail(LX2V_ERR_BAD_ARG, "copy to or from an E4M3 buffer");
     if (!len) return ok();
     if (int rc = set_dev(ctx)) return rc;
     const char *s = (const char *)src->ptr + src_off * src->elem_bytes();
@@ -404,6 +444,7 @@ int lx2v_hip_copy(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t src_off, lx
 int lx2v_hip_buf_free(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf) {
     NEED(ctx, "ctx");
     if (!buf) return ok();
+    if (int rc = not_capturing(ctx, "buf_free")) return rc;
     if (int rc = set_dev(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(free)");
     (void)hipFree(buf->ptr);
@@ -416,6 +457,7 @@ int lx2v_hip_buf_free(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf) {
 int lx2v_hip_weight_f32(lx2v_hip_ctx *ctx, const float *data, size_t rows, size_t cols,
                         lx2v_hip_weight **out) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "weight_f32")) return rc;
     NEED(out, "out");
     NEED(data, "data");
     if (!rows || !cols) return fail(LX2V_ERR_BAD_SHAPE, "empty weight %zux%zu", rows, cols);
@@ -439,6 +481,7 @@ int lx2v_hip_weight_f32(lx2v_hip_ctx *ctx, const float *data, size_t rows, size_
 int lx2v_hip_weight_q8(lx2v_hip_ctx *ctx, const int8_t *q, const float *scales, size_t rows,
                        size_t cols, size_t group, lx2v_hip_weight **out) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "weight_q8")) return rc;
     NEED(out, "out");
     NEED(q, "q");
     NEED(scales, "scales");
@@ -466,6 +509,7 @@ int lx2v_hip_weight_q4(lx2v_hip_ctx *ctx, const uint8_t *codes, int packed, cons
                        const float *zeros, size_t rows, size_t cols, size_t group,
                        lx2v_hip_weight **out) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "weight_q4")) return rc;
     NEED(out, "out");
     NEED(codes, "codes");
     NEED(scales, "scales");
@@ -507,6 +551,7 @@ int lx2v_hip_weight_q4(lx2v_hip_ctx *ctx, const uint8_t *codes, int packed, cons
 int lx2v_hip_weight_fp8(lx2v_hip_ctx *ctx, const uint8_t *q, const float *scales, size_t rows,
                         size_t cols, size_t group, lx2v_hip_weight **out) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "weight_fp8")) return rc;
     NEED(out, "out");
     NEED(q, "q");
     NEED(scales, "scales");
@@ -544,6 +589,7 @@ int lx2v_hip_weight_fp8(lx2v_hip_ctx *ctx, const uint8_t *q, const float *scales
 
 int lx2v_hip_weight_free(lx2v_hip_ctx *ctx, lx2v_hip_weight *w) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "weight_free")) return rc;
     if (!w) return ok();
     if (int rc = set_dev(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(weight_free)");
@@ -565,6 +611,7 @@ int lx2v_hip_weight_info(const lx2v_hip_weight *w, lx2v_hip_weight_info_t *info)
 
 int lx2v_hip_weight_dequantize(lx2v_hip_ctx *ctx, const lx2v_hip_weight *w, float *out, size_t len) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "weight_dequantize")) return rc;
     NEED(w, "weight");
     NEED(out, "out");
     size_t n = w->rows * w->cols;
@@ -585,6 +632,7 @@ static int quant_src_check(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t ro
                            size_t group) {
     NEED(ctx, "ctx");
     NEED(src, "src");
+    if (int rc = not_capturing(ctx, "quantize")) return rc;
     if (src->dtype != LX2V_DTYPE_F32) return fail(LX2V_ERR_BAD_ARG, "quantizer source must be an f32 buffer");
     if (int rc = check_quant_shape(rows, cols, group)) return rc;
     if (rows * cols > src->len)
@@ -684,11 +732,119 @@ int lx2v_hip_quantize_fp8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t row
 int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std) {
     NEED(ctx, "ctx");
     NEED(buf, "buf");
+    if (buf->dtype == LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "fill_normal into an E4M3 buffer");
     if (int rc = set_dev(ctx)) return rc;
     if (int rc = run(ctx, "fill_normal", [&] {
             launch_fill_normal(ctx->stream, buf->ptr, buf->dtype, buf->len, seed, std);
         }))
         return rc;
+    return ok();
+}
+
+// ---- pre-quantized activations ------------------------------------------------------
+
+int lx2v_hip_alloc_e4m3(lx2v_hip_ctx *ctx, size_t rows, size_t cols, lx2v_hip_buf **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (int rc = not_capturing(ctx, "alloc_e4m3")) return rc;
+    if (cols && rows > ((size_t)1 << 40) / cols) return fail(LX2V_ERR_BAD_SHAPE, "E4M3 buffer %zux%zu too large", rows, cols);
+    if (int rc = set_dev(ctx)) return rc;
+    const size_t codes = (rows * cols + 255) & ~(size_t)255;
+    auto *b = new lx2v_hip_buf;
+    b->len = rows * cols;
+    b->dtype = LX2V_DTYPE_E4M3;
+    b->rows = rows;
+    b->cols = cols;
+    const size_t bytes = std::max<size_t>(codes + rows * 4, 4);
+    hipError_t e = hipMalloc(&b->ptr, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(b->ptr, 0, bytes, ctx->stream);
+    if (e != hipSuccess) {
+        if (b->ptr) (void)hipFree(b->ptr);
+        delete b;
+        return hip_fail(e, "hipMalloc(E4M3 buffer)");
+    }
+    b->scales = (float *)((uint8_t *)b->ptr + codes);
+    *out = b;
+    return ok();
+}
+
+int lx2v_hip_quantize_act(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                          lx2v_hip_buf *xq) {
+    NEED(ctx, "ctx");
+    NEED(x, "x");
+    NEED(xq, "xq");
+    if (xq->dtype != LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "quantize_act writes an E4M3 buffer");
+    if (x->dtype == LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "quantize_act reads an F32 or BF16 buffer");
+    const size_t cols = xq->cols;
+    if (rows > xq->rows) return fail(LX2V_ERR_BAD_SHAPE, "%zu rows into an E4M3 buffer of %zu", rows, xq->rows);
+    if (x_row + rows < x_row || (x_row + rows) * cols > x->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "x has %zu elements, rows [%zu,+%zu) x %zu", x->len, x_row, rows, cols);
+    if (!rows || !cols) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    const char *xp = (const char *)x->ptr + x_row * cols * x->elem_bytes();
+    return run(ctx, "act_quant_e4m3",
+               [&] { launch_act_quant(ctx->stream, xp, x->dtype, rows, cols, (uint8_t *)xq->ptr, xq->scales); });
+}
+
+// ---- HIP graphs ------------------------------------------------------------------------
+
+}  // extern "C"
+
+struct lx2v_hip_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+extern "C" {
+
+int lx2v_hip_graph_begin(lx2v_hip_ctx *ctx) {
+    NEED(ctx, "ctx");
+    if (ctx->capturing) return fail(LX2V_ERR_BAD_ARG, "graph capture already in progress");
+    if (int rc = set_dev(ctx)) return rc;
+    prof_harvest(ctx);  // pending profiler events must not straddle the capture
+    HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    ctx->capturing = true;
+    return ok();
+}
+
+int lx2v_hip_graph_end(lx2v_hip_ctx *ctx, lx2v_hip_graph **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (!ctx->capturing) return fail(LX2V_ERR_BAD_ARG, "no graph capture in progress");
+    if (int rc = set_dev(ctx)) return rc;
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture(ctx->stream, &g), "hipStreamEndCapture");
+    auto *gr = new lx2v_hip_graph;
+    gr->graph = g;
+    hipError_t e = hipGraphInstantiate(&gr->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        delete gr;
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    *out = gr;
+    return ok();
+}
+
+int lx2v_hip_graph_launch(lx2v_hip_ctx *ctx, const lx2v_hip_graph *g) {
+    NEED(ctx, "ctx");
+    NEED(g, "graph");
+    if (int rc = not_capturing(ctx, "graph_launch")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    HIP_TRY(hipGraphLaunch(g->exec, ctx->stream), "hipGraphLaunch");
+    return ok();
+}
+
+int lx2v_hip_graph_free(lx2v_hip_ctx *ctx, lx2v_hip_graph *g) {
+    NEED(ctx, "ctx");
+    if (!g) return ok();
+    if (int rc = not_capturing(ctx, "graph_free")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(graph_free)");
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
     return ok();
 }
 
@@ -719,9 +875,17 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
         return fail(LX2V_ERR_BAD_SHAPE, "y has %zu elements, rows [%zu,+%zu) x %zu need %zu", y->len, y_row, rows,
                     N, (y_row + rows) * N);
     if (bias && bias->len < N) return fail(LX2V_ERR_BAD_SHAPE, "bias has %zu elements, weight has %zu rows", bias->len, N);
+    if (y->dtype == LX2V_DTYPE_E4M3 || (bias && bias->dtype == LX2V_DTYPE_E4M3))
+        return fail(LX2V_ERR_BAD_ARG, "linear writes F32 or BF16 and reads an F32 or BF16 bias");
+    if (x->dtype == LX2V_DTYPE_E4M3) {
+        if (x->cols != K) return fail(LX2V_ERR_BAD_SHAPE, "E4M3 x has %zu cols, weight has %zu", x->cols, K);
+        if (w->fmt != LX2V_WFMT_FP8)
+            return fail(LX2V_ERR_UNSUPPORTED, "E4M3 activations need an FP8 weight");
+    }
     const char *xp = (const char *)x->ptr + x_row * K * x->elem_bytes();
     char *yp = (char *)y->ptr + y_row * N * y->elem_bytes();
-    if (overlap(yp, rows * N * y->elem_bytes(), xp, rows * K * x->elem_bytes()))
+    if (overlap(yp, rows * N * y->elem_bytes(), xp, rows * K * x->elem_bytes()) ||
+        (x->scales && overlap(yp, rows * N * y->elem_bytes(), x->scales + x_row, rows * 4)))
         return fail(LX2V_ERR_ALIAS, "linear output overlaps its input");
     if (bias && overlap(yp, rows * N * y->elem_bytes(), bias->ptr, N * bias->elem_bytes()))
         return fail(LX2V_ERR_ALIAS, "linear output overlaps its bias");
@@ -744,10 +908,19 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
         }
     }
 
-    if (w->fmt == LX2V_WFMT_FP8 && ctx->fp8_act == LX2V_FP8_ACT_E4M3) {
-        uint8_t *q;
-        float *s;
-        if (int rc = act_quant_into_ws(ctx, xp, x->dtype, rows, K, &q, &s)) return rc;
+    if (w->fmt == LX2V_WFMT_FP8 && (ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->dtype == LX2V_DTYPE_E4M3)) {
+        const uint8_t *q;
+        const float *s;
+        if (x->dtype == LX2V_DTYPE_E4M3) {
+            q = (const uint8_t *)xp;
+            s = x->scales + x_row;
+        } else {
+            uint8_t *wq;
+            float *ws;
+            if (int rc = act_quant_into_ws(ctx, xp, x->dtype, rows, K, &wq, &ws)) return rc;
+            q = wq;
+            s = ws;
+        }
         if (w->group == K && gemm_fp8_supported(rows, N, K)) {
             if (int rc = run(ctx, "gemm_fp8_e4m3", [&] {
                     launch_gemm_fp8(ctx->stream, ctx->num_cu, q, s, (const uint8_t *)w->codes, w->scales, bp, act,
@@ -785,6 +958,7 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
 int lx2v_hip_act_quant(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows, size_t cols,
                        uint8_t *q, float *s) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "act_quant")) return rc;
     NEED(x, "x");
     if (rows) {
         NEED(q, "q");
@@ -808,6 +982,7 @@ int lx2v_hip_act_quant(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, s
 
 int lx2v_hip_sync(lx2v_hip_ctx *ctx) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "sync")) return rc;
     if (int rc = set_dev(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     return ok();
@@ -815,6 +990,7 @@ int lx2v_hip_sync(lx2v_hip_ctx *ctx) {
 
 int lx2v_hip_profile_enable(lx2v_hip_ctx *ctx, int on) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "profile_enable")) return rc;
     if (!on) prof_harvest(ctx);
     ctx->prof.on = on != 0;
     return ok();
@@ -822,6 +998,7 @@ int lx2v_hip_profile_enable(lx2v_hip_ctx *ctx, int on) {
 
 int lx2v_hip_profile_report(lx2v_hip_ctx *ctx, char *out, size_t cap) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "profile_report")) return rc;
     NEED(out, "out");
     if (!cap) return fail(LX2V_ERR_BAD_ARG, "cap is 0");
     if (int rc = set_dev(ctx)) return rc;
@@ -851,13 +1028,51 @@ int lx2v_hip_profile_report(lx2v_hip_ctx *ctx, char *out, size_t cap) {
 
 int lx2v_hip_profile_reset(lx2v_hip_ctx *ctx) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "profile_reset")) return rc;
     prof_harvest(ctx);
     ctx->prof.stats.clear();
     return ok();
 }
 
+int lx2v_hip_profile_region(lx2v_hip_ctx *ctx, const char *name, int begin) {
+    NEED(ctx, "ctx");
+    NEED(name, "name");
+    if (int rc = not_capturing(ctx, "profile_region")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    auto &p = ctx->prof;
+    auto it = p.open_regions.find(name);
+    if (begin) {
+        if (it != p.open_regions.end()) return fail(LX2V_ERR_BAD_ARG, "region %s is already open", name);
+        hipEvent_t a;
+        HIP_TRY(hipEventCreate(&a), "hipEventCreate(region)");
+        hipError_t e = hipEventRecord(a, ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipEventDestroy(a);
+            return hip_fail(e, "hipEventRecord(region)");
+        }
+        p.open_regions[name] = a;
+        return ok();
+    }
+    if (it == p.open_regions.end()) return fail(LX2V_ERR_BAD_ARG, "region %s was not opened", name);
+    hipEvent_t b;
+    HIP_TRY(hipEventCreate(&b), "hipEventCreate(region)");
+    hipError_t e = hipEventRecord(b, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, it->second, b);
+    (void)hipEventDestroy(it->second);
+    (void)hipEventDestroy(b);
+    p.open_regions.erase(it);
+    if (e != hipSuccess) return hip_fail(e, "region timing");
+    auto &st = p.stats[name];
+    st.first += 1;
+    st.second += ms;
+    return ok();
+}
+
 int lx2v_hip_profile_kernel(lx2v_hip_ctx *ctx, const char *name, uint64_t *calls, double *total_ms) {
     NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "profile_kernel")) return rc;
     NEED(name, "name");
     NEED(calls, "calls");
     NEED(total_ms, "total_ms");

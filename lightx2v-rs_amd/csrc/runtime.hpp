@@ -15,7 +15,11 @@ struct lx2v_hip_buf {
     void *ptr = nullptr;
     size_t len = 0;    // elements
     int dtype = LX2V_DTYPE_F32;
-    size_t elem_bytes() const { return dtype == LX2V_DTYPE_BF16 ? 2 : 4; }
+    // LX2V_DTYPE_E4M3 only: [rows, cols] codes at ptr, f32 row scales at
+    // `scales` (inside the same allocation).
+    size_t rows = 0, cols = 0;
+    float *scales = nullptr;
+    size_t elem_bytes() const { return dtype == LX2V_DTYPE_BF16 ? 2 : dtype == LX2V_DTYPE_E4M3 ? 1 : 4; }
     size_t bytes() const { return len * elem_bytes(); }
 };
 
@@ -43,6 +47,7 @@ struct Profiler {
     std::vector<Pending> pending;
     std::vector<hipEvent_t> pool;
     std::map<std::string, std::pair<uint64_t, double>> stats;  // calls, total ms
+    std::map<std::string, hipEvent_t> open_regions;            // lx2v_hip_profile_region
 };
 
 }  // namespace lx2v
@@ -58,6 +63,9 @@ struct lx2v_hip_ctx {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     lx2v::Profiler prof;
+    // Stream capture in progress (lx2v_hip_graph_begin): nothing may
+    // allocate, free or synchronise until lx2v_hip_graph_end.
+    bool capturing = false;
 };
 
 namespace lx2v {
@@ -93,6 +101,9 @@ void launch_fp8_canon_count(hipStream_t s, uint8_t *codes, size_t n, unsigned lo
 void launch_q4_pack(hipStream_t s, const uint8_t *codes, size_t n, uint8_t *packed);
 void launch_act_quant(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols,
                       uint8_t *q, float *scale);
+// out[r, c] = e4m3(q[r, c]) * scale[r] (OCP decode), f32.
+void launch_decode_e4m3_rows(hipStream_t s, const uint8_t *q, const float *scale, size_t rows, size_t cols,
+                             float *out);
 void launch_quantize_q8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,
                         int8_t *q, float *scales);
 void launch_quantize_q4_sym(hipStream_t s, const float *src, size_t rows, size_t cols,

@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(_HERE, "liblightx2v_hip.so")
 
 OK, ERR_NO_DEVICE, ERR_BAD_SHAPE, ERR_ALIAS, ERR_HIP, ERR_BAD_ARG, ERR_OOM, ERR_UNSUPPORTED = range(8)
 ACT_NONE, ACT_GELU_TANH = 0, 1
-DTYPE_F32, DTYPE_BF16 = 0, 1
+DTYPE_F32, DTYPE_BF16, DTYPE_E4M3 = 0, 1, 2
 WFMT_F32, WFMT_Q8, WFMT_Q4, WFMT_FP8 = 0, 1, 2, 3
 FP8_ACT_E4M3, FP8_ACT_BF16 = 0, 1
 
@@ -39,7 +39,8 @@ EXPORTS = [
     "lx2v_hip_quantize_q8", "lx2v_hip_quantize_q4_sym", "lx2v_hip_quantize_fp8",
     "lx2v_hip_fill_normal", "lx2v_hip_linear", "lx2v_hip_act_quant", "lx2v_hip_sync",
     "lx2v_hip_profile_enable", "lx2v_hip_profile_report", "lx2v_hip_profile_reset",
-    "lx2v_hip_profile_kernel",
+    "lx2v_hip_profile_kernel", "lx2v_hip_alloc_e4m3", "lx2v_hip_quantize_act", "lx2v_hip_graph_begin",
+    "lx2v_hip_graph_end", "lx2v_hip_graph_launch", "lx2v_hip_graph_free", "lx2v_hip_profile_region",
 ]
 
 
@@ -97,6 +98,13 @@ def _load():
         "lx2v_hip_profile_reset": (ip, [vp]),
         "lx2v_hip_profile_kernel": (ip, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64),
                                          ctypes.POINTER(ctypes.c_double)]),
+        "lx2v_hip_alloc_e4m3": (ip, [vp, sz, sz, pp]),
+        "lx2v_hip_quantize_act": (ip, [vp, vp, sz, sz, vp]),
+        "lx2v_hip_graph_begin": (ip, [vp]),
+        "lx2v_hip_graph_end": (ip, [vp, pp]),
+        "lx2v_hip_graph_launch": (ip, [vp, vp]),
+        "lx2v_hip_graph_free": (ip, [vp, vp]),
+        "lx2v_hip_profile_region": (ip, [vp, ctypes.c_char_p, ip]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -166,6 +174,27 @@ class Weight:
     def free(self):
         if self.h and self._be.ctx:
             lib.lx2v_hip_weight_free(self._be.ctx, self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Graph:
+    """A captured sequence of device work, replayed with one launch."""
+
+    def __init__(self, be: "HipBackend", h: int):
+        self._be, self.h = be, h
+
+    def launch(self):
+        _check(lib.lx2v_hip_graph_launch(self._be.ctx, self.h))
+
+    def free(self):
+        if self.h and self._be.ctx:
+            lib.lx2v_hip_graph_free(self._be.ctx, self.h)
         self.h = None
 
     def __del__(self):
@@ -321,6 +350,23 @@ class HipBackend:
         _check(lib.lx2v_hip_act_quant(self.ctx, x.h, x_row, rows, cols, _ptr(q), _ptr(s)))
         return q, s
 
+    def alloc_e4m3(self, rows: int, cols: int) -> Buf:
+        """Per-token e4m3 activations [rows, cols] (codes + row scales)."""
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_alloc_e4m3(self.ctx, rows, cols, ctypes.byref(h)))
+        return Buf(self, h.value)
+
+    def quantize_act(self, x: Buf, x_row: int, rows: int, xq: Buf):
+        _check(lib.lx2v_hip_quantize_act(self.ctx, x.h, x_row, rows, xq.h))
+
+    def graph_begin(self):
+        _check(lib.lx2v_hip_graph_begin(self.ctx))
+
+    def graph_end(self) -> Graph:
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_graph_end(self.ctx, ctypes.byref(h)))
+        return Graph(self, h.value)
+
     def sync(self):
         _check(lib.lx2v_hip_sync(self.ctx))
 
@@ -335,6 +381,9 @@ class HipBackend:
 
     def profile_reset(self):
         _check(lib.lx2v_hip_profile_reset(self.ctx))
+
+    def profile_region(self, name: str, begin: bool):
+        _check(lib.lx2v_hip_profile_region(self.ctx, name.encode(), int(begin)))
 
     def profile_kernel(self, name: str):
         c = ctypes.c_uint64(0)
