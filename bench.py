@@ -286,7 +286,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
             "traffic": traffic,
-            "kernel": "k_gemm_fp8_dma (all 7 shapes of the chunk)",
+            "kernel": "fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma 256x128 tiles; k_gemm_fp8_pp 256x256 for ffn1)",
             "avg_launch_us": round(gemm_ms * 1e3 / n_linear, 2),
             "launches_per_step": n_linear,
         },

@@ -136,10 +136,13 @@ __device__ __forceinline__ float gelu_tanh_fast(float x) {
 // compact block of tiles: bands of up to 4 tile-rows walked column by
 // column, so an XCD's L2 holds the few A row-panels and B column-panels
 // its workgroups share.
-__device__ __forceinline__ void xcd_tile(int bid, int nb, int tiles_m, int tiles_n, int *tm, int *tn) {
+__device__ __forceinline__ int xcd_order(int bid, int nb) {
     const int per = nb / 8, rem = nb % 8;
     const int x = bid % 8, j = bid / 8;
-    const int id = x * per + (x < rem ? x : rem) + j;
+    return x * per + (x < rem ? x : rem) + j;
+}
+
+__device__ __forceinline__ void band_tile(int id, int tiles_m, int tiles_n, int *tm, int *tn) {
     const int G = tiles_m < 4 ? tiles_m : 4;
     const int group = id / (G * tiles_n);
     const int first = group * G;
@@ -147,6 +150,10 @@ __device__ __forceinline__ void xcd_tile(int bid, int nb, int tiles_m, int tiles
     const int in = id - first * tiles_n;
     *tm = first + in % gsz;
     *tn = in / gsz;
+}
+
+__device__ __forceinline__ void xcd_tile(int bid, int nb, int tiles_m, int tiles_n, int *tm, int *tn) {
+    band_tile(xcd_order(bid, nb), tiles_m, tiles_n, tm, tn);
 }
 
 // ---- epilogue stores ----------------------------------------------------------------

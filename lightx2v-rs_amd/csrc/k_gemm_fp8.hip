@@ -96,7 +96,168 @@ __device__ __forceinline__ void epilogue_fp8(const f32x16 (&acc)[TN][TM], int mb
                         if (nb + q < N) store1(yp + q, v[q]);
                 }
             }
+            // One channel group at a time: keeps the accumulators in AGPRs
+            // instead of moving them all to VGPRs up front.
+            __builtin_amdgcn_sched_barrier(0);
         }
+    }
+}
+
+// One 16-byte-per-lane buffer load straight into LDS at `lds` + 16 * lane.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff) {
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds, 16, voff, 0, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS-staged epilogue, used where the main loop leaves a large LDS ring
+// free.  Stage 1 (acc_to_lds): each wave applies the token scale, channel
+// scale, bias and GELU exactly as epilogue_fp8 does and writes the results,
+// already in the output type, into a staging tile of R rows x BN columns.
+// Stage 2 (lds_to_global, after a barrier): the whole block stores the tile
+// with consecutive lanes on consecutive 16-byte chunks of a row, so each
+// store instruction writes whole 128-byte lines instead of 16-byte pieces
+// of 32 rows.  The 16-byte chunks of staging row r sit at chunk c ^ (r % 16):
+// the column-fragment writes of stage 1 (32 rows, one chunk each) and the
+// row reads of stage 2 both spread over all 64 banks.  Needs a row of at
+// least 16 chunks (BN * sizeof(TY) >= 256).
+
+// Epilogue operands of one wave: token scales of its rows, channel scales
+// and bias of its columns (lane l: rows mbase + 32 i + l % 32, columns
+// nbase + 32 j + 8 g + 4 (l / 32) + 0..3).  Zero outside M x N.
+template <int TM, int TN>
+struct EpiRegs {
+    float sam[TM];
+    f32x4 s[TN][4], b[TN][4];
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void load_epi(EpiRegs<TM, TN> &e, int mbase, int nbase, int lane, int M, int N,
+                                         const float *__restrict__ sa, const float *__restrict__ sb,
+                                         const float *__restrict__ bias) {
+    const bool vec = (N & 3) == 0;
+    const int l32 = lane & 31, hf = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int m = mbase + i * 32 + l32;
+        e.sam[i] = m < M ? sa[m] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int nb = nbase + j * 32 + 8 * g + 4 * hf;
+            if (vec && nb + 3 < N) {
+                e.s[j][g] = *(const f32x4 *)(sb + nb);
+                e.b[j][g] = bias ? *(const f32x4 *)(bias + nb) : (f32x4){};
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    bool ok = nb + q < N;
+                    e.s[j][g][q] = ok ? sb[nb + q] : 0.0f;
+                    e.b[j][g][q] = (ok && bias) ? bias[nb + q] : 0.0f;
+                }
+            }
+        }
+    }
+}
+
+template <int TM, int TN, int BN, typename TY>
+__device__ __forceinline__ void acc_to_lds_regs(const f32x16 (&acc)[TN][TM], const EpiRegs<TM, TN> &e,
+                                                uint8_t *stg, int rloc, int cloc, int lane, int act) {
+    constexpr int EB = sizeof(TY), RB = BN * EB;
+    static_assert(RB >= 256 && (RB & (RB - 1)) == 0, "staging row must be a power of two >= 256 bytes");
+    const int l32 = lane & 31, hf = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int cb = (cloc + j * 32 + 8 * g + 4 * hf) * EB;  // byte column in the row
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                float v[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    v[q] = acc[j][i][4 * g + q] * e.sam[i] * e.s[j][g][q] + e.b[j][g][q];
+                    if (act == LX2V_ACT_GELU_TANH) v[q] = gelu_tanh_fast(v[q]);
+                }
+                const int r = rloc + i * 32 + l32;
+                uint8_t *p = stg + r * RB + ((((cb >> 4) ^ (r & 15))) << 4) + (cb & 15);
+                if constexpr (EB == 4) {
+                    *(f32x4 *)p = (f32x4){v[0], v[1], v[2], v[3]};
+                } else {
+                    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                    *(u32x2_t *)p = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                }
+            }
+        }
+    }
+}
+
+template <int TM, int TN, int BN, typename TY>
+__device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], uint8_t *stg, int rloc, int cloc,
+                                           int mbase, int nbase, int lane, int M, int N,
+                                           const float *__restrict__ sa, const float *__restrict__ sb,
+                                           const float *__restrict__ bias, int act) {
+    EpiRegs<TM, TN> e;
+    load_epi(e, mbase, nbase, lane, M, N, sa, sb, bias);
+    acc_to_lds_regs<TM, TN, BN, TY>(acc, e, stg, rloc, cloc, lane, act);
+}
+
+template <int R, int BN, int NT, typename TY>
+__device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m0, int n0, int M, int N,
+                                              TY *__restrict__ Y) {
+    constexpr int EB = sizeof(TY), RB = BN * EB, CPR = RB / 16, EPC = 16 / EB;
+    static_assert((R * CPR) % NT == 0, "staging tile must split evenly over the block");
+    const bool vec = N % EPC == 0;
+#pragma unroll
+    for (int it = 0; it < R * CPR / NT; it++) {
+        const int idx = it * NT + tid, r = idx / CPR, c = idx % CPR;
+        const int m = m0 + r, n = n0 + c * EPC;
+        if (m >= M || n >= N) continue;
+        const u32x4 v = *(const u32x4 *)(stg + r * RB + ((c ^ (r & 15)) << 4));
+        TY *yp = Y + (size_t)m * N + n;
+        if (vec) {
+            *(u32x4 *)yp = v;
+        } else {
+            const TY *e = (const TY *)&v;
+#pragma unroll
+            for (int q = 0; q < EPC; q++)
+                if (n + q < N) yp[q] = e[q];
+        }
+    }
+}
+
+constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
+
+// The staged epilogue of a BM x BN block tile through SMEM bytes of LDS,
+// in passes of R rows when the whole tile does not fit.  Waits for every
+// outstanding DMA of the main loop (stages past K still write zeros) and
+// for every wave's last fragment reads before reusing the ring.  The wave
+// owns tile rows [wr, wr + 32 TM) and columns [wc, wc + 32 TN).
+template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY>
+__device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, int wr, int wc,
+                                                int tid, int lane, int m0, int n0, int M, int N,
+                                                const float *__restrict__ sa, const float *__restrict__ sb,
+                                                const float *__restrict__ bias, int act, TY *__restrict__ Y) {
+    constexpr int RB = BN * (int)sizeof(TY);
+    constexpr int R = pow2_floor(SMEM / RB < BM ? SMEM / RB : BM);
+    static_assert(BM % R == 0 && R % (32 * TM) == 0, "a wave's rows must fall in one pass");
+    wait_vmcnt<0>();
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < BM / R; p++) {
+        if (p) __syncthreads();
+        if (wr >= p * R && wr < (p + 1) * R)
+            acc_to_lds<TM, TN, BN, TY>(acc, smem, wr - p * R, wc, m0 + wr, n0 + wc, lane, M, N, sa, sb, bias, act);
+        __syncthreads();
+        lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y);
     }
 }
 
@@ -247,19 +408,6 @@ __device__ __forceinline__ uint32_t dma_slot(uint32_t row, uint32_t c) {
     return c ^ ((row / RW) % CPR);
 }
 
-// One 16-byte-per-lane buffer load straight into LDS at `lds` + 16 * lane.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff) {
-    typedef __attribute__((address_space(3))) void *lds_ptr;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds, 16, voff, 0, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 template <int BM, int BN, int WGM, int WGN, int BKB, int NS, typename TY>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_dma(const uint8_t *__restrict__ A,
                                                                    const float *__restrict__ sa,
@@ -376,7 +524,300 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_dma(const uint8_
             }
         }
     }
+    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY>(acc, smem, wm * WM, wn * WN, tid, lane, m0, n0, M, N,
+                                                          sa, sb, bias, act, Y);
+}
+
+// ---- software-pipelined direct-to-LDS kernel ----------------------------------------
+//
+// Same data movement as k_gemm_fp8_dma (16-byte buffer_load ... lds into an
+// NS-stage LDS ring, global-side swizzle), one wave per SIMD, and a
+// schedule that keeps the matrix cores fed across the per-stage barrier:
+// the MFMA fragments of stage s + 1 are read from LDS into a second
+// register set while the MFMAs of stage s issue, and the DMA loads of stage
+// s + NS - 1 are issued between those MFMAs.  Per stage:
+//
+//   wait (own loads of stage s + 1 landed); barrier (everyone's have, and
+//   everyone has consumed stage s - 1, whose buffer is refilled next);
+//   for t over the stage's MFMAs:  MFMA t (fragments of stage s)
+//                                  + one LDS fragment read for stage s + 1
+//                                  + one DMA load of stage s + NS - 1
+//
+// The order is pinned with scheduling barriers.  Fragment registers:
+// 2 sets x (TM + TN) x (BK / 64) x 8 VGPRs; accumulators TM x TN x 16 AGPRs.
+
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS, typename TY>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_sp(const uint8_t *__restrict__ A,
+                                                                  const float *__restrict__ sa,
+                                                                  const uint8_t *__restrict__ B,
+                                                                  const float *__restrict__ sb,
+                                                                  const float *__restrict__ bias,
+                                                                  TY *__restrict__ Y, int M, int N, int K,
+                                                                  int act, int tiles_m, int tiles_n) {
+    constexpr int NW = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int KK = BKB / 64;                  // MFMA k-steps per stage
+    constexpr int CPR = BKB / 16;                 // 16-byte chunks per tile row
+    constexpr int RPI = 64 / CPR;                 // tile rows per 1 KB load
+    constexpr int ALD = BM / RPI / NW, BLD = BN / RPI / NW;  // loads per wave per stage
+    constexpr int LPS = ALD + BLD;
+    constexpr int STAGE = (BM + BN) * BKB;
+    constexpr int NMMA = KK * TM * TN;            // MFMAs per wave per stage
+    static_assert(ALD * RPI * NW == BM && BLD * RPI * NW == BN, "tile rows must split over the waves");
+    static_assert(NS >= 3 && NS * STAGE <= 160 * 1024, "LDS");
+    static_assert(KK * (TM + TN) <= NMMA && LPS <= NMMA, "interleave slots");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wid / WGN, wn = wid % WGN;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = K / BKB;
+
+    const auto ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K);
+    const auto rb_src = make_rsrc(B + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
+
+    // DMA load j of a stage (j < ALD: activation rows, else weight rows):
+    // tile rows [(i NW + wid) RPI, +RPI) with i = j or j - ALD; lane l fills
+    // slot l % CPR of row l / CPR.
+    const uint32_t lrow = (uint32_t)lane / CPR, lslot = (uint32_t)lane % CPR;
+    uint32_t g_off[LPS];
+#pragma unroll
+    for (int j = 0; j < LPS; j++) {
+        const bool isa = j < ALD;
+        const uint32_t row = (uint32_t)((isa ? j : j - ALD) * NW + wid) * RPI + lrow;
+        g_off[j] = row * (uint32_t)K + dma_slot<BKB>(isa ? row : BM + row, lslot) * 16;
+    }
+    auto dma = [&](int j, int kt) {
+        const bool isa = j < ALD;
+        const int i = isa ? j : j - ALD;
+        uint8_t *dst = smem + (kt % NS) * STAGE + ((isa ? 0 : BM) + (i * NW + wid) * RPI) * BKB;
+        const uint32_t off = kt < KT ? g_off[j] + (uint32_t)kt * BKB : kOob;
+        dma16(isa ? ra_src : rb_src, dst, off);
+    };
+
+    // Fragment f of a stage, f = kk (TM + TN) + blk: activation block blk
+    // (< TM) or weight block blk - TM; each is two 16-byte LDS reads.
+    constexpr int NF = KK * (TM + TN);
+    const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
+    auto frag = [&](int f, int buf) -> i32x8 {
+        const int kk = f / (TM + TN), blk = f % (TM + TN);
+        const uint32_t row = blk < TM ? (uint32_t)(wm * WM + blk * 32) + frow
+                                      : (uint32_t)(BM + wn * WN + (blk - TM) * 32) + frow;
+        const uint32_t c = (uint32_t)kk * 4 + fhalf;
+        const uint8_t *rp = smem + buf * STAGE + row * BKB;
+        const u32x4 lo = *(const u32x4 *)(rp + (dma_slot<BKB>(row, c) << 4));
+        const u32x4 hi = *(const u32x4 *)(rp + (dma_slot<BKB>(row, c + 1) << 4));
+        return (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    };
+
+    f32x16 acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
+
+    i32x8 fr0[NF], fr1[NF];
+    // One stage: MFMAs on `cur` interleaved with the fragment reads of
+    // stage s + 1 into `nxt` and the DMA loads of stage s + NS - 1.
+    auto stage = [&](const i32x8(&cur)[NF], i32x8(&nxt)[NF], int s) {
+        wait_vmcnt<(NS - 3) * LPS>();  // own loads of stage s + 1 landed
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int nb = (s + 1) % NS;
+#pragma unroll
+        for (int t = 0; t < NMMA; t++) {
+            const int kk = t / (TM * TN), j = (t % (TM * TN)) / TM, i = t % TM;
+            acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                cur[kk * (TM + TN) + TM + j], cur[kk * (TM + TN) + i], acc[j][i], 0, 0, 0, 0, 0, 0);
+            // fragment reads and loads spread evenly over the stage's MFMAs
+#pragma unroll
+            for (int f = 0; f < NF; f++)
+                if (f * NMMA / NF == t) nxt[f] = frag(f, nb);
+#pragma unroll
+            for (int j2 = 0; j2 < LPS; j2++)
+                if (j2 * NMMA / LPS == t) dma(j2, s + NS - 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Prologue: stages 0 .. NS - 2 in flight, stage 0's fragments in fr0.
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++)
+#pragma unroll
+        for (int j = 0; j < LPS; j++) dma(j, st);
+    wait_vmcnt<(NS - 2) * LPS>();  // stage 0 landed (own loads)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int f = 0; f < NF; f++) fr0[f] = frag(f, 0);
+    // KT >= 1 (the launcher requires K to be a positive multiple of BK); a
+    // do-while keeps the accumulators in AGPRs on every path.
+    int s = 0;
+    do {
+        stage(fr0, fr1, s);
+        if (s + 1 < KT) stage(fr1, fr0, s + 1);
+        s += 2;
+    } while (s < KT);
+    // Drain what is still in flight (loads past KT are out of range and
+    // write nothing) before the waves retire their LDS.
+    wait_vmcnt<0>();
     epilogue_fp8<TM, TN, TY>(acc, m0 + wm * WM, n0 + wn * WN, lane, M, N, sa, sb, bias, act, Y);
+}
+
+// ---- ping-pong kernel: two wave groups alternate MFMA and LDS phases ---------------
+//
+// Measured on gfx950: a ds_read_b128 costs its own wave ~25 MFMA cycles of
+// issue, but does not slow the MFMAs of the other wave on the same SIMD.
+// So the 8 waves of a 256 x BN tile form two groups of four (waves w and
+// w + 4 share a SIMD); every phase one group issues the MFMAs of one LDS
+// stage (BKB bytes of K) for its 128 x BN half while the other group reads
+// its fragments of the next stage, and a barrier swaps the roles.  Group 0
+// also issues the direct-to-LDS loads of stage S + NS - 1 in its read phase
+// of stage S (an NS-stage ring), and waits for stage S + 1 at the end of its
+// following MFMA phase:
+//
+//   phase 2S:   group 0 reads stage S (+ loads S + NS - 1);  group 1 computes S - 1
+//   phase 2S+1: group 0 computes S (then waits for S + 1);   group 1 reads S
+//
+// so a load has 2 NS - 2 phases to land.  Group g owns tile rows
+// 128 g .. 128 g + 127, split GM x GN over its four waves.
+
+template <int BN, int GM, int GN, int BKB, int NS, typename TY>
+__global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restrict__ A,
+                                                       const float *__restrict__ sa,
+                                                       const uint8_t *__restrict__ B,
+                                                       const float *__restrict__ sb,
+                                                       const float *__restrict__ bias,
+                                                       TY *__restrict__ Y, int M, int N, int K, int act,
+                                                       int tiles_m, int tiles_n) {
+    constexpr int BM = 256;
+    static_assert(GM * GN == 4, "four waves per group");
+    constexpr int WM = BM / 2 / GM, WN = BN / GN, TM = WM / 32, TN = WN / 32, KK = BKB / 64;
+    constexpr int NF = KK * (TM + TN);        // fragments per read phase
+    constexpr int STAGE = (BM + BN) * BKB;
+    constexpr int CPR = BKB / 16;             // 16-byte chunks per tile row
+    constexpr int RPI = 64 / CPR;             // tile rows per 1 KB load
+    constexpr int LPW = (BM + BN) / RPI / 4;  // loads per group-0 wave per stage
+    constexpr int AJ = BM / RPI / 4;          // the first AJ of them are activation rows
+    static_assert(AJ * RPI * 4 == BM && LPW * RPI * 4 == BM + BN, "stage rows must split over four waves");
+    static_assert(NS >= 2 && NS * STAGE <= 160 * 1024 && (NS - 2) * LPW < 64, "LDS ring / vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wid >> 2, q = wid & 3, wm = q / GN, wn = q % GN;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = K / BKB;
+
+    const auto ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K);
+    const auto rb_src = make_rsrc(B + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
+
+    // Load j of a group-0 wave fills 1 KB block b = 4 j + q of the stage
+    // (activation rows for j < AJ, weight rows after).  The swizzle repeats
+    // every 16 rows and 4 RPI is a multiple of 16, so one lane offset serves
+    // every j.
+    const uint32_t lrow = (uint32_t)lane / CPR, lslot = (uint32_t)lane % CPR;
+    const uint32_t g_lane = ((uint32_t)q * RPI + lrow) * (uint32_t)K + dma_slot<BKB>((uint32_t)q * RPI + lrow, lslot) * 16;
+    const uint32_t g_step = 4u * RPI * (uint32_t)K;
+    auto load_stage = [&](int ss) {
+        uint8_t *base = smem + (ss % NS) * STAGE;
+        const bool in = ss < KT;
+        const uint32_t k0 = (uint32_t)ss * BKB;
+#pragma unroll
+        for (int j = 0; j < LPW; j++) {
+            const bool isa = j < AJ;
+            const uint32_t off = in ? g_lane + (uint32_t)(isa ? j : j - AJ) * g_step + k0 : kOob;
+            dma16(isa ? ra_src : rb_src, base + (j * 4 + q) * RPI * BKB, off);
+        }
+    };
+
+    // Fragment rows are (multiple of 32) + lane % 32, so their swizzle bits
+    // depend on the lane only: one byte offset per chunk pair and kk.
+    const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
+    uint32_t f_lane[KK][2];
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            f_lane[kk][h] = frow * BKB + (dma_slot<BKB>(frow, (uint32_t)kk * 4 + fhalf + h) << 4);
+    i32x8 fr[NF];
+    auto read_frags = [&](int ss) {
+        const uint8_t *base = smem + (ss % NS) * STAGE;
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+            const int kk = f / (TM + TN), blk = f % (TM + TN);
+            const int row0 = blk < TM ? grp * (BM / 2) + wm * WM + blk * 32 : BM + wn * WN + (blk - TM) * 32;
+            const uint8_t *rp = base + row0 * BKB;
+            const u32x4 lo = *(const u32x4 *)(rp + f_lane[kk][0]);
+            const u32x4 hi = *(const u32x4 *)(rp + f_lane[kk][1]);
+            fr[f] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+    };
+
+    f32x16 acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
+
+    // Prologue: stages 0 .. NS - 2 issued, stage 0 in LDS.
+    if (grp == 0) {
+#pragma unroll
+        for (int st = 0; st < NS - 1; st++) load_stage(st);
+        wait_vmcnt<(NS - 2) * LPW>();
+    }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Phases 0 .. 2 KT, each closed by a barrier; group 1 runs one phase
+    // behind (an idle phase 0 first).  The loop body is the same straight
+    // line for both groups, so the accumulators never cross a branch.
+    if (grp == 1) {
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int ss = 0; ss < KT; ss++) {
+        if (grp == 0) load_stage(ss + NS - 1);  // its buffer held stage ss - 1: read by both groups already
+        read_frags(ss);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): fragments in registers
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        fr[kk * (TM + TN) + TM + j], fr[kk * (TM + TN) + i], acc[j][i], 0, 0, 0, 0, 0, 0);
+        if (grp == 0) wait_vmcnt<(NS - 2) * LPW>();  // stage ss + 1 landed (group 0 issues every load)
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (grp == 0) __builtin_amdgcn_s_barrier();
+    staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY>(acc, smem, grp * (BM / 2) + wm * WM, wn * WN, tid, lane, m0,
+                                                        n0, M, N, sa, sb, bias, act, Y);
+}
+
+template <int BN, int GM, int GN, int BKB, int NS>
+void launch_pp(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
+               const float *bias, int act, void *y, int y_dtype, int M, int N, int K) {
+    int tiles_m = (M + 255) / 256, tiles_n = (N + BN - 1) / BN;
+    dim3 grid(tiles_m * tiles_n), block(512);
+    if (y_dtype == LX2V_DTYPE_BF16)
+        hipLaunchKernelGGL((k_gemm_fp8_pp<BN, GM, GN, BKB, NS, uint16_t>), grid, block, 0, s, a, sa, b, sb, bias,
+                           (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((k_gemm_fp8_pp<BN, GM, GN, BKB, NS, float>), grid, block, 0, s, a, sa, b, sb, bias,
+                           (float *)y, M, N, K, act, tiles_m, tiles_n);
 }
 
 template <int BM, int BN>
@@ -405,6 +846,19 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
                            (float *)y, M, N, K, act, tiles_m, tiles_n);
 }
 
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS>
+void launch_sp(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
+               const float *bias, int act, void *y, int y_dtype, int M, int N, int K) {
+    int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
+    if (y_dtype == LX2V_DTYPE_BF16)
+        hipLaunchKernelGGL((k_gemm_fp8_sp<BM, BN, WGM, WGN, BKB, NS, uint16_t>), grid, block, 0, s, a, sa, b, sb,
+                           bias, (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((k_gemm_fp8_sp<BM, BN, WGM, WGN, BKB, NS, float>), grid, block, 0, s, a, sa, b, sb, bias,
+                           (float *)y, M, N, K, act, tiles_m, tiles_n);
+}
+
 // Direct-to-LDS configurations: tile (activation rows x channels), wave
 // grid, K bytes per stage, stages.
 struct DmaCfg {
@@ -418,6 +872,21 @@ constexpr DmaCfg kDma[] = {
     {128, 256, 2, 4, 128, 3},  // 4  (8 waves)
     {256, 256, 2, 4, 64, 4},   // 5  (8 waves)
     {256, 256, 2, 2, 64, 4},   // 6
+    // software-pipelined (k_gemm_fp8_sp)
+    {256, 256, 2, 2, 64, 4},   // 7
+    {256, 128, 2, 2, 64, 4},   // 8
+    {128, 256, 2, 2, 64, 4},   // 9
+    {256, 128, 2, 2, 128, 3},  // 10
+    {128, 128, 2, 2, 128, 4},  // 11
+    {256, 256, 2, 2, 64, 5},   // 12
+    {256, 256, 2, 4, 64, 5},   // 13 (8 waves)
+    {256, 128, 2, 2, 64, 6},   // 14
+    {256, 256, 1, 4, 128, 2},  // 15 ping-pong (k_gemm_fp8_pp); WGM x WGN = one group's waves
+    {256, 256, 1, 4, 64, 4},   // 16
+    {256, 256, 1, 4, 64, 5},   // 17
+    {256, 128, 2, 2, 128, 3},  // 18
+    {256, 128, 2, 2, 64, 6},   // 19
+    {256, 128, 1, 4, 128, 3},  // 20
 };
 
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
@@ -429,7 +898,21 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 3: launch_dma<256, 128, 4, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 4: launch_dma<128, 256, 2, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 5: launch_dma<256, 256, 2, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        default: launch_dma<256, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 6: launch_dma<256, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 7: launch_sp<256, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 8: launch_sp<256, 128, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 9: launch_sp<128, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 10: launch_sp<256, 128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 11: launch_sp<128, 128, 2, 2, 128, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 12: launch_sp<256, 256, 2, 2, 64, 5>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 13: launch_sp<256, 256, 2, 4, 64, 5>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 14: launch_sp<256, 128, 2, 2, 64, 6>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 15: launch_pp<256, 1, 4, 128, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 16: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 17: launch_pp<256, 1, 4, 64, 5>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 18: launch_pp<128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 19: launch_pp<128, 2, 2, 64, 6>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        default: launch_pp<128, 1, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
     }
 }
 
@@ -452,31 +935,48 @@ bool gemm_fp8_supported(size_t M, size_t N, size_t K) {
            N * K < (1ull << 31) && M < (1u << 30) && N < (1u << 30);
 }
 
-void launch_gemm_fp8(hipStream_t s, int num_cu, const uint8_t *a, const float *a_scale,
+// Time model of the K % 128 == 0 configurations, fitted to measured
+// kernel times at the Wan shapes (M 512..4680, K 1536..8960, N 1536..14336):
+// t = rounds * (stages * per_stage + per_round), one stage = 128 bytes of K
+// over the whole tile, per_round = the prologue + epilogue of a workgroup.
+// The 256 x 256 ping-pong tile does twice the work per stage at 0.70x the
+// 8-wave 256 x 128 tile's time per unit of work, but its epilogue costs
+// 3x more per round.
+struct CfgCost {
+    int idx;
+    double per_stage_us, per_round_us;
+};
+constexpr CfgCost kAuto[] = {{3, 0.89, 4.4}, {4, 0.89, 4.4}, {16, 1.25, 14.1}};
+
+Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K) {
+    Fp8Plan p;
+    if (K % 128 != 0) return p;  // the register-staged kernel
+    const int nd = (int)(sizeof(kDma) / sizeof(kDma[0]));
+    const int forced = forced_cfg();
+    if (forced >= 0 && forced < nd) {
+        p.kernel = forced;
+        return p;
+    }
+    double best = 0.0;
+    for (const CfgCost &c : kAuto) {
+        const DmaCfg &d = kDma[c.idx];
+        const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
+        const double rounds = (double)((tiles + num_cu - 1) / num_cu);
+        const double t = rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us);
+        if (p.kernel < 0 || t < best * 0.9999) {  // ties keep the earlier
+            best = t;
+            p.kernel = c.idx;
+        }
+    }
+    return p;
+}
+
+void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t *a, const float *a_scale,
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
                      int y_dtype, size_t M, size_t N, size_t K) {
     int m = (int)M, n = (int)N, k = (int)K;
-    const int nd = (int)(sizeof(kDma) / sizeof(kDma[0]));
-    if (K % 128 == 0) {
-        int pick = forced_cfg();
-        if (pick < 0 || pick >= nd) {
-            // The 8-wave tiles (measured fastest at every Wan shape); of
-            // those, the one that fills the chip best: fraction of issued
-            // MFMA work that is useful over whole waves of workgroups; ties
-            // keep the earlier.
-            double best = -1.0;
-            pick = 3;
-            for (int i = 3; i < 5; i++) {
-                size_t tiles = ((M + kDma[i].bm - 1) / kDma[i].bm) * ((N + kDma[i].bn - 1) / kDma[i].bn);
-                size_t waves = (tiles + num_cu - 1) / num_cu;
-                double eff = (double)M * N / ((double)waves * num_cu * kDma[i].bm * kDma[i].bn);
-                if (eff > best * 1.0001) {
-                    best = eff;
-                    pick = i;
-                }
-            }
-        }
-        launch_dma_idx(pick, s, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k);
+    if (p.kernel >= 0) {
+        launch_dma_idx(p.kernel, s, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k);
         return;
     }
     // K not a multiple of 128: the register-staged kernel.

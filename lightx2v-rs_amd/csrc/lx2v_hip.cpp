@@ -74,6 +74,7 @@ int ensure(lx2v_hip_ctx *ctx, void **ptr, size_t *have, size_t need, const char 
     return LX2V_OK;
 }
 
+
 // Byte ranges [a, a+na) and [b, b+nb) overlap.
 bool overlap(const void *a, size_t na, const void *b, size_t nb) {
     uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
@@ -922,9 +923,10 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
             s = ws;
         }
         if (w->group == K && gemm_fp8_supported(rows, N, K)) {
+            const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K);
             if (int rc = run(ctx, "gemm_fp8_e4m3", [&] {
-                    launch_gemm_fp8(ctx->stream, ctx->num_cu, q, s, (const uint8_t *)w->codes, w->scales, bp, act,
-                                    yp, y->dtype, rows, N, K);
+                    launch_gemm_fp8(ctx->stream, ctx->num_cu, plan, q, s, (const uint8_t *)w->codes, w->scales, bp,
+                                    act, yp, y->dtype, rows, N, K);
                 }))
                 return rc;
         } else {

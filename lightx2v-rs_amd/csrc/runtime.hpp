@@ -125,8 +125,13 @@ void launch_gemm_generic(hipStream_t s, const void *a, int amode, const float *a
                          int y_dtype, size_t M);
 
 // k_gemm_fp8.hip: fp8 MFMA, per-output-channel weight scale (group == K).
+// plan_gemm_fp8 picks the kernel configuration for a shape.
+struct Fp8Plan {
+    int kernel = -1;  // configuration index, or -1: the register-staged kernel (K % 128 != 0)
+};
 bool gemm_fp8_supported(size_t M, size_t N, size_t K);
-void launch_gemm_fp8(hipStream_t s, int num_cu, const uint8_t *a, const float *a_scale,
+Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K);
+void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t *a, const float *a_scale,
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
                      int y_dtype, size_t M, size_t N, size_t K);
 

@@ -90,6 +90,23 @@ def test_fp8_epilogue_dtypes_offsets(be, act, ydt, xdt):
         assert_close(y, want, 4e-3, 8e-3, what="fp8 epilogue bf16 out")
 
 
+@pytest.mark.parametrize("M,K,N", [(77, 256, 130), (300, 1536, 1000), (513, 512, 2056), (1, 128, 8),
+                                   (260, 384, 1540)])
+def test_fp8_bf16_out_is_rounded_f32_out(be, M, K, N):
+    """The bf16 output is the f32 output of the same contraction rounded to
+    nearest-even bf16, bit for bit, ragged N included (N % 8 != 0 takes the
+    per-element stores); the f32 output is checked against the oracle."""
+    x = normal(2001 + M, M * K).reshape(M, K)
+    _, q, s = fp8_weight(2002 + N, N, K, K)
+    b = normal(2003, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, K)
+    for act in (H.ACT_NONE, H.ACT_GELU_TANH):
+        y32 = run_linear(be, x, w, b, act)
+        y16 = run_linear(be, x, w, b, act, y_dtype=H.DTYPE_BF16)
+        assert np.array_equal(u32(y16), u32(O.bf16_round(y32))), f"act {act}"
+        assert_close(y32, oracle_w8a8(x, q, s, K, b, act), *FP8_TIGHT, what="fp8 f32 out")
+
+
 def test_fp8_no_bias(be):
     M, K, N = 96, 640, 320
     x = normal(8, M * K).reshape(M, K)
