@@ -128,63 +128,64 @@ __device__ __forceinline__ void wait_vmcnt() {
 // row reads of stage 2 both spread over all 64 banks.  Needs a row of at
 // least 16 chunks (BN * sizeof(TY) >= 256).
 
-// Epilogue operands of one wave: token scales of its rows, channel scales
-// and bias of its columns (lane l: rows mbase + 32 i + l % 32, columns
-// nbase + 32 j + 8 g + 4 (l / 32) + 0..3).  Zero outside M x N.
-template <int TM, int TN>
-struct EpiRegs {
-    float sam[TM];
-    f32x4 s[TN][4], b[TN][4];
-};
-
-template <int TM, int TN>
-__device__ __forceinline__ void load_epi(EpiRegs<TM, TN> &e, int mbase, int nbase, int lane, int M, int N,
-                                         const float *__restrict__ sa, const float *__restrict__ sb,
-                                         const float *__restrict__ bias) {
-    const bool vec = (N & 3) == 0;
-    const int l32 = lane & 31, hf = lane >> 5;
+// Epilogue operands of a BM x BN tile: sc[r] is the token scale of tile row
+// r, sc[BM + c] the channel scale and sc[BM + BN + c] the bias of tile
+// column c, zero outside M x N.  Loaded into registers when the workgroup
+// starts (at most three per thread), so their latency hides under the K
+// loop, and parked in a small LDS array after it.
+template <int BM, int BN, int NT>
+struct TileOps {
+    static constexpr int NV = BM + 2 * BN, PER = (NV + NT - 1) / NT;
+    float v[PER];
+    __device__ __forceinline__ void load(int tid, int m0, int n0, int M, int N, const float *__restrict__ sa,
+                                         const float *__restrict__ sb, const float *__restrict__ bias) {
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
-        const int m = mbase + i * 32 + l32;
-        e.sam[i] = m < M ? sa[m] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int nb = nbase + j * 32 + 8 * g + 4 * hf;
-            if (vec && nb + 3 < N) {
-                e.s[j][g] = *(const f32x4 *)(sb + nb);
-                e.b[j][g] = bias ? *(const f32x4 *)(bias + nb) : (f32x4){};
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    bool ok = nb + q < N;
-                    e.s[j][g][q] = ok ? sb[nb + q] : 0.0f;
-                    e.b[j][g][q] = (ok && bias) ? bias[nb + q] : 0.0f;
-                }
+        for (int p = 0; p < PER; p++) {
+            const int i = tid + p * NT;
+            float x = 0.0f;
+            if (i < BM) {
+                if (m0 + i < M) x = sa[m0 + i];
+            } else if (i < BM + BN) {
+                if (n0 + i - BM < N) x = sb[n0 + i - BM];
+            } else if (i < NV) {
+                if (bias && n0 + i - BM - BN < N) x = bias[n0 + i - BM - BN];
             }
+            v[p] = x;
         }
     }
-}
+    __device__ __forceinline__ void park(float *sc, int tid) const {
+#pragma unroll
+        for (int p = 0; p < PER; p++)
+            if (tid + p * NT < NV) sc[tid + p * NT] = v[p];
+    }
+};
 
-template <int TM, int TN, int BN, typename TY>
-__device__ __forceinline__ void acc_to_lds_regs(const f32x16 (&acc)[TN][TM], const EpiRegs<TM, TN> &e,
-                                                uint8_t *stg, int rloc, int cloc, int lane, int act) {
+// Stage 1 of the staged epilogue for one wave: its accumulators, scaled by
+// token and channel scale, biased and GELU'd, into staging rows rloc ..
+// (the wave's tile rows start at wr, its columns at wc).
+template <int BM, int BN, int TM, int TN, typename TY>
+__device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const float *sc, uint8_t *stg, int rloc,
+                                           int wr, int wc, int lane, int act) {
     constexpr int EB = sizeof(TY), RB = BN * EB;
     static_assert(RB >= 256 && (RB & (RB - 1)) == 0, "staging row must be a power of two >= 256 bytes");
     const int l32 = lane & 31, hf = lane >> 5;
+    float sam[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++) sam[i] = sc[wr + i * 32 + l32];
 #pragma unroll
     for (int j = 0; j < TN; j++) {
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            const int cb = (cloc + j * 32 + 8 * g + 4 * hf) * EB;  // byte column in the row
+            const int c = wc + j * 32 + 8 * g + 4 * hf;
+            const f32x4 s4 = *(const f32x4 *)(sc + BM + c);
+            const f32x4 b4 = *(const f32x4 *)(sc + BM + BN + c);
+            const int cb = c * EB;  // byte column in the row
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 float v[4];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    v[q] = acc[j][i][4 * g + q] * e.sam[i] * e.s[j][g][q] + e.b[j][g][q];
+                    v[q] = acc[j][i][4 * g + q] * sam[i] * s4[q] + b4[q];
                     if (act == LX2V_ACT_GELU_TANH) v[q] = gelu_tanh_fast(v[q]);
                 }
                 const int r = rloc + i * 32 + l32;
@@ -196,18 +197,9 @@ __device__ __forceinline__ void acc_to_lds_regs(const f32x16 (&acc)[TN][TM], con
                     *(u32x2_t *)p = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
-}
-
-template <int TM, int TN, int BN, typename TY>
-__device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], uint8_t *stg, int rloc, int cloc,
-                                           int mbase, int nbase, int lane, int M, int N,
-                                           const float *__restrict__ sa, const float *__restrict__ sb,
-                                           const float *__restrict__ bias, int act) {
-    EpiRegs<TM, TN> e;
-    load_epi(e, mbase, nbase, lane, M, N, sa, sb, bias);
-    acc_to_lds_regs<TM, TN, BN, TY>(acc, e, stg, rloc, cloc, lane, act);
 }
 
 template <int R, int BN, int NT, typename TY>
@@ -239,13 +231,13 @@ constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
 // The staged epilogue of a BM x BN block tile through SMEM bytes of LDS,
 // in passes of R rows when the whole tile does not fit.  Waits for every
 // outstanding DMA of the main loop (stages past K still write zeros) and
-// for every wave's last fragment reads before reusing the ring.  The wave
-// owns tile rows [wr, wr + 32 TM) and columns [wc, wc + 32 TN).
+// for every wave's last fragment reads before reusing the ring; the
+// operands in sc (TileOps) must be parked before the call.  The wave owns
+// tile rows [wr, wr + 32 TM) and columns [wc, wc + 32 TN).
 template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY>
-__device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, int wr, int wc,
-                                                int tid, int lane, int m0, int n0, int M, int N,
-                                                const float *__restrict__ sa, const float *__restrict__ sb,
-                                                const float *__restrict__ bias, int act, TY *__restrict__ Y) {
+__device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, const float *sc, int wr,
+                                                int wc, int tid, int lane, int m0, int n0, int M, int N, int act,
+                                                TY *__restrict__ Y) {
     constexpr int RB = BN * (int)sizeof(TY);
     constexpr int R = pow2_floor(SMEM / RB < BM ? SMEM / RB : BM);
     static_assert(BM % R == 0 && R % (32 * TM) == 0, "a wave's rows must fall in one pass");
@@ -254,8 +246,7 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uin
 #pragma unroll
     for (int p = 0; p < BM / R; p++) {
         if (p) __syncthreads();
-        if (wr >= p * R && wr < (p + 1) * R)
-            acc_to_lds<TM, TN, BN, TY>(acc, smem, wr - p * R, wc, m0 + wr, n0 + wc, lane, M, N, sa, sb, bias, act);
+        if (wr >= p * R && wr < (p + 1) * R) acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, wr, wc, lane, act);
         __syncthreads();
         lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y);
     }
@@ -424,8 +415,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_dma(const uint8_
     constexpr int ALD = BM / RPI / NW, BLD = BN / RPI / NW;  // loads per wave per stage
     constexpr int STAGE = (BM + BN) * BKB;
     static_assert(ALD * RPI * NW == BM && BLD * RPI * NW == BN, "tile rows must split over the waves");
-    static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS");
+    using Ops = TileOps<BM, BN, 64 * NW>;
+    static_assert(NS >= 2 && NS * STAGE + Ops::NV * 4 <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid / WGN, wn = wid % WGN;
@@ -433,6 +426,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_dma(const uint8_
     xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int KT = K / BKB;
+    Ops ops;
+    ops.load(tid, m0, n0, M, N, sa, sb, bias);
 
     // Rows past the matrix read zero (or leave LDS as it was): they only
     // feed output rows / channels that are never stored.
@@ -524,8 +519,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_dma(const uint8_
             }
         }
     }
-    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY>(acc, smem, wm * WM, wn * WN, tid, lane, m0, n0, M, N,
-                                                          sa, sb, bias, act, Y);
+    ops.park(sc, tid);
+    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N,
+                                                          act, Y);
 }
 
 // ---- software-pipelined direct-to-LDS kernel ----------------------------------------
@@ -704,8 +700,10 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
     constexpr int LPW = (BM + BN) / RPI / 4;  // loads per group-0 wave per stage
     constexpr int AJ = BM / RPI / 4;          // the first AJ of them are activation rows
     static_assert(AJ * RPI * 4 == BM && LPW * RPI * 4 == BM + BN, "stage rows must split over four waves");
-    static_assert(NS >= 2 && NS * STAGE <= 160 * 1024 && (NS - 2) * LPW < 64, "LDS ring / vmcnt range");
+    using Ops = TileOps<BM, BN, 512>;
+    static_assert(NS >= 2 && NS * STAGE + Ops::NV * 4 <= 160 * 1024 && (NS - 2) * LPW < 64, "LDS ring / vmcnt range");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -714,6 +712,8 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
     xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int KT = K / BKB;
+    Ops ops;
+    ops.load(tid, m0, n0, M, N, sa, sb, bias);
 
     const auto ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K);
     const auto rb_src = make_rsrc(B + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
@@ -803,8 +803,9 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
         __builtin_amdgcn_sched_barrier(0);
     }
     if (grp == 0) __builtin_amdgcn_s_barrier();
-    staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY>(acc, smem, grp * (BM / 2) + wm * WM, wn * WN, tid, lane, m0,
-                                                        n0, M, N, sa, sb, bias, act, Y);
+    ops.park(sc, tid);
+    staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY>(acc, smem, sc, grp * (BM / 2) + wm * WM, wn * WN, tid, lane,
+                                                        m0, n0, M, N, act, Y);
 }
 
 template <int BN, int GM, int GN, int BKB, int NS>
@@ -883,7 +884,7 @@ constexpr DmaCfg kDma[] = {
     {256, 128, 2, 2, 64, 6},   // 14
     {256, 256, 1, 4, 128, 2},  // 15 ping-pong (k_gemm_fp8_pp); WGM x WGN = one group's waves
     {256, 256, 1, 4, 64, 4},   // 16
-    {256, 256, 1, 4, 64, 5},   // 17
+    {256, 128, 2, 2, 64, 4},   // 17
     {256, 128, 2, 2, 128, 3},  // 18
     {256, 128, 2, 2, 64, 6},   // 19
     {256, 128, 1, 4, 128, 3},  // 20
@@ -909,7 +910,7 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 14: launch_sp<256, 128, 2, 2, 64, 6>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 15: launch_pp<256, 1, 4, 128, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 16: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 17: launch_pp<256, 1, 4, 64, 5>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 17: launch_pp<128, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 18: launch_pp<128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 19: launch_pp<128, 2, 2, 64, 6>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         default: launch_pp<128, 1, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
