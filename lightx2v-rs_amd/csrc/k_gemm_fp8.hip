@@ -399,8 +399,8 @@ __device__ __forceinline__ uint32_t dma_slot(uint32_t row, uint32_t c) {
     return c ^ ((row / RW) % CPR);
 }
 
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS, typename TY>
-__global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_dma(const uint8_t *__restrict__ A,
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC, typename TY>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint8_t *__restrict__ A,
                                                                    const float *__restrict__ sa,
                                                                    const uint8_t *__restrict__ B,
                                                                    const float *__restrict__ sb,
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_dma(const uint8_
     constexpr int STAGE = (BM + BN) * BKB;
     static_assert(ALD * RPI * NW == BM && BLD * RPI * NW == BN, "tile rows must split over the waves");
     using Ops = TileOps<BM, BN, 64 * NW>;
-    static_assert(NS >= 2 && NS * STAGE + Ops::NV * 4 <= 160 * 1024, "LDS");
+    static_assert(NS >= 2 && OCC * (NS * STAGE + Ops::NV * 4) <= 160 * 1024, "LDS for OCC workgroups per CU");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
     __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
 
@@ -834,16 +834,16 @@ void launch_cfg(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
                            (float *)y, M, N, K, act, tiles_m, tiles_n);
 }
 
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS>
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC = 1>
 void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
                 const float *bias, int act, void *y, int y_dtype, int M, int N, int K) {
     int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
     if (y_dtype == LX2V_DTYPE_BF16)
-        hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, uint16_t>), grid, block, 0, s, a, sa, b, sb,
+        hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, uint16_t>), grid, block, 0, s, a, sa, b, sb,
                            bias, (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
     else
-        hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, float>), grid, block, 0, s, a, sa, b, sb, bias,
+        hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, float>), grid, block, 0, s, a, sa, b, sb, bias,
                            (float *)y, M, N, K, act, tiles_m, tiles_n);
 }
 
@@ -888,6 +888,10 @@ constexpr DmaCfg kDma[] = {
     {256, 128, 2, 2, 128, 3},  // 18
     {256, 128, 2, 2, 64, 6},   // 19
     {256, 128, 1, 4, 128, 3},  // 20
+    // direct-to-LDS, small enough for two (three) workgroups per CU
+    {256, 128, 4, 2, 64, 3},   // 21 (8 waves, 2 per CU)
+    {128, 128, 2, 2, 64, 3},   // 22 (4 waves, 3 per CU)
+    {128, 256, 2, 4, 64, 3},   // 23 (8 waves, 2 per CU)
 };
 
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
@@ -913,7 +917,10 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 17: launch_pp<128, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 18: launch_pp<128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 19: launch_pp<128, 2, 2, 64, 6>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        default: launch_pp<128, 1, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 20: launch_pp<128, 1, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 21: launch_dma<256, 128, 4, 2, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 22: launch_dma<128, 128, 2, 2, 64, 3, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        default: launch_dma<128, 256, 2, 4, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
     }
 }
 
@@ -937,17 +944,24 @@ bool gemm_fp8_supported(size_t M, size_t N, size_t K) {
 }
 
 // Time model of the K % 128 == 0 configurations, fitted to measured
-// kernel times at the Wan shapes (M 512..4680, K 1536..8960, N 1536..14336):
-// t = rounds * (stages * per_stage + per_round), one stage = 128 bytes of K
-// over the whole tile, per_round = the prologue + epilogue of a workgroup.
-// The 256 x 256 ping-pong tile does twice the work per stage at 0.70x the
-// 8-wave 256 x 128 tile's time per unit of work, but its epilogue costs
-// 3x more per round.
+// launch times at the Wan shapes (M 512..4680, K 1536..8960, N 1536..14336):
+//   t = per_stage * rounds * stages + per_round * rounds + fixed,
+// rounds = ceil(tiles / CUs), stages = K / 128.  The configurations that
+// fit two or three workgroups per CU pay a slower K loop (64-byte stages)
+// but hide most of each workgroup's prologue and epilogue behind another's
+// K loop; the 256 x 256 ping-pong tile has the cheapest K loop per unit of
+// work and the most expensive rounds.
 struct CfgCost {
     int idx;
-    double per_stage_us, per_round_us;
+    double per_stage_us, per_round_us, fixed_us;
 };
-constexpr CfgCost kAuto[] = {{3, 0.89, 4.4}, {4, 0.89, 4.4}, {16, 1.25, 14.1}};
+constexpr CfgCost kAuto[] = {
+    {3, 0.78, 5.65, 3.63},    // 256 x 128, one workgroup per CU
+    {21, 0.92, 1.32, 7.64},   // 256 x 128, two per CU
+    {23, 0.90, 1.26, 8.42},   // 128 x 256, two per CU
+    {22, 0.528, 1.0, 6.65},   // 128 x 128, three per CU
+    {16, 1.15, 13.5, 0.0},    // 256 x 256 ping-pong
+};
 
 Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K) {
     Fp8Plan p;
@@ -963,7 +977,7 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K) {
         const DmaCfg &d = kDma[c.idx];
         const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
         const double rounds = (double)((tiles + num_cu - 1) / num_cu);
-        const double t = rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us);
+        const double t = rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us) + c.fixed_us;
         if (p.kernel < 0 || t < best * 0.9999) {  // ties keep the earlier
             best = t;
             p.kernel = c.idx;
