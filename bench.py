@@ -6,9 +6,13 @@ tokens), 30 layers x 4 DMD steps, 7 linears per layer-step (self-attn QKV,
 O; cross-attn Q, K/V on 512 text tokens, O; FFN up with GELU, FFN down),
 with 30 distinct layers of random-init FP8 per-output-channel weights
 resident in HBM (1.39 GB) and bf16 activations, which each linear quantizes
-per token to e4m3 before its fp8 GEMM.  One "step" is one chunk: 840
-Backend::linear calls (crates/lightx2v-model/src/dit.rs:602-759).  Inputs are
-synthetic and resident before timing starts.
+per token to e4m3 before its fp8 GEMM -- except the FFN hand-off: FFN up
+writes MX e4m3 (one power-of-two scale per 32 columns of a row, quantized in
+its GEMM epilogue) and FFN down reads it directly.  The same chunk with a
+bf16 FFN hand-off is timed too (ms_per_chunk_bf16_ffn_handoff).  One "step"
+is one chunk: 840 Backend::linear calls
+(crates/lightx2v-model/src/dit.rs:602-759).  Inputs are synthetic and
+resident before timing starts.
 
 Timed two ways over the same calls: eagerly (one C-ABI call per linear from
 Python) and as one replayed HIP graph of the whole chunk; `value` is the
@@ -131,6 +135,7 @@ def main():
     acts["x_text"] = be.alloc(TEXT * DIM)
     be.fill_normal(acts["x_text"], 1099, 1.0)
     outs = {name: be.alloc(rows * n) for name, rows, n, _, _, _ in GEMMS}
+    ffn_mx = be.alloc_mx(M, FFN)  # FFN up -> FFN down in MX e4m3
     acts["y_ffn1"] = outs["ffn1"]
     tmp = be.alloc(FFN * DIM, H.DTYPE_F32)
     layers = []
@@ -149,12 +154,21 @@ def main():
     wbytes = sum(w.info()["device_bytes"] for lw in layers for w, _ in lw.values())
     log(f"bench: setup {time.perf_counter() - t0:.1f} s, {wbytes / 1e9:.2f} GB FP8 weights resident")
 
-    def step():
-        for _ in range(DMD):
-            for lw in layers:
-                for name, rows, n, k, act, src in GEMMS:
-                    w, b = lw[name]
-                    be.linear(acts[src], 0, rows, w, b, act, outs[name], 0)
+    def chunk(mx_handoff):
+        def run():
+            for _ in range(DMD):
+                for lw in layers:
+                    for name, rows, n, k, act, src in GEMMS:
+                        w, b = lw[name]
+                        x, y = acts[src], outs[name]
+                        if mx_handoff and name == "ffn1":
+                            y = ffn_mx
+                        if mx_handoff and name == "ffn2":
+                            x = ffn_mx
+                        be.linear(x, 0, rows, w, b, act, y, 0)
+        return run
+
+    step = chunk(True)
 
     step_flops = flops_of(GEMMS) * LAYERS * DMD
     n_linear = len(GEMMS) * LAYERS * DMD
@@ -180,24 +194,33 @@ def main():
         ms_graph = timed(graph.launch, args.steps, args.warmup)
         log(f"bench: graph {ms_graph:.2f} ms/chunk, {step_flops / ms_graph / 1e9:.1f} TFLOP/s")
     ms = min(ms_eager, ms_graph) if ms_graph else ms_eager
+    # the same chunk with the FFN hand-off in bf16 (per-token e4m3 inside FFN down)
+    ms_bf16_handoff = timed(chunk(False), args.steps, args.warmup)
+    log(f"bench: bf16 FFN hand-off (eager) {ms_bf16_handoff:.2f} ms/chunk")
     value = step_flops / ms / 1e9
 
     # ---- the dominant kernel alone: GEMMs on pre-quantized activations ----------
-    xq = {src: be.alloc_e4m3(rows, k) for _, rows, _, k, _, src in GEMMS}
-    for _, rows, _, k, _, src in GEMMS:
+    # (the chunk's GEMMs exactly: FFN up writes the MX buffer FFN down reads;
+    # the other inputs come per-token quantized; act_quant_step is the
+    # chunk's remaining per-token quantization)
+    per_token = [g for g in GEMMS if g[0] != "ffn2"]
+    xq = {src: be.alloc_e4m3(rows, k) for _, rows, _, k, _, src in per_token}
+    for _, rows, _, k, _, src in per_token:
         be.quantize_act(acts[src], 0, rows, xq[src])
+    gx = {name: (ffn_mx if name == "ffn2" else xq[src]) for name, _, _, _, _, src in GEMMS}
+    gy = {name: (ffn_mx if name == "ffn1" else outs[name]) for name, _, _, _, _, _ in GEMMS}
 
     def gemm_step():
         for _ in range(DMD):
             for lw in layers:
                 for name, rows, n, k, act, src in GEMMS:
                     w, b = lw[name]
-                    be.linear(xq[src], 0, rows, w, b, act, outs[name], 0)
+                    be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
 
     def act_quant_step():
         for _ in range(DMD):
             for _ in range(LAYERS):
-                for _, rows, _, k, _, src in GEMMS:
+                for _, rows, _, k, _, src in per_token:
                     be.quantize_act(acts[src], 0, rows, xq[src])
 
     reps = max(1, min(args.steps, 3))
@@ -219,17 +242,19 @@ def main():
     per = {}
     for name, rows, n, k, act, src in GEMMS:
         w, b = layers[0][name]
-        be.linear(xq[src], 0, rows, w, b, act, outs[name], 0)
+        be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
         be.profile_region("g_" + name, True)
         for _ in range(50):
-            be.linear(xq[src], 0, rows, w, b, act, outs[name], 0)
+            be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
         be.profile_region("g_" + name, False)
-        be.profile_region("q_" + name, True)
-        for _ in range(50):
-            be.quantize_act(acts[src], 0, rows, xq[src])
-        be.profile_region("q_" + name, False)
         us = be.profile_kernel("g_" + name)[1] * 1e3 / 50
-        uq = be.profile_kernel("q_" + name)[1] * 1e3 / 50
+        uq = 0.0  # FFN down's input is quantized in FFN up's epilogue
+        if name != "ffn2":
+            be.profile_region("q_" + name, True)
+            for _ in range(50):
+                be.quantize_act(acts[src], 0, rows, xq[src])
+            be.profile_region("q_" + name, False)
+            uq = be.profile_kernel("q_" + name)[1] * 1e3 / 50
         per[name] = {"shape": f"{rows}x{k}->{n}", "gemm_us": round(us, 2), "act_quant_us": round(uq, 2),
                      "tflops": round(2.0 * rows * n * k / (us * 1e-6) / 1e12, 1),
                      "pct_fp8_peak": round(2.0 * rows * n * k / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS * 100, 1)}
@@ -269,13 +294,15 @@ def main():
             "workload": "cfg4: Wan2.1-1.3B 30-layer x 4-step FP8 block-linear set, one 3-frame chunk",
             "tokens": M, "text_tokens": TEXT, "layers": LAYERS, "dmd_steps": DMD,
             "gemms_per_layer_step": len(GEMMS), "tflop_per_step": round(step_flops / 1e12, 3),
-            "activations": "bf16 in/out, per-token dynamic e4m3 inside linear",
+            "activations": "bf16 in/out, per-token dynamic e4m3 inside linear; FFN up -> FFN down in MX e4m3 "
+                           "(per-32-column power-of-two scales, quantized in FFN up's epilogue)",
             "weights_gb": round(wbytes / 1e9, 3),
         },
         "pct_fp8_peak": round(value / PEAK_FP8_TFLOPS * 100, 2),
         "ms_per_chunk": round(ms, 3),
         "ms_per_chunk_eager": round(ms_eager, 3),
         "ms_per_chunk_graph": round(ms_graph, 3) if ms_graph else None,
+        "ms_per_chunk_bf16_ffn_handoff": round(ms_bf16_handoff, 3),
         "gemm_only_ms_per_chunk": round(gemm_ms, 3),
         "act_quant_ms_per_chunk": round(region["act_quant_chunk"], 3),
         "per_gemm": per,
@@ -286,7 +313,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
             "traffic": traffic,
-            "kernel": "fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma 256x128 tiles; k_gemm_fp8_pp 256x256 for ffn1)",
+            "kernel": "fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma: 256x128, 128x256 and 128x128 tiles)",
             "avg_launch_us": round(gemm_ms * 1e3 / n_linear, 2),
             "launches_per_step": n_linear,
         },

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define LX2V_HIP_ABI_VERSION 2
+#define LX2V_HIP_ABI_VERSION 3
 
 typedef struct lx2v_hip_ctx lx2v_hip_ctx;
 typedef struct lx2v_hip_buf lx2v_hip_buf;
@@ -57,8 +57,11 @@ enum { LX2V_ACT_NONE = 0, LX2V_ACT_GELU_TANH = 1 };
 
 /* device activation dtypes.  E4M3 buffers hold per-token quantized
  * activations (e4m3 codes [rows, cols] plus one f32 scale per row, value =
- * code * scale) and are made only by lx2v_hip_alloc_e4m3. */
-enum { LX2V_DTYPE_F32 = 0, LX2V_DTYPE_BF16 = 1, LX2V_DTYPE_E4M3 = 2 };
+ * code * scale) and are made only by lx2v_hip_alloc_e4m3.  MXE4M3 buffers
+ * hold MX-scaled e4m3 activations (codes [rows, cols] plus one power-of-two
+ * scale per 32 columns of a row, value = code * 2^k) and are made only by
+ * lx2v_hip_alloc_mx. */
+enum { LX2V_DTYPE_F32 = 0, LX2V_DTYPE_BF16 = 1, LX2V_DTYPE_E4M3 = 2, LX2V_DTYPE_MXE4M3 = 3 };
 
 /* weight formats (quant.rs:134-140 plus the native f32 matrix) */
 enum { LX2V_WFMT_F32 = 0, LX2V_WFMT_Q8 = 1, LX2V_WFMT_Q4 = 2, LX2V_WFMT_FP8 = 3 };
@@ -192,13 +195,35 @@ int lx2v_hip_alloc_e4m3(lx2v_hip_ctx *ctx, size_t rows, size_t cols, lx2v_hip_bu
 int lx2v_hip_quantize_act(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
                           lx2v_hip_buf *xq);
 
+/* A [rows, cols] MXE4M3 activation buffer (len = rows * cols, cols a
+ * multiple of 32).  It is what an FP8 linear writes when a second FP8
+ * linear consumes its output directly (FFN up -> FFN down): the producing
+ * GEMM's epilogue quantizes each 32-column block of a row with the scale
+ * 2^k, k the smallest integer such that max |v| * 2^-k <= 448 (k in
+ * [-127, 127]), codes = RNE e4m3 of v * 2^-k, and the consuming GEMM feeds
+ * the scales to the block-scaled fp8 MFMA.  The per-32 scale is never
+ * coarser than the per-token one of E4M3 buffers. */
+int lx2v_hip_alloc_mx(lx2v_hip_ctx *ctx, size_t rows, size_t cols, lx2v_hip_buf **out);
+/* xq rows [0, rows) = MX e4m3 quantization (the rule above) of x rows
+ * [x_row, x_row + rows); x is F32 or BF16 with xq's cols per row, rows <=
+ * xq's rows. */
+int lx2v_hip_quantize_mx(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                         lx2v_hip_buf *xq);
+/* Test hook: an MXE4M3 buffer's raw contents, copied to host: codes [rows,
+ * cols] and E8M0 scale bytes [cols / 32, rows] (block-major). */
+int lx2v_hip_download_mx(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, uint8_t *codes, uint8_t *scales);
+
 /* ---- the op (backend.rs:198-212) ----------------------------------------- */
 
 /* Backend::linear: y[y_row + i, :] = act(x[x_row + i, :] . W^T + b) for
  * i < rows; x has row stride w.cols, y row stride w.rows, bias (nullable)
  * has w.rows elements.  y must not overlap x or bias (LX2V_ERR_ALIAS).
- * An E4M3 x (its cols == w.cols) needs an FP8 weight and skips the
- * activation quantization; y is F32 or BF16. */
+ * An E4M3 or MXE4M3 x (its cols == w.cols) needs an FP8 weight and skips
+ * the activation quantization.  y is F32, BF16 or MXE4M3 (its cols ==
+ * w.rows; the result is MX-quantized in the GEMM's epilogue).  MXE4M3 on
+ * either side needs an FP8 weight with one scale per output channel,
+ * w.cols a multiple of 128 and that buffer's row offset a multiple of 16;
+ * otherwise LX2V_ERR_UNSUPPORTED. */
 int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
                     const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act,
                     lx2v_hip_buf *y, size_t y_row);

@@ -111,6 +111,33 @@ __device__ __forceinline__ uint32_t e4m3_canon_encode(float v) {
     return sign | (exp << 3) | mant;
 }
 
+// Four clamped, scaled values -> four e4m3 codes (byte j = element j) with
+// the hardware pack conversion, round to nearest even.  An exhaustive sweep
+// of every f32 in [-448, 448] on gfx950 found it bit-identical to
+// e4m3_ocp_encode, the rule the oracle restates.
+__device__ __forceinline__ uint32_t quant4(const float *v, float inv) {
+    float t[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) t[j] = fminf(fmaxf(v[j] * inv, -448.0f), 448.0f);
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[1], 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(t[2], t[3], r, true);
+    return (uint32_t)r;
+}
+
+// ---- MX e4m3 blocks (32 columns of a row, one power-of-two scale) -------------
+
+// The block's scale exponent: the smallest k with amax * 2^-k <= 448,
+// clamped to [-127, 127].  amax = 1.m * 2^(E-127) lies in (448 * 2^(k-1),
+// 448 * 2^k] exactly when k = E - 135 + [1.m > 1.75], so no division.
+__device__ __forceinline__ int mx_exponent(float amax) {
+    const uint32_t b = __float_as_uint(amax) & 0x7FFFFFFFu;
+    const int k = (int)(b >> 23) - 135 + ((b & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+    return k < -127 ? -127 : (k > 127 ? 127 : k);
+}
+
+// 2^-k as an f32 for k in [-127, 126] (every finite amax gives k <= 121).
+__device__ __forceinline__ float mx_inv(int k) { return __uint_as_float((uint32_t)(127 - k) << 23); }
+
 // ---- GELU (crates/lightx2v-cpu/src/lib.rs:151-153) --------------------------
 
 __device__ __forceinline__ float gelu_tanh(float x) {

@@ -129,8 +129,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 // least 16 chunks (BN * sizeof(TY) >= 256).
 
 // Epilogue operands of a BM x BN tile: sc[r] is the token scale of tile row
-// r, sc[BM + c] the channel scale and sc[BM + BN + c] the bias of tile
-// column c, zero outside M x N.  Loaded into registers when the workgroup
+// r (1 for MX activations), sc[BM + c] the channel scale and sc[BM + BN + c]
+// the bias of tile column c, zero outside M x N.  Loaded into registers when the workgroup
 // starts (at most three per thread), so their latency hides under the K
 // loop, and parked in a small LDS array after it.
 template <int BM, int BN, int NT>
@@ -144,7 +144,7 @@ struct TileOps {
             const int i = tid + p * NT;
             float x = 0.0f;
             if (i < BM) {
-                if (m0 + i < M) x = sa[m0 + i];
+                if (m0 + i < M) x = sa ? sa[m0 + i] : 1.0f;
             } else if (i < BM + BN) {
                 if (n0 + i - BM < N) x = sb[n0 + i - BM];
             } else if (i < NV) {
@@ -160,18 +160,78 @@ struct TileOps {
     }
 };
 
+// Staging rows hold BN outputs of TY; their 16-byte chunks are XOR-swizzled
+// by row (chunk ^ row % SWZ) so the column-fragment writes of stage 1 (32
+// rows, one chunk each) and the row reads of stage 2 spread over the banks.
+template <int BN, typename TY>
+constexpr int stage_swz() {
+    return (BN * (int)sizeof(TY) / 16) < 16 ? BN * (int)sizeof(TY) / 16 : 16;
+}
+
+// Where MX output goes besides the codes: E8M0 scale bytes (mx_sidx
+// layout, `rows` rows per 128-column group), starting at the output's row 0.
+struct MxOut {
+    uint8_t *scales = nullptr;
+    int rows = 0;
+};
+
 // Stage 1 of the staged epilogue for one wave: its accumulators, scaled by
 // token and channel scale, biased and GELU'd, into staging rows rloc ..
-// (the wave's tile rows start at wr, its columns at wc).
+// (the wave's tile rows start at wr, its columns at wc).  TY = uint8_t is
+// MX e4m3 output: each 32-column block of a row (one j of one lane pair
+// l, l + 32) gets the scale 2^k of mx_exponent over its 32 values; the
+// codes go to the staging tile and the scale byte straight to global
+// memory (tile origin m0, n0).
 template <int BM, int BN, int TM, int TN, typename TY>
 __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const float *sc, uint8_t *stg, int rloc,
-                                           int wr, int wc, int lane, int act) {
-    constexpr int EB = sizeof(TY), RB = BN * EB;
-    static_assert(RB >= 256 && (RB & (RB - 1)) == 0, "staging row must be a power of two >= 256 bytes");
+                                           int wr, int wc, int lane, int act, MxOut mx, int m0, int n0, int M,
+                                           int N) {
+    constexpr int EB = sizeof(TY), RB = BN * EB, SWZ = stage_swz<BN, TY>();
+    static_assert(RB >= 128 && (RB & (RB - 1)) == 0, "staging row must be a power of two >= 128 bytes");
     const int l32 = lane & 31, hf = lane >> 5;
     float sam[TM];
 #pragma unroll
     for (int i = 0; i < TM; i++) sam[i] = sc[wr + i * 32 + l32];
+    if constexpr (EB == 1) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            f32x4 s4[4], b4[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int c = wc + j * 32 + 8 * g + 4 * hf;
+                s4[g] = *(const f32x4 *)(sc + BM + c);
+                b4[g] = *(const f32x4 *)(sc + BM + BN + c);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                float v[16];
+                float amax = 0.0f;
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        float t = acc[j][i][4 * g + q] * sam[i] * s4[g][q] + b4[g][q];
+                        if (act == LX2V_ACT_GELU_TANH) t = gelu_tanh_fast(t);
+                        v[4 * g + q] = t;
+                        amax = fmaxf(amax, fabsf(t));
+                    }
+                amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+                const int k = mx_exponent(amax);
+                const float inv = mx_inv(k);
+                const int r = rloc + i * 32 + l32;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int cb = wc + j * 32 + 8 * g + 4 * hf;
+                    *(uint32_t *)(stg + r * RB + ((((cb >> 4) ^ (r & (SWZ - 1)))) << 4) + (cb & 15)) =
+                        quant4(v + 4 * g, inv);
+                }
+                const int m = m0 + wr + i * 32 + l32, n = n0 + wc + j * 32;
+                if (hf == 0 && m < M && n < N) mx.scales[mx_sidx(m, n / 32, mx.rows)] = (uint8_t)(k + 127);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
 #pragma unroll
@@ -189,7 +249,7 @@ __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const fl
                     if (act == LX2V_ACT_GELU_TANH) v[q] = gelu_tanh_fast(v[q]);
                 }
                 const int r = rloc + i * 32 + l32;
-                uint8_t *p = stg + r * RB + ((((cb >> 4) ^ (r & 15))) << 4) + (cb & 15);
+                uint8_t *p = stg + r * RB + ((((cb >> 4) ^ (r & (SWZ - 1)))) << 4) + (cb & 15);
                 if constexpr (EB == 4) {
                     *(f32x4 *)p = (f32x4){v[0], v[1], v[2], v[3]};
                 } else {
@@ -205,7 +265,7 @@ __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const fl
 template <int R, int BN, int NT, typename TY>
 __device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m0, int n0, int M, int N,
                                               TY *__restrict__ Y) {
-    constexpr int EB = sizeof(TY), RB = BN * EB, CPR = RB / 16, EPC = 16 / EB;
+    constexpr int EB = sizeof(TY), RB = BN * EB, CPR = RB / 16, EPC = 16 / EB, SWZ = stage_swz<BN, TY>();
     static_assert((R * CPR) % NT == 0, "staging tile must split evenly over the block");
     const bool vec = N % EPC == 0;
 #pragma unroll
@@ -213,7 +273,7 @@ __device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m
         const int idx = it * NT + tid, r = idx / CPR, c = idx % CPR;
         const int m = m0 + r, n = n0 + c * EPC;
         if (m >= M || n >= N) continue;
-        const u32x4 v = *(const u32x4 *)(stg + r * RB + ((c ^ (r & 15)) << 4));
+        const u32x4 v = *(const u32x4 *)(stg + r * RB + ((c ^ (r & (SWZ - 1))) << 4));
         TY *yp = Y + (size_t)m * N + n;
         if (vec) {
             *(u32x4 *)yp = v;
@@ -237,7 +297,7 @@ constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
 template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY>
 __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, const float *sc, int wr,
                                                 int wc, int tid, int lane, int m0, int n0, int M, int N, int act,
-                                                TY *__restrict__ Y) {
+                                                TY *__restrict__ Y, MxOut mx = MxOut()) {
     constexpr int RB = BN * (int)sizeof(TY);
     constexpr int R = pow2_floor(SMEM / RB < BM ? SMEM / RB : BM);
     static_assert(BM % R == 0 && R % (32 * TM) == 0, "a wave's rows must fall in one pass");
@@ -246,7 +306,8 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uin
 #pragma unroll
     for (int p = 0; p < BM / R; p++) {
         if (p) __syncthreads();
-        if (wr >= p * R && wr < (p + 1) * R) acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, wr, wc, lane, act);
+        if (wr >= p * R && wr < (p + 1) * R)
+            acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, wr, wc, lane, act, mx, m0, n0, M, N);
         __syncthreads();
         lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y);
     }
@@ -399,14 +460,25 @@ __device__ __forceinline__ uint32_t dma_slot(uint32_t row, uint32_t c) {
     return c ^ ((row / RW) % CPR);
 }
 
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC, typename TY>
+// MX activations (AM = 1): A's E8M0 block scales (mx_sidx layout, amx_rows
+// rows per 128-column group, amx_len bytes readable from amx) travel with
+// each stage -- wave 0 adds one 16-byte DMA of the stage's 128-column group,
+// BM rows x 4 bytes -- and feed the block-scaled MFMA: each lane reads its
+// row's 4 bytes once per stage and shifts the one its K block needs into
+// byte 0 (the byte the MFMA's scale operand reads); the weight's scale
+// operand is 2^0.  TY = uint8_t writes MX e4m3 output (codes to Y, scales
+// to ymx).
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC, int AM, typename TY>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint8_t *__restrict__ A,
                                                                    const float *__restrict__ sa,
                                                                    const uint8_t *__restrict__ B,
                                                                    const float *__restrict__ sb,
                                                                    const float *__restrict__ bias,
                                                                    TY *__restrict__ Y, int M, int N, int K,
-                                                                   int act, int tiles_m, int tiles_n) {
+                                                                   int act, int tiles_m, int tiles_n,
+                                                                   const uint8_t *__restrict__ amx,
+                                                                   uint32_t amx_len, int amx_rows,
+                                                                   uint8_t *__restrict__ ymx, int ymx_rows) {
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -416,9 +488,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     constexpr int STAGE = (BM + BN) * BKB;
     static_assert(ALD * RPI * NW == BM && BLD * RPI * NW == BN, "tile rows must split over the waves");
     using Ops = TileOps<BM, BN, 64 * NW>;
-    static_assert(NS >= 2 && OCC * (NS * STAGE + Ops::NV * 4) <= 160 * 1024, "LDS for OCC workgroups per CU");
+    constexpr int ASL = AM ? 1024 : 16;  // per-stage LDS for A's block scales (BM rows x 4 bytes)
+    static_assert(!AM || BM * 4 <= ASL, "A scale slot");
+    static_assert(NS >= 2 && OCC * (NS * STAGE + Ops::NV * 4 + NS * ASL) <= 160 * 1024, "LDS for OCC workgroups per CU");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
     __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
+    __shared__ __attribute__((aligned(16))) uint8_t asl[NS * ASL];
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid / WGN, wn = wid % WGN;
@@ -433,6 +508,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // feed output rows / channels that are never stored.
     const auto ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K);
     const auto rb_src = make_rsrc(B + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
+    const auto rs_src =
+        make_rsrc(AM ? amx + 4 * m0 : A, AM ? (amx_len > 4u * m0 ? amx_len - 4u * (uint32_t)m0 : 0u) : 0u);
 
     // Load i of this wave covers tile rows [(i NW + wid) RPI, +RPI); lane l
     // fills slot l % CPR of row l / CPR.
@@ -452,6 +529,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         const uint32_t k0 = (uint32_t)kt * BKB;
         const bool in = kt < KT;
         uint8_t *sbuf = smem + buf * STAGE;
+        if constexpr (AM) {
+            // First in the stage's issue order: issued after the A / B
+            // loads, this load's return gated wave 0's stage waits (measured
+            // ~15% on the K-heavy shapes).  Wave 0; lane l: rows 4 l .. 4 l
+            // + 3 of the stage's 128-column group.
+            if (tid < 64) {
+                const bool ok = in && lane < BM / 4;
+                dma16(rs_src, asl + buf * ASL,
+                      ok ? (uint32_t)(kt * BKB / 128) * (uint32_t)amx_rows * 4u + (uint32_t)lane * 16u : kOob);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < ALD; i++)
             dma16(ra_src, sbuf + (i * NW + wid) * RPI * BKB, in ? a_off[i] + k0 : kOob);
@@ -467,17 +555,32 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
 
     const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
-    auto compute = [&](int buf) {
+    auto compute = [&](int buf, int stage) {
         const uint8_t *s = smem + buf * STAGE;
+        uint32_t sraw[AM ? TM : 1];
+        if constexpr (AM) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                sraw[i] = *(const uint32_t *)(asl + buf * ASL + (wm * WM + i * 32 + frow) * 4);
+        }
 #pragma unroll
         for (int kk = 0; kk < BKB / 64; kk++) {
             i32x8 af[TM], bf[TN];
-            const uint32_t c0 = kk * 4 + fhalf;
+            // 16-byte chunks of the 64-byte K slice each lane supplies.  The
+            // block-scaled MFMA reads a lane's bytes 0..15 as K [16 h, 16 h
+            // + 16) and bytes 16..31 as K [32 + 16 h, +16) of the slice (h =
+            // lane / 32) and scales K [0, 32) with the lanes-0..31 scale and
+            // K [32, 64) with the lanes-32..63 one (probed on gfx950), so
+            // with MX activations lane half h takes chunks h and h + 2 and
+            // each MX block is one hardware scale block.  Unscaled, any K
+            // order shared by both operands is the same product.
+            const uint32_t c0 = AM ? kk * 4 + (lane >> 5) : kk * 4 + fhalf;
+            const uint32_t c1 = AM ? c0 + 2 : c0 + 1;
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 const uint32_t row = wm * WM + i * 32 + frow;
                 u32x4 lo = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c0) << 4));
-                u32x4 hi = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c0 + 1) << 4));
+                u32x4 hi = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c1) << 4));
                 af[i] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                                 (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
             }
@@ -485,16 +588,31 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             for (int j = 0; j < TN; j++) {
                 const uint32_t row = BM + wn * WN + j * 32 + frow;
                 u32x4 lo = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c0) << 4));
-                u32x4 hi = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c0 + 1) << 4));
+                u32x4 hi = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c1) << 4));
                 bf[j] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                                 (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
             }
+            if constexpr (AM) {
+                // lane l holds block 2 s + l / 32 of its row's 128-column group
+                // (s: the 64-column slice): that block's scale into byte 0
+                const int sh = 8 * (int)(lane >> 5) + 16 * (BKB == 128 ? kk : (stage & 1));
+                int as[TM];
 #pragma unroll
-            for (int j = 0; j < TN; j++)
+                for (int i = 0; i < TM; i++) as[i] = (int)(sraw[i] >> sh);
 #pragma unroll
-                for (int i = 0; i < TM; i++)
-                    acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        bf[j], af[i], acc[j][i], 0, 0, 0, 0, 0, 0);
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+                        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            bf[j], af[i], acc[j][i], 0, 0, 0, 127, 0, as[i]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+                        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            bf[j], af[i], acc[j][i], 0, 0, 0, 0, 0, 0);
+            }
         }
     };
 
@@ -510,18 +628,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 #pragma unroll
         for (int j = 0; j < NS; j++) {
             if (kt + j < KT) {
-                wait_vmcnt<(NS - 2) * LPS>();
+                if (AM && tid < 64)  // wave 0 also loads each stage's A scales
+                    wait_vmcnt<(NS - 2) * (LPS + 1)>();
+                else
+                    wait_vmcnt<(NS - 2) * LPS>();
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
                 issue(kt + j + NS - 1, (j + NS - 1) % NS);
-                compute(j);
+                compute(j, kt + j);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
     ops.park(sc, tid);
+    MxOut mx;
+    mx.scales = ymx;
+    mx.rows = ymx_rows;
     staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N,
-                                                          act, Y);
+                                                          act, Y, mx);
 }
 
 // ---- software-pipelined direct-to-LDS kernel ----------------------------------------
@@ -834,17 +958,40 @@ void launch_cfg(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
                            (float *)y, M, N, K, act, tiles_m, tiles_n);
 }
 
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC = 1>
+// MXOUT / MXIN: also instantiate the MX-output / MX-activation kernels (only
+// for the configurations the planner offers such shapes to).
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC = 1, bool MXOUT = false, bool MXIN = false>
 void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
-                const float *bias, int act, void *y, int y_dtype, int M, int N, int K) {
+                const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
     int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
+    const uint32_t alen = (uint32_t)mx.a_len;
+    const int arows = (int)mx.a_rows, yrows = (int)mx.y_rows;
+#define LX2V_DMA(AMV, T)                                                                                         \
+    hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, AMV, T>), grid, block, 0, s, a, sa, b, sb, \
+                       bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y, yrows)
+    if constexpr (MXIN) {
+        if (mx.a) {
+            if (y_dtype == LX2V_DTYPE_BF16)
+                LX2V_DMA(1, uint16_t);
+            else if (y_dtype == LX2V_DTYPE_F32)
+                LX2V_DMA(1, float);
+            else
+                LX2V_DMA(1, uint8_t);
+            return;
+        }
+    }
+    if constexpr (MXOUT) {
+        if (y_dtype == LX2V_DTYPE_MXE4M3) {
+            LX2V_DMA(0, uint8_t);
+            return;
+        }
+    }
     if (y_dtype == LX2V_DTYPE_BF16)
-        hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, uint16_t>), grid, block, 0, s, a, sa, b, sb,
-                           bias, (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
+        LX2V_DMA(0, uint16_t);
     else
-        hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, float>), grid, block, 0, s, a, sa, b, sb, bias,
-                           (float *)y, M, N, K, act, tiles_m, tiles_n);
+        LX2V_DMA(0, float);
+#undef LX2V_DMA
 }
 
 template <int BM, int BN, int WGM, int WGN, int BKB, int NS>
@@ -895,15 +1042,15 @@ constexpr DmaCfg kDma[] = {
 };
 
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
-                    const float *bias, int act, void *y, int y_dtype, int M, int N, int K) {
+                    const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
     switch (idx) {
-        case 0: launch_dma<256, 128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 1: launch_dma<128, 256, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 2: launch_dma<128, 128, 2, 2, 128, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 3: launch_dma<256, 128, 4, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 4: launch_dma<128, 256, 2, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 5: launch_dma<256, 256, 2, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 6: launch_dma<256, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 0: launch_dma<256, 128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 1: launch_dma<128, 256, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 2: launch_dma<128, 128, 2, 2, 128, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 3: launch_dma<256, 128, 4, 2, 128, 3, 1, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 4: launch_dma<128, 256, 2, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 5: launch_dma<256, 256, 2, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 6: launch_dma<256, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
         case 7: launch_sp<256, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 8: launch_sp<256, 128, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 9: launch_sp<128, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
@@ -918,9 +1065,13 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 18: launch_pp<128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 19: launch_pp<128, 2, 2, 64, 6>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 20: launch_pp<128, 1, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 21: launch_dma<256, 128, 4, 2, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 22: launch_dma<128, 128, 2, 2, 64, 3, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        default: launch_dma<128, 256, 2, 4, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 21: launch_dma<256, 128, 4, 2, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 22:
+            launch_dma<128, 128, 2, 2, 64, 3, 3, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
+            break;
+        default:
+            launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
+            break;
     }
 }
 
@@ -963,17 +1114,23 @@ constexpr CfgCost kAuto[] = {
     {16, 1.15, 13.5, 0.0},    // 256 x 256 ping-pong
 };
 
-Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K) {
+// The configurations with MX-activation / MX-output kernels.  The 128 x 256
+// two-per-CU tile takes no MX activations: their scale handling needs more
+// than the 128 VGPRs two workgroups per CU leave a wave.
+bool mx_capable(int idx, bool mx_in) { return idx == 3 || idx == 22 || (idx == 23 && !mx_in); }
+
+Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in) {
     Fp8Plan p;
     if (K % 128 != 0) return p;  // the register-staged kernel
     const int nd = (int)(sizeof(kDma) / sizeof(kDma[0]));
     const int forced = forced_cfg();
-    if (forced >= 0 && forced < nd) {
+    if (forced >= 0 && forced < nd && (!mx || mx_capable(forced, mx_in))) {
         p.kernel = forced;
         return p;
     }
     double best = 0.0;
     for (const CfgCost &c : kAuto) {
+        if (mx && !mx_capable(c.idx, mx_in)) continue;
         const DmaCfg &d = kDma[c.idx];
         const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
         const double rounds = (double)((tiles + num_cu - 1) / num_cu);
@@ -988,10 +1145,10 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K) {
 
 void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t *a, const float *a_scale,
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
-                     int y_dtype, size_t M, size_t N, size_t K) {
+                     int y_dtype, size_t M, size_t N, size_t K, const Fp8Mx &mx) {
     int m = (int)M, n = (int)N, k = (int)K;
     if (p.kernel >= 0) {
-        launch_dma_idx(p.kernel, s, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k);
+        launch_dma_idx(p.kernel, s, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k, mx);
         return;
     }
     // K not a multiple of 128: the register-staged kernel.

@@ -124,19 +124,6 @@ __device__ __forceinline__ void unpack8(const u32x4 *raw, float v[8]) {
     }
 }
 
-// Four clamped, scaled values -> four e4m3 codes (byte j = element j) with
-// the hardware pack conversion, round to nearest even.  An exhaustive sweep
-// of every f32 in [-448, 448] on gfx950 found it bit-identical to
-// e4m3_ocp_encode, the rule the oracle restates.
-__device__ __forceinline__ uint32_t quant4(const float *v, float inv) {
-    float t[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) t[j] = fminf(fmaxf(v[j] * inv, -448.0f), 448.0f);
-    int r = __builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[1], 0, false);
-    r = __builtin_amdgcn_cvt_pk_fp8_f32(t[2], t[3], r, true);
-    return (uint32_t)r;
-}
-
 // W waves share a row (W = 1, 2 or 4; the workgroup holds 4 / W rows); T =
 // chunks of 8 per lane, 64 * W * T * 8 >= cols, cols % 8 == 0.  Wave part p
 // of a row owns chunks lane + 64 (p + W t).
@@ -287,7 +274,70 @@ __global__ __launch_bounds__(kThreads) void k_quantize_fp8(const float *src, siz
     if (lane == 0) scales[g] = s;
 }
 
+// ---- MX e4m3 activation quantization --------------------------------------------
+//
+// One thread per 32-column block of a row (cols % 32 == 0): amax = max |x|
+// of the block, k = mx_exponent(amax), codes = e4m3(clamp(x * 2^-k, +-448))
+// rounded to nearest even, scale byte k + 127 at s[mx_sidx(r, c / 32, srows)].
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_act_quant_mx(const void *x, size_t rows, size_t cols, uint8_t *q,
+                                                           uint8_t *s, size_t srows) {
+    constexpr int W = DT == LX2V_DTYPE_BF16 ? 1 : 2;  // 16-byte loads per 8 elements
+    const size_t nb = cols / 32;
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i >= rows * nb) return;
+    const size_t r = i / nb, b = i - r * nb;
+    const u32x4 *src = (const u32x4 *)((const uint8_t *)x + (r * cols + b * 32) * (DT == LX2V_DTYPE_BF16 ? 2 : 4));
+    u32x4 raw[4 * W];
+#pragma unroll
+    for (int j = 0; j < 4 * W; j++) raw[j] = src[j];
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; c++) unpack8<DT>(raw + c * W, v + 8 * c);
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+    const int k = mx_exponent(amax);
+    const float inv = mx_inv(k);
+    uint32_t w[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) w[j] = quant4(v + 4 * j, inv);
+    u32x4 *dst = (u32x4 *)(q + r * cols + b * 32);
+    dst[0] = (u32x4){w[0], w[1], w[2], w[3]};
+    dst[1] = (u32x4){w[4], w[5], w[6], w[7]};
+    s[mx_sidx(r, b, srows)] = (uint8_t)(k + 127);
+}
+
+__global__ void k_decode_mx(const uint8_t *q, const uint8_t *s, size_t rows, size_t cols, size_t srows, float *out) {
+    const size_t n = rows * cols;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / cols, c = i - r * cols;
+        out[i] = __builtin_amdgcn_ldexpf(e4m3_ocp_decode(q[i]), (int)s[mx_sidx(r, c / 32, srows)] - 127);
+    }
+}
+
 }  // namespace
+
+void launch_act_quant_mx(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols, uint8_t *q,
+                         uint8_t *scales, size_t srows) {
+    const size_t n = rows * (cols / 32);
+    if (n == 0) return;
+    if (dtype == LX2V_DTYPE_BF16)
+        hipLaunchKernelGGL(k_act_quant_mx<LX2V_DTYPE_BF16>, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, x,
+                           rows, cols, q, scales, srows);
+    else
+        hipLaunchKernelGGL(k_act_quant_mx<LX2V_DTYPE_F32>, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, x,
+                           rows, cols, q, scales, srows);
+}
+
+void launch_decode_mx(hipStream_t s, const uint8_t *q, const uint8_t *scales, size_t rows, size_t cols, size_t srows,
+                      float *out) {
+    const size_t n = rows * cols;
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_decode_mx, dim3(grid_for(n, kThreads * 4)), dim3(kThreads), 0, s, q, scales, rows, cols,
+                       srows, out);
+}
 
 void launch_convert(hipStream_t s, const void *src, int sd, void *dst, int dd, size_t n) {
     if (n == 0) return;

@@ -330,7 +330,9 @@ int lx2v_hip_set_fp8_act(lx2v_hip_ctx *ctx, int mode) {
 int lx2v_hip_alloc_dtype(lx2v_hip_ctx *ctx, size_t len, int dtype, lx2v_hip_buf **out) {
     NEED(ctx, "ctx");
     NEED(out, "out");
-    if (!valid_dtype(dtype)) return fail(LX2V_ERR_BAD_ARG, "unknown dtype %d (E4M3 buffers come from lx2v_hip_alloc_e4m3)", dtype);
+    if (!valid_dtype(dtype))
+        return fail(LX2V_ERR_BAD_ARG, "unknown dtype %d (E4M3 / MXE4M3 buffers come from lx2v_hip_alloc_e4m3 / _mx)",
+                    dtype);
     if (int rc = not_capturing(ctx, "alloc")) return rc;
     if (int rc = set_dev(ctx)) return rc;
     if (int rc = alloc_buf(ctx, len, dtype, out)) return rc;
@@ -363,7 +365,8 @@ int lx2v_hip_write(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, const float *data, size
     NEED(ctx, "ctx");
     NEED(buf, "buf");
     if (len) NEED(data, "data");
-    if (buf->dtype == LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "write into an E4M3 buffer (use lx2v_hip_quantize_act)");
+    if (buf->quantized())
+        return fail(LX2V_ERR_BAD_ARG, "write into an E4M3 / MXE4M3 buffer (use lx2v_hip_quantize_act / _mx)");
     if (len > buf->len) return fail(LX2V_ERR_BAD_SHAPE, "write of %zu elements into a buffer of %zu", len, buf->len);
     if (int rc = not_capturing(ctx, "write")) return rc;
     if (int rc = set_dev(ctx)) return rc;
@@ -386,6 +389,15 @@ int lx2v_hip_download(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, float *out, si
             if (int rc = run(ctx, "convert", [&] {
                     launch_decode_e4m3_rows(ctx->stream, (const uint8_t *)buf->ptr, buf->scales, buf->rows, buf->cols,
                                             (float *)st);
+                }))
+                return rc;
+            src = st;
+        } else if (buf->dtype == LX2V_DTYPE_MXE4M3) {  // code * 2^(scale byte - 127)
+            void *st;
+            if (int rc = stage_for(ctx, len * 4, &st)) return rc;
+            if (int rc = run(ctx, "convert", [&] {
+                    launch_decode_mx(ctx->stream, (const uint8_t *)buf->ptr, buf->mxs, buf->rows, buf->cols,
+                                     buf->srows, (float *)st);
                 }))
                 return rc;
             src = st;
@@ -426,8 +438,7 @@ int lx2v_hip_copy(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t src_off, lx
     if (src_off > src->len || len > src->len - src_off || dst_off > dst->len || len > dst->len - dst_off)
         return fail(LX2V_ERR_BAD_SHAPE, "copy [%zu,+%zu) -> [%zu,+%zu) out of range (%zu, %zu)", src_off, len,
                     dst_off, len, src->len, dst->len);
-    if (src->dtype == LX2V_DTYPE_E4M3 || dst->dtype == LX2V_DTYPE_E4M3)
-        return fail(LX2V_ERR_BAD_ARG, "copy to or from an E4M3 buffer");
+    if (src->quantized() || dst->quantized()) return fail(LX2V_ERR_BAD_ARG, "copy to or from an E4M3 / MXE4M3 buffer");
     if (!len) return ok();
     if (int rc = set_dev(ctx)) return rc;
     const char *s = (const char *)src->ptr + src_off * src->elem_bytes();
@@ -733,7 +744,7 @@ int lx2v_hip_quantize_fp8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t row
 int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std) {
     NEED(ctx, "ctx");
     NEED(buf, "buf");
-    if (buf->dtype == LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "fill_normal into an E4M3 buffer");
+    if (buf->quantized()) return fail(LX2V_ERR_BAD_ARG, "fill_normal into an E4M3 / MXE4M3 buffer");
     if (int rc = set_dev(ctx)) return rc;
     if (int rc = run(ctx, "fill_normal", [&] {
             launch_fill_normal(ctx->stream, buf->ptr, buf->dtype, buf->len, seed, std);
@@ -775,7 +786,7 @@ int lx2v_hip_quantize_act(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row
     NEED(x, "x");
     NEED(xq, "xq");
     if (xq->dtype != LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "quantize_act writes an E4M3 buffer");
-    if (x->dtype == LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "quantize_act reads an F32 or BF16 buffer");
+    if (x->quantized()) return fail(LX2V_ERR_BAD_ARG, "quantize_act reads an F32 or BF16 buffer");
     const size_t cols = xq->cols;
     if (rows > xq->rows) return fail(LX2V_ERR_BAD_SHAPE, "%zu rows into an E4M3 buffer of %zu", rows, xq->rows);
     if (x_row + rows < x_row || (x_row + rows) * cols > x->len)
@@ -785,6 +796,74 @@ int lx2v_hip_quantize_act(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row
     const char *xp = (const char *)x->ptr + x_row * cols * x->elem_bytes();
     return run(ctx, "act_quant_e4m3",
                [&] { launch_act_quant(ctx->stream, xp, x->dtype, rows, cols, (uint8_t *)xq->ptr, xq->scales); });
+}
+
+int lx2v_hip_alloc_mx(lx2v_hip_ctx *ctx, size_t rows, size_t cols, lx2v_hip_buf **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (int rc = not_capturing(ctx, "alloc_mx")) return rc;
+    if (cols % 32) return fail(LX2V_ERR_BAD_SHAPE, "MXE4M3 buffer cols %zu not a multiple of 32", cols);
+    if (cols && rows > ((size_t)1 << 40) / cols) return fail(LX2V_ERR_BAD_SHAPE, "MXE4M3 buffer %zux%zu too large", rows, cols);
+    if (int rc = set_dev(ctx)) return rc;
+    const size_t codes = (rows * cols + 255) & ~(size_t)255;
+    const size_t srows = (rows + 15) & ~(size_t)15;
+    auto *b = new lx2v_hip_buf;
+    b->len = rows * cols;
+    b->dtype = LX2V_DTYPE_MXE4M3;
+    b->rows = rows;
+    b->cols = cols;
+    b->srows = srows;
+    const size_t bytes = std::max<size_t>(codes + srows * 4 * ((cols + 127) / 128), 4);
+    hipError_t e = hipMalloc(&b->ptr, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(b->ptr, 0, bytes, ctx->stream);
+    if (e != hipSuccess) {
+        if (b->ptr) (void)hipFree(b->ptr);
+        delete b;
+        return hip_fail(e, "hipMalloc(MXE4M3 buffer)");
+    }
+    b->mxs = (uint8_t *)b->ptr + codes;
+    *out = b;
+    return ok();
+}
+
+int lx2v_hip_download_mx(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, uint8_t *codes, uint8_t *scales) {
+    NEED(ctx, "ctx");
+    NEED(buf, "buf");
+    if (buf->dtype != LX2V_DTYPE_MXE4M3) return fail(LX2V_ERR_BAD_ARG, "download_mx reads an MXE4M3 buffer");
+    if (buf->len) {
+        NEED(codes, "codes");
+        NEED(scales, "scales");
+    }
+    if (int rc = not_capturing(ctx, "download_mx")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    std::vector<uint8_t> raw(buf->srows * 4 * ((buf->cols + 127) / 128));
+    if (buf->len) {
+        HIP_TRY(hipMemcpyAsync(codes, buf->ptr, buf->len, hipMemcpyDeviceToHost, ctx->stream), "download_mx codes");
+        HIP_TRY(hipMemcpyAsync(raw.data(), buf->mxs, raw.size(), hipMemcpyDeviceToHost, ctx->stream),
+                "download_mx scales");
+    }
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(download_mx)");
+    for (size_t b = 0; b < buf->cols / 32; b++)
+        for (size_t r = 0; r < buf->rows; r++) scales[b * buf->rows + r] = raw[mx_sidx(r, b, buf->srows)];
+    return ok();
+}
+
+int lx2v_hip_quantize_mx(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows, lx2v_hip_buf *xq) {
+    NEED(ctx, "ctx");
+    NEED(x, "x");
+    NEED(xq, "xq");
+    if (xq->dtype != LX2V_DTYPE_MXE4M3) return fail(LX2V_ERR_BAD_ARG, "quantize_mx writes an MXE4M3 buffer");
+    if (x->quantized()) return fail(LX2V_ERR_BAD_ARG, "quantize_mx reads an F32 or BF16 buffer");
+    const size_t cols = xq->cols;
+    if (rows > xq->rows) return fail(LX2V_ERR_BAD_SHAPE, "%zu rows into an MXE4M3 buffer of %zu", rows, xq->rows);
+    if (x_row + rows < x_row || (x_row + rows) * cols > x->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "x has %zu elements, rows [%zu,+%zu) x %zu", x->len, x_row, rows, cols);
+    if (!rows || !cols) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    const char *xp = (const char *)x->ptr + x_row * cols * x->elem_bytes();
+    return run(ctx, "act_quant_mx", [&] {
+        launch_act_quant_mx(ctx->stream, xp, x->dtype, rows, cols, (uint8_t *)xq->ptr, xq->mxs, xq->srows);
+    });
 }
 
 // ---- HIP graphs ------------------------------------------------------------------------
@@ -876,13 +955,21 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
         return fail(LX2V_ERR_BAD_SHAPE, "y has %zu elements, rows [%zu,+%zu) x %zu need %zu", y->len, y_row, rows,
                     N, (y_row + rows) * N);
     if (bias && bias->len < N) return fail(LX2V_ERR_BAD_SHAPE, "bias has %zu elements, weight has %zu rows", bias->len, N);
-    if (y->dtype == LX2V_DTYPE_E4M3 || (bias && bias->dtype == LX2V_DTYPE_E4M3))
-        return fail(LX2V_ERR_BAD_ARG, "linear writes F32 or BF16 and reads an F32 or BF16 bias");
-    if (x->dtype == LX2V_DTYPE_E4M3) {
-        if (x->cols != K) return fail(LX2V_ERR_BAD_SHAPE, "E4M3 x has %zu cols, weight has %zu", x->cols, K);
+    if (y->dtype == LX2V_DTYPE_E4M3 || (bias && bias->quantized()))
+        return fail(LX2V_ERR_BAD_ARG, "linear writes F32, BF16 or MXE4M3 and reads an F32 or BF16 bias");
+    if (x->quantized()) {
+        if (x->cols != K) return fail(LX2V_ERR_BAD_SHAPE, "E4M3 / MXE4M3 x has %zu cols, weight has %zu", x->cols, K);
         if (w->fmt != LX2V_WFMT_FP8)
-            return fail(LX2V_ERR_UNSUPPORTED, "E4M3 activations need an FP8 weight");
+            return fail(LX2V_ERR_UNSUPPORTED, "E4M3 / MXE4M3 activations need an FP8 weight");
     }
+    const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3, y_mx = y->dtype == LX2V_DTYPE_MXE4M3;
+    if (y_mx && y->cols != N) return fail(LX2V_ERR_BAD_SHAPE, "MXE4M3 y has %zu cols, weight has %zu rows", y->cols, N);
+    if ((x_mx || y_mx) && (w->fmt != LX2V_WFMT_FP8 || w->group != K || K % 128 || !gemm_fp8_supported(rows, N, K) ||
+                           (x_mx && x_row % 16)))
+        return fail(LX2V_ERR_UNSUPPORTED,
+                    "MXE4M3 operands need an FP8 weight with one scale per channel, cols %% 128 == 0 and an MX "
+                    "input row offset %% 16 == 0 (weight %zux%zu group %zu, x_row %zu)",
+                    N, K, w->group, x_row);
     const char *xp = (const char *)x->ptr + x_row * K * x->elem_bytes();
     char *yp = (char *)y->ptr + y_row * N * y->elem_bytes();
     if (overlap(yp, rows * N * y->elem_bytes(), xp, rows * K * x->elem_bytes()) ||
@@ -909,12 +996,18 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
         }
     }
 
-    if (w->fmt == LX2V_WFMT_FP8 && (ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->dtype == LX2V_DTYPE_E4M3)) {
+    if (w->fmt == LX2V_WFMT_FP8 && (ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized() || y_mx)) {
         const uint8_t *q;
-        const float *s;
+        const float *s = nullptr;
+        Fp8Mx mx;
         if (x->dtype == LX2V_DTYPE_E4M3) {
             q = (const uint8_t *)xp;
             s = x->scales + x_row;
+        } else if (x_mx) {
+            q = (const uint8_t *)xp;
+            mx.a = x->mxs + 4 * x_row;
+            mx.a_rows = x->srows;
+            mx.a_len = x->srows * 4 * (K / 128) - 4 * x_row;
         } else {
             uint8_t *wq;
             float *ws;
@@ -922,11 +1015,15 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
             q = wq;
             s = ws;
         }
+        if (y_mx) {
+            mx.y = y->mxs + 4 * y_row;
+            mx.y_rows = y->srows;
+        }
         if (w->group == K && gemm_fp8_supported(rows, N, K)) {
-            const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K);
+            const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx);
             if (int rc = run(ctx, "gemm_fp8_e4m3", [&] {
                     launch_gemm_fp8(ctx->stream, ctx->num_cu, plan, q, s, (const uint8_t *)w->codes, w->scales, bp,
-                                    act, yp, y->dtype, rows, N, K);
+                                    act, yp, y->dtype, rows, N, K, mx);
                 }))
                 return rc;
         } else {

@@ -11,6 +11,15 @@
 
 #include "../../include/lightx2v_hip.h"
 
+// Byte offset of the E8M0 scale of 32-column block b of row r in an MX
+// buffer: the four blocks of a 128-column group sit together,
+// [cols / 128][srows][4], so a GEMM reads a row's scales for 128 columns of
+// K with one 32-bit load and a stage's scales for BM rows are one
+// contiguous run.
+__host__ __device__ inline size_t mx_sidx(size_t r, size_t b, size_t srows) {
+    return ((b >> 2) * srows + r) * 4 + (b & 3);
+}
+
 struct lx2v_hip_buf {
     void *ptr = nullptr;
     size_t len = 0;    // elements
@@ -19,7 +28,13 @@ struct lx2v_hip_buf {
     // `scales` (inside the same allocation).
     size_t rows = 0, cols = 0;
     float *scales = nullptr;
-    size_t elem_bytes() const { return dtype == LX2V_DTYPE_BF16 ? 2 : dtype == LX2V_DTYPE_E4M3 ? 1 : 4; }
+    // LX2V_DTYPE_MXE4M3 only: [rows, cols] codes at ptr, E8M0 block scales
+    // at `mxs` (same allocation), [cols / 128][srows][4] (mx_sidx), srows =
+    // rows rounded up to 16.
+    uint8_t *mxs = nullptr;
+    size_t srows = 0;
+    bool quantized() const { return dtype == LX2V_DTYPE_E4M3 || dtype == LX2V_DTYPE_MXE4M3; }
+    size_t elem_bytes() const { return dtype == LX2V_DTYPE_BF16 ? 2 : quantized() ? 1 : 4; }
     size_t bytes() const { return len * elem_bytes(); }
 };
 
@@ -102,6 +117,10 @@ void launch_q4_pack(hipStream_t s, const uint8_t *codes, size_t n, uint8_t *pack
 void launch_act_quant(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols,
                       uint8_t *q, float *scale);
 // out[r, c] = e4m3(q[r, c]) * scale[r] (OCP decode), f32.
+void launch_act_quant_mx(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols, uint8_t *q,
+                         uint8_t *scales, size_t srows);
+void launch_decode_mx(hipStream_t s, const uint8_t *q, const uint8_t *scales, size_t rows, size_t cols, size_t srows,
+                      float *out);
 void launch_decode_e4m3_rows(hipStream_t s, const uint8_t *q, const float *scale, size_t rows, size_t cols,
                              float *out);
 void launch_quantize_q8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,
@@ -129,11 +148,22 @@ void launch_gemm_generic(hipStream_t s, const void *a, int amode, const float *a
 struct Fp8Plan {
     int kernel = -1;  // configuration index, or -1: the register-staged kernel (K % 128 != 0)
 };
+// MX e4m3 operands of a launch: A's block scales ([K / 128][a_rows][4],
+// a_len bytes readable from a; a_scale is then null) and/or the output's
+// (y_dtype LX2V_DTYPE_MXE4M3: codes to y, scales to this.y in the same
+// layout with y_rows).  Both pointers start at the linear's row offset
+// (4 bytes per row).
+struct Fp8Mx {
+    const uint8_t *a = nullptr;
+    size_t a_len = 0, a_rows = 0;
+    uint8_t *y = nullptr;
+    size_t y_rows = 0;
+};
 bool gemm_fp8_supported(size_t M, size_t N, size_t K);
-Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K);
+Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in);
 void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t *a, const float *a_scale,
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
-                     int y_dtype, size_t M, size_t N, size_t K);
+                     int y_dtype, size_t M, size_t N, size_t K, const Fp8Mx &mx);
 
 // k_gemm_w16.hip: bf16 MFMA with the weight dequantized to bf16 in the
 // tile loader (Q8, Q4, FP8 with any group that is a multiple of 32).

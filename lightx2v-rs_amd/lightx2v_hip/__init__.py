@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(_HERE, "liblightx2v_hip.so")
 
 OK, ERR_NO_DEVICE, ERR_BAD_SHAPE, ERR_ALIAS, ERR_HIP, ERR_BAD_ARG, ERR_OOM, ERR_UNSUPPORTED = range(8)
 ACT_NONE, ACT_GELU_TANH = 0, 1
-DTYPE_F32, DTYPE_BF16, DTYPE_E4M3 = 0, 1, 2
+DTYPE_F32, DTYPE_BF16, DTYPE_E4M3, DTYPE_MXE4M3 = 0, 1, 2, 3
 WFMT_F32, WFMT_Q8, WFMT_Q4, WFMT_FP8 = 0, 1, 2, 3
 FP8_ACT_E4M3, FP8_ACT_BF16 = 0, 1
 
@@ -41,6 +41,7 @@ EXPORTS = [
     "lx2v_hip_profile_enable", "lx2v_hip_profile_report", "lx2v_hip_profile_reset",
     "lx2v_hip_profile_kernel", "lx2v_hip_alloc_e4m3", "lx2v_hip_quantize_act", "lx2v_hip_graph_begin",
     "lx2v_hip_graph_end", "lx2v_hip_graph_launch", "lx2v_hip_graph_free", "lx2v_hip_profile_region",
+    "lx2v_hip_alloc_mx", "lx2v_hip_quantize_mx", "lx2v_hip_download_mx",
 ]
 
 
@@ -100,6 +101,9 @@ def _load():
                                          ctypes.POINTER(ctypes.c_double)]),
         "lx2v_hip_alloc_e4m3": (ip, [vp, sz, sz, pp]),
         "lx2v_hip_quantize_act": (ip, [vp, vp, sz, sz, vp]),
+        "lx2v_hip_alloc_mx": (ip, [vp, sz, sz, pp]),
+        "lx2v_hip_quantize_mx": (ip, [vp, vp, sz, sz, vp]),
+        "lx2v_hip_download_mx": (ip, [vp, vp, vp, vp]),
         "lx2v_hip_graph_begin": (ip, [vp]),
         "lx2v_hip_graph_end": (ip, [vp, pp]),
         "lx2v_hip_graph_launch": (ip, [vp, vp]),
@@ -358,6 +362,22 @@ class HipBackend:
 
     def quantize_act(self, x: Buf, x_row: int, rows: int, xq: Buf):
         _check(lib.lx2v_hip_quantize_act(self.ctx, x.h, x_row, rows, xq.h))
+
+    def alloc_mx(self, rows: int, cols: int) -> Buf:
+        """MX e4m3 activations [rows, cols] (codes + one E8M0 scale per 32 columns of a row)."""
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_alloc_mx(self.ctx, rows, cols, ctypes.byref(h)))
+        return Buf(self, h.value)
+
+    def quantize_mx(self, x: Buf, x_row: int, rows: int, xq: Buf):
+        _check(lib.lx2v_hip_quantize_mx(self.ctx, x.h, x_row, rows, xq.h))
+
+    def download_mx(self, buf: Buf, rows: int, cols: int):
+        """Raw codes [rows, cols] and scale bytes [cols / 32, rows] of an MXE4M3 buffer."""
+        q = np.empty((rows, cols), np.uint8)
+        s = np.empty((cols // 32, rows), np.uint8)
+        _check(lib.lx2v_hip_download_mx(self.ctx, buf.h, _ptr(q), _ptr(s)))
+        return q, s
 
     def graph_begin(self):
         _check(lib.lx2v_hip_graph_begin(self.ctx))

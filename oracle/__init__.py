@@ -67,6 +67,8 @@ def lib():
         L.orc_q8_ref_group.argtypes = [_sz]
         L.orc_fp8_ref_group.restype = _sz
         L.orc_fp8_ref_group.argtypes = [_sz]
+        L.orc_mx_exponent.restype = ctypes.c_int
+        L.orc_mx_exponent.argtypes = [ctypes.c_float]
         _lib = L
     return _lib
 
@@ -303,6 +305,32 @@ def act_quant_e4m3(x: np.ndarray):
     s = np.empty(rows, np.float32)
     lib().orc_act_quant_e4m3(_p(x, _f32p), _sz(rows), _sz(cols), _p(q, _u8p), _p(s, _f32p))
     return q, s
+
+
+def act_quant_mx(x: np.ndarray):
+    """Build-defined MX e4m3 quantization: codes [rows, cols] and E8M0 scale
+    bytes, block-major [cols / 32, rows] (one per 32 columns of a row)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    assert cols % 32 == 0
+    q = np.empty((rows, cols), np.uint8)
+    s = np.empty((cols // 32, rows), np.uint8)
+    lib().orc_act_quant_mx(_p(x, _f32p), _sz(rows), _sz(cols), _p(q, _u8p), _p(s, _u8p))
+    return q, s
+
+
+def dequant_mx(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """Values of MX e4m3 codes: e4m3(q) * 2^(s - 127)."""
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.ascontiguousarray(s, np.uint8)
+    rows, cols = q.shape
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_dequant_mx(_p(q, _u8p), _p(s, _u8p), _sz(rows), _sz(cols), _p(out, _f32p))
+    return out
+
+
+def mx_exponent(amax: float) -> int:
+    return int(lib().orc_mx_exponent(ctypes.c_float(amax)))
 
 
 # ---- decode tables -------------------------------------------------------------

@@ -420,6 +420,46 @@ void orc_act_quant_e4m3(const float *x, size_t rows, size_t cols, uint8_t *q,
     }
 }
 
+/* Build-defined MX e4m3 quantization (the FFN hand-off format): per block of
+ * 32 consecutive columns of a row, the power-of-two scale 2^k with k the
+ * smallest integer such that amax * 2^-k <= 448, clamped to [-127, 127],
+ * where amax = max |v| of the block; codes = OCP e4m3 RNE of clamp(v * 2^-k,
+ * +-448).  k comes from amax's bits (no division): amax = 1.m * 2^(E-127)
+ * lies in (448 * 2^(k-1), 448 * 2^k] exactly when k = E - 135 + [1.m > 1.75].
+ * Scales are stored as E8M0 bytes k + 127, block-major: s[(c/32) * rows + r].
+ * Value of a code: e4m3 * 2^k. */
+int orc_mx_exponent(float amax) {
+    uint32_t b;
+    memcpy(&b, &amax, 4);
+    b &= 0x7FFFFFFFu;
+    int e = (int)(b >> 23);
+    int k = e - 135 + ((b & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+    return k < -127 ? -127 : (k > 127 ? 127 : k);
+}
+
+void orc_act_quant_mx(const float *x, size_t rows, size_t cols, uint8_t *q, uint8_t *s) {
+    for (size_t r = 0; r < rows; r++) {
+        for (size_t b = 0; b < cols / 32; b++) {
+            const float *v = x + r * cols + b * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+            int k = orc_mx_exponent(amax);
+            float inv = ldexpf(1.0f, -k);
+            for (int i = 0; i < 32; i++) {
+                float t = fminf(fmaxf(v[i] * inv, -448.0f), 448.0f);
+                q[r * cols + b * 32 + i] = orc_f32_to_e4m3_ocp_rne(t);
+            }
+            s[b * rows + r] = (uint8_t)(k + 127);
+        }
+    }
+}
+
+void orc_dequant_mx(const uint8_t *q, const uint8_t *s, size_t rows, size_t cols, float *out) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++)
+            out[r * cols + c] = ldexpf(orc_e4m3_to_f32_ocp(q[r * cols + c]), (int)s[(c / 32) * rows + r] - 127);
+}
+
 /* ---- element-wise maps over arrays (for large test inputs) ------------------- */
 
 void orc_map_e4m3_ref(const float *v, size_t n, uint8_t *out) {

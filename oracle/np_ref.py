@@ -177,3 +177,19 @@ def bf16_round(v) -> np.ndarray:
     r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
     r = np.where((b & 0x7FFFFFFF) > 0x7F800000, ((b >> 16) | 0x40) << 16, r)
     return (r & 0xFFFFFFFF).astype(np.uint32).view(F32).reshape(a.shape)
+
+
+def act_quant_mx(x) -> tuple:
+    """MX e4m3 quantization restated with numpy (independent of the C):
+    the scale exponent is found by search -- the smallest k in [-127, 127]
+    with amax * 2^-k <= 448, over float64 -- and the codes by the
+    nearest-value search of e4m3_encode_ocp_rne."""
+    x = np.asarray(x, F32)
+    rows, cols = x.shape
+    blocks = np.abs(x.reshape(rows, cols // 32, 32)).max(axis=2).astype(np.float64)
+    ks = np.arange(-127, 128)
+    ok = blocks[..., None] * np.ldexp(1.0, -ks)[None, None, :] <= 448.0
+    k = np.where(ok.any(axis=2), ks[np.argmax(ok, axis=2)], 127)
+    scaled = (x.reshape(rows, cols // 32, 32).astype(np.float64) * np.ldexp(1.0, -k)[..., None]).astype(F32)
+    q = e4m3_encode_ocp_rne(np.clip(scaled, F32(-448.0), F32(448.0))).reshape(rows, cols)
+    return q, (k + 127).astype(np.uint8).T.copy()

@@ -308,3 +308,56 @@ def test_act_quant_oracle_properties():
         # within half an e4m3 step (2^-4 relative) or half the subnormal step
         tol = np.maximum(np.abs(x[r]) * 2.0**-4, s[r] * 2.0**-10) + 1e-12
         assert np.all(np.abs(d[r] - x[r]) <= tol)
+
+
+# ---- MX e4m3 (the FFN hand-off format, build-defined) -------------------------------
+
+def _mx_inputs():
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((41, 320)) * np.exp(rng.uniform(-30, 30, (41, 10))).repeat(32, axis=1)).astype(np.float32)
+    x[0, :32] = 0.0                                   # all-zero block
+    x[1, :32] = 448.0                                 # amax exactly 448 * 2^0
+    x[2, :32] = np.float32(448.0 * 2.0**-60)          # exactly 448 * 2^-60
+    x[3, :32] = np.float32(np.nextafter(np.float32(448.0), np.float32(1e9)))  # just above: next scale
+    x[4, :32] = np.float32(1e-42)                     # subnormal block
+    x[5, :32] = np.float32(3.0e38)                    # near f32 max
+    x[6, 32:64] = np.float32(1.75)                    # mantissa exactly 1.75
+    x[7, 32:64] = np.float32(np.nextafter(np.float32(1.75), np.float32(2)))
+    # an RNE tie on the scaled grid: with k = 0, 1.0625 is halfway between
+    # the e4m3 neighbours 1.0 and 1.125 (step 2^-3 in [1, 2)) and goes to 1.0
+    x[8, :32] = 448.0
+    x[8, 1:32] = np.float32(1.0625)
+    return x
+
+
+def test_mx_quant_c_vs_numpy():
+    x = _mx_inputs()
+    q, s = O.act_quant_mx(x)
+    q2, s2 = N.act_quant_mx(x)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+def test_mx_quant_closed_form():
+    x = _mx_inputs()
+    q, s = O.act_quant_mx(x)
+    rows, cols = x.shape
+    k = s.T.astype(np.int64) - 127                    # [rows, blocks]
+    assert k[0, 0] == -127 and np.all(q[0, :32] == 0)  # zero block: smallest scale, zero codes
+    assert k[1, 0] == 0 and np.all(q[1, :32] == 0x7E)  # 448 = 448 * 2^0
+    assert k[2, 0] == -60 and np.all(q[2, :32] == 0x7E)
+    assert k[3, 0] == 1                                # 448+ needs 2^1 (then 224 = 0x76)
+    assert k[6, 1] == k[7, 1] - 1                      # mantissa 1.75 stays, 1.75+ steps up
+    assert k[8, 0] == 0 and np.all(q[8, 1:32] == 0x38)  # the tie went to even (1.0)
+    amax = np.abs(x).reshape(rows, cols // 32, 32).max(axis=2).astype(np.float64)
+    scaled = amax * np.ldexp(1.0, -k)
+    live = (amax > 0) & (k > -127) & (k < 127)
+    assert np.all(scaled <= 448.0)                     # no block saturates
+    assert np.all(scaled[live] > 224.0)                # and k is the smallest such exponent
+    d = O.dequant_mx(q, s)
+    ref = (N.e4m3_decode_ocp(q.ravel()).reshape(q.shape).astype(np.float64)
+           * np.ldexp(1.0, k).repeat(32, axis=1))
+    assert np.array_equal(d.astype(np.float64), ref)  # dequantization is exact
+    blk = np.ldexp(1.0, k).repeat(32, axis=1)
+    err = np.abs(d.astype(np.float64) - x)
+    # half an e4m3 step (2^-4 relative) or half the subnormal step 2^-10 of the block scale
+    assert np.all(err <= np.maximum(np.abs(x) * 2.0**-4, blk * 2.0**-10) * (1 + 1e-6) + 1e-45)
