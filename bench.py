@@ -36,6 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "lightx2v-rs_amd"))
 
 PEAK_FP8_TFLOPS = 5000.0   # MI355X dense fp8 MFMA
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 HBM_GBS = 8000.0
 
 DIM, FFN, TEXT, LAYERS, DMD = 1536, 8960, 512, 30, 4
@@ -60,6 +61,102 @@ def flops_of(gemms):
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def per_config(be, H):
+    """The baseline's other configs (1, 2, 3 and 5), one linear per shape:
+    weights quantized on the device from the Rng's normals, inputs resident,
+    30 back-to-back launches timed in a HIP-event region after 5 warm-ups.
+    Each is reported against the peak of the MFMA it runs on (fp8 for FP8
+    weights, bf16 for Q8 / Q4, whose tile loader dequantizes to bf16)."""
+    import numpy as np
+    out = {}
+
+    def weight(kind, n, k, std, seed, heavy=False):
+        tmp = be.alloc(n * k, H.DTYPE_F32)
+        be.fill_normal(tmp, seed, std)
+        if heavy:  # 1% of the weight's K columns x20 (columns k % 100 == 37)
+            w = be.download(tmp).reshape(n, k)
+            w[:, 37::100] *= 20.0
+            tmp.free()
+            be.set_act_dtype(H.DTYPE_F32)
+            tmp = be.upload(w.ravel())
+        if kind == "fp8":
+            w = be.quantize_fp8(tmp, n, k, k)
+        elif kind == "q8":
+            w = be.quantize_q8(tmp, n, k, 32)
+        else:
+            w = be.quantize_q4_sym(tmp, n, k, 32)
+        tmp.free()
+        return w
+
+    def time_linear(name, x, rows, k, w, n, act, xdt, ydt, peak, path):
+        be.set_act_dtype(ydt)
+        y = be.alloc(rows * n)
+        b = be.alloc(n, H.DTYPE_F32)
+        be.fill_normal(b, 7, 0.01)
+        for _ in range(5):
+            be.linear(x, 0, rows, w, b, act, y, 0)
+        be.profile_region("c_" + name, True)
+        for _ in range(30):
+            be.linear(x, 0, rows, w, b, act, y, 0)
+        be.profile_region("c_" + name, False)
+        us = be.profile_kernel("c_" + name)[1] * 1e3 / 30
+        tf = 2.0 * rows * n * k / (us * 1e-6) / 1e12
+        out[name] = {"shape": f"{rows}x{k}->{n}", "us_per_linear": round(us, 2), "tflops": round(tf, 1),
+                     "peak_tflops": peak, "pct_peak": round(100.0 * tf / peak, 1), "path": path}
+        y.free()
+        b.free()
+
+    fp8_path = "per-token e4m3 activations (quantized inside linear) x FP8 weight, fp8 MFMA"
+    # config 1: FP8 self-attn Q projection, f32 activations in and out
+    be.set_act_dtype(H.DTYPE_F32)
+    x = be.alloc(M * DIM)
+    be.fill_normal(x, 1001, 1.0)
+    w = weight("fp8", DIM, DIM, 0.02, 1002)
+    time_linear("cfg1_fp8_q_proj_f32", x, M, DIM, w, DIM, 0, H.DTYPE_F32, H.DTYPE_F32, PEAK_FP8_TFLOPS, fp8_path)
+    w.free()
+    x.free()
+    # config 2: Q8 (per-32 scales) FFN up + GELU, bf16 activations
+    be.set_act_dtype(H.DTYPE_BF16)
+    x = be.alloc(M * DIM)
+    be.fill_normal(x, 1011, 1.0)
+    w = weight("q8", FFN, DIM, 0.02, 1012)
+    time_linear("cfg2_q8_ffn_up_gelu", x, M, DIM, w, FFN, 1, H.DTYPE_BF16, H.DTYPE_BF16, PEAK_BF16_TFLOPS,
+                "bf16 activations x Q8 weight dequantized to bf16 in the tile loader, bf16 MFMA")
+    w.free()
+    x.free()
+    # config 3: Q4 (symmetric, per-32 scales) FFN down, input = GELU of N(0,1); plain and heavy-tailed
+    be.set_act_dtype(H.DTYPE_F32)
+    xr = be.alloc(M * FFN)
+    be.fill_normal(xr, 1021, 1.0)
+    v = be.download(xr)
+    xr.free()
+    g = 0.5 * v * (1.0 + np.tanh(np.float32(0.7978845608) * (v + np.float32(0.044715) * v * v * v)))
+    be.set_act_dtype(H.DTYPE_BF16)
+    x = be.upload(g.astype(np.float32))
+    del v, g
+    for heavy in (False, True):
+        w = weight("q4", DIM, FFN, 0.02, 1022, heavy=heavy)
+        time_linear("cfg3_q4_ffn_down" + ("_heavy_tailed" if heavy else ""), x, M, FFN, w, DIM, 0,
+                    H.DTYPE_BF16, H.DTYPE_BF16, PEAK_BF16_TFLOPS,
+                    "bf16 activations x Q4 weight dequantized to bf16 in the tile loader, bf16 MFMA")
+        w.free()
+    x.free()
+    # config 5: Wan2.2-TI2V-5B shapes in FP8, M = 2640 and 880
+    for rows in (2640, 880):
+        for nm, n, k, act in (("qkv", 3 * 3072, 3072, 0), ("o", 3072, 3072, 0), ("ffn1", 14336, 3072, 1),
+                              ("ffn2", 3072, 14336, 0)):
+            be.set_act_dtype(H.DTYPE_BF16)
+            x = be.alloc(rows * k)
+            be.fill_normal(x, 1031 + rows, 1.0)
+            w = weight("fp8", n, k, 0.015, 1032 + n + k)
+            time_linear(f"cfg5_{nm}_m{rows}", x, rows, k, w, n, act, H.DTYPE_BF16, H.DTYPE_BF16,
+                        PEAK_FP8_TFLOPS, fp8_path)
+            w.free()
+            x.free()
+    be.set_act_dtype(H.DTYPE_BF16)
+    return out
 
 
 def cpu_baseline(seconds_target=12.0):
@@ -112,6 +209,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config linears")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eagerly only (rocprofv3 cannot trace hipGraphLaunch here)")
     args = ap.parse_args()
@@ -267,6 +365,12 @@ def main():
     ca.free()
     cb.free()
 
+    configs = None
+    if not args.no_configs:
+        configs = per_config(be, H)
+        log("bench: configs " + ", ".join(f"{k} {v['us_per_linear']:.1f} us ({v['pct_peak']:.0f}%)"
+                                          for k, v in configs.items()))
+
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
@@ -306,6 +410,7 @@ def main():
         "gemm_only_ms_per_chunk": round(gemm_ms, 3),
         "act_quant_ms_per_chunk": round(region["act_quant_chunk"], 3),
         "per_gemm": per,
+        "per_config": configs,
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 1),
