@@ -10,21 +10,21 @@
 // both are K-major, the layout the MFMA operands want, so codes go from HBM
 // to LDS to the matrix cores untouched.
 //
-// Work decomposition.  One workgroup (4 waves, 2 x 2) per BM x BN output
-// tile; each wave owns a (BM/2) x (BN/2) sub-tile of 32 x 32 MFMA blocks
-// whose accumulators stay in AGPRs for the whole K loop.  K advances 128
-// bytes per stage through two LDS buffers (16-byte chunks XOR-swizzled so
-// the fragment reads are bank-conflict free) fed from two register stages:
-// the global loads of stage k+2 are in flight while stage k is contracted
-// and stage k+1 waits in registers, which gives the loads two stages of
-// MFMA time to arrive.
+// Kernels (one workgroup per BM x BN output tile, waves of 64 x 64 or 128 x
+// 64 sub-tiles of 32 x 32 MFMA blocks, K-major operands from HBM to LDS):
+//   k_gemm_fp8_dma -- the main kernel: 16-byte buffer_load ... lds straight
+//     into an NS-stage LDS ring (K % 128 == 0), one to three workgroups per
+//     CU, an LDS-staged epilogue, per-token or MX e4m3 activations, bf16 /
+//     f32 / MX e4m3 output;
+//   k_gemm_fp8_pp  -- 256 x 256 tiles whose two wave groups alternate MFMA
+//     and LDS phases (ping-pong);
+//   k_gemm_fp8     -- register-staged, for K a multiple of 16 but not 128.
+// plan_gemm_fp8 picks the configuration per shape from a fitted time model.
 //
 // Operand roles: the weight tile is the MFMA's A operand and the activation
 // tile its B operand, so the 32 x 32 result block D[n][m] leaves each lane
 // one activation row m and, per group of four accumulator registers, four
-// consecutive output channels n -- the epilogue applies both scales, bias
-// and GELU and writes those four outputs with one 16-byte (f32) or 8-byte
-// (bf16) store.
+// consecutive output channels n.
 #include "device_common.hpp"
 #include "runtime.hpp"
 
@@ -648,146 +648,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                                                           act, Y, mx);
 }
 
-// ---- software-pipelined direct-to-LDS kernel ----------------------------------------
-//
-// Same data movement as k_gemm_fp8_dma (16-byte buffer_load ... lds into an
-// NS-stage LDS ring, global-side swizzle), one wave per SIMD, and a
-// schedule that keeps the matrix cores fed across the per-stage barrier:
-// the MFMA fragments of stage s + 1 are read from LDS into a second
-// register set while the MFMAs of stage s issue, and the DMA loads of stage
-// s + NS - 1 are issued between those MFMAs.  Per stage:
-//
-//   wait (own loads of stage s + 1 landed); barrier (everyone's have, and
-//   everyone has consumed stage s - 1, whose buffer is refilled next);
-//   for t over the stage's MFMAs:  MFMA t (fragments of stage s)
-//                                  + one LDS fragment read for stage s + 1
-//                                  + one DMA load of stage s + NS - 1
-//
-// The order is pinned with scheduling barriers.  Fragment registers:
-// 2 sets x (TM + TN) x (BK / 64) x 8 VGPRs; accumulators TM x TN x 16 AGPRs.
-
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS, typename TY>
-__global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_fp8_sp(const uint8_t *__restrict__ A,
-                                                                  const float *__restrict__ sa,
-                                                                  const uint8_t *__restrict__ B,
-                                                                  const float *__restrict__ sb,
-                                                                  const float *__restrict__ bias,
-                                                                  TY *__restrict__ Y, int M, int N, int K,
-                                                                  int act, int tiles_m, int tiles_n) {
-    constexpr int NW = WGM * WGN;
-    constexpr int WM = BM / WGM, WN = BN / WGN;
-    constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int KK = BKB / 64;                  // MFMA k-steps per stage
-    constexpr int CPR = BKB / 16;                 // 16-byte chunks per tile row
-    constexpr int RPI = 64 / CPR;                 // tile rows per 1 KB load
-    constexpr int ALD = BM / RPI / NW, BLD = BN / RPI / NW;  // loads per wave per stage
-    constexpr int LPS = ALD + BLD;
-    constexpr int STAGE = (BM + BN) * BKB;
-    constexpr int NMMA = KK * TM * TN;            // MFMAs per wave per stage
-    static_assert(ALD * RPI * NW == BM && BLD * RPI * NW == BN, "tile rows must split over the waves");
-    static_assert(NS >= 3 && NS * STAGE <= 160 * 1024, "LDS");
-    static_assert(KK * (TM + TN) <= NMMA && LPS <= NMMA, "interleave slots");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wid / WGN, wn = wid % WGN;
-    int tm, tn;
-    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int KT = K / BKB;
-
-    const auto ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K);
-    const auto rb_src = make_rsrc(B + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
-
-    // DMA load j of a stage (j < ALD: activation rows, else weight rows):
-    // tile rows [(i NW + wid) RPI, +RPI) with i = j or j - ALD; lane l fills
-    // slot l % CPR of row l / CPR.
-    const uint32_t lrow = (uint32_t)lane / CPR, lslot = (uint32_t)lane % CPR;
-    uint32_t g_off[LPS];
-#pragma unroll
-    for (int j = 0; j < LPS; j++) {
-        const bool isa = j < ALD;
-        const uint32_t row = (uint32_t)((isa ? j : j - ALD) * NW + wid) * RPI + lrow;
-        g_off[j] = row * (uint32_t)K + dma_slot<BKB>(isa ? row : BM + row, lslot) * 16;
-    }
-    auto dma = [&](int j, int kt) {
-        const bool isa = j < ALD;
-        const int i = isa ? j : j - ALD;
-        uint8_t *dst = smem + (kt % NS) * STAGE + ((isa ? 0 : BM) + (i * NW + wid) * RPI) * BKB;
-        const uint32_t off = kt < KT ? g_off[j] + (uint32_t)kt * BKB : kOob;
-        dma16(isa ? ra_src : rb_src, dst, off);
-    };
-
-    // Fragment f of a stage, f = kk (TM + TN) + blk: activation block blk
-    // (< TM) or weight block blk - TM; each is two 16-byte LDS reads.
-    constexpr int NF = KK * (TM + TN);
-    const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
-    auto frag = [&](int f, int buf) -> i32x8 {
-        const int kk = f / (TM + TN), blk = f % (TM + TN);
-        const uint32_t row = blk < TM ? (uint32_t)(wm * WM + blk * 32) + frow
-                                      : (uint32_t)(BM + wn * WN + (blk - TM) * 32) + frow;
-        const uint32_t c = (uint32_t)kk * 4 + fhalf;
-        const uint8_t *rp = smem + buf * STAGE + row * BKB;
-        const u32x4 lo = *(const u32x4 *)(rp + (dma_slot<BKB>(row, c) << 4));
-        const u32x4 hi = *(const u32x4 *)(rp + (dma_slot<BKB>(row, c + 1) << 4));
-        return (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    };
-
-    f32x16 acc[TN][TM];
-#pragma unroll
-    for (int j = 0; j < TN; j++)
-#pragma unroll
-        for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
-
-    i32x8 fr0[NF], fr1[NF];
-    // One stage: MFMAs on `cur` interleaved with the fragment reads of
-    // stage s + 1 into `nxt` and the DMA loads of stage s + NS - 1.
-    auto stage = [&](const i32x8(&cur)[NF], i32x8(&nxt)[NF], int s) {
-        wait_vmcnt<(NS - 3) * LPS>();  // own loads of stage s + 1 landed
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        const int nb = (s + 1) % NS;
-#pragma unroll
-        for (int t = 0; t < NMMA; t++) {
-            const int kk = t / (TM * TN), j = (t % (TM * TN)) / TM, i = t % TM;
-            acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                cur[kk * (TM + TN) + TM + j], cur[kk * (TM + TN) + i], acc[j][i], 0, 0, 0, 0, 0, 0);
-            // fragment reads and loads spread evenly over the stage's MFMAs
-#pragma unroll
-            for (int f = 0; f < NF; f++)
-                if (f * NMMA / NF == t) nxt[f] = frag(f, nb);
-#pragma unroll
-            for (int j2 = 0; j2 < LPS; j2++)
-                if (j2 * NMMA / LPS == t) dma(j2, s + NS - 1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    // Prologue: stages 0 .. NS - 2 in flight, stage 0's fragments in fr0.
-#pragma unroll
-    for (int st = 0; st < NS - 1; st++)
-#pragma unroll
-        for (int j = 0; j < LPS; j++) dma(j, st);
-    wait_vmcnt<(NS - 2) * LPS>();  // stage 0 landed (own loads)
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int f = 0; f < NF; f++) fr0[f] = frag(f, 0);
-    // KT >= 1 (the launcher requires K to be a positive multiple of BK); a
-    // do-while keeps the accumulators in AGPRs on every path.
-    int s = 0;
-    do {
-        stage(fr0, fr1, s);
-        if (s + 1 < KT) stage(fr1, fr0, s + 1);
-        s += 2;
-    } while (s < KT);
-    // Drain what is still in flight (loads past KT are out of range and
-    // write nothing) before the waves retire their LDS.
-    wait_vmcnt<0>();
-    epilogue_fp8<TM, TN, TY>(acc, m0 + wm * WM, n0 + wn * WN, lane, M, N, sa, sb, bias, act, Y);
-}
-
 // ---- ping-pong kernel: two wave groups alternate MFMA and LDS phases ---------------
 //
 // Measured on gfx950: a ds_read_b128 costs its own wave ~25 MFMA cycles of
@@ -994,18 +854,6 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
 #undef LX2V_DMA
 }
 
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS>
-void launch_sp(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
-               const float *bias, int act, void *y, int y_dtype, int M, int N, int K) {
-    int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
-    if (y_dtype == LX2V_DTYPE_BF16)
-        hipLaunchKernelGGL((k_gemm_fp8_sp<BM, BN, WGM, WGN, BKB, NS, uint16_t>), grid, block, 0, s, a, sa, b, sb,
-                           bias, (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
-    else
-        hipLaunchKernelGGL((k_gemm_fp8_sp<BM, BN, WGM, WGN, BKB, NS, float>), grid, block, 0, s, a, sa, b, sb, bias,
-                           (float *)y, M, N, K, act, tiles_m, tiles_n);
-}
 
 // Direct-to-LDS configurations: tile (activation rows x channels), wave
 // grid, K bytes per stage, stages.
@@ -1013,65 +861,31 @@ struct DmaCfg {
     int bm, bn, wgm, wgn, bk, ns;
 };
 constexpr DmaCfg kDma[] = {
-    {256, 128, 2, 2, 128, 3},  // 0
-    {128, 256, 2, 2, 128, 3},  // 1
-    {128, 128, 2, 2, 128, 4},  // 2
-    {256, 128, 4, 2, 128, 3},  // 3  (8 waves)
-    {128, 256, 2, 4, 128, 3},  // 4  (8 waves)
-    {256, 256, 2, 4, 64, 4},   // 5  (8 waves)
-    {256, 256, 2, 2, 64, 4},   // 6
-    // software-pipelined (k_gemm_fp8_sp)
-    {256, 256, 2, 2, 64, 4},   // 7
-    {256, 128, 2, 2, 64, 4},   // 8
-    {128, 256, 2, 2, 64, 4},   // 9
-    {256, 128, 2, 2, 128, 3},  // 10
-    {128, 128, 2, 2, 128, 4},  // 11
-    {256, 256, 2, 2, 64, 5},   // 12
-    {256, 256, 2, 4, 64, 5},   // 13 (8 waves)
-    {256, 128, 2, 2, 64, 6},   // 14
-    {256, 256, 1, 4, 128, 2},  // 15 ping-pong (k_gemm_fp8_pp); WGM x WGN = one group's waves
-    {256, 256, 1, 4, 64, 4},   // 16
-    {256, 128, 2, 2, 64, 4},   // 17
-    {256, 128, 2, 2, 128, 3},  // 18
-    {256, 128, 2, 2, 64, 6},   // 19
-    {256, 128, 1, 4, 128, 3},  // 20
-    // direct-to-LDS, small enough for two (three) workgroups per CU
-    {256, 128, 4, 2, 64, 3},   // 21 (8 waves, 2 per CU)
-    {128, 128, 2, 2, 64, 3},   // 22 (4 waves, 3 per CU)
-    {128, 256, 2, 4, 64, 3},   // 23 (8 waves, 2 per CU)
+    // direct-to-LDS (k_gemm_fp8_dma)
+    {256, 128, 4, 2, 128, 3},  // 0: one workgroup per CU
+    {128, 256, 2, 4, 128, 3},  // 1: one per CU
+    {256, 128, 4, 2, 64, 3},   // 2: two per CU
+    {128, 128, 2, 2, 64, 3},   // 3: three per CU (4 waves)
+    {128, 256, 2, 4, 64, 3},   // 4: two per CU
+    // ping-pong (k_gemm_fp8_pp); wgm x wgn = one group's waves
+    {256, 256, 1, 4, 64, 4},   // 5
 };
 
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
                     const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
     switch (idx) {
-        case 0: launch_dma<256, 128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 1: launch_dma<128, 256, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 2: launch_dma<128, 128, 2, 2, 128, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 3: launch_dma<256, 128, 4, 2, 128, 3, 1, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 4: launch_dma<128, 256, 2, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 5: launch_dma<256, 256, 2, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 6: launch_dma<256, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 7: launch_sp<256, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 8: launch_sp<256, 128, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 9: launch_sp<128, 256, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 10: launch_sp<256, 128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 11: launch_sp<128, 128, 2, 2, 128, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 12: launch_sp<256, 256, 2, 2, 64, 5>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 13: launch_sp<256, 256, 2, 4, 64, 5>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 14: launch_sp<256, 128, 2, 2, 64, 6>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 15: launch_pp<256, 1, 4, 128, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 16: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 17: launch_pp<128, 2, 2, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 18: launch_pp<128, 2, 2, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 19: launch_pp<128, 2, 2, 64, 6>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 20: launch_pp<128, 1, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        case 21: launch_dma<256, 128, 4, 2, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 22:
+        case 0:
+            launch_dma<256, 128, 4, 2, 128, 3, 1, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
+            break;
+        case 1: launch_dma<128, 256, 2, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 2: launch_dma<256, 128, 4, 2, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 3:
             launch_dma<128, 128, 2, 2, 64, 3, 3, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
-        default:
+        case 4:
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
+        default: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
     }
 }
 
@@ -1107,17 +921,17 @@ struct CfgCost {
     double per_stage_us, per_round_us, fixed_us;
 };
 constexpr CfgCost kAuto[] = {
-    {3, 0.78, 5.65, 3.63},    // 256 x 128, one workgroup per CU
-    {21, 0.92, 1.32, 7.64},   // 256 x 128, two per CU
-    {23, 0.90, 1.26, 8.42},   // 128 x 256, two per CU
-    {22, 0.528, 1.0, 6.65},   // 128 x 128, three per CU
-    {16, 1.15, 13.5, 0.0},    // 256 x 256 ping-pong
+    {0, 0.78, 5.65, 3.63},    // 256 x 128, one workgroup per CU
+    {2, 0.92, 1.32, 7.64},    // 256 x 128, two per CU
+    {4, 0.90, 1.26, 8.42},    // 128 x 256, two per CU
+    {3, 0.528, 1.0, 6.65},    // 128 x 128, three per CU
+    {5, 1.15, 13.5, 0.0},     // 256 x 256 ping-pong
 };
 
 // The configurations with MX-activation / MX-output kernels.  The 128 x 256
 // two-per-CU tile takes no MX activations: their scale handling needs more
 // than the 128 VGPRs two workgroups per CU leave a wave.
-bool mx_capable(int idx, bool mx_in) { return idx == 3 || idx == 22 || (idx == 23 && !mx_in); }
+bool mx_capable(int idx, bool mx_in) { return idx == 0 || idx == 3 || (idx == 4 && !mx_in); }
 
 Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in) {
     Fp8Plan p;
