@@ -146,7 +146,8 @@ int lx2v_hip_weight_free(lx2v_hip_ctx *ctx, lx2v_hip_weight *w);
 typedef struct {
     int fmt;            /* LX2V_WFMT_* */
     size_t rows, cols, group;
-    size_t device_bytes;
+    size_t device_bytes;  /* codes, scales (and zeros), and the bf16 GEMM's
+                             stage-major copy of the scales */
     size_t canonicalized; /* FP8 exponent-0 codes stored as zero */
 } lx2v_hip_weight_info_t;
 int lx2v_hip_weight_info(const lx2v_hip_weight *w, lx2v_hip_weight_info_t *info);

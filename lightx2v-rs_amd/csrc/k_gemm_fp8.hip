@@ -25,8 +25,7 @@
 // tile its B operand, so the 32 x 32 result block D[n][m] leaves each lane
 // one activation row m and, per group of four accumulator registers, four
 // consecutive output channels n.
-#include "device_common.hpp"
-#include "runtime.hpp"
+#include "gemm_common.hpp"
 
 namespace lx2v {
 
@@ -100,216 +99,6 @@ __device__ __forceinline__ void epilogue_fp8(const f32x16 (&acc)[TN][TM], int mb
             // instead of moving them all to VGPRs up front.
             __builtin_amdgcn_sched_barrier(0);
         }
-    }
-}
-
-// One 16-byte-per-lane buffer load straight into LDS at `lds` + 16 * lane.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff) {
-    typedef __attribute__((address_space(3))) void *lds_ptr;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds, 16, voff, 0, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// LDS-staged epilogue, used where the main loop leaves a large LDS ring
-// free.  Stage 1 (acc_to_lds): each wave applies the token scale, channel
-// scale, bias and GELU exactly as epilogue_fp8 does and writes the results,
-// already in the output type, into a staging tile of R rows x BN columns.
-// Stage 2 (lds_to_global, after a barrier): the whole block stores the tile
-// with consecutive lanes on consecutive 16-byte chunks of a row, so each
-// store instruction writes whole 128-byte lines instead of 16-byte pieces
-// of 32 rows.  The 16-byte chunks of staging row r sit at chunk c ^ (r % 16):
-// the column-fragment writes of stage 1 (32 rows, one chunk each) and the
-// row reads of stage 2 both spread over all 64 banks.  Needs a row of at
-// least 16 chunks (BN * sizeof(TY) >= 256).
-
-// Epilogue operands of a BM x BN tile: sc[r] is the token scale of tile row
-// r (1 for MX activations), sc[BM + c] the channel scale and sc[BM + BN + c]
-// the bias of tile column c, zero outside M x N.  Loaded into registers when the workgroup
-// starts (at most three per thread), so their latency hides under the K
-// loop, and parked in a small LDS array after it.
-template <int BM, int BN, int NT>
-struct TileOps {
-    static constexpr int NV = BM + 2 * BN, PER = (NV + NT - 1) / NT;
-    float v[PER];
-    __device__ __forceinline__ void load(int tid, int m0, int n0, int M, int N, const float *__restrict__ sa,
-                                         const float *__restrict__ sb, const float *__restrict__ bias) {
-#pragma unroll
-        for (int p = 0; p < PER; p++) {
-            const int i = tid + p * NT;
-            float x = 0.0f;
-            if (i < BM) {
-                if (m0 + i < M) x = sa ? sa[m0 + i] : 1.0f;
-            } else if (i < BM + BN) {
-                if (n0 + i - BM < N) x = sb[n0 + i - BM];
-            } else if (i < NV) {
-                if (bias && n0 + i - BM - BN < N) x = bias[n0 + i - BM - BN];
-            }
-            v[p] = x;
-        }
-    }
-    __device__ __forceinline__ void park(float *sc, int tid) const {
-#pragma unroll
-        for (int p = 0; p < PER; p++)
-            if (tid + p * NT < NV) sc[tid + p * NT] = v[p];
-    }
-};
-
-// Staging rows hold BN outputs of TY; their 16-byte chunks are XOR-swizzled
-// by row (chunk ^ row % SWZ) so the column-fragment writes of stage 1 (32
-// rows, one chunk each) and the row reads of stage 2 spread over the banks.
-template <int BN, typename TY>
-constexpr int stage_swz() {
-    return (BN * (int)sizeof(TY) / 16) < 16 ? BN * (int)sizeof(TY) / 16 : 16;
-}
-
-// Where MX output goes besides the codes: E8M0 scale bytes (mx_sidx
-// layout, `rows` rows per 128-column group), starting at the output's row 0.
-struct MxOut {
-    uint8_t *scales = nullptr;
-    int rows = 0;
-};
-
-// Stage 1 of the staged epilogue for one wave: its accumulators, scaled by
-// token and channel scale, biased and GELU'd, into staging rows rloc ..
-// (the wave's tile rows start at wr, its columns at wc).  TY = uint8_t is
-// MX e4m3 output: each 32-column block of a row (one j of one lane pair
-// l, l + 32) gets the scale 2^k of mx_exponent over its 32 values; the
-// codes go to the staging tile and the scale byte straight to global
-// memory (tile origin m0, n0).
-template <int BM, int BN, int TM, int TN, typename TY>
-__device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const float *sc, uint8_t *stg, int rloc,
-                                           int wr, int wc, int lane, int act, MxOut mx, int m0, int n0, int M,
-                                           int N) {
-    constexpr int EB = sizeof(TY), RB = BN * EB, SWZ = stage_swz<BN, TY>();
-    static_assert(RB >= 128 && (RB & (RB - 1)) == 0, "staging row must be a power of two >= 128 bytes");
-    const int l32 = lane & 31, hf = lane >> 5;
-    float sam[TM];
-#pragma unroll
-    for (int i = 0; i < TM; i++) sam[i] = sc[wr + i * 32 + l32];
-    if constexpr (EB == 1) {
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            f32x4 s4[4], b4[4];
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int c = wc + j * 32 + 8 * g + 4 * hf;
-                s4[g] = *(const f32x4 *)(sc + BM + c);
-                b4[g] = *(const f32x4 *)(sc + BM + BN + c);
-            }
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                float v[16];
-                float amax = 0.0f;
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        float t = acc[j][i][4 * g + q] * sam[i] * s4[g][q] + b4[g][q];
-                        if (act == LX2V_ACT_GELU_TANH) t = gelu_tanh_fast(t);
-                        v[4 * g + q] = t;
-                        amax = fmaxf(amax, fabsf(t));
-                    }
-                amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-                const int k = mx_exponent(amax);
-                const float inv = mx_inv(k);
-                const int r = rloc + i * 32 + l32;
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const int cb = wc + j * 32 + 8 * g + 4 * hf;
-                    *(uint32_t *)(stg + r * RB + ((((cb >> 4) ^ (r & (SWZ - 1)))) << 4) + (cb & 15)) =
-                        quant4(v + 4 * g, inv);
-                }
-                const int m = m0 + wr + i * 32 + l32, n = n0 + wc + j * 32;
-                if (hf == 0 && m < M && n < N) mx.scales[mx_sidx(m, n / 32, mx.rows)] = (uint8_t)(k + 127);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        return;
-    }
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int c = wc + j * 32 + 8 * g + 4 * hf;
-            const f32x4 s4 = *(const f32x4 *)(sc + BM + c);
-            const f32x4 b4 = *(const f32x4 *)(sc + BM + BN + c);
-            const int cb = c * EB;  // byte column in the row
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                float v[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    v[q] = acc[j][i][4 * g + q] * sam[i] * s4[q] + b4[q];
-                    if (act == LX2V_ACT_GELU_TANH) v[q] = gelu_tanh_fast(v[q]);
-                }
-                const int r = rloc + i * 32 + l32;
-                uint8_t *p = stg + r * RB + ((((cb >> 4) ^ (r & (SWZ - 1)))) << 4) + (cb & 15);
-                if constexpr (EB == 4) {
-                    *(f32x4 *)p = (f32x4){v[0], v[1], v[2], v[3]};
-                } else {
-                    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-                    *(u32x2_t *)p = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-}
-
-template <int R, int BN, int NT, typename TY>
-__device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m0, int n0, int M, int N,
-                                              TY *__restrict__ Y) {
-    constexpr int EB = sizeof(TY), RB = BN * EB, CPR = RB / 16, EPC = 16 / EB, SWZ = stage_swz<BN, TY>();
-    static_assert((R * CPR) % NT == 0, "staging tile must split evenly over the block");
-    const bool vec = N % EPC == 0;
-#pragma unroll
-    for (int it = 0; it < R * CPR / NT; it++) {
-        const int idx = it * NT + tid, r = idx / CPR, c = idx % CPR;
-        const int m = m0 + r, n = n0 + c * EPC;
-        if (m >= M || n >= N) continue;
-        const u32x4 v = *(const u32x4 *)(stg + r * RB + ((c ^ (r & (SWZ - 1))) << 4));
-        TY *yp = Y + (size_t)m * N + n;
-        if (vec) {
-            *(u32x4 *)yp = v;
-        } else {
-            const TY *e = (const TY *)&v;
-#pragma unroll
-            for (int q = 0; q < EPC; q++)
-                if (n + q < N) yp[q] = e[q];
-        }
-    }
-}
-
-constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
-
-// The staged epilogue of a BM x BN block tile through SMEM bytes of LDS,
-// in passes of R rows when the whole tile does not fit.  Waits for every
-// outstanding DMA of the main loop (stages past K still write zeros) and
-// for every wave's last fragment reads before reusing the ring; the
-// operands in sc (TileOps) must be parked before the call.  The wave owns
-// tile rows [wr, wr + 32 TM) and columns [wc, wc + 32 TN).
-template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY>
-__device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, const float *sc, int wr,
-                                                int wc, int tid, int lane, int m0, int n0, int M, int N, int act,
-                                                TY *__restrict__ Y, MxOut mx = MxOut()) {
-    constexpr int RB = BN * (int)sizeof(TY);
-    constexpr int R = pow2_floor(SMEM / RB < BM ? SMEM / RB : BM);
-    static_assert(BM % R == 0 && R % (32 * TM) == 0, "a wave's rows must fall in one pass");
-    wait_vmcnt<0>();
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < BM / R; p++) {
-        if (p) __syncthreads();
-        if (wr >= p * R && wr < (p + 1) * R)
-            acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, wr, wc, lane, act, mx, m0, n0, M, N);
-        __syncthreads();
-        lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y);
     }
 }
 
@@ -449,16 +238,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8(const uint8_t *__restrict__
 // slot).  NS LDS stages form a ring: stage kt + NS - 1 is in flight while
 // stage kt is contracted, with one barrier per stage and no register
 // staging or LDS store instructions.  WGM x WGN waves (4 or 8: two waves per
-// SIMD let one wave's MFMAs run while the other waits).
-
-// Chunk slot of 16-byte chunk `c` in row `row` of a BK-byte-row tile:
-// consecutive rows of one 256-byte LDS bank window keep their chunks in
-// distinct banks, and a 16-lane read of one chunk column is conflict free.
-template <int BKB>
-__device__ __forceinline__ uint32_t dma_slot(uint32_t row, uint32_t c) {
-    constexpr uint32_t CPR = BKB / 16, RW = 256 / BKB;
-    return c ^ ((row / RW) % CPR);
-}
+// SIMD let one wave's MFMAs run while the other waits); dma_slot gives the
+// LDS swizzle.
 
 // MX activations (AM = 1): A's E8M0 block scales (mx_sidx layout, amx_rows
 // rows per 128-column group, amx_len bytes readable from amx) travel with
@@ -486,6 +267,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     constexpr int RPI = 64 / CPR;                 // tile rows per 1 KB load
     constexpr int ALD = BM / RPI / NW, BLD = BN / RPI / NW;  // loads per wave per stage
     constexpr int STAGE = (BM + BN) * BKB;
+    // Fragment-read offsets inside a stage's A rows / B rows, masked (no-op
+    // masks: the regions are powers of two) so that the compiler can bound
+    // them: it then sees a read never touches a slot a pending DMA writes
+    // and waits only for the loads the read needs, not for every load.
+    constexpr uint32_t AMASK = BM * BKB - 1, BMASK = BN * BKB - 1;
+    static_assert(((BM * BKB) & AMASK) == 0 && ((BN * BKB) & BMASK) == 0, "tile regions are powers of two");
     static_assert(ALD * RPI * NW == BM && BLD * RPI * NW == BN, "tile rows must split over the waves");
     using Ops = TileOps<BM, BN, 64 * NW>;
     constexpr int ASL = AM ? 1024 : 16;  // per-stage LDS for A's block scales (BM rows x 4 bytes)
@@ -497,6 +284,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid / WGN, wn = wid % WGN;
+    const int wid_u = __builtin_amdgcn_readfirstlane(wid);  // DMA LDS addresses only (scalar)
     int tm, tn;
     xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
     const int m0 = tm * BM, n0 = tn * BN;
@@ -508,8 +296,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // feed output rows / channels that are never stored.
     const auto ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K);
     const auto rb_src = make_rsrc(B + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
-    const auto rs_src =
-        make_rsrc(AM ? amx + 4 * m0 : A, AM ? (amx_len > 4u * m0 ? amx_len - 4u * (uint32_t)m0 : 0u) : 0u);
+    // (readfirstlane: the saturating length would otherwise be computed on
+    // the VALU and take the descriptor out of SGPRs)
+    const auto rs_src = make_rsrc(
+        AM ? amx + 4 * m0 : A,
+        __builtin_amdgcn_readfirstlane(AM ? (amx_len > 4u * m0 ? amx_len - 4u * (uint32_t)m0 : 0u) : 0u));
 
     // Load i of this wave covers tile rows [(i NW + wid) RPI, +RPI); lane l
     // fills slot l % CPR of row l / CPR.
@@ -534,7 +325,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             // loads, this load's return gated wave 0's stage waits (measured
             // ~15% on the K-heavy shapes).  Wave 0; lane l: rows 4 l .. 4 l
             // + 3 of the stage's 128-column group.
-            if (tid < 64) {
+            if (wid_u == 0) {
                 const bool ok = in && lane < BM / 4;
                 dma16(rs_src, asl + buf * ASL,
                       ok ? (uint32_t)(kt * BKB / 128) * (uint32_t)amx_rows * 4u + (uint32_t)lane * 16u : kOob);
@@ -542,10 +333,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         }
 #pragma unroll
         for (int i = 0; i < ALD; i++)
-            dma16(ra_src, sbuf + (i * NW + wid) * RPI * BKB, in ? a_off[i] + k0 : kOob);
+            dma16(ra_src, sbuf + (i * NW + wid_u) * RPI * BKB, in ? a_off[i] + k0 : kOob);
 #pragma unroll
         for (int i = 0; i < BLD; i++)
-            dma16(rb_src, sbuf + (BM + (i * NW + wid) * RPI) * BKB, in ? b_off[i] + k0 : kOob);
+            dma16(rb_src, sbuf + (BM + (i * NW + wid_u) * RPI) * BKB, in ? b_off[i] + k0 : kOob);
     };
 
     f32x16 acc[TN][TM];
@@ -579,16 +370,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 const uint32_t row = wm * WM + i * 32 + frow;
-                u32x4 lo = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c0) << 4));
-                u32x4 hi = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c1) << 4));
+                u32x4 lo = *(const u32x4 *)(s + ((row * BKB + (dma_slot<BKB>(row, c0) << 4)) & AMASK));
+                u32x4 hi = *(const u32x4 *)(s + ((row * BKB + (dma_slot<BKB>(row, c1) << 4)) & AMASK));
                 af[i] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                                 (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
             }
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const uint32_t row = BM + wn * WN + j * 32 + frow;
-                u32x4 lo = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c0) << 4));
-                u32x4 hi = *(const u32x4 *)(s + row * BKB + (dma_slot<BKB>(row, c1) << 4));
+                const uint32_t rb = row - BM;
+                u32x4 lo = *(const u32x4 *)(s + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c0) << 4)) & BMASK));
+                u32x4 hi = *(const u32x4 *)(s + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c1) << 4)) & BMASK));
                 bf[j] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                                 (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
             }
@@ -628,7 +420,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 #pragma unroll
         for (int j = 0; j < NS; j++) {
             if (kt + j < KT) {
-                if (AM && tid < 64)  // wave 0 also loads each stage's A scales
+                if (AM && wid_u == 0)  // wave 0 also loads each stage's A scales
                     wait_vmcnt<(NS - 2) * (LPS + 1)>();
                 else
                     wait_vmcnt<(NS - 2) * LPS>();
@@ -640,7 +432,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             }
         }
     }
-    ops.park(sc, tid);
+    ops.park(sc, tid, m0, n0, M, N, sa, sb);
     MxOut mx;
     mx.scales = ymx;
     mx.rows = ymx_rows;
@@ -787,7 +579,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
         __builtin_amdgcn_sched_barrier(0);
     }
     if (grp == 0) __builtin_amdgcn_s_barrier();
-    ops.park(sc, tid);
+    ops.park(sc, tid, m0, n0, M, N, sa, sb);
     staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY>(acc, smem, sc, grp * (BM / 2) + wm * WM, wn * WN, tid, lane,
                                                         m0, n0, M, N, act, Y);
 }
@@ -869,6 +661,8 @@ constexpr DmaCfg kDma[] = {
     {128, 256, 2, 4, 64, 3},   // 4: two per CU
     // ping-pong (k_gemm_fp8_pp); wgm x wgn = one group's waves
     {256, 256, 1, 4, 64, 4},   // 5
+    {256, 256, 2, 4, 64, 4},   // 6: 128 x 64 wave tiles, one per CU
+    {256, 256, 2, 4, 128, 2},  // 7
 };
 
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
@@ -885,6 +679,8 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 4:
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
+        case 6: launch_dma<256, 256, 2, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 7: launch_dma<256, 256, 2, 4, 128, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
         default: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
     }
 }

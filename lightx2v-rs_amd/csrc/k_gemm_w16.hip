@@ -14,8 +14,9 @@
 // operand roles (weights = MFMA A operand, so the epilogue writes four
 // consecutive channels per lane) follow k_gemm_fp8.hip, with a 64-element K
 // stage (128 bytes of bf16 per row).
-#include "device_common.hpp"
-#include "runtime.hpp"
+#include <utility>
+
+#include "gemm_common.hpp"
 
 namespace lx2v {
 
@@ -315,6 +316,359 @@ void launch_tile(hipStream_t s, const void *x, int x_dtype, const lx2v_hip_weigh
     }
 }
 
+// ---- direct-to-LDS kernel (bf16 activations, K a multiple of 64) --------------------
+//
+// Every operand of a 64-column stage travels HBM -> LDS with the 16-byte
+// buffer_load ... lds into NS-slot rings: the activation tile, the weight's
+// packed codes (in the reference's byte layout) and its group scales (and
+// Q4 zeros) from the stage-major copy (lx2v_hip_weight::sscale).  One stage
+// ahead of the contraction every thread dequantizes its 16-element units
+// exactly as the reference's dequantize() and writes them, rounded to bf16,
+// into a two-slot bf16 weight ring, so each weight element is decoded once
+// per workgroup and the MFMAs read both operands as bf16 fragments.  With
+// no load into registers in the main loop, explicit vmcnt waits carry every
+// dependency (see dma16).
+//
+// Stage kt (one barrier):
+//   wait for this wave's loads of X(kt) and of the weight stage kt + 1 (one
+//   batch, issued NS - 1 stages earlier) and for its bf16 stores of kt;
+//   barrier (publishes them, retires every read of kt - 1);
+//   load X(kt + NS - 1) and the weight stage kt + NS into the slots kt - 1
+//   and kt freed; read the fragments of kt; dequantize kt + 1 into the bf16
+//   slot kt - 1 used; MFMAs.
+
+constexpr int BKE = 64;        // K elements per stage
+constexpr int XRB = BKE * 2;   // bytes per LDS tile row (bf16)
+
+// f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// 16 consecutive K elements of one weight row, as 8 packed bf16 pairs
+// (element 2i low), each rounded from the reference's f32 dequantization
+// (quant.rs:183-191, 279-289, 432-440): c = 16 code bytes (Q8, FP8) or 8
+// (Q4, in c.x, c.y), s / z = the group's scale / zero.
+template <int WF>
+__device__ __forceinline__ void unit_dequant(u32x4 c, float s, float z, uint32_t (&o)[8]) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    if constexpr (WF == LX2V_WFMT_Q8) {
+        // byte ^ 0x80 reads as q + 128 unsigned, and fma(q + 128, s, -128 s)
+        // rounds the exact q * s once (128 s is exact): the reference's q * s.
+        const float nb = -128.0f * s;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t b = w[q] ^ 0x80808080u;
+            const float f0 = __builtin_fmaf((float)(b & 0xFFu), s, nb);
+            const float f1 = __builtin_fmaf((float)((b >> 8) & 0xFFu), s, nb);
+            const float f2 = __builtin_fmaf((float)((b >> 16) & 0xFFu), s, nb);
+            const float f3 = __builtin_fmaf((float)(b >> 24), s, nb);
+            o[2 * q] = pack_bf16x2(f0, f1);
+            o[2 * q + 1] = pack_bf16x2(f2, f3);
+        }
+    } else if constexpr (WF == LX2V_WFMT_Q4) {
+        // element 2i in the low nibble of byte i (quant.rs:305-311)
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const uint32_t lo = w[q] & 0x0F0F0F0Fu, hi = (w[q] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float e0 = ((float)((lo >> (8 * b)) & 0xFFu) - z) * s;
+                const float e1 = ((float)((hi >> (8 * b)) & 0xFFu) - z) * s;
+                o[4 * q + b] = pack_bf16x2(e0, e1);
+            }
+        }
+    } else {
+        // e4m3 through the hardware OCP decode; the reference decodes
+        // exponent field 0 as m * 2^-12, an eighth of OCP's m * 2^-9.
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            typedef float f32x2_t __attribute__((ext_vector_type(2)));
+            const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], false);
+            const f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], true);
+            float f[4] = {a.x, a.y, b.x, b.y};
+            const uint32_t e = w[q] & 0x78787878u;
+            if ((e - 0x01010101u) & ~e & 0x80808080u) {  // some byte has exponent field 0
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (((e >> (8 * k)) & 0xFFu) == 0) f[k] *= 0.125f;
+            }
+            o[2 * q] = pack_bf16x2(f[0] * s, f[1] * s);
+            o[2 * q + 1] = pack_bf16x2(f[2] * s, f[3] * s);
+        }
+    }
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int WF, typename TY>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16_t *__restrict__ X,
+                                                                 const uint8_t *__restrict__ Wc,
+                                                                 const float *__restrict__ Wss,
+                                                                 const float *__restrict__ Wsz, int spr,
+                                                                 const float *__restrict__ bias,
+                                                                 TY *__restrict__ Y, int M, int N, int K,
+                                                                 int act, int tiles_m, int tiles_n) {
+    constexpr int NW = WGM * WGN, NT = 64 * NW;
+    constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+    constexpr bool Q4 = WF == LX2V_WFMT_Q4;
+    constexpr int DEN = Q4 ? 2 : 1;          // elements per code byte
+    constexpr int CBS = BKE / DEN;           // code bytes per weight row per stage
+    constexpr int XS = BM * XRB;             // activation slot
+    constexpr int CS = BN * CBS;             // code slot
+    constexpr int SS = BN * 16;              // scale (zero) slot: up to 4 per row
+    constexpr int WSL = BN * XRB;            // bf16 weight slot
+    constexpr int RING = XS + CS + SS * (Q4 ? 2 : 1);  // one stage of every ring
+    constexpr int XJ = XS / 1024, CJ = CS / 1024, SJ = SS / 1024, ZJ = Q4 ? SJ : 0;
+    constexpr int ALD = XJ / NW;             // activation loads per wave per stage
+    constexpr int EJ = CJ + SJ + ZJ;         // weight loads per stage, spread over the waves
+    constexpr int EPW = (EJ + NW - 1) / NW;  // ... at most this many per wave
+    constexpr int UPT = BN * (BKE / 16) / NT;  // 16-element units per thread per stage
+    using Ops = TileOps<BM, BN, NT>;
+    static_assert(ALD * NW == XJ && CS % 1024 == 0 && SS % 1024 == 0 && UPT * NT == BN * (BKE / 16),
+                  "tile loads must split over the waves");
+    static_assert(NS >= 2 && (NS - 1) * (ALD + EPW) < 64, "vmcnt range");
+    static_assert(NS * RING + 2 * WSL + Ops::NV * 4 <= 160 * 1024, "LDS");
+    static_assert((XS & (XS - 1)) == 0 && (WSL & (WSL - 1)) == 0, "slot sizes are powers of two");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * RING + 2 * WSL];
+    __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
+    uint8_t *const xr = smem;                      // NS activation slots
+    uint8_t *const cr = smem + NS * XS;            // NS code slots
+    uint8_t *const sr = cr + NS * CS;              // NS scale slots
+    uint8_t *const zr = sr + NS * SS;              // NS zero slots (Q4)
+    uint8_t *const wr = smem + NS * RING;          // 2 bf16 weight slots
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int wid_u = __builtin_amdgcn_readfirstlane(wid);  // DMA addresses and job choice (scalar)
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = K / BKE;
+    Ops ops;
+    ops.load(tid, m0, n0, M, N, nullptr, nullptr, bias);
+
+    // Rows past the matrix read zero (codes) or another row's scales: they
+    // only feed outputs that are never stored.
+    const uint32_t cbrow = (uint32_t)K / DEN;  // code bytes per weight row
+    const uint32_t sstage = (uint32_t)N * (uint32_t)spr * 4u;  // bytes of one stage of scales
+    const auto rx = make_rsrc(X + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K * 2u);
+    const auto rw = make_rsrc(Wc + (size_t)n0 * cbrow, (uint32_t)(N - n0) * cbrow);
+    const auto rs = make_rsrc(Wss, (uint32_t)KT * sstage);
+    const auto rz = make_rsrc(Q4 ? Wsz : Wss, Q4 ? (uint32_t)KT * sstage : 0u);
+
+    // Activation load i of this wave: tile rows [(i NW + wid) 8, +8), lane l
+    // fills slot l % 8 of row l / 8.
+    const uint32_t lrow = (uint32_t)lane / 8u, lslot = (uint32_t)lane % 8u;
+    uint32_t x_off[ALD];
+#pragma unroll
+    for (int i = 0; i < ALD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * 8u + lrow;
+        x_off[i] = row * (uint32_t)K * 2u + dma_slot<XRB>(row, lslot) * 16u;
+    }
+    // Weight load x of this wave: job e = x NW + wid of [CJ code KBs, SJ
+    // scale KBs, ZJ zero KBs]; its lane offset without the stage term.
+    uint32_t e_off[EPW];
+#pragma unroll
+    for (int x = 0; x < EPW; x++) {
+        const int e = x * NW + wid;
+        const uint32_t b = (uint32_t)(e < CJ ? e : (e < CJ + SJ ? e - CJ : e - CJ - SJ)) * 1024u + lane * 16u;
+        if (e < CJ)
+            e_off[x] = (b / CBS) * cbrow + b % CBS;
+        else
+            e_off[x] = b < (uint32_t)BN * (uint32_t)spr * 4u ? (uint32_t)n0 * (uint32_t)spr * 4u + b : kOob;
+    }
+
+    // Activation stage kt into X slot slot_x and weight stage kt + 1 into
+    // code / scale slot slot_w: one batch of this wave's loads.
+    auto issue = [&](int kt, int slot_x, int slot_w) {
+        const bool in_x = kt >= 0 && kt < KT;
+#pragma unroll
+        for (int i = 0; i < ALD; i++)
+            dma16(rx, xr + slot_x * XS + (i * NW + wid_u) * 1024, in_x ? x_off[i] + (uint32_t)kt * XRB : kOob);
+        const int kw = kt + 1;
+        const bool in = kw < KT;
+#pragma unroll
+        for (int x = 0; x < EPW; x++) {
+            const int e = x * NW + wid_u;
+            if (e < CJ) {
+                dma16(rw, cr + slot_w * CS + e * 1024, in ? e_off[x] + (uint32_t)kw * CBS : kOob);
+            } else if (e < CJ + SJ) {
+                dma16(rs, sr + slot_w * SS + (e - CJ) * 1024,
+                      in && e_off[x] != kOob ? e_off[x] + (uint32_t)kw * sstage : kOob);
+            } else if (e < EJ) {
+                dma16(rz, zr + slot_w * SS + (e - CJ - SJ) * 1024,
+                      in && e_off[x] != kOob ? e_off[x] + (uint32_t)kw * sstage : kOob);
+            }
+        }
+    };
+    // Weight stage kt from its code / scale slot into bf16 weight slot `ws`.
+    auto dequant = [&](int slot_w, int ws) {
+        const uint8_t *cs = cr + slot_w * CS;
+        const float *ss = (const float *)(sr + slot_w * SS);
+        const float *zs = (const float *)(zr + slot_w * SS);
+        uint8_t *d = wr + ws * WSL;
+#pragma unroll
+        for (int u = 0; u < UPT; u++) {
+            const uint32_t id = (uint32_t)(u * NT + tid), row = id / 4u, k16 = id % 4u;
+            u32x4 c;
+            if constexpr (Q4) {
+                const u32x2 h = *(const u32x2 *)(cs + row * CBS + k16 * 8u);
+                c = (u32x4){h.x, h.y, 0u, 0u};
+            } else {
+                c = *(const u32x4 *)(cs + row * CBS + k16 * 16u);
+            }
+            const uint32_t si = row * (uint32_t)spr + ((k16 * (uint32_t)spr) >> 2);
+            uint32_t o[8];
+            unit_dequant<WF>(c, ss[si], Q4 ? zs[si] : 0.0f, o);
+            const uint32_t cc = k16 * 2u;
+            *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc) << 4)) & (WSL - 1))) = (u32x4){o[0], o[1], o[2], o[3]};
+            *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc + 1) << 4)) & (WSL - 1))) =
+                (u32x4){o[4], o[5], o[6], o[7]};
+        }
+    };
+
+    f32x16 acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
+
+    // Loads per wave per stage batch: ALD activation loads and this wave's
+    // share of the weight loads (waves below EJ % NW take one more).
+    const bool extra = wid_u < EJ % NW;
+    const uint32_t frow = lane & 31, fhalf = lane >> 5;
+    // Stage kt = (multiple of U) + J, U = lcm(NS, 2): ring slots are
+    // compile-time offsets.
+    auto stage = [&](auto J, int kt) {
+        constexpr int j = decltype(J)::value;
+        constexpr int LB = ALD + EJ / NW, VM0 = (NS - 2) * LB, VM1 = (NS - 2) * (LB + 1);
+        if (EJ % NW && extra)
+            __builtin_amdgcn_s_waitcnt((VM1 & 15) | ((VM1 >> 4) << 14) | (7 << 4));  // lgkmcnt(0) too
+        else
+            __builtin_amdgcn_s_waitcnt((VM0 & 15) | ((VM0 >> 4) << 14) | (7 << 4));
+        asm volatile("s_barrier" ::: "memory");
+        // X(kt + NS - 1) into the slot X(kt - 1) used; weight stage kt + NS
+        // into the slot of stage kt (dequantized in stage kt - 1).
+        issue(kt + NS - 1, (j + NS - 1) % NS, j % NS);
+        const uint8_t *xs = xr + (j % NS) * XS;
+        const uint8_t *ws = wr + (j & 1) * WSL;
+        u32x4 xf[4][TM], wf[4][TN];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const uint32_t c = (uint32_t)kk * 2u + fhalf;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const uint32_t row = (uint32_t)(wm * WM + i * 32) + frow;
+                xf[kk][i] = *(const u32x4 *)(xs + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (XS - 1)));
+            }
+#pragma unroll
+            for (int jj = 0; jj < TN; jj++) {
+                const uint32_t row = (uint32_t)(wn * WN + jj * 32) + frow;
+                wf[kk][jj] = *(const u32x4 *)(ws + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (WSL - 1)));
+            }
+        }
+        dequant((j + 1) % NS, (j + 1) & 1);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int jj = 0; jj < TN; jj++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    acc[jj][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[kk][jj]),
+                                                                       __builtin_bit_cast(bf16x8, xf[kk][i]),
+                                                                       acc[jj][i], 0, 0, 0);
+    };
+
+    // Prologue: weight stage 0 alone, then as stages -NS+1 .. -1 would:
+    // X(s) and weight stage s + 1 for s = 0 .. NS - 2; wait for weight
+    // stage 0 (everything but those NS - 1 batches), publish it, dequantize.
+    issue(-1, NS - 1, 0);  // X(-1) loads nothing (kOob)
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++) issue(st, st, (st + 1) % NS);
+    {
+        constexpr int LB = ALD + EJ / NW, VM0 = (NS - 1) * LB, VM1 = (NS - 1) * (LB + 1);
+        if (EJ % NW && extra)
+            __builtin_amdgcn_s_waitcnt((VM1 & 15) | ((VM1 >> 4) << 14) | (7 << 4) | (15 << 8));
+        else
+            __builtin_amdgcn_s_waitcnt((VM0 & 15) | ((VM0 >> 4) << 14) | (7 << 4) | (15 << 8));
+    }
+    asm volatile("s_barrier" ::: "memory");
+    dequant(0, 0);
+    constexpr int U = NS % 2 ? 2 * NS : NS;
+    for (int kt = 0; kt < KT; kt += U) {
+        static_for<U>([&](auto J) {
+            if (kt + decltype(J)::value < KT) stage(J, kt + decltype(J)::value);
+        });
+    }
+    ops.park(sc, tid, m0, n0, M, N, nullptr, nullptr);
+    staged_epilogue<BM, BN, NT, NS * RING + 2 * WSL, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0,
+                                                              M, N, act, Y);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int WF>
+void launch_dma_fmt(hipStream_t s, const uint16_t *x, const lx2v_hip_weight *w, const float *bias, int act, void *y,
+                    int y_dtype, int M) {
+    const int N = (int)w->rows, K = (int)w->cols;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
+    const uint8_t *c = (const uint8_t *)w->codes;
+    if (y_dtype == LX2V_DTYPE_BF16)
+        hipLaunchKernelGGL((k_gemm_w16_dma<BM, BN, WGM, WGN, NS, WF, uint16_t>), grid, block, 0, s, x, c, w->sscale,
+                           w->szero, w->spr, bias, (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((k_gemm_w16_dma<BM, BN, WGM, WGN, NS, WF, float>), grid, block, 0, s, x, c, w->sscale,
+                           w->szero, w->spr, bias, (float *)y, M, N, K, act, tiles_m, tiles_n);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS>
+void launch_dma_cfg(hipStream_t s, const uint16_t *x, const lx2v_hip_weight *w, const float *bias, int act, void *y,
+                    int y_dtype, int M) {
+    switch (w->fmt) {
+        case LX2V_WFMT_Q8:
+            launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q8>(s, x, w, bias, act, y, y_dtype, M);
+            break;
+        case LX2V_WFMT_Q4:
+            launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q4>(s, x, w, bias, act, y, y_dtype, M);
+            break;
+        default:
+            launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_FP8>(s, x, w, bias, act, y, y_dtype, M);
+            break;
+    }
+}
+
+// Direct-to-LDS configurations: tile, waves, ring depth (one workgroup per CU).
+struct DmaCfg {
+    int bm, bn, wgm, wgn, ns;
+};
+constexpr DmaCfg kDmaW16[] = {
+    {256, 128, 4, 2, 3},
+    {128, 256, 2, 4, 2},
+};
+constexpr int kNumDmaW16 = sizeof(kDmaW16) / sizeof(kDmaW16[0]);
+
+void launch_dma_idx(int idx, hipStream_t s, const uint16_t *x, const lx2v_hip_weight *w, const float *bias, int act,
+                    void *y, int y_dtype, int M) {
+    switch (idx) {
+        case 0: launch_dma_cfg<256, 128, 4, 2, 3>(s, x, w, bias, act, y, y_dtype, M); break;
+        default: launch_dma_cfg<128, 256, 2, 4, 2>(s, x, w, bias, act, y, y_dtype, M); break;
+    }
+}
+
+// LIGHTX2V_HIP_W16_CFG=<index> forces a configuration (for sweeps).
+int forced_w16_cfg() {
+    static const int v = [] {
+        const char *e = getenv("LIGHTX2V_HIP_W16_CFG");
+        if (!e || !*e) return -1;
+        const int i = atoi(e);
+        return (i >= 0 && i < kNumDmaW16) ? i : -1;
+    }();
+    return v;
+}
+
 }  // namespace
 
 bool gemm_w16_supported(const lx2v_hip_weight *w) {
@@ -349,6 +703,40 @@ void launch_gemm_w16(hipStream_t s, int num_cu, const void *x, int x_dtype, cons
         case 1: launch_tile<128, 256>(s, x, x_dtype, w, bias, act, y, y_dtype, m); break;
         default: launch_tile<128, 128>(s, x, x_dtype, w, bias, act, y, y_dtype, m); break;
     }
+}
+
+bool gemm_w16_dma_supported(const lx2v_hip_weight *w, size_t M) {
+    const size_t N = w->rows, K = w->cols, g = w->group;
+    if (w->fmt != LX2V_WFMT_Q8 && w->fmt != LX2V_WFMT_Q4 && w->fmt != LX2V_WFMT_FP8) return false;
+    const size_t cb = w->fmt == LX2V_WFMT_Q4 ? K / 2 : K;
+    return w->sscale && M > 0 && N > 0 && K >= BKE && K % BKE == 0 && g % 16 == 0 && K % g == 0 &&
+           M * K * 2 < (1ull << 31) && N * cb < (1ull << 31) && (K / BKE) * N * (size_t)w->spr * 4 < (1ull << 31) &&
+           M < (1u << 30) && N < (1u << 30);
+}
+
+// Fill efficiency of each configuration (useful tiles over tile slots of
+// the rounds the grid takes), the larger workgroup tile on ties.
+int plan_gemm_w16_dma(int num_cu, size_t M, size_t N) {
+    if (forced_w16_cfg() >= 0) return forced_w16_cfg();
+    double best = -1.0;
+    int pick = 0;
+    for (int i = 0; i < kNumDmaW16; i++) {
+        const DmaCfg &c = kDmaW16[i];
+        const size_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+        const size_t slots = (size_t)num_cu;
+        const size_t rounds = (tiles + slots - 1) / slots;
+        const double eff = (double)M * N / ((double)rounds * slots * c.bm * c.bn);
+        if (eff > best * 1.0001) {
+            best = eff;
+            pick = i;
+        }
+    }
+    return pick;
+}
+
+void launch_gemm_w16_dma(hipStream_t s, int cfg, const uint16_t *x, const lx2v_hip_weight *w, const float *bias,
+                         int act, void *y, int y_dtype, size_t M) {
+    launch_dma_idx(cfg, s, x, w, bias, act, y, y_dtype, (int)M);
 }
 
 }  // namespace lx2v

@@ -367,6 +367,27 @@ void launch_dequant(hipStream_t s, const lx2v_hip_weight *w, const uint8_t *fp8_
                        codes, w->scales, w->zeros, w->group ? w->group : 1, n, out);
 }
 
+// out[(s * rows + r) * spr + i] = in[r * (cols / group) + (64 s + i * 64 / spr) / group]
+__global__ void k_stage_scales(const float *__restrict__ in, float *__restrict__ out, size_t rows, size_t cols,
+                               size_t group, int spr, size_t n) {
+    for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
+        const size_t i = t % spr, rs = t / spr, r = rs % rows, st = rs / rows;
+        const size_t col = st * 64 + i * (64 / spr);
+        out[t] = in[r * (cols / group) + col / group];
+    }
+}
+
+void launch_stage_scales(hipStream_t s, const lx2v_hip_weight *w) {
+    const size_t n = w->cols / 64 * w->rows * (size_t)w->spr;
+    if (n == 0) return;
+    const dim3 grid(grid_for(n, kThreads));
+    hipLaunchKernelGGL(k_stage_scales, grid, dim3(kThreads), 0, s, w->scales, w->sscale, w->rows, w->cols,
+                       w->group, w->spr, n);
+    if (w->szero)
+        hipLaunchKernelGGL(k_stage_scales, grid, dim3(kThreads), 0, s, w->zeros, w->szero, w->rows, w->cols,
+                           w->group, w->spr, n);
+}
+
 template <int DT>
 void act_quant_rows(hipStream_t s, const void *x, size_t rows, size_t cols, uint8_t *q, float *scale) {
     const size_t per = (cols / 8 + 63) / 64;  // chunks per lane with one wave per row

@@ -223,7 +223,22 @@ void free_weight(lx2v_hip_weight *w) {
     if (w->scales) (void)hipFree(w->scales);
     if (w->zeros) (void)hipFree(w->zeros);
     if (w->raw_e4m3) (void)hipFree(w->raw_e4m3);
+    if (w->sscale) (void)hipFree(w->sscale);
+    if (w->szero) (void)hipFree(w->szero);
     delete w;
+}
+
+// The stage-major scale copy (lx2v_hip_weight::sscale) of a weight the
+// direct-to-LDS bf16 GEMM takes, built on the stream after the scales.
+int stage_scales(lx2v_hip_ctx *ctx, lx2v_hip_weight *w) {
+    if (w->fmt == LX2V_WFMT_F32 || w->cols % 64 || w->group % 16) return LX2V_OK;
+    const size_t g = w->group;
+    w->spr = g % 64 == 0 ? 1 : (g == 32 ? 2 : 4);
+    const size_t n = w->cols / 64 * w->rows * (size_t)w->spr;
+    HIP_TRY(hipMalloc((void **)&w->sscale, n * 4), "stage_scales alloc");
+    if (w->fmt == LX2V_WFMT_Q4) HIP_TRY(hipMalloc((void **)&w->szero, n * 4), "stage_scales alloc");
+    w->device_bytes += n * 4 * (w->szero ? 2 : 1);
+    return run(ctx, "stage_scales", [&] { launch_stage_scales(ctx->stream, w); });
 }
 
 int check_quant_shape(size_t rows, size_t cols, size_t group) {
@@ -512,6 +527,10 @@ int lx2v_hip_weight_q8(lx2v_hip_ctx *ctx, const int8_t *q, const float *scales, 
         return rc;
     }
     w->device_bytes = n + ns * 4;
+    if (int rc2 = stage_scales(ctx, w)) {
+        free_weight(w);
+        return rc2;
+    }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload");
     *out = w;
     return ok();
@@ -555,6 +574,10 @@ int lx2v_hip_weight_q4(lx2v_hip_ctx *ctx, const uint8_t *codes, int packed, cons
         return rc;
     }
     w->device_bytes = np + 2 * ns * 4;
+    if (int rc2 = stage_scales(ctx, w)) {
+        free_weight(w);
+        return rc2;
+    }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload");  // pk must outlive the copy
     *out = w;
     return ok();
@@ -594,6 +617,10 @@ int lx2v_hip_weight_fp8(lx2v_hip_ctx *ctx, const uint8_t *q, const float *scales
         return rc;
     }
     w->device_bytes = n + ns * 4;
+    if (int rc2 = stage_scales(ctx, w)) {
+        free_weight(w);
+        return rc2;
+    }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload");
     *out = w;
     return ok();
@@ -677,6 +704,10 @@ int lx2v_hip_quantize_q8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows
         free_weight(w);
         return rc;
     }
+    if (int rc2 = stage_scales(ctx, w)) {
+        free_weight(w);
+        return rc2;
+    }
     *out = w;
     return ok();
 }
@@ -708,6 +739,10 @@ int lx2v_hip_quantize_q4_sym(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t 
         free_weight(w);
         return rc;
     }
+    if (int rc2 = stage_scales(ctx, w)) {
+        free_weight(w);
+        return rc2;
+    }
     *out = w;
     return ok();
 }
@@ -736,6 +771,10 @@ int lx2v_hip_quantize_fp8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t row
     if (rc) {
         free_weight(w);
         return rc;
+    }
+    if (int rc2 = stage_scales(ctx, w)) {
+        free_weight(w);
+        return rc2;
     }
     *out = w;
     return ok();
@@ -1036,9 +1075,28 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
         }
         return ok();
     }
+    const char *name = w->fmt == LX2V_WFMT_Q8 ? "gemm_w16_q8" : w->fmt == LX2V_WFMT_Q4 ? "gemm_w16_q4" : "gemm_w16_fp8";
+    if (gemm_w16_dma_supported(w, rows)) {
+        // The direct-to-LDS kernel reads bf16 activations; f32 ones are
+        // rounded (RNE, as the register-staged loader would) into the workspace.
+        const uint16_t *xb = (const uint16_t *)xp;
+        if (x->dtype == LX2V_DTYPE_F32) {
+            if (int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, rows * K * 2, "workspace alloc")) return rc;
+            if (int rc = run(ctx, "convert", [&] {
+                    launch_convert(ctx->stream, xp, LX2V_DTYPE_F32, ctx->ws, LX2V_DTYPE_BF16, rows * K);
+                }))
+                return rc;
+            xb = (const uint16_t *)ctx->ws;
+        }
+        const int cfg = plan_gemm_w16_dma(ctx->num_cu, rows, N);
+        if (int rc = run(ctx, name, [&] {
+                launch_gemm_w16_dma(ctx->stream, cfg, xb, w, bp, act, yp, y->dtype, rows);
+            }))
+            return rc;
+        return ok();
+    }
     // The tile loaders address X with 32-bit buffer offsets.
     if (w->fmt != LX2V_WFMT_F32 && gemm_w16_supported(w) && rows * K * x->elem_bytes() < (1ull << 31)) {
-        const char *name = w->fmt == LX2V_WFMT_Q8 ? "gemm_w16_q8" : w->fmt == LX2V_WFMT_Q4 ? "gemm_w16_q4" : "gemm_w16_fp8";
         if (int rc = run(ctx, name, [&] {
                 launch_gemm_w16(ctx->stream, ctx->num_cu, xp, x->dtype, w, bp, act, yp, y->dtype, rows);
             }))

@@ -48,6 +48,14 @@ struct lx2v_hip_weight {
                                   // kept when canonicalization changed a code
     size_t device_bytes = 0;
     size_t canonicalized = 0;
+    // Stage-major copy of the group scales (and Q4 zeros) that the
+    // direct-to-LDS bf16 GEMM loads with each 64-column stage:
+    // [cols / 64][rows][spr] f32, entry i of (stage s, row r) = the scale of
+    // the group holding column 64 s + i * 64 / spr, spr = 1 (group % 64 ==
+    // 0), 2 (group 32) or 4 (other multiples of 16).  Null where that kernel
+    // does not apply (F32, cols % 64 != 0, group % 16 != 0).
+    float *sscale = nullptr, *szero = nullptr;
+    int spr = 0;
 };
 
 namespace lx2v {
@@ -112,6 +120,8 @@ void launch_convert(hipStream_t s, const void *src, int src_dtype, void *dst, in
 void launch_f32_to_bf16(hipStream_t s, const float *src, uint16_t *dst, size_t n);
 void launch_fill_normal(hipStream_t s, void *dst, int dtype, size_t n, uint64_t seed, float std);
 void launch_dequant(hipStream_t s, const lx2v_hip_weight *w, const uint8_t *fp8_codes, float *out);
+// Fills w->sscale / w->szero (allocated, w->spr set) from w->scales / w->zeros.
+void launch_stage_scales(hipStream_t s, const lx2v_hip_weight *w);
 void launch_fp8_canon_count(hipStream_t s, uint8_t *codes, size_t n, unsigned long long *count);
 void launch_q4_pack(hipStream_t s, const uint8_t *codes, size_t n, uint8_t *packed);
 void launch_act_quant(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols,
@@ -165,11 +175,18 @@ void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t 
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
                      int y_dtype, size_t M, size_t N, size_t K, const Fp8Mx &mx);
 
-// k_gemm_w16.hip: bf16 MFMA with the weight dequantized to bf16 in the
-// tile loader (Q8, Q4, FP8 with any group that is a multiple of 32).
+// k_gemm_w16.hip: bf16 MFMA with the weight dequantized to bf16 inside
+// the GEMM (Q8, Q4, FP8 with any group).  The direct-to-LDS kernel takes
+// bf16 activations with K % 64 == 0 and a group that is a multiple of 16;
+// the register-staged one f32 or bf16 activations with K and the group
+// multiples of 16 (32 for Q4).
 bool gemm_w16_supported(const lx2v_hip_weight *w);
 void launch_gemm_w16(hipStream_t s, int num_cu, const void *x, int x_dtype,
                      const lx2v_hip_weight *w, const float *bias, int act, void *y, int y_dtype,
                      size_t M);
+bool gemm_w16_dma_supported(const lx2v_hip_weight *w, size_t M);
+int plan_gemm_w16_dma(int num_cu, size_t M, size_t N);
+void launch_gemm_w16_dma(hipStream_t s, int cfg, const uint16_t *x, const lx2v_hip_weight *w, const float *bias,
+                         int act, void *y, int y_dtype, size_t M);
 
 }  // namespace lx2v

@@ -160,7 +160,8 @@ def test_fp8_grouped_paths(be):
 # ---- Q8 / Q4: bf16 MFMA with in-loader dequantization ----------------------------------
 
 @pytest.mark.parametrize("M,K,N,group", [(64, 256, 192, 32), (77, 288, 130, 32), (300, 1536, 1000, 128),
-                                         (129, 512, 256, 512), (256, 1536, 896, 32)])
+                                         (129, 512, 256, 512), (256, 1536, 896, 32), (96, 256, 320, 16),
+                                         (130, 384, 200, 48)])
 @pytest.mark.parametrize("xdt", [H.DTYPE_F32, H.DTYPE_BF16])
 def test_q8_vs_oracle(be, M, K, N, group, xdt):
     x = normal(20 + M, M * K).reshape(M, K)
@@ -175,8 +176,10 @@ def test_q8_vs_oracle(be, M, K, N, group, xdt):
 
 @pytest.mark.parametrize("M,K,N,group,hqq", [(64, 256, 192, 32, None), (77, 320, 130, 32, None),
                                              (300, 1536, 512, 64, True), (200, 512, 384, 64, False),
-                                             (129, 896, 256, 128, None)])
-def test_q4_vs_oracle(be, M, K, N, group, hqq):
+                                             (129, 896, 256, 128, None), (70, 384, 136, 16, False),
+                                             (260, 384, 264, 48, None)])
+@pytest.mark.parametrize("xdt", [H.DTYPE_F32, H.DTYPE_BF16])
+def test_q4_vs_oracle(be, M, K, N, group, hqq, xdt):
     x = normal(30 + M, M * K).reshape(M, K)
     if hqq is None:
         _, c, s, z = q4_sym_weight(31 + N, N, K, group)
@@ -185,7 +188,7 @@ def test_q4_vs_oracle(be, M, K, N, group, hqq):
         c, s, z = O.q4_quantize(wf, N, K, group, hqq)
     b = normal(32, N, 0.01)
     w = be.weight_q4(O.q4_pack(c), s, z, N, K, group, packed=True)
-    y = run_linear(be, x, w, b, H.ACT_NONE)
+    y = run_linear(be, x, w, b, H.ACT_NONE, x_dtype=xdt)
     wd = O.q4_dequantize(c, s, z, N, K, group)
     assert_close(y, oracle_w16(x, wd, b, 0), *W16_TIGHT, what="q4 vs oracle(bf16 operands)")
     assert_close(y, O.linear(x, wd, b, 0, nthreads=8), 5e-3, 0.05, what="q4 vs f32 oracle")
