@@ -105,34 +105,42 @@ struct MxOut {
 };
 
 // Stage 1 of the staged epilogue for one wave: its accumulators, scaled by
-// token and channel scale, biased and GELU'd, into staging rows rloc ..
-// (the wave's tile rows start at wr, its columns at wc).  TY = uint8_t is
-// MX e4m3 output: each 32-column block of a row (one j of one lane pair
-// l, l + 32) gets the scale 2^k of mx_exponent over its 32 values; the
-// codes go to the staging tile and the scale byte straight to global
-// memory (tile origin m0, n0).
+// token and channel scale, biased and GELU'd, into the staging tile of a
+// pass of R rows, where the wave's tile rows (from wr; columns from wc)
+// start at staging row rloc: its 32-row blocks outside [0, R) wait for
+// another pass.  TY = uint8_t is MX e4m3 output: each 32-column block of a
+// row (one j of one lane pair l, l + 32) gets the scale 2^k of mx_exponent
+// over its 32 values; the codes go to the staging tile and the scale byte
+// straight to global memory (tile origin m0, n0).
 template <int BM, int BN, int TM, int TN, typename TY>
 __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const float *sc, uint8_t *stg, int rloc,
-                                           int wr, int wc, int lane, int act, MxOut mx, int m0, int n0, int M,
-                                           int N) {
+                                           int R, int wr, int wc, int lane, int act, MxOut mx, int m0, int n0,
+                                           int M, int N) {
     constexpr int EB = sizeof(TY), RB = BN * EB, SWZ = stage_swz<BN, TY>();
     static_assert(RB >= 128 && (RB & (RB - 1)) == 0, "staging row must be a power of two >= 128 bytes");
     const int l32 = lane & 31, hf = lane >> 5;
     float sam[TM];
 #pragma unroll
     for (int i = 0; i < TM; i++) sam[i] = sc[wr + i * 32 + l32];
+    // A 32-column block's channel scales and biases, read from LDS in one
+    // round trip (one per channel group would be serialized by the
+    // scheduling barriers that keep the accumulators in place).
+    auto col_ops = [&](int j, f32x4 (&s4)[4], f32x4 (&b4)[4]) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int c = wc + j * 32 + 8 * g + 4 * hf;
+            s4[g] = *(const f32x4 *)(sc + BM + c);
+            b4[g] = *(const f32x4 *)(sc + BM + BN + c);
+        }
+    };
     if constexpr (EB == 1) {
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             f32x4 s4[4], b4[4];
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int c = wc + j * 32 + 8 * g + 4 * hf;
-                s4[g] = *(const f32x4 *)(sc + BM + c);
-                b4[g] = *(const f32x4 *)(sc + BM + BN + c);
-            }
+            col_ops(j, s4, b4);
 #pragma unroll
             for (int i = 0; i < TM; i++) {
+                if (rloc + i * 32 < 0 || rloc + i * 32 >= R) continue;
                 float v[16];
                 float amax = 0.0f;
 #pragma unroll
@@ -161,16 +169,28 @@ __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const fl
         }
         return;
     }
+    // f32 output keeps one group's operands live at a time: the block's
+    // would push the two-per-CU tiles past the 128 VGPRs they may use.
+    constexpr bool BLOCK_OPS = EB != 4;
 #pragma unroll
     for (int j = 0; j < TN; j++) {
+        f32x4 s4j[4], b4j[4];
+        if constexpr (BLOCK_OPS) col_ops(j, s4j, b4j);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const int c = wc + j * 32 + 8 * g + 4 * hf;
-            const f32x4 s4 = *(const f32x4 *)(sc + BM + c);
-            const f32x4 b4 = *(const f32x4 *)(sc + BM + BN + c);
+            f32x4 s4, b4;
+            if constexpr (BLOCK_OPS) {
+                s4 = s4j[g];
+                b4 = b4j[g];
+            } else {
+                s4 = *(const f32x4 *)(sc + BM + c);
+                b4 = *(const f32x4 *)(sc + BM + BN + c);
+            }
             const int cb = c * EB;  // byte column in the row
 #pragma unroll
             for (int i = 0; i < TM; i++) {
+                if (rloc + i * 32 < 0 || rloc + i * 32 >= R) continue;
                 float v[4];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -186,8 +206,9 @@ __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const fl
                     *(u32x2_t *)p = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (!BLOCK_OPS) __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -218,7 +239,7 @@ __device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m
 constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
 
 // The staged epilogue of a BM x BN block tile through SMEM bytes of LDS,
-// in passes of R rows when the whole tile does not fit.  Waits for every
+// in passes of R rows (whole 32-row blocks) when the whole tile does not fit.  Waits for every
 // outstanding DMA of the main loop (stages past K still write zeros) and
 // for every wave's last fragment reads before reusing the ring; the
 // operands in sc (TileOps) must be parked before the call.  The wave owns
@@ -229,14 +250,14 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uin
                                                 TY *__restrict__ Y, MxOut mx = MxOut()) {
     constexpr int RB = BN * (int)sizeof(TY);
     constexpr int R = pow2_floor(SMEM / RB < BM ? SMEM / RB : BM);
-    static_assert(BM % R == 0 && R % (32 * TM) == 0, "a wave's rows must fall in one pass");
+    static_assert(BM % R == 0 && R % 32 == 0, "passes of whole 32-row blocks");
     wait_vmcnt<0>();
     __syncthreads();
 #pragma unroll
     for (int p = 0; p < BM / R; p++) {
         if (p) __syncthreads();
-        if (wr >= p * R && wr < (p + 1) * R)
-            acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, wr, wc, lane, act, mx, m0, n0, M, N);
+        if (wr < (p + 1) * R && wr + 32 * TM > p * R)
+            acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, R, wr, wc, lane, act, mx, m0, n0, M, N);
         __syncthreads();
         lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y);
     }

@@ -316,10 +316,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         const uint32_t row = (uint32_t)(i * NW + wid) * RPI + lrow;  // swizzle rows counted from B's first row
         b_off[i] = row * (uint32_t)K + dma_slot<BKB>(BM + row, lslot) * 16;
     }
+    // Load n (< ALD: A rows, then B rows) of this wave's share of stage kt.
+    auto piece = [&](int n, int kt, int buf) {
+        const uint32_t k0 = (uint32_t)kt * BKB;
+        const bool in = kt < KT;
+        uint8_t *sbuf = smem + buf * STAGE;
+        if (n < ALD)
+            dma16(ra_src, sbuf + (n * NW + wid_u) * RPI * BKB, in ? a_off[n < ALD ? n : 0] + k0 : kOob);
+        else
+            dma16(rb_src, sbuf + (BM + ((n - ALD) * NW + wid_u) * RPI) * BKB,
+                  in ? b_off[n >= ALD ? n - ALD : 0] + k0 : kOob);
+    };
     auto issue = [&](int kt, int buf) {
         const uint32_t k0 = (uint32_t)kt * BKB;
         const bool in = kt < KT;
         uint8_t *sbuf = smem + buf * STAGE;
+        (void)k0, (void)in, (void)sbuf;
         if constexpr (AM) {
             // First in the stage's issue order: issued after the A / B
             // loads, this load's return gated wave 0's stage waits (measured
@@ -332,11 +344,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             }
         }
 #pragma unroll
-        for (int i = 0; i < ALD; i++)
-            dma16(ra_src, sbuf + (i * NW + wid_u) * RPI * BKB, in ? a_off[i] + k0 : kOob);
-#pragma unroll
-        for (int i = 0; i < BLD; i++)
-            dma16(rb_src, sbuf + (BM + (i * NW + wid_u) * RPI) * BKB, in ? b_off[i] + k0 : kOob);
+        for (int n = 0; n < ALD + BLD; n++) piece(n, kt, buf);
     };
 
     f32x16 acc[TN][TM];
@@ -346,7 +354,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
 
     const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
-    auto compute = [&](int buf, int stage) {
+    // compute(buf, stage, dkt, dbuf): the MFMAs of `stage` from slot buf; the
+    // unscaled path issues the loads of stage dkt (slot dbuf) one after each
+    // of its first MFMAs -- issued back to back right after the barrier, the
+    // loads held both waves of a SIMD off the MFMA pipe (7-9% at one
+    // workgroup per CU).  The MX path issues them before (dkt < 0).
+    auto compute = [&](int buf, int stage, int dkt, int dbuf) {
         const uint8_t *s = smem + buf * STAGE;
         uint32_t sraw[AM ? TM : 1];
         if constexpr (AM) {
@@ -401,12 +414,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 #pragma unroll
                 for (int j = 0; j < TN; j++)
 #pragma unroll
-                    for (int i = 0; i < TM; i++)
+                    for (int i = 0; i < TM; i++) {
                         acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                             bf[j], af[i], acc[j][i], 0, 0, 0, 0, 0, 0);
+                        const int n = kk * TN * TM + j * TM + i;
+                        if (n < ALD + BLD && dkt >= 0) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            piece(n, dkt, dbuf);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
             }
         }
     };
+    static_assert(AM || (BKB / 64) * TN * TM >= ALD + BLD, "a stage's loads interleave with its MFMAs");
 
     // Entering stage kt: stages kt .. kt + NS - 2 are in flight (stages past
     // KT load nothing), so waiting until (NS - 2) stages' loads remain
@@ -426,8 +447,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                     wait_vmcnt<(NS - 2) * LPS>();
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                issue(kt + j + NS - 1, (j + NS - 1) % NS);
-                compute(j, kt + j);
+                if constexpr (AM) {
+                    issue(kt + j + NS - 1, (j + NS - 1) % NS);
+                    compute(j, kt + j, -1, 0);
+                } else {
+                    compute(j, kt + j, kt + j + NS - 1, (j + NS - 1) % NS);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -661,8 +686,6 @@ constexpr DmaCfg kDma[] = {
     {128, 256, 2, 4, 64, 3},   // 4: two per CU
     // ping-pong (k_gemm_fp8_pp); wgm x wgn = one group's waves
     {256, 256, 1, 4, 64, 4},   // 5
-    {256, 256, 2, 4, 64, 4},   // 6: 128 x 64 wave tiles, one per CU
-    {256, 256, 2, 4, 128, 2},  // 7
 };
 
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
@@ -679,8 +702,6 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 4:
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
-        case 6: launch_dma<256, 256, 2, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
-        case 7: launch_dma<256, 256, 2, 4, 128, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
         default: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
     }
 }
@@ -704,8 +725,9 @@ bool gemm_fp8_supported(size_t M, size_t N, size_t K) {
            N * K < (1ull << 31) && M < (1u << 30) && N < (1u << 30);
 }
 
-// Time model of the K % 128 == 0 configurations, fitted to measured
-// launch times at the Wan shapes (M 512..4680, K 1536..8960, N 1536..14336):
+// Time model of the K % 128 == 0 configurations, fitted (least squares)
+// to measured launch times at 19 shapes: the Wan ones (M 512..4680, K
+// 1536..14336, N 1536..14336) and 256..9360-row, 1024..4096-square ones:
 //   t = per_stage * rounds * stages + per_round * rounds + fixed,
 // rounds = ceil(tiles / CUs), stages = K / 128.  The configurations that
 // fit two or three workgroups per CU pay a slower K loop (64-byte stages)
@@ -717,11 +739,11 @@ struct CfgCost {
     double per_stage_us, per_round_us, fixed_us;
 };
 constexpr CfgCost kAuto[] = {
-    {0, 0.78, 5.65, 3.63},    // 256 x 128, one workgroup per CU
-    {2, 0.92, 1.32, 7.64},    // 256 x 128, two per CU
-    {4, 0.90, 1.26, 8.42},    // 128 x 256, two per CU
-    {3, 0.528, 1.0, 6.65},    // 128 x 128, three per CU
-    {5, 1.15, 13.5, 0.0},     // 256 x 256 ping-pong
+    {0, 0.625, 8.16, 0.21},   // 256 x 128, one workgroup per CU
+    {2, 0.826, 4.21, 2.44},   // 256 x 128, two per CU
+    {4, 0.926, 2.43, 4.47},   // 128 x 256, two per CU
+    {3, 0.606, 0.44, 4.59},   // 128 x 128, three per CU
+    {5, 1.121, 14.77, 0.0},   // 256 x 256 ping-pong
 };
 
 // The configurations with MX-activation / MX-output kernels.  The 128 x 256

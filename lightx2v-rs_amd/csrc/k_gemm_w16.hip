@@ -483,27 +483,32 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
     }
 
     // Activation stage kt into X slot slot_x and weight stage kt + 1 into
-    // code / scale slot slot_w: one batch of this wave's loads.
-    auto issue = [&](int kt, int slot_x, int slot_w) {
-        const bool in_x = kt >= 0 && kt < KT;
-#pragma unroll
-        for (int i = 0; i < ALD; i++)
-            dma16(rx, xr + slot_x * XS + (i * NW + wid_u) * 1024, in_x ? x_off[i] + (uint32_t)kt * XRB : kOob);
+    // code / scale slot slot_w: one batch of this wave's loads, load n of
+    // which is piece(n) (n < ALD: activation rows; then this wave's weight
+    // jobs, if it has one at that index).
+    auto piece = [&](int n, int kt, int slot_x, int slot_w) {
+        if (n < ALD) {
+            const bool in_x = kt >= 0 && kt < KT;
+            dma16(rx, xr + slot_x * XS + (n * NW + wid_u) * 1024,
+                  in_x ? x_off[n < ALD ? n : 0] + (uint32_t)kt * XRB : kOob);
+            return;
+        }
+        const int x = n - ALD, e = x * NW + wid_u, xe = x < EPW ? x : 0;
         const int kw = kt + 1;
         const bool in = kw < KT;
-#pragma unroll
-        for (int x = 0; x < EPW; x++) {
-            const int e = x * NW + wid_u;
-            if (e < CJ) {
-                dma16(rw, cr + slot_w * CS + e * 1024, in ? e_off[x] + (uint32_t)kw * CBS : kOob);
-            } else if (e < CJ + SJ) {
-                dma16(rs, sr + slot_w * SS + (e - CJ) * 1024,
-                      in && e_off[x] != kOob ? e_off[x] + (uint32_t)kw * sstage : kOob);
-            } else if (e < EJ) {
-                dma16(rz, zr + slot_w * SS + (e - CJ - SJ) * 1024,
-                      in && e_off[x] != kOob ? e_off[x] + (uint32_t)kw * sstage : kOob);
-            }
+        if (e < CJ) {
+            dma16(rw, cr + slot_w * CS + e * 1024, in ? e_off[xe] + (uint32_t)kw * CBS : kOob);
+        } else if (e < CJ + SJ) {
+            dma16(rs, sr + slot_w * SS + (e - CJ) * 1024,
+                  in && e_off[xe] != kOob ? e_off[xe] + (uint32_t)kw * sstage : kOob);
+        } else if (e < EJ) {
+            dma16(rz, zr + slot_w * SS + (e - CJ - SJ) * 1024,
+                  in && e_off[xe] != kOob ? e_off[xe] + (uint32_t)kw * sstage : kOob);
         }
+    };
+    auto issue = [&](int kt, int slot_x, int slot_w) {
+#pragma unroll
+        for (int n = 0; n < ALD + EPW; n++) piece(n, kt, slot_x, slot_w);
     };
     // Weight stage kt from its code / scale slot into bf16 weight slot `ws`.
     auto dequant = [&](int slot_w, int ws) {
@@ -551,9 +556,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
         else
             __builtin_amdgcn_s_waitcnt((VM0 & 15) | ((VM0 >> 4) << 14) | (7 << 4));
         asm volatile("s_barrier" ::: "memory");
-        // X(kt + NS - 1) into the slot X(kt - 1) used; weight stage kt + NS
-        // into the slot of stage kt (dequantized in stage kt - 1).
-        issue(kt + NS - 1, (j + NS - 1) % NS, j % NS);
         const uint8_t *xs = xr + (j % NS) * XS;
         const uint8_t *ws = wr + (j & 1) * WSL;
         u32x4 xf[4][TM], wf[4][TN];
@@ -571,17 +573,31 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
                 wf[kk][jj] = *(const u32x4 *)(ws + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (WSL - 1)));
             }
         }
-        dequant((j + 1) % NS, (j + 1) & 1);
+        // MFMAs; after each of the first ALD + EPW, one load of the batch
+        // of X(kt + NS - 1) (into the slot X(kt - 1) used) and weight stage
+        // kt + NS (into the slot of stage kt, dequantized in stage kt - 1):
+        // issued back to back, the loads held both waves of a SIMD off the
+        // MFMA pipe.  Then the dequantization of weight stage kt + 1, whose
+        // VALU work can run under the MFMAs.
 #pragma unroll
         for (int kk = 0; kk < 4; kk++)
 #pragma unroll
             for (int jj = 0; jj < TN; jj++)
 #pragma unroll
-                for (int i = 0; i < TM; i++)
+                for (int i = 0; i < TM; i++) {
                     acc[jj][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[kk][jj]),
                                                                        __builtin_bit_cast(bf16x8, xf[kk][i]),
                                                                        acc[jj][i], 0, 0, 0);
+                    const int n = (kk * TN + jj) * TM + i;
+                    if (n < ALD + EPW) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        piece(n, kt + NS - 1, (j + NS - 1) % NS, j % NS);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+        dequant((j + 1) % NS, (j + 1) & 1);
     };
+    static_assert(4 * TN * TM >= ALD + EPW, "a stage's loads interleave with its MFMAs");
 
     // Prologue: weight stage 0 alone, then as stages -NS+1 .. -1 would:
     // X(s) and weight stage s + 1 for s = 0 .. NS - 2; wait for weight
