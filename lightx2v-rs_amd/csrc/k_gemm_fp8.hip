@@ -327,12 +327,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             dma16(rb_src, sbuf + (BM + ((n - ALD) * NW + wid_u) * RPI) * BKB,
                   in ? b_off[n >= ALD ? n - ALD : 0] + k0 : kOob);
     };
-    auto issue = [&](int kt, int buf) {
-        const uint32_t k0 = (uint32_t)kt * BKB;
-        const bool in = kt < KT;
-        uint8_t *sbuf = smem + buf * STAGE;
-        (void)k0, (void)in, (void)sbuf;
+    // Wave 0's MX scale load of stage kt (slot buf).
+    auto issue_scales = [&](int kt, int buf) {
         if constexpr (AM) {
+            const bool in = kt < KT;
             // First in the stage's issue order: issued after the A / B
             // loads, this load's return gated wave 0's stage waits (measured
             // ~15% on the K-heavy shapes).  Wave 0; lane l: rows 4 l .. 4 l
@@ -343,6 +341,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                       ok ? (uint32_t)(kt * BKB / 128) * (uint32_t)amx_rows * 4u + (uint32_t)lane * 16u : kOob);
             }
         }
+    };
+    auto issue = [&](int kt, int buf) {
+        issue_scales(kt, buf);
 #pragma unroll
         for (int n = 0; n < ALD + BLD; n++) piece(n, kt, buf);
     };
@@ -354,11 +355,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
 
     const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
-    // compute(buf, stage, dkt, dbuf): the MFMAs of `stage` from slot buf; the
-    // unscaled path issues the loads of stage dkt (slot dbuf) one after each
-    // of its first MFMAs -- issued back to back right after the barrier, the
+    // compute(buf, stage, dkt, dbuf): the MFMAs of `stage` from slot buf,
+    // with the A / B loads of stage dkt (slot dbuf) issued one after each of
+    // its first MFMAs -- issued back to back right after the barrier, the
     // loads held both waves of a SIMD off the MFMA pipe (7-9% at one
-    // workgroup per CU).  The MX path issues them before (dkt < 0).
+    // workgroup per CU).  dkt < 0: no loads.
     auto compute = [&](int buf, int stage, int dkt, int dbuf) {
         const uint8_t *s = smem + buf * STAGE;
         uint32_t sraw[AM ? TM : 1];
@@ -407,9 +408,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 #pragma unroll
                 for (int j = 0; j < TN; j++)
 #pragma unroll
-                    for (int i = 0; i < TM; i++)
+                    for (int i = 0; i < TM; i++) {
                         acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                             bf[j], af[i], acc[j][i], 0, 0, 0, 127, 0, as[i]);
+                        const int n = kk * TN * TM + j * TM + i;
+                        if (n < ALD + BLD && dkt >= 0) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            piece(n, dkt, dbuf);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
             } else {
 #pragma unroll
                 for (int j = 0; j < TN; j++)
@@ -427,7 +435,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             }
         }
     };
-    static_assert(AM || (BKB / 64) * TN * TM >= ALD + BLD, "a stage's loads interleave with its MFMAs");
+    static_assert((BKB / 64) * TN * TM >= ALD + BLD, "a stage's loads interleave with its MFMAs");
 
     // Entering stage kt: stages kt .. kt + NS - 2 are in flight (stages past
     // KT load nothing), so waiting until (NS - 2) stages' loads remain
@@ -447,12 +455,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                     wait_vmcnt<(NS - 2) * LPS>();
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (AM) {
-                    issue(kt + j + NS - 1, (j + NS - 1) % NS);
-                    compute(j, kt + j, -1, 0);
-                } else {
-                    compute(j, kt + j, kt + j + NS - 1, (j + NS - 1) % NS);
-                }
+                if constexpr (AM) issue_scales(kt + j + NS - 1, (j + NS - 1) % NS);
+                compute(j, kt + j, kt + j + NS - 1, (j + NS - 1) % NS);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
