@@ -176,6 +176,30 @@ int lx2v_hip_quantize_q4_sym(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t 
 int lx2v_hip_quantize_fp8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
                           size_t cols, size_t group, lx2v_hip_weight **out);
 
+/* Q4::quantize (quant.rs:226-292) with the reference's arithmetic: affine
+ * min/max codes, with hqq != 0 the HQQ-refined zero point (quant.rs:248-276),
+ * scale 1/is and zero rounded to f16 as stored (quant.rs:280-281); codes
+ * packed two per byte, element 2i in the low nibble.  The group must be even
+ * and divide cols (the caller applies the reference's fallback to cols,
+ * quant.rs:227-231).  HQQ's powf is taken in double: glibc's powf differs
+ * from that in the last ulp for ~0.06% of arguments. */
+int lx2v_hip_quantize_q4(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
+                         size_t cols, size_t group, int hqq, lx2v_hip_weight **out);
+/* Fp8E4M3::quantize (quant.rs:423-447) with f32_to_e4m3 (quant.rs:376-406)
+ * verbatim, exponent wrap included: the weight then holds exactly what
+ * weight_fp8 would hold for the reference's Fp8E4M3 (codes canonicalized
+ * for the MFMA, the reference bytes kept for dequantize / export). */
+int lx2v_hip_quantize_fp8_ref(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
+                              size_t cols, size_t group, lx2v_hip_weight **out);
+/* Read a weight back in the reference's layouts (no reference counterpart:
+ * the host struct a Backend::weight_* call consumed, for writing a
+ * quantized checkpoint, export.rs:44-130): codes_bytes = rows*cols (Q8 i8,
+ * FP8 the reference bytes), rows*cols/2 rounded up (Q4 packed) or
+ * 4*rows*cols (F32 values); scales [rows * cols/group] f32 (not for F32);
+ * zeros likewise, Q4 only. */
+int lx2v_hip_weight_export(lx2v_hip_ctx *ctx, const lx2v_hip_weight *w, void *codes,
+                           size_t codes_bytes, float *scales, float *zeros);
+
 /* Synthetic data for benchmarks (Rng::normal, rng.rs:39-54, drawn per element
  * index on the device; values agree with the host Rng to libm ulps):
  * buf[i] = normal(seed)[i] * std. */

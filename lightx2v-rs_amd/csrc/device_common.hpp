@@ -16,6 +16,13 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Max over the 64 lanes of a wave (every lane gets it).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
 // ---- bf16 ------------------------------------------------------------------
 
 // f32 -> bf16 bits, round to nearest even, NaN kept quiet (bit-exact with the

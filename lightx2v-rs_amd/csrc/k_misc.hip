@@ -19,12 +19,6 @@ inline unsigned grid_for(size_t n, int per_block) {
     return (unsigned)(g > 0x7FFFFFFF ? 0x7FFFFFFF : (g == 0 ? 1 : g));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
 // ---- conversion ----------------------------------------------------------------
 
 __global__ void k_convert(const void *src, int sd, void *dst, int dd, size_t n) {

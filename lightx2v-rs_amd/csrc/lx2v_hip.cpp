@@ -780,6 +780,116 @@ int lx2v_hip_quantize_fp8(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t row
     return ok();
 }
 
+int lx2v_hip_quantize_q4(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows, size_t cols, size_t group,
+                         int hqq, lx2v_hip_weight **out) {
+    NEED(out, "out");
+    if (int rc = quant_src_check(ctx, src, rows, cols, group)) return rc;
+    if (group % 2) return fail(LX2V_ERR_BAD_SHAPE, "q4 group %zu must be even (two codes per byte)", group);
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_Q4;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = group;
+    size_t n = rows * cols, ns = n / group;
+    hipError_t e = hipMalloc(&w->codes, n / 2);
+    if (e == hipSuccess) e = hipMalloc((void **)&w->scales, ns * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&w->zeros, ns * 4);
+    if (e != hipSuccess) {
+        free_weight(w);
+        return hip_fail(e, "quantize_q4 alloc");
+    }
+    w->device_bytes = n / 2 + 2 * ns * 4;
+    int rc = run(ctx, "quantize_q4_ref", [&] {
+        launch_quantize_q4_ref(ctx->stream, (const float *)src->ptr, rows, cols, group, hqq ? 1 : 0,
+                               (uint8_t *)w->codes, w->scales, w->zeros);
+    });
+    if (!rc) rc = stage_scales(ctx, w);
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_quantize_fp8_ref(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows, size_t cols, size_t group,
+                              lx2v_hip_weight **out) {
+    NEED(out, "out");
+    if (int rc = quant_src_check(ctx, src, rows, cols, group)) return rc;
+    auto *w = new lx2v_hip_weight;
+    w->fmt = LX2V_WFMT_FP8;
+    w->rows = rows;
+    w->cols = cols;
+    w->group = group;
+    size_t n = rows * cols, ns = n / group;
+    unsigned long long *count = nullptr;
+    hipError_t e = hipMalloc(&w->codes, n);
+    if (e == hipSuccess) e = hipMalloc((void **)&w->raw_e4m3, n);
+    if (e == hipSuccess) e = hipMalloc((void **)&w->scales, ns * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&count, sizeof(*count));
+    if (e != hipSuccess) {
+        if (count) (void)hipFree(count);
+        free_weight(w);
+        return hip_fail(e, "quantize_fp8_ref alloc");
+    }
+    w->device_bytes = n + ns * 4;
+    // The reference's codes go to raw_e4m3 (what dequantize and export read);
+    // the GEMMs read the canonical copy.
+    unsigned long long changed = 0;
+    int rc = run(ctx, "quantize_fp8_ref", [&] {
+        (void)hipMemsetAsync(count, 0, sizeof(*count), ctx->stream);
+        launch_quantize_fp8_ref(ctx->stream, (const float *)src->ptr, rows, cols, group, w->raw_e4m3, w->scales);
+        launch_fp8_canon(ctx->stream, w->raw_e4m3, (uint8_t *)w->codes, n, count);
+    });
+    if (!rc) {
+        hipError_t e2 = hipMemcpyAsync(&changed, count, sizeof(changed), hipMemcpyDeviceToHost, ctx->stream);
+        if (e2 == hipSuccess) e2 = hipStreamSynchronize(ctx->stream);
+        if (e2 != hipSuccess) rc = hip_fail(e2, "quantize_fp8_ref count");
+    }
+    (void)hipFree(count);
+    if (!rc && !changed) {  // every code is already canonical: drop the copy
+        (void)hipFree(w->raw_e4m3);
+        w->raw_e4m3 = nullptr;
+    }
+    w->canonicalized = changed;
+    if (!rc) rc = stage_scales(ctx, w);
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    *out = w;
+    return ok();
+}
+
+int lx2v_hip_weight_export(lx2v_hip_ctx *ctx, const lx2v_hip_weight *w, void *codes, size_t codes_bytes,
+                           float *scales, float *zeros) {
+    NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "weight_export")) return rc;
+    NEED(w, "weight");
+    NEED(codes, "codes");
+    const size_t n = w->rows * w->cols;
+    size_t cb = n;  // Q8, FP8: one byte per element
+    if (w->fmt == LX2V_WFMT_F32) cb = n * 4;
+    if (w->fmt == LX2V_WFMT_Q4) cb = (n + 1) / 2;
+    if (codes_bytes != cb)
+        return fail(LX2V_ERR_BAD_SHAPE, "export codes into %zu bytes, the weight has %zu", codes_bytes, cb);
+    if (w->fmt != LX2V_WFMT_F32 && !scales) return fail(LX2V_ERR_BAD_ARG, "scales is null");
+    if (w->fmt == LX2V_WFMT_Q4 && !zeros) return fail(LX2V_ERR_BAD_ARG, "zeros is null");
+    if (int rc = set_dev(ctx)) return rc;
+    const void *src = w->fmt == LX2V_WFMT_FP8 && w->raw_e4m3 ? (const void *)w->raw_e4m3 : w->codes;
+    HIP_TRY(hipMemcpyAsync(codes, src, cb, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(export codes)");
+    if (w->fmt != LX2V_WFMT_F32) {
+        const size_t ns = n / w->group;
+        HIP_TRY(hipMemcpyAsync(scales, w->scales, ns * 4, hipMemcpyDeviceToHost, ctx->stream),
+                "hipMemcpyAsync(export scales)");
+        if (w->fmt == LX2V_WFMT_Q4)
+            HIP_TRY(hipMemcpyAsync(zeros, w->zeros, ns * 4, hipMemcpyDeviceToHost, ctx->stream),
+                    "hipMemcpyAsync(export zeros)");
+    }
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(export)");
+    return ok();
+}
+
 int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std) {
     NEED(ctx, "ctx");
     NEED(buf, "buf");

@@ -122,7 +122,6 @@ void launch_fill_normal(hipStream_t s, void *dst, int dtype, size_t n, uint64_t 
 void launch_dequant(hipStream_t s, const lx2v_hip_weight *w, const uint8_t *fp8_codes, float *out);
 // Fills w->sscale / w->szero (allocated, w->spr set) from w->scales / w->zeros.
 void launch_stage_scales(hipStream_t s, const lx2v_hip_weight *w);
-void launch_fp8_canon_count(hipStream_t s, uint8_t *codes, size_t n, unsigned long long *count);
 void launch_q4_pack(hipStream_t s, const uint8_t *codes, size_t n, uint8_t *packed);
 void launch_act_quant(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols,
                       uint8_t *q, float *scale);
@@ -139,6 +138,16 @@ void launch_quantize_q4_sym(hipStream_t s, const float *src, size_t rows, size_t
                             size_t group, uint8_t *packed, float *scales, float *zeros);
 void launch_quantize_fp8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,
                          uint8_t *q, float *scales);
+
+// ---- reference-exact load-time quantizers (k_quant.hip) ------------------------
+// Fp8E4M3::quantize with quant.rs's own encoder: raw codes, exponent wrap included.
+void launch_quantize_fp8_ref(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group, uint8_t *q,
+                             float *scales);
+// codes = raw with exponent-0 non-zero codes set to signed zero; *count += replaced.
+void launch_fp8_canon(hipStream_t s, const uint8_t *raw, uint8_t *codes, size_t n, unsigned long long *count);
+// Q4::quantize (affine, optional HQQ, f16-rounded scale / zero), packed codes.
+void launch_quantize_q4_ref(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group, int hqq,
+                            uint8_t *packed, float *scales, float *zeros);
 
 // ---- GEMM launchers -----------------------------------------------------------
 // Y[m, n] = act(sum_k A[m,k] B[n,k] * scales + bias[n]); A/Y already offset to

@@ -42,6 +42,7 @@ EXPORTS = [
     "lx2v_hip_profile_kernel", "lx2v_hip_alloc_e4m3", "lx2v_hip_quantize_act", "lx2v_hip_graph_begin",
     "lx2v_hip_graph_end", "lx2v_hip_graph_launch", "lx2v_hip_graph_free", "lx2v_hip_profile_region",
     "lx2v_hip_alloc_mx", "lx2v_hip_quantize_mx", "lx2v_hip_download_mx",
+    "lx2v_hip_quantize_q4", "lx2v_hip_quantize_fp8_ref", "lx2v_hip_weight_export",
 ]
 
 
@@ -90,6 +91,9 @@ def _load():
         "lx2v_hip_quantize_q8": (ip, [vp, vp, sz, sz, sz, pp]),
         "lx2v_hip_quantize_q4_sym": (ip, [vp, vp, sz, sz, sz, pp]),
         "lx2v_hip_quantize_fp8": (ip, [vp, vp, sz, sz, sz, pp]),
+        "lx2v_hip_quantize_q4": (ip, [vp, vp, sz, sz, sz, ip, pp]),
+        "lx2v_hip_quantize_fp8_ref": (ip, [vp, vp, sz, sz, sz, pp]),
+        "lx2v_hip_weight_export": (ip, [vp, vp, vp, sz, vp, vp]),
         "lx2v_hip_fill_normal": (ip, [vp, vp, ctypes.c_uint64, ctypes.c_float]),
         "lx2v_hip_linear": (ip, [vp, vp, sz, sz, vp, vp, ip, vp, sz]),
         "lx2v_hip_act_quant": (ip, [vp, vp, sz, sz, sz, vp, vp]),
@@ -339,6 +343,44 @@ class HipBackend:
         h = ctypes.c_void_p()
         _check(lib.lx2v_hip_quantize_fp8(self.ctx, src.h, rows, cols, group, ctypes.byref(h)))
         return Weight(self, h.value)
+
+    def quantize_q4(self, src: Buf, rows: int, cols: int, group: int, hqq: bool) -> Weight:
+        """Q4::quantize (quant.rs:226-292) on the device: affine, optional HQQ, f16 scale / zero."""
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_quantize_q4(self.ctx, src.h, rows, cols, group, int(bool(hqq)), ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def quantize_fp8_ref(self, src: Buf, rows: int, cols: int, group: int) -> Weight:
+        """Fp8E4M3::quantize (quant.rs:423-447) with the reference's encoder, verbatim."""
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_quantize_fp8_ref(self.ctx, src.h, rows, cols, group, ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def weight_export(self, w: Weight) -> dict:
+        """The weight in the reference's host layouts: ``q`` (Q8 int8 [rows, cols], Q4 packed
+        uint8 [rows, cols / 2], FP8 the reference's code bytes [rows, cols], F32 values),
+        ``scales`` / ``zeros`` f32 [rows, cols / group]."""
+        i = w.info()
+        rows, cols, fmt = i["rows"], i["cols"], i["fmt"]
+        if fmt == WFMT_F32:
+            q = np.empty((rows, cols), np.float32)
+        elif fmt == WFMT_Q4:
+            q = np.empty((rows * cols + 1) // 2, np.uint8)
+        else:
+            q = np.empty((rows, cols), np.int8 if fmt == WFMT_Q8 else np.uint8)
+        ng = cols // i["group"] if fmt != WFMT_F32 else 0
+        s = np.empty((rows, ng), np.float32)
+        z = np.empty((rows, ng), np.float32)
+        _check(lib.lx2v_hip_weight_export(self.ctx, w.h, _ptr(q), q.nbytes, _ptr(s) if ng else None,
+                                          _ptr(z) if fmt == WFMT_Q4 else None))
+        if fmt == WFMT_Q4 and cols % 2 == 0:
+            q = q.reshape(rows, cols // 2)
+        out = {"fmt": fmt, "rows": rows, "cols": cols, "group": i["group"], "q": q}
+        if fmt != WFMT_F32:
+            out["scales"] = s
+        if fmt == WFMT_Q4:
+            out["zeros"] = z
+        return out
 
     def fill_normal(self, buf: Buf, seed: int, std: float):
         _check(lib.lx2v_hip_fill_normal(self.ctx, buf.h, ctypes.c_uint64(seed), ctypes.c_float(std)))
