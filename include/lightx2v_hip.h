@@ -200,6 +200,36 @@ int lx2v_hip_quantize_fp8_ref(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t
 int lx2v_hip_weight_export(lx2v_hip_ctx *ctx, const lx2v_hip_weight *w, void *codes,
                            size_t codes_bytes, float *scales, float *zeros);
 
+/* ---- the norms and residuals around the linears ---------------------------
+ * Backend::layer_norm / residual_norm / gate_residual (backend.rs:214-256,
+ * CPU reference crates/lightx2v-cpu/src/lib.rs:328-400): the producers of the
+ * block linears' inputs and the consumer of their outputs.  NormKind
+ * (backend.rs:47-52): AFFINE is LN(x) * w + b, MOD is LN(x) * (1 +
+ * mods[scale]) + mods[shift] over rows of `mods` ([slots, dim]).
+ * Extension: `out` / `normed` may be an E4M3 buffer (lx2v_hip_alloc_e4m3,
+ * cols == dim) or an MXE4M3 buffer (lx2v_hip_alloc_mx): the norm then writes
+ * the quantized activations an FP8 linear contracts, in the same pass (no
+ * separate quantize_act).  Mean and variance are summed across lanes, not
+ * sequentially. */
+enum { LX2V_NORM_AFFINE = 0, LX2V_NORM_MOD = 1 };
+typedef struct {
+    int kind;                     /* LX2V_NORM_AFFINE or LX2V_NORM_MOD */
+    const lx2v_hip_buf *w, *b;    /* AFFINE: [dim] each */
+    size_t scale, shift;          /* MOD: rows of mods */
+} lx2v_hip_norm_t;
+/* out = norm(x) over rows of width dim (backend.rs:214-225). */
+int lx2v_hip_layer_norm(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t rows, size_t dim,
+                        const lx2v_hip_norm_t *norm, const lx2v_hip_buf *mods, float eps,
+                        lx2v_hip_buf *out);
+/* In place on h: h += a * mods[gate] (has_gate) or h += a, then normed =
+ * norm(h), the norm reading the unrounded sum (backend.rs:227-241). */
+int lx2v_hip_residual_norm(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_buf *a, size_t rows,
+                           size_t dim, const lx2v_hip_buf *mods, int has_gate, size_t gate,
+                           const lx2v_hip_norm_t *norm, float eps, lx2v_hip_buf *normed);
+/* In place on h: h += a * mods[gate] (backend.rs:243-252). */
+int lx2v_hip_gate_residual(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_buf *a, size_t rows,
+                           size_t dim, const lx2v_hip_buf *mods, size_t gate);
+
 /* Synthetic data for benchmarks (Rng::normal, rng.rs:39-54, drawn per element
  * index on the device; values agree with the host Rng to libm ulps):
  * buf[i] = normal(seed)[i] * std. */
@@ -237,6 +267,9 @@ int lx2v_hip_quantize_mx(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row,
 /* Test hook: an MXE4M3 buffer's raw contents, copied to host: codes [rows,
  * cols] and E8M0 scale bytes [cols / 32, rows] (block-major). */
 int lx2v_hip_download_mx(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, uint8_t *codes, uint8_t *scales);
+/* Raw codes [rows, cols] and row scales [rows] of an E4M3 buffer (a test hook,
+ * like download_mx; plain lx2v_hip_download returns the decoded values). */
+int lx2v_hip_download_e4m3(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, uint8_t *codes, float *scales);
 
 /* ---- the op (backend.rs:198-212) ----------------------------------------- */
 

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/lightx2v_hip.h"
+
 namespace lx2v {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -45,6 +47,26 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     f32x2_t v = {a, b};
     bf16x2_t r = __builtin_convertvector(v, bf16x2_t);
     return __builtin_bit_cast(uint32_t, r);
+}
+
+// Eight elements of an F32 (two 16-byte words) or BF16 (one word) buffer as f32.
+template <int DT>
+__device__ __forceinline__ void unpack8(const u32x4 *raw, float v[8]) {
+    if (DT == LX2V_DTYPE_BF16) {
+        const u32x4 a = raw[0];
+        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            f32x4 a = __builtin_bit_cast(f32x4, raw[h]);
+            v[4 * h] = a.x, v[4 * h + 1] = a.y, v[4 * h + 2] = a.z, v[4 * h + 3] = a.w;
+        }
+    }
 }
 
 // ---- e4m3 ------------------------------------------------------------------

@@ -99,24 +99,6 @@ __global__ void k_dequant(int fmt, const void *codes, const float *scales, const
 // l, l + 64, ... of its row and keeps them in registers between the max and
 // the quantization, so the row is read from HBM once.
 
-template <int DT>
-__device__ __forceinline__ void unpack8(const u32x4 *raw, float v[8]) {
-    if (DT == LX2V_DTYPE_BF16) {
-        const u32x4 a = raw[0];
-        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            v[2 * j] = __uint_as_float(w[j] << 16);
-            v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-        }
-    } else {
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            f32x4 a = __builtin_bit_cast(f32x4, raw[h]);
-            v[4 * h] = a.x, v[4 * h + 1] = a.y, v[4 * h + 2] = a.z, v[4 * h + 3] = a.w;
-        }
-    }
-}
 
 // W waves share a row (W = 1, 2 or 4; the workgroup holds 4 / W rows); T =
 // chunks of 8 per lane, 64 * W * T * 8 >= cols, cols % 8 == 0.  Wave part p

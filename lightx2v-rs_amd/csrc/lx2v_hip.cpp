@@ -890,6 +890,114 @@ int lx2v_hip_weight_export(lx2v_hip_ctx *ctx, const lx2v_hip_weight *w, void *co
     return ok();
 }
 
+// ---- norms and residuals around the linears --------------------------------------
+
+// `dim` f32 values of parameter buffer b from element off: an F32 buffer in
+// place, a BF16 one converted into staging slot `slot` (3 slots of dim).
+static int param_f32(lx2v_hip_ctx *ctx, const lx2v_hip_buf *b, size_t off, size_t dim, int slot, const float **out,
+                     const char *what) {
+    if (!b) return fail(LX2V_ERR_BAD_ARG, "%s: buffer is null", what);
+    if (b->quantized()) return fail(LX2V_ERR_BAD_ARG, "%s: an F32 or BF16 buffer is needed", what);
+    if (off + dim < off || off + dim > b->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "%s: elements [%zu, +%zu) of a buffer of %zu", what, off, dim, b->len);
+    if (b->dtype == LX2V_DTYPE_F32) {
+        *out = (const float *)b->ptr + off;
+        return LX2V_OK;
+    }
+    void *st;
+    if (int rc = stage_for(ctx, 3 * dim * 4, &st)) return rc;
+    float *dst = (float *)st + (size_t)slot * dim;
+    if (int rc = run(ctx, "convert", [&] {
+            launch_convert(ctx->stream, (const uint16_t *)b->ptr + off, LX2V_DTYPE_BF16, dst, LX2V_DTYPE_F32, dim);
+        }))
+        return rc;
+    *out = dst;
+    return LX2V_OK;
+}
+
+// Shared body of layer_norm / residual_norm: x (h), a (null for layer_norm).
+static int norm_common(lx2v_hip_ctx *ctx, lx2v_hip_buf *x, const lx2v_hip_buf *a, size_t rows, size_t dim,
+                       const lx2v_hip_buf *mods, const size_t *gate, const lx2v_hip_norm_t *norm, float eps,
+                       lx2v_hip_buf *out, const char *what) {
+    NEED(ctx, "ctx");
+    NEED(x, "x");
+    NEED(norm, "norm");
+    NEED(out, "out");
+    if (x->quantized() || (a && a->quantized()))
+        return fail(LX2V_ERR_BAD_ARG, "%s reads F32 or BF16 activations", what);
+    if (a && a->dtype != x->dtype) return fail(LX2V_ERR_BAD_ARG, "%s: h and a differ in dtype", what);
+    if (dim && rows > x->len / dim) return fail(LX2V_ERR_BAD_SHAPE, "%s: %zux%zu rows, buffer has %zu", what, rows, dim, x->len);
+    if (a && dim && rows > a->len / dim) return fail(LX2V_ERR_BAD_SHAPE, "%s: a has %zu elements", what, a->len);
+    if (norm->kind != LX2V_NORM_AFFINE && norm->kind != LX2V_NORM_MOD)
+        return fail(LX2V_ERR_BAD_ARG, "%s: unknown norm kind %d", what, norm->kind);
+    const bool q = out->dtype == LX2V_DTYPE_E4M3 || out->dtype == LX2V_DTYPE_MXE4M3;
+    if (q) {
+        if (out->cols != dim || rows > out->rows)
+            return fail(LX2V_ERR_BAD_SHAPE, "%s: %zux%zu into a quantized buffer of %zux%zu", what, rows, dim, out->rows,
+                        out->cols);
+    } else if (dim && rows > out->len / dim) {
+        return fail(LX2V_ERR_BAD_SHAPE, "%s: out has %zu elements, %zux%zu needed", what, out->len, rows, dim);
+    }
+    const size_t n = rows * dim;
+    if (overlap(out->ptr, std::max<size_t>(out->bytes(), 1), x->ptr, n * x->elem_bytes()) ||
+        (a && overlap(out->ptr, std::max<size_t>(out->bytes(), 1), a->ptr, n * a->elem_bytes())) ||
+        (mods && overlap(out->ptr, std::max<size_t>(out->bytes(), 1), mods->ptr, mods->bytes())))
+        return fail(LX2V_ERR_ALIAS, "%s: out overlaps an input", what);
+    if (a && overlap(x->ptr, n * x->elem_bytes(), a->ptr, n * a->elem_bytes()))
+        return fail(LX2V_ERR_ALIAS, "%s: h overlaps a", what);
+    if (!n) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    const float *g = nullptr, *pm = nullptr, *pa = nullptr;
+    if (gate) {
+        if (int rc = param_f32(ctx, mods, *gate * dim, dim, 0, &g, "mods (gate)")) return rc;
+    }
+    if (norm->kind == LX2V_NORM_MOD) {
+        if (int rc = param_f32(ctx, mods, norm->scale * dim, dim, 1, &pm, "mods (scale)")) return rc;
+        if (int rc = param_f32(ctx, mods, norm->shift * dim, dim, 2, &pa, "mods (shift)")) return rc;
+    } else {
+        if (int rc = param_f32(ctx, norm->w, 0, dim, 1, &pm, "norm w")) return rc;
+        if (int rc = param_f32(ctx, norm->b, 0, dim, 2, &pa, "norm b")) return rc;
+    }
+    return run(ctx, a ? "residual_norm" : "layer_norm", [&] {
+        launch_norm(ctx->stream, x->ptr, a ? a->ptr : nullptr, x->dtype, g, pm, pa, norm->kind == LX2V_NORM_MOD, eps,
+                    rows, dim, out->ptr, out->dtype, out->dtype == LX2V_DTYPE_E4M3 ? out->scales : nullptr,
+                    out->dtype == LX2V_DTYPE_MXE4M3 ? out->mxs : nullptr, out->srows);
+    });
+}
+
+int lx2v_hip_layer_norm(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t rows, size_t dim,
+                        const lx2v_hip_norm_t *norm, const lx2v_hip_buf *mods, float eps, lx2v_hip_buf *out) {
+    return norm_common(ctx, const_cast<lx2v_hip_buf *>(x), nullptr, rows, dim, mods, nullptr, norm, eps, out,
+                       "layer_norm");
+}
+
+int lx2v_hip_residual_norm(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_buf *a, size_t rows, size_t dim,
+                           const lx2v_hip_buf *mods, int has_gate, size_t gate, const lx2v_hip_norm_t *norm, float eps,
+                           lx2v_hip_buf *normed) {
+    NEED(a, "a");
+    return norm_common(ctx, h, a, rows, dim, mods, has_gate ? &gate : nullptr, norm, eps, normed, "residual_norm");
+}
+
+int lx2v_hip_gate_residual(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_buf *a, size_t rows, size_t dim,
+                           const lx2v_hip_buf *mods, size_t gate) {
+    NEED(ctx, "ctx");
+    NEED(h, "h");
+    NEED(a, "a");
+    if (h->quantized() || a->quantized() || h->dtype != a->dtype)
+        return fail(LX2V_ERR_BAD_ARG, "gate_residual reads h and a of one F32 or BF16 dtype");
+    if (dim && (rows > h->len / dim || rows > a->len / dim))
+        return fail(LX2V_ERR_BAD_SHAPE, "gate_residual: %zux%zu, h has %zu, a %zu elements", rows, dim, h->len, a->len);
+    const size_t n = rows * dim;
+    if (overlap(h->ptr, n * h->elem_bytes(), a->ptr, n * a->elem_bytes()))
+        return fail(LX2V_ERR_ALIAS, "gate_residual: h overlaps a");
+    if (!n) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    const float *g = nullptr;
+    if (int rc = param_f32(ctx, mods, gate * dim, dim, 0, &g, "mods (gate)")) return rc;
+    return run(ctx, "gate_residual",
+               [&] { launch_gate_residual(ctx->stream, h->ptr, a->ptr, h->dtype, g, rows, dim); });
+}
+
 int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std) {
     NEED(ctx, "ctx");
     NEED(buf, "buf");
@@ -994,6 +1102,25 @@ int lx2v_hip_download_mx(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, uint8_t *co
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(download_mx)");
     for (size_t b = 0; b < buf->cols / 32; b++)
         for (size_t r = 0; r < buf->rows; r++) scales[b * buf->rows + r] = raw[mx_sidx(r, b, buf->srows)];
+    return ok();
+}
+
+int lx2v_hip_download_e4m3(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, uint8_t *codes, float *scales) {
+    NEED(ctx, "ctx");
+    NEED(buf, "buf");
+    if (buf->dtype != LX2V_DTYPE_E4M3) return fail(LX2V_ERR_BAD_ARG, "download_e4m3 reads an E4M3 buffer");
+    if (buf->len) {
+        NEED(codes, "codes");
+        NEED(scales, "scales");
+    }
+    if (int rc = not_capturing(ctx, "download_e4m3")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    if (buf->len) {
+        HIP_TRY(hipMemcpyAsync(codes, buf->ptr, buf->len, hipMemcpyDeviceToHost, ctx->stream), "download_e4m3 codes");
+        HIP_TRY(hipMemcpyAsync(scales, buf->scales, buf->rows * 4, hipMemcpyDeviceToHost, ctx->stream),
+                "download_e4m3 scales");
+    }
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(download_e4m3)");
     return ok();
 }
 

@@ -139,6 +139,18 @@ void launch_quantize_q4_sym(hipStream_t s, const float *src, size_t rows, size_t
 void launch_quantize_fp8(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group,
                          uint8_t *q, float *scales);
 
+// ---- norms and residuals around the linears (k_norm.hip) ----------------------
+// out = norm(x) (a == null) or, with a: x += a * gate (gate null: 1), out =
+// norm(x); norm = (v - mean) * rsqrt(var + eps) * (mod ? 1 + pm : pm) + pa.
+// x / a of dtype dt (F32 / BF16); pm, pa, gate f32 [dim]; out of dtype od:
+// F32 / BF16 values, E4M3 codes (+ oscale [rows]) or MXE4M3 codes (+ omx
+// block scales, mx_sidx layout with srows).
+void launch_norm(hipStream_t s, void *x, const void *a, int dt, const float *gate, const float *pm, const float *pa,
+                 int mod, float eps, size_t rows, size_t dim, void *out, int od, float *oscale, uint8_t *omx,
+                 size_t srows);
+// h += a * g[column] over rows x dim (h, a of dtype dt).
+void launch_gate_residual(hipStream_t s, void *h, const void *a, int dt, const float *g, size_t rows, size_t dim);
+
 // ---- reference-exact load-time quantizers (k_quant.hip) ------------------------
 // Fp8E4M3::quantize with quant.rs's own encoder: raw codes, exponent wrap included.
 void launch_quantize_fp8_ref(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group, uint8_t *q,

@@ -43,6 +43,7 @@ EXPORTS = [
     "lx2v_hip_graph_end", "lx2v_hip_graph_launch", "lx2v_hip_graph_free", "lx2v_hip_profile_region",
     "lx2v_hip_alloc_mx", "lx2v_hip_quantize_mx", "lx2v_hip_download_mx",
     "lx2v_hip_quantize_q4", "lx2v_hip_quantize_fp8_ref", "lx2v_hip_weight_export",
+    "lx2v_hip_layer_norm", "lx2v_hip_residual_norm", "lx2v_hip_gate_residual", "lx2v_hip_download_e4m3",
 ]
 
 
@@ -50,6 +51,34 @@ class HipError(RuntimeError):
     def __init__(self, status: int, msg: str):
         super().__init__(f"lightx2v-hip status {status}: {msg}")
         self.status = status
+
+
+NORM_AFFINE, NORM_MOD = 0, 1
+
+
+class _Norm(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("w", ctypes.c_void_p), ("b", ctypes.c_void_p),
+                ("scale", ctypes.c_size_t), ("shift", ctypes.c_size_t)]
+
+
+class NormKind:
+    """``NormKind`` (backend.rs:47-52): ``affine(w, b)`` is LN(x) * w + b,
+    ``mod(scale, shift)`` is LN(x) * (1 + mods[scale]) + mods[shift]."""
+
+    def __init__(self, kind: int, w=None, b=None, scale: int = 0, shift: int = 0):
+        self.kind, self.w, self.b, self.scale, self.shift = kind, w, b, scale, shift
+
+    @staticmethod
+    def affine(w: "Buf", b: "Buf") -> "NormKind":
+        return NormKind(NORM_AFFINE, w=w, b=b)
+
+    @staticmethod
+    def mod(scale: int, shift: int) -> "NormKind":
+        return NormKind(NORM_MOD, scale=scale, shift=shift)
+
+    def _c(self) -> _Norm:
+        return _Norm(self.kind, self.w.h if self.w is not None else None, self.b.h if self.b is not None else None,
+                     self.scale, self.shift)
 
 
 class _WeightInfo(ctypes.Structure):
@@ -94,6 +123,10 @@ def _load():
         "lx2v_hip_quantize_q4": (ip, [vp, vp, sz, sz, sz, ip, pp]),
         "lx2v_hip_quantize_fp8_ref": (ip, [vp, vp, sz, sz, sz, pp]),
         "lx2v_hip_weight_export": (ip, [vp, vp, vp, sz, vp, vp]),
+        "lx2v_hip_layer_norm": (ip, [vp, vp, sz, sz, ctypes.POINTER(_Norm), vp, ctypes.c_float, vp]),
+        "lx2v_hip_residual_norm": (ip, [vp, vp, vp, sz, sz, vp, ip, sz, ctypes.POINTER(_Norm), ctypes.c_float,
+                                        vp]),
+        "lx2v_hip_gate_residual": (ip, [vp, vp, vp, sz, sz, vp, sz]),
         "lx2v_hip_fill_normal": (ip, [vp, vp, ctypes.c_uint64, ctypes.c_float]),
         "lx2v_hip_linear": (ip, [vp, vp, sz, sz, vp, vp, ip, vp, sz]),
         "lx2v_hip_act_quant": (ip, [vp, vp, sz, sz, sz, vp, vp]),
@@ -108,6 +141,7 @@ def _load():
         "lx2v_hip_alloc_mx": (ip, [vp, sz, sz, pp]),
         "lx2v_hip_quantize_mx": (ip, [vp, vp, sz, sz, vp]),
         "lx2v_hip_download_mx": (ip, [vp, vp, vp, vp]),
+        "lx2v_hip_download_e4m3": (ip, [vp, vp, vp, vp]),
         "lx2v_hip_graph_begin": (ip, [vp]),
         "lx2v_hip_graph_end": (ip, [vp, pp]),
         "lx2v_hip_graph_launch": (ip, [vp, vp]),
@@ -390,6 +424,25 @@ class HipBackend:
         _check(lib.lx2v_hip_linear(self.ctx, x.h, x_row, rows, w.h, bias.h if bias else None, act, y.h,
                                    y_row))
 
+    # ---- backend.rs:214-252: the norms around the linears ----
+    def layer_norm(self, x: Buf, rows: int, dim: int, norm: NormKind, mods: Optional[Buf], eps: float, out: Buf):
+        """out = norm(x); ``out`` may be E4M3 / MXE4M3 (the next FP8 linear's input)."""
+        n = norm._c()
+        _check(lib.lx2v_hip_layer_norm(self.ctx, x.h, rows, dim, ctypes.byref(n), mods.h if mods else None,
+                                       ctypes.c_float(eps), out.h))
+
+    def residual_norm(self, h: Buf, a: Buf, rows: int, dim: int, mods: Optional[Buf], gate: Optional[int],
+                      norm: NormKind, eps: float, normed: Buf):
+        """h += a * mods[gate] (gate None: h += a), then normed = norm(h)."""
+        n = norm._c()
+        _check(lib.lx2v_hip_residual_norm(self.ctx, h.h, a.h, rows, dim, mods.h if mods else None,
+                                          int(gate is not None), gate or 0, ctypes.byref(n), ctypes.c_float(eps),
+                                          normed.h))
+
+    def gate_residual(self, h: Buf, a: Buf, rows: int, dim: int, mods: Buf, gate: int):
+        """h += a * mods[gate]."""
+        _check(lib.lx2v_hip_gate_residual(self.ctx, h.h, a.h, rows, dim, mods.h, gate))
+
     def act_quant(self, x: Buf, x_row: int, rows: int, cols: int):
         q = np.empty((rows, cols), np.uint8)
         s = np.empty(rows, np.float32)
@@ -419,6 +472,13 @@ class HipBackend:
         q = np.empty((rows, cols), np.uint8)
         s = np.empty((cols // 32, rows), np.uint8)
         _check(lib.lx2v_hip_download_mx(self.ctx, buf.h, _ptr(q), _ptr(s)))
+        return q, s
+
+    def download_e4m3(self, buf: Buf, rows: int, cols: int):
+        """Raw codes [rows, cols] and row scales [rows] of an E4M3 buffer."""
+        q = np.empty((rows, cols), np.uint8)
+        s = np.empty(rows, np.float32)
+        _check(lib.lx2v_hip_download_e4m3(self.ctx, buf.h, _ptr(q), _ptr(s)))
         return q, s
 
     def graph_begin(self):

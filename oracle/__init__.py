@@ -297,6 +297,48 @@ def linear_f64(x: np.ndarray, w: np.ndarray, bias) -> np.ndarray:
     return y
 
 
+# ---- norms around the linears ------------------------------------------------
+
+def _fp(a):
+    return None if a is None else _p(np.ascontiguousarray(a, np.float32), _f32p)
+
+
+def layer_norm(x: np.ndarray, kind: int, w=None, b=None, mods=None, scale: int = 0, shift: int = 0,
+               eps: float = 1e-6) -> np.ndarray:
+    """crates/lightx2v-cpu/src/lib.rs:328-361; kind 0 Affine (w, b), 1 Mod (mods rows scale, shift)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, dim = x.shape
+    keep = [np.ascontiguousarray(v, np.float32) if v is not None else None for v in (w, b, mods)]
+    out = np.empty_like(x)
+    lib().orc_layer_norm(_p(x, _f32p), _sz(rows), _sz(dim), ctypes.c_int(kind), _fp(keep[0]), _fp(keep[1]),
+                         _fp(keep[2]), _sz(scale), _sz(shift), ctypes.c_float(eps), _p(out, _f32p))
+    return out
+
+
+def residual_norm(h: np.ndarray, a: np.ndarray, mods, gate, kind: int, w=None, b=None, scale: int = 0,
+                  shift: int = 0, eps: float = 1e-6):
+    """lib.rs:363-388: returns (h after h += a * gate, normed); gate None = 1."""
+    h = np.array(h, np.float32, copy=True)
+    a = np.ascontiguousarray(a, np.float32)
+    rows, dim = h.shape
+    keep = [np.ascontiguousarray(v, np.float32) if v is not None else None for v in (w, b, mods)]
+    out = np.empty_like(h)
+    lib().orc_residual_norm(_p(h, _f32p), _p(a, _f32p), _sz(rows), _sz(dim), _fp(keep[2]),
+                            ctypes.c_long(-1 if gate is None else gate), ctypes.c_int(kind), _fp(keep[0]),
+                            _fp(keep[1]), _sz(scale), _sz(shift), ctypes.c_float(eps), _p(out, _f32p))
+    return h, out
+
+
+def gate_residual(h: np.ndarray, a: np.ndarray, mods, gate: int) -> np.ndarray:
+    """lib.rs:390-400: returns h + a * mods[gate]."""
+    h = np.array(h, np.float32, copy=True)
+    a = np.ascontiguousarray(a, np.float32)
+    m = np.ascontiguousarray(mods, np.float32)
+    rows, dim = h.shape
+    lib().orc_gate_residual(_p(h, _f32p), _p(a, _f32p), _sz(rows), _sz(dim), _p(m, _f32p), _sz(gate))
+    return h
+
+
 def act_quant_e4m3(x: np.ndarray):
     """Build-defined per-token e4m3 activation quantization."""
     x = np.ascontiguousarray(x, np.float32)

@@ -398,6 +398,48 @@ void orc_linear_f64(const float *x, size_t rows, const float *w, size_t n,
         }
 }
 
+/* ---- norms around the linears ---------------------------------------------- */
+
+void orc_layer_norm(const float *x, size_t rows, size_t dim, int kind, const float *w,
+                    const float *b, const float *mods, size_t scale, size_t shift, float eps,
+                    float *out) { /* crates/lightx2v-cpu/src/lib.rs:328-361 */
+    for (size_t r = 0; r < rows; r++) {
+        const float *row = x + r * dim;
+        float sum = 0.0f; /* Iterator::sum: a sequential fold */
+        for (size_t j = 0; j < dim; j++) sum += row[j];
+        const float mean = sum / (float)dim;
+        float sq = 0.0f;
+        for (size_t j = 0; j < dim; j++) {
+            const float d = row[j] - mean;
+            sq += d * d; /* powi(2) */
+        }
+        const float var = sq / (float)dim;
+        const float inv = 1.0f / sqrtf(var + eps);
+        for (size_t j = 0; j < dim; j++) {
+            const float n = (row[j] - mean) * inv;
+            out[r * dim + j] = kind == 0 ? n * w[j] + b[j]
+                                         : n * (1.0f + mods[scale * dim + j]) + mods[shift * dim + j];
+        }
+    }
+}
+
+void orc_residual_norm(float *h, const float *a, size_t rows, size_t dim, const float *mods,
+                       long gate, int kind, const float *w, const float *b, size_t scale,
+                       size_t shift, float eps, float *normed) { /* lib.rs:363-388 */
+    for (size_t r = 0; r < rows; r++)
+        for (size_t j = 0; j < dim; j++) {
+            const float gv = gate >= 0 ? mods[(size_t)gate * dim + j] : 1.0f;
+            h[r * dim + j] += a[r * dim + j] * gv;
+        }
+    orc_layer_norm(h, rows, dim, kind, w, b, mods, scale, shift, eps, normed);
+}
+
+void orc_gate_residual(float *h, const float *a, size_t rows, size_t dim, const float *mods,
+                       size_t gate) { /* lib.rs:390-400 */
+    for (size_t r = 0; r < rows; r++)
+        for (size_t j = 0; j < dim; j++) h[r * dim + j] += a[r * dim + j] * mods[gate * dim + j];
+}
+
 /* ---- activation quantization (build-defined) ----------------------------- */
 
 void orc_act_quant_e4m3(const float *x, size_t rows, size_t cols, uint8_t *q,

@@ -117,6 +117,21 @@ void orc_linear_f64(const float *x, size_t rows, const float *w, size_t n,
 void orc_act_quant_e4m3(const float *x, size_t rows, size_t cols, uint8_t *q,
                         float *s);
 
+/* ---- norms around the linears: crates/lightx2v-cpu/src/lib.rs:328-400 ----- */
+/* NormKind (backend.rs:47-52): kind 0 = Affine, LN(x) * w[j] + b[j];
+ * kind 1 = Mod, LN(x) * (1 + mods[scale*dim + j]) + mods[shift*dim + j].
+ * mean and variance are the reference's sequential f32 sums. */
+void orc_layer_norm(const float *x, size_t rows, size_t dim, int kind, const float *w,
+                    const float *b, const float *mods, size_t scale, size_t shift, float eps,
+                    float *out);                                      /* lib.rs:328-361 */
+/* h += a * (gate >= 0 ? mods[gate*dim + j] : 1), then normed = norm(h). */
+void orc_residual_norm(float *h, const float *a, size_t rows, size_t dim, const float *mods,
+                       long gate, int kind, const float *w, const float *b, size_t scale,
+                       size_t shift, float eps, float *normed);       /* lib.rs:363-388 */
+/* h += a * mods[gate*dim + j]. */
+void orc_gate_residual(float *h, const float *a, size_t rows, size_t dim, const float *mods,
+                       size_t gate);                                  /* lib.rs:390-400 */
+
 /* ---- element-wise maps of the scalar functions above over arrays ---------- */
 void orc_map_e4m3_ref(const float *v, size_t n, uint8_t *out);
 void orc_map_e4m3_canon(const float *v, size_t n, uint8_t *out);
