@@ -302,6 +302,62 @@ def main():
     log(f"bench: bf16 FFN hand-off (eager) {ms_bf16_handoff:.2f} ms/chunk")
     value = step_flops / ms / 1e9
 
+    # ---- the block's linear path with its producers and consumers ---------------
+    # (crates/lightx2v-model/src/dit.rs:590-770 minus attention and the KV
+    # cache): AdaLN layer_norm -> QKV; O -> residual_norm (gated, affine) ->
+    # cross Q; cross O -> residual_norm (mod) -> FFN up -> FFN down ->
+    # gate_residual, per layer with its own modulation table.  "unfused":
+    # the norms write bf16 and each linear quantizes its input per token;
+    # "fused": the norms write the e4m3 input directly (no quantize pass).
+    NK = H.NormKind
+    h = be.alloc(M * DIM)
+    be.fill_normal(h, 1201, 1.0)
+    normed = be.alloc(M * DIM)
+    xq_blk = be.alloc_e4m3(M, DIM)
+    lmods, lnw = [], []
+    for l in range(LAYERS):
+        md = be.alloc(6 * DIM, H.DTYPE_F32)
+        be.fill_normal(md, 1300 + l, 0.1)
+        nw, nb = be.alloc(DIM, H.DTYPE_F32), be.alloc(DIM, H.DTYPE_F32)
+        be.fill_normal(nw, 1400 + l, 0.1)
+        be.fill_normal(nb, 1500 + l, 0.1)
+        lmods.append(md)
+        lnw.append((nw, nb))
+
+    def block_path(fused):
+        def run():
+            xin = xq_blk if fused else normed
+            for _ in range(DMD):
+                for l, lw in enumerate(layers):
+                    md, (nw, nb) = lmods[l], lnw[l]
+                    be.layer_norm(h, M, DIM, NK.mod(1, 0), md, 1e-6, xin)
+                    be.linear(xin, 0, M, *lw["qkv"], 0, outs["qkv"], 0)
+                    be.linear(acts["x_o"], 0, M, *lw["o"], 0, outs["o"], 0)
+                    be.residual_norm(h, outs["o"], M, DIM, md, 2, NK.affine(nw, nb), 1e-6, xin)
+                    be.linear(xin, 0, M, *lw["q2"], 0, outs["q2"], 0)
+                    be.linear(acts["x_text"], 0, TEXT, *lw["kv2"], 0, outs["kv2"], 0)
+                    be.linear(acts["x_o2"], 0, M, *lw["o2"], 0, outs["o2"], 0)
+                    be.residual_norm(h, outs["o2"], M, DIM, md, None, NK.mod(4, 3), 1e-6, xin)
+                    be.linear(xin, 0, M, *lw["ffn1"], 1, ffn_mx, 0)
+                    be.linear(ffn_mx, 0, M, *lw["ffn2"], 0, outs["ffn2"], 0)
+                    be.gate_residual(h, outs["ffn2"], M, DIM, md, 5)
+        return run
+
+    block = {}
+    for nm, fused in (("unfused", False), ("fused", True)):
+        fn = block_path(fused)
+        ms_e = timed(fn, args.steps, args.warmup)
+        ms_g = None
+        if not args.no_graph:
+            be.graph_begin()
+            fn()
+            g = be.graph_end()
+            ms_g = timed(g.launch, args.steps, args.warmup)
+            g.free()
+        block[nm] = round(min(ms_e, ms_g) if ms_g else ms_e, 3)
+    log(f"bench: block linear path with norms: unfused {block['unfused']:.2f} ms/chunk, "
+        f"fused {block['fused']:.2f} ms/chunk")
+
     # ---- the dominant kernel alone: GEMMs on pre-quantized activations ----------
     # (the chunk's GEMMs exactly: FFN up writes the MX buffer FFN down reads;
     # the other inputs come per-token quantized; act_quant_step is the
@@ -413,6 +469,12 @@ def main():
         "ms_per_chunk_graph": round(ms_graph, 3) if ms_graph else None,
         "ms_per_chunk_bf16_ffn_handoff": round(ms_bf16_handoff, 3),
         "gemm_only_ms_per_chunk": round(gemm_ms, 3),
+        "block_path_ms_per_chunk": {
+            "unfused": block["unfused"], "fused": block["fused"],
+            "what": "the chunk's 840 linears plus their producers and consumers (layer_norm, 2 residual_norm, "
+                    "gate_residual per layer-step; attention excluded); fused = the norms write the FP8 "
+                    "linears' e4m3 inputs in the same pass",
+        },
         "act_quant_ms_per_chunk": round(region["act_quant_chunk"], 3),
         "per_gemm": per,
         "per_config": configs,
