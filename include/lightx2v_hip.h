@@ -230,6 +230,35 @@ int lx2v_hip_residual_norm(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_bu
 int lx2v_hip_gate_residual(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_buf *a, size_t rows,
                            size_t dim, const lx2v_hip_buf *mods, size_t gate);
 
+/* ---- attention (backend.rs:273-305) -----------------------------------------
+ * q [heads, sq, head_dim], k / v [heads, sk, head_dim] (F32 or BF16, one
+ * dtype); out [sq, heads*head_dim] (F32 or BF16), heads merged.  Scores
+ * q.k / sqrt(head_dim), softmax over keys; masked pairs are -inf (a query
+ * with no allowed key gives NaN, as the reference).  head_dim 64 and 128
+ * run on the bf16 MFMA (operands rounded to bf16, f32 accumulation and
+ * softmax); other head_dim up to 256 on a per-query kernel. */
+int lx2v_hip_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k,
+                       const lx2v_hip_buf *v, size_t heads, size_t sq, size_t sk, size_t head_dim,
+                       lx2v_hip_buf *out);
+/* Backend::causal_attention: mask is the host's [sq, sk] bool array (one byte
+ * per pair, nonzero = allowed) or NULL (= attention).  The mask is copied to
+ * the device on every call and the call returns once the host array may be
+ * reused; lx2v_hip_mask_upload + lx2v_hip_attention_masked keep a mask
+ * resident instead. */
+int lx2v_hip_causal_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k,
+                              const lx2v_hip_buf *v, size_t heads, size_t sq, size_t sk,
+                              size_t head_dim, const uint8_t *mask, lx2v_hip_buf *out);
+/* A mask resident in HBM with its per-tile summary (no reference counterpart:
+ * the reference passes the mask per call; the MemRoPE mask is the same for
+ * every layer of a step). */
+typedef struct lx2v_hip_mask lx2v_hip_mask;
+int lx2v_hip_mask_upload(lx2v_hip_ctx *ctx, const uint8_t *mask, size_t sq, size_t sk,
+                         lx2v_hip_mask **out);
+int lx2v_hip_mask_free(lx2v_hip_ctx *ctx, lx2v_hip_mask *mask);
+int lx2v_hip_attention_masked(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k,
+                              const lx2v_hip_buf *v, size_t heads, size_t sq, size_t sk,
+                              size_t head_dim, const lx2v_hip_mask *mask, lx2v_hip_buf *out);
+
 /* Synthetic data for benchmarks (Rng::normal, rng.rs:39-54, drawn per element
  * index on the device; values agree with the host Rng to libm ulps):
  * buf[i] = normal(seed)[i] * std. */

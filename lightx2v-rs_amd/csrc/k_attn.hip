@@ -1,0 +1,322 @@
+// k_attn.hip -- softmax attention (Backend::attention / causal_attention,
+// crates/lightx2v-core/src/backend.rs:276-305; CPU reference
+// crates/lightx2v-cpu/src/lib.rs:155-203) on the gfx950 bf16 MFMA.
+//
+//   out[q, h*d + j] = sum_k softmax_k(q.k / sqrt(d), masked) v[k, j]
+//   q [heads, sq, d], k / v [heads, sk, d], mask [sq, sk] (1 = allowed)
+//
+// k_attn_mfma (d = 64 or 128): one workgroup per (head, 128 queries), four
+// waves of 32 queries, keys in tiles of 64 through LDS, online softmax
+// (running max and sum per query, exp2 with log2(e)/sqrt(d) folded in).
+// Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (K is the A
+// operand, Q the B operand held in registers), so a lane owns one query and
+// 32 of its keys: the row max and sum take one cross-lane step.  P^T stays
+// in the registers it was computed in and is the B operand of O^T = V^T P^T;
+// the keys of each 16-key MFMA step are taken in the order the S^T layout
+// left them in the lane (4 keys of group g, then 4 of group g + 1), and V^T
+// is read from LDS in that same order, so no transpose of P is needed.
+// A per-(query tile, key tile) mask summary skips fully masked tiles and
+// reads mask bytes only in mixed ones.
+//
+// k_attn_rows: any d <= 256, one wave per (head, query), keys one at a
+// time -- the correctness path for other head sizes.
+#include "device_common.hpp"
+#include "runtime.hpp"
+
+namespace lx2v {
+
+namespace {
+
+constexpr int AQ = 128;  // queries per workgroup
+constexpr int AK = 64;   // keys per tile
+constexpr int AT = 256;  // threads per workgroup (4 waves)
+
+__device__ __forceinline__ float ld_f(const void *p, size_t i, int dt) {
+    return dt == LX2V_DTYPE_BF16 ? bf16_bits_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+}
+
+// Eight elements i .. i + 7 of an F32 or BF16 array as packed bf16 (RNE).
+template <int DT>
+__device__ __forceinline__ u32x4 ld8_bf16(const void *p, size_t i) {
+    if constexpr (DT == LX2V_DTYPE_BF16) {
+        return *(const u32x4 *)((const uint16_t *)p + i);
+    } else {
+        const f32x4 a = *(const f32x4 *)((const float *)p + i), b = *(const f32x4 *)((const float *)p + i + 4);
+        return (u32x4){pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)};
+    }
+}
+
+template <int D, int DT, int ODT>
+__global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, const void *__restrict__ K,
+                                                  const void *__restrict__ V, int heads, int sq, int sk,
+                                                  const uint8_t *__restrict__ tiles, const uint8_t *__restrict__ mask,
+                                                  float c, void *__restrict__ out) {
+    constexpr int KSTR = D * 2 + 16;   // bytes per K row in LDS (padded: conflict-free fragment reads)
+    constexpr int VSTR = AK * 2 + 16;  // bytes per V^T row (one d, 64 keys)
+    constexpr int QS = D / 16;         // 16-wide d steps of S^T
+    constexpr int DB = D / 32;         // 32-row d blocks of O^T
+    __shared__ __attribute__((aligned(16))) uint8_t ks[AK * KSTR];
+    __shared__ __attribute__((aligned(16))) uint8_t vt[D * VSTR];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l32 = lane & 31, hf = lane >> 5;
+    const int head = blockIdx.y, qt = blockIdx.x, nkt = (sk + AK - 1) / AK;
+    const int q = qt * AQ + wv * 32 + l32;  // this lane's query
+    const bool qin = q < sq;
+    const size_t qbase = ((size_t)head * sq + (qin ? q : 0)) * D;
+    const size_t kvbase = (size_t)head * sk * D;
+
+    // Q^T fragments (B operand): d 16 s + 8 hf .. + 8 of this lane's query.
+    bf16x8 qf[QS];
+#pragma unroll
+    for (int s = 0; s < QS; s++)
+        qf[s] = __builtin_bit_cast(bf16x8, qin ? ld8_bf16<DT>(Q, qbase + 16 * s + 8 * hf) : (u32x4){});
+
+    f32x16 o[DB];
+#pragma unroll
+    for (int b = 0; b < DB; b++) o[b] = (f32x16){};
+    float m = -INFINITY, lsum = 0.0f;
+
+    for (int kt = 0; kt < nkt; kt++) {
+        const int state = tiles ? tiles[(size_t)qt * nkt + kt] : 1;  // 0 none allowed, 1 all, 2 mixed
+        if (state == 0) continue;                                    // uniform over the workgroup
+        const int k0 = kt * AK;
+        __syncthreads();  // the previous tile's fragment reads are done
+        // K tile: 64 keys x D, 16-byte chunks; V^T: two keys x 8 d per item.
+#pragma unroll
+        for (int it = 0; it < AK * D / 8 / AT; it++) {
+            const int idx = it * AT + tid, key = idx / (D / 8), ch = idx % (D / 8);
+            const bool in = k0 + key < sk;
+            const u32x4 w = in ? ld8_bf16<DT>(K, kvbase + (size_t)(k0 + key) * D + 8 * ch) : (u32x4){};
+            *(u32x4 *)(ks + key * KSTR + ch * 16) = w;
+        }
+#pragma unroll
+        for (int it = 0; it < AK * D / 16 / AT; it++) {
+            const int idx = it * AT + tid, kp = idx / (D / 8), ch = idx % (D / 8);
+            const int key = 2 * kp;
+            const u32x4 a = k0 + key < sk ? ld8_bf16<DT>(V, kvbase + (size_t)(k0 + key) * D + 8 * ch) : (u32x4){};
+            const u32x4 b =
+                k0 + key + 1 < sk ? ld8_bf16<DT>(V, kvbase + (size_t)(k0 + key + 1) * D + 8 * ch) : (u32x4){};
+            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t lo = (e & 1) ? av[e / 2] >> 16 : av[e / 2] & 0xFFFFu;
+                const uint32_t hi = (e & 1) ? bv[e / 2] >> 16 : bv[e / 2] & 0xFFFFu;
+                *(uint32_t *)(vt + (8 * ch + e) * VSTR + key * 2) = lo | (hi << 16);
+            }
+        }
+        __syncthreads();
+
+        // S^T = K Q^T for keys k0 + 32 kb + (8 g + 4 hf + r), r = 0..3 in registers 4 g + r.
+        f32x16 st[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            st[kb] = (f32x16){};
+#pragma unroll
+            for (int s = 0; s < QS; s++) {
+                const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + (32 * kb + l32) * KSTR + (2 * s + hf) * 16));
+                st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb], 0, 0, 0);
+            }
+        }
+        // scale (log2 domain) and mask; keys past sk are masked, and so is
+        // every key of a query past sq only through k < sk (its output is
+        // never stored)
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * hf + (i % 4);
+                bool ok = key < sk;
+                if (state == 2 && ok && qin) ok = mask[(size_t)q * sk + key] != 0;
+                const float x = ok ? st[kb][i] * c : -INFINITY;
+                st[kb][i] = x;
+                tmax = fmaxf(tmax, x);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mn = fmaxf(m, tmax);
+        // no key allowed yet for this query: nothing to add
+        const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+        float psum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float p = mn == -INFINITY ? 0.0f : exp2f(st[kb][i] - mn);
+                st[kb][i] = p;
+                psum += p;
+            }
+        psum += __shfl_xor(psum, 32, 64);
+        lsum = lsum * alpha + psum;
+        m = mn;
+#pragma unroll
+        for (int b = 0; b < DB; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[b][i] *= alpha;
+
+        // O^T += V^T P^T, four 16-key steps: step (kb, t) takes registers
+        // 8 t .. 8 t + 7 of st[kb], i.e. keys 32 kb + 16 t + 4 hf + 0..3 and
+        // 32 kb + 16 t + 8 + 4 hf + 0..3, and V^T in the same key order.
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const f32x16 &sp = st[kb];
+                const u32x4 pw = (u32x4){pack_bf16x2(sp[8 * t + 0], sp[8 * t + 1]), pack_bf16x2(sp[8 * t + 2], sp[8 * t + 3]),
+                                         pack_bf16x2(sp[8 * t + 4], sp[8 * t + 5]), pack_bf16x2(sp[8 * t + 6], sp[8 * t + 7])};
+                const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
+                const int kk = 32 * kb + 16 * t + 4 * hf;
+#pragma unroll
+                for (int b = 0; b < DB; b++) {
+                    const uint8_t *row = vt + (32 * b + l32) * VSTR;
+                    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                    const u32x2_t lo = *(const u32x2_t *)(row + kk * 2), hi = *(const u32x2_t *)(row + (kk + 8) * 2);
+                    const bf16x8 vf = __builtin_bit_cast(bf16x8, (u32x4){lo.x, lo.y, hi.x, hi.y});
+                    o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[b], 0, 0, 0);
+                }
+            }
+    }
+
+    if (!qin) return;
+    // No allowed key: 0 / 0 = NaN, as the reference's softmax of all -inf;
+    // no key at all (sk = 0): 0, the reference's empty sum.
+    const float inv = sk == 0 ? 0.0f : 1.0f / lsum;
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int d0 = 32 * b + 8 * g + 4 * hf;
+            const size_t oi = ((size_t)q * heads + head) * D + d0;
+            const float v0 = o[b][4 * g] * inv, v1 = o[b][4 * g + 1] * inv, v2 = o[b][4 * g + 2] * inv,
+                        v3 = o[b][4 * g + 3] * inv;
+            if constexpr (ODT == LX2V_DTYPE_BF16) {
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                *(u32x2_t *)((uint16_t *)out + oi) = (u32x2_t){pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+            } else {
+                *(f32x4 *)((float *)out + oi) = (f32x4){v0, v1, v2, v3};
+            }
+        }
+}
+
+// Any head size d <= 256: one wave per (head, query), lane j owning
+// elements j, j + 64, ...; keys one at a time with an online softmax in f32.
+__global__ __launch_bounds__(AT) void k_attn_rows(const void *__restrict__ Q, const void *__restrict__ K,
+                                                  const void *__restrict__ V, int dt, int heads, int sq, int sk,
+                                                  int d, const uint8_t *__restrict__ mask, float c,
+                                                  void *__restrict__ out, int odt) {
+    const int lane = threadIdx.x & 63;
+    const size_t row = blockIdx.x * (size_t)(AT / 64) + (threadIdx.x >> 6);  // head * sq + query
+    if (row >= (size_t)heads * sq) return;
+    const int head = (int)(row / sq), q = (int)(row % sq);
+    float qv[4], acc[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int j = lane + 64 * e;
+        qv[e] = j < d ? ld_f(Q, row * d + j, dt) : 0.0f;
+        acc[e] = 0.0f;
+    }
+    float m = -INFINITY, lsum = 0.0f;
+    for (int key = 0; key < sk; key++) {
+        if (mask && !mask[(size_t)q * sk + key]) continue;
+        const size_t kb = ((size_t)head * sk + key) * d;
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int j = lane + 64 * e;
+            if (j < d) s += qv[e] * ld_f(K, kb + j, dt);
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+        const float x = s * c, mn = fmaxf(m, x), alpha = exp2f(m - mn), p = exp2f(x - mn);
+        lsum = lsum * alpha + p;
+        m = mn;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int j = lane + 64 * e;
+            acc[e] = acc[e] * alpha + (j < d ? p * ld_f(V, kb + j, dt) : 0.0f);
+        }
+    }
+    const float inv = sk == 0 ? 0.0f : 1.0f / lsum;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int j = lane + 64 * e;
+        if (j >= d) continue;
+        const size_t oi = ((size_t)q * heads + head) * d + j;
+        if (odt == LX2V_DTYPE_BF16)
+            ((uint16_t *)out)[oi] = f32_to_bf16_bits(acc[e] * inv);
+        else
+            ((float *)out)[oi] = acc[e] * inv;
+    }
+}
+
+// Mask summary per (128-query, 64-key) tile: 0 no pair allowed, 1 every
+// pair allowed, 2 mixed.  One wave per tile; pairs past sq / sk ignored.
+__global__ __launch_bounds__(AT) void k_mask_tiles(const uint8_t *__restrict__ mask, int sq, int sk, int nqt, int nkt,
+                                                   uint8_t *__restrict__ tiles) {
+    const int lane = threadIdx.x & 63;
+    const size_t t = blockIdx.x * (size_t)(AT / 64) + (threadIdx.x >> 6);
+    if (t >= (size_t)nqt * nkt) return;
+    const int qt = (int)(t / nkt), kt = (int)(t % nkt);
+    bool any = false, all = true;
+    for (int i = lane; i < AQ * AK; i += 64) {
+        const int q = qt * AQ + i / AK, k = kt * AK + i % AK;
+        if (q < sq && k < sk) {
+            const bool a = mask[(size_t)q * sk + k] != 0;
+            any |= a;
+            all &= a;
+        }
+    }
+    const bool wany = __ballot(any) != 0, wall = __ballot(!all) == 0;
+    if (lane == 0) tiles[t] = !wany ? 0 : (wall ? 1 : 2);
+}
+
+template <int D, int DT>
+void attn_mfma_od(hipStream_t s, dim3 grid, const void *q, const void *k, const void *v, int heads, int sq, int sk,
+                  const uint8_t *tiles, const uint8_t *mask, float c, void *out, int odt) {
+    if (odt == LX2V_DTYPE_BF16)
+        hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_BF16>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, tiles,
+                           mask, c, out);
+    else
+        hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_F32>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, tiles,
+                           mask, c, out);
+}
+
+}  // namespace
+
+bool attention_mfma_supported(size_t d) { return d == 64 || d == 128; }
+
+void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint8_t *tiles) {
+    const int nqt = (int)((sq + AQ - 1) / AQ), nkt = (int)((sk + AK - 1) / AK);
+    const size_t n = (size_t)nqt * nkt;
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_mask_tiles, dim3((unsigned)((n + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, mask, (int)sq,
+                       (int)sk, nqt, nkt, tiles);
+}
+
+size_t mask_tile_count(size_t sq, size_t sk) { return ((sq + AQ - 1) / AQ) * ((sk + AK - 1) / AK); }
+
+void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
+                      size_t sk, size_t d, const uint8_t *mask, const uint8_t *tiles, void *out, int odt) {
+    if (heads == 0 || sq == 0) return;
+    const float c = 1.4426950408889634f / sqrtf((float)d);  // log2(e) / sqrt(d): softmax in base 2
+    if (attention_mfma_supported(d)) {
+        const dim3 grid((unsigned)((sq + AQ - 1) / AQ), (unsigned)heads);
+        const int hq = (int)heads, iq = (int)sq, ik = (int)sk;
+        if (d == 128) {
+            if (dt == LX2V_DTYPE_BF16)
+                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, tiles, mask, c, out, odt);
+            else
+                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, tiles, mask, c, out, odt);
+        } else {
+            if (dt == LX2V_DTYPE_BF16)
+                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, tiles, mask, c, out, odt);
+            else
+                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, tiles, mask, c, out, odt);
+        }
+        return;
+    }
+    const size_t rows = heads * sq;
+    hipLaunchKernelGGL(k_attn_rows, dim3((unsigned)((rows + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, q, k, v, dt,
+                       (int)heads, (int)sq, (int)sk, (int)d, mask, c, out, odt);
+}
+
+}  // namespace lx2v

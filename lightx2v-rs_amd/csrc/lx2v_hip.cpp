@@ -96,6 +96,7 @@ int not_capturing(const lx2v_hip_ctx *ctx, const char *what) {
 // Context-owned staging buffer (one per context, grown on demand).
 struct CtxExtra {
     Stage stage;
+    Stage mask;  // causal_attention's host mask, uploaded per call, and its tile summary
 };
 
 }  // namespace
@@ -309,6 +310,7 @@ int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
     if (ctx->ws) (void)hipFree(ctx->ws);
     auto &x = extras()[ctx];
     if (x.stage.ptr) (void)hipFree(x.stage.ptr);
+    if (x.mask.ptr) (void)hipFree(x.mask.ptr);
     extras().erase(ctx);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -996,6 +998,133 @@ int lx2v_hip_gate_residual(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_bu
     if (int rc = param_f32(ctx, mods, gate * dim, dim, 0, &g, "mods (gate)")) return rc;
     return run(ctx, "gate_residual",
                [&] { launch_gate_residual(ctx->stream, h->ptr, a->ptr, h->dtype, g, rows, dim); });
+}
+
+// ---- attention ------------------------------------------------------------------
+
+struct lx2v_hip_mask {
+    uint8_t *bytes = nullptr;  // [sq, sk], then the tile summary
+    uint8_t *tiles = nullptr;
+    size_t sq = 0, sk = 0;
+};
+
+static int attn_check(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                      size_t heads, size_t sq, size_t sk, size_t d, const lx2v_hip_buf *out) {
+    NEED(ctx, "ctx");
+    NEED(q, "q");
+    NEED(k, "k");
+    NEED(v, "v");
+    NEED(out, "out");
+    if (q->quantized() || k->quantized() || v->quantized() || out->quantized())
+        return fail(LX2V_ERR_BAD_ARG, "attention reads and writes F32 or BF16 buffers");
+    if (q->dtype != k->dtype || q->dtype != v->dtype) return fail(LX2V_ERR_BAD_ARG, "attention: q, k, v differ in dtype");
+    if (d == 0 || d > 256) return fail(LX2V_ERR_UNSUPPORTED, "attention: head_dim %zu (1..256)", d);
+    if (sq >= (1u << 30) || sk >= (1u << 30) || heads >= (1u << 16))
+        return fail(LX2V_ERR_BAD_SHAPE, "attention: %zu heads, sq %zu, sk %zu too large", heads, sq, sk);
+    const size_t nq = heads * sq * d, nk = heads * sk * d;
+    if (q->len < nq || k->len < nk || v->len < nk || out->len < nq)
+        return fail(LX2V_ERR_BAD_SHAPE, "attention: q %zu / k %zu / v %zu / out %zu elements, need %zu, %zu, %zu, %zu",
+                    q->len, k->len, v->len, out->len, nq, nk, nk, nq);
+    const size_t ob = nq * out->elem_bytes();
+    if (overlap(out->ptr, ob, q->ptr, nq * q->elem_bytes()) || overlap(out->ptr, ob, k->ptr, nk * k->elem_bytes()) ||
+        overlap(out->ptr, ob, v->ptr, nk * v->elem_bytes()))
+        return fail(LX2V_ERR_ALIAS, "attention: out overlaps q, k or v");
+    return set_dev(ctx);
+}
+
+static int attn_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                    size_t heads, size_t sq, size_t sk, size_t d, const uint8_t *mask, const uint8_t *tiles,
+                    lx2v_hip_buf *out) {
+    if (!heads || !sq) return ok();
+    return run(ctx, mask ? "causal_attention" : "attention", [&] {
+        launch_attention(ctx->stream, q->ptr, k->ptr, v->ptr, q->dtype, heads, sq, sk, d, mask, tiles, out->ptr,
+                         out->dtype);
+    });
+}
+
+int lx2v_hip_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                       size_t heads, size_t sq, size_t sk, size_t head_dim, lx2v_hip_buf *out) {
+    if (int rc = attn_check(ctx, q, k, v, heads, sq, sk, head_dim, out)) return rc;
+    return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, nullptr, nullptr, out);
+}
+
+// The mask bytes and their tile summary in device memory at `base`.
+static int mask_fill(lx2v_hip_ctx *ctx, const uint8_t *host, size_t sq, size_t sk, uint8_t *base, uint8_t **tiles) {
+    const size_t nb = sq * sk;
+    *tiles = base + ((nb + 255) & ~(size_t)255);
+    HIP_TRY(hipMemcpyAsync(base, host, nb, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(mask)");
+    if (attention_mfma_supported(128))
+        return run(ctx, "mask_tiles", [&] { launch_mask_tiles(ctx->stream, base, sq, sk, *tiles); });
+    return ok();
+}
+
+static size_t mask_bytes(size_t sq, size_t sk) { return ((sq * sk + 255) & ~(size_t)255) + mask_tile_count(sq, sk); }
+
+int lx2v_hip_causal_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                              size_t heads, size_t sq, size_t sk, size_t head_dim, const uint8_t *mask,
+                              lx2v_hip_buf *out) {
+    if (!mask) return lx2v_hip_attention(ctx, q, k, v, heads, sq, sk, head_dim, out);
+    if (int rc = attn_check(ctx, q, k, v, heads, sq, sk, head_dim, out)) return rc;
+    if (int rc = not_capturing(ctx, "causal_attention with a host mask")) return rc;
+    if (!heads || !sq || !sk) return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, nullptr, nullptr, out);  // sk = 0: zeros
+    auto &mb = extras()[ctx].mask;
+    if (int rc = ensure(ctx, &mb.ptr, &mb.bytes, mask_bytes(sq, sk), "mask alloc")) return rc;
+    uint8_t *tiles;
+    if (int rc = mask_fill(ctx, mask, sq, sk, (uint8_t *)mb.ptr, &tiles)) return rc;
+    if (int rc = attn_run(ctx, q, k, v, heads, sq, sk, head_dim, (const uint8_t *)mb.ptr, tiles, out)) return rc;
+    // the host mask is the caller's again when the call returns
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(causal_attention)");
+    return ok();
+}
+
+int lx2v_hip_mask_upload(lx2v_hip_ctx *ctx, const uint8_t *mask, size_t sq, size_t sk, lx2v_hip_mask **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (sq * sk) NEED(mask, "mask");
+    if (int rc = not_capturing(ctx, "mask_upload")) return rc;
+    if (sq >= (1u << 30) || sk >= (1u << 30)) return fail(LX2V_ERR_BAD_SHAPE, "mask %zux%zu too large", sq, sk);
+    if (int rc = set_dev(ctx)) return rc;
+    auto *m = new lx2v_hip_mask;
+    m->sq = sq;
+    m->sk = sk;
+    hipError_t e = hipMalloc((void **)&m->bytes, std::max<size_t>(mask_bytes(sq, sk), 4));
+    if (e != hipSuccess) {
+        delete m;
+        return hip_fail(e, "hipMalloc(mask)");
+    }
+    int rc = sq * sk ? mask_fill(ctx, mask, sq, sk, m->bytes, &m->tiles) : LX2V_OK;
+    if (!rc) {
+        hipError_t e2 = hipStreamSynchronize(ctx->stream);
+        if (e2 != hipSuccess) rc = hip_fail(e2, "mask_upload");
+    }
+    if (rc) {
+        (void)hipFree(m->bytes);
+        delete m;
+        return rc;
+    }
+    *out = m;
+    return ok();
+}
+
+int lx2v_hip_mask_free(lx2v_hip_ctx *ctx, lx2v_hip_mask *m) {
+    NEED(ctx, "ctx");
+    if (!m) return ok();
+    if (int rc = not_capturing(ctx, "mask_free")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(mask_free)");
+    (void)hipFree(m->bytes);
+    delete m;
+    return ok();
+}
+
+int lx2v_hip_attention_masked(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                              size_t heads, size_t sq, size_t sk, size_t head_dim, const lx2v_hip_mask *mask,
+                              lx2v_hip_buf *out) {
+    if (int rc = attn_check(ctx, q, k, v, heads, sq, sk, head_dim, out)) return rc;
+    if (mask && (mask->sq != sq || mask->sk != sk))
+        return fail(LX2V_ERR_BAD_SHAPE, "attention: mask is %zux%zu, scores are %zux%zu", mask->sq, mask->sk, sq, sk);
+    return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, mask ? mask->bytes : nullptr, mask ? mask->tiles : nullptr,
+                    out);
 }
 
 int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std) {

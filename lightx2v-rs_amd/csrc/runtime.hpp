@@ -151,6 +151,16 @@ void launch_norm(hipStream_t s, void *x, const void *a, int dt, const float *gat
 // h += a * g[column] over rows x dim (h, a of dtype dt).
 void launch_gate_residual(hipStream_t s, void *h, const void *a, int dt, const float *g, size_t rows, size_t dim);
 
+// ---- attention (k_attn.hip) -------------------------------------------------------
+// out [sq, heads*d] = softmax(q k^T / sqrt(d), mask) v; q [heads, sq, d], k / v
+// [heads, sk, d] of dtype dt; mask [sq, sk] bytes or null; tiles its summary
+// (launch_mask_tiles, mask_tile_count entries) or null; out of dtype odt.
+bool attention_mfma_supported(size_t d);
+size_t mask_tile_count(size_t sq, size_t sk);
+void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint8_t *tiles);
+void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
+                      size_t sk, size_t d, const uint8_t *mask, const uint8_t *tiles, void *out, int odt);
+
 // ---- reference-exact load-time quantizers (k_quant.hip) ------------------------
 // Fp8E4M3::quantize with quant.rs's own encoder: raw codes, exponent wrap included.
 void launch_quantize_fp8_ref(hipStream_t s, const float *src, size_t rows, size_t cols, size_t group, uint8_t *q,

@@ -44,6 +44,8 @@ EXPORTS = [
     "lx2v_hip_alloc_mx", "lx2v_hip_quantize_mx", "lx2v_hip_download_mx",
     "lx2v_hip_quantize_q4", "lx2v_hip_quantize_fp8_ref", "lx2v_hip_weight_export",
     "lx2v_hip_layer_norm", "lx2v_hip_residual_norm", "lx2v_hip_gate_residual", "lx2v_hip_download_e4m3",
+    "lx2v_hip_attention", "lx2v_hip_causal_attention", "lx2v_hip_mask_upload", "lx2v_hip_mask_free",
+    "lx2v_hip_attention_masked",
 ]
 
 
@@ -127,6 +129,11 @@ def _load():
         "lx2v_hip_residual_norm": (ip, [vp, vp, vp, sz, sz, vp, ip, sz, ctypes.POINTER(_Norm), ctypes.c_float,
                                         vp]),
         "lx2v_hip_gate_residual": (ip, [vp, vp, vp, sz, sz, vp, sz]),
+        "lx2v_hip_attention": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp]),
+        "lx2v_hip_causal_attention": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),
+        "lx2v_hip_mask_upload": (ip, [vp, vp, sz, sz, pp]),
+        "lx2v_hip_mask_free": (ip, [vp, vp]),
+        "lx2v_hip_attention_masked": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),
         "lx2v_hip_fill_normal": (ip, [vp, vp, ctypes.c_uint64, ctypes.c_float]),
         "lx2v_hip_linear": (ip, [vp, vp, sz, sz, vp, vp, ip, vp, sz]),
         "lx2v_hip_act_quant": (ip, [vp, vp, sz, sz, sz, vp, vp]),
@@ -216,6 +223,24 @@ class Weight:
     def free(self):
         if self.h and self._be.ctx:
             lib.lx2v_hip_weight_free(self._be.ctx, self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Mask:
+    """A [sq, sk] attention mask resident in HBM (with its tile summary)."""
+
+    def __init__(self, be: "HipBackend", h: int, sq: int, sk: int):
+        self._be, self.h, self.sq, self.sk = be, h, sq, sk
+
+    def free(self):
+        if self.h and self._be.ctx:
+            lib.lx2v_hip_mask_free(self._be.ctx, self.h)
         self.h = None
 
     def __del__(self):
@@ -442,6 +467,31 @@ class HipBackend:
     def gate_residual(self, h: Buf, a: Buf, rows: int, dim: int, mods: Buf, gate: int):
         """h += a * mods[gate]."""
         _check(lib.lx2v_hip_gate_residual(self.ctx, h.h, a.h, rows, dim, mods.h, gate))
+
+    # ---- backend.rs:273-305: attention ----
+    def attention(self, q: Buf, k: Buf, v: Buf, heads: int, sq: int, sk: int, head_dim: int, out: Buf):
+        """q [heads, sq, d], k / v [heads, sk, d] -> out [sq, heads * d]."""
+        _check(lib.lx2v_hip_attention(self.ctx, q.h, k.h, v.h, heads, sq, sk, head_dim, out.h))
+
+    def causal_attention(self, q: Buf, k: Buf, v: Buf, heads: int, sq: int, sk: int, head_dim: int, mask,
+                         out: Buf):
+        """``mask``: host [sq, sk] bool array (True = allowed), a resident ``Mask``, or None."""
+        if isinstance(mask, Mask):
+            _check(lib.lx2v_hip_attention_masked(self.ctx, q.h, k.h, v.h, heads, sq, sk, head_dim, mask.h, out.h))
+            return
+        m = None if mask is None else np.ascontiguousarray(mask, np.uint8).ravel()
+        if m is not None and m.size != sq * sk:
+            raise HipError(ERR_BAD_SHAPE, f"mask has {m.size} entries, {sq}x{sk} expected")
+        _check(lib.lx2v_hip_causal_attention(self.ctx, q.h, k.h, v.h, heads, sq, sk, head_dim,
+                                             None if m is None else _ptr(m), out.h))
+
+    def mask_upload(self, mask, sq: int, sk: int) -> Mask:
+        m = np.ascontiguousarray(mask, np.uint8).ravel()
+        if m.size != sq * sk:
+            raise HipError(ERR_BAD_SHAPE, f"mask has {m.size} entries, {sq}x{sk} expected")
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_mask_upload(self.ctx, _ptr(m), sq, sk, ctypes.byref(h)))
+        return Mask(self, h.value, sq, sk)
 
     def act_quant(self, x: Buf, x_row: int, rows: int, cols: int):
         q = np.empty((rows, cols), np.uint8)

@@ -339,6 +339,21 @@ def gate_residual(h: np.ndarray, a: np.ndarray, mods, gate: int) -> np.ndarray:
     return h
 
 
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask=None, nthreads: int = 8) -> np.ndarray:
+    """crates/lightx2v-cpu/src/lib.rs:155-203: q [heads, sq, d], k / v [heads,
+    sk, d], mask [sq, sk] bool or None -> out [sq, heads * d]."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    heads, sq, d = q.shape
+    sk = k.shape[1]
+    m = None if mask is None else np.ascontiguousarray(mask, np.uint8)
+    out = np.empty((sq, heads * d), np.float32)
+    lib().orc_attention(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p), _sz(heads), _sz(sq), _sz(sk), _sz(d),
+                        None if m is None else _p(m, _u8p), _p(out, _f32p), ctypes.c_int(nthreads))
+    return out
+
+
 def act_quant_e4m3(x: np.ndarray):
     """Build-defined per-token e4m3 activation quantization."""
     x = np.ascontiguousarray(x, np.float32)

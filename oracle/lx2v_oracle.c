@@ -15,6 +15,7 @@
 
 #include <float.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -438,6 +439,56 @@ void orc_gate_residual(float *h, const float *a, size_t rows, size_t dim, const 
                        size_t gate) { /* lib.rs:390-400 */
     for (size_t r = 0; r < rows; r++)
         for (size_t j = 0; j < dim; j++) h[r * dim + j] += a[r * dim + j] * mods[gate * dim + j];
+}
+
+/* ---- attention ------------------------------------------------------------ */
+
+static void attention_row(const float *q, const float *k, const float *v, size_t heads, size_t sq,
+                          size_t sk, size_t d, const uint8_t *mask, float *out, size_t h,
+                          size_t qi, float *scores) { /* lib.rs:171-203, one (head, query) */
+    const float scale = 1.0f / sqrtf((float)d);
+    for (size_t ki = 0; ki < sk; ki++) {
+        if (mask && !mask[qi * sk + ki]) {
+            scores[ki] = -INFINITY;
+            continue;
+        }
+        float s = 0.0f;
+        for (size_t j = 0; j < d; j++) s += q[(h * sq + qi) * d + j] * k[(h * sk + ki) * d + j];
+        scores[ki] = s * scale;
+    }
+    /* softmax_row, lib.rs:155-166 */
+    float m = -INFINITY;
+    for (size_t ki = 0; ki < sk; ki++) m = fmaxf(m, scores[ki]); /* f32::max ignores NaN */
+    float sum = 0.0f;
+    for (size_t ki = 0; ki < sk; ki++) {
+        scores[ki] = expf(scores[ki] - m);
+        sum += scores[ki];
+    }
+    const float inv = 1.0f / sum;
+    for (size_t ki = 0; ki < sk; ki++) scores[ki] *= inv;
+    for (size_t j = 0; j < d; j++) {
+        float acc = 0.0f;
+        for (size_t ki = 0; ki < sk; ki++) acc += scores[ki] * v[(h * sk + ki) * d + j];
+        out[(qi * heads + h) * d + j] = acc;
+    }
+}
+
+void orc_attention(const float *q, const float *k, const float *v, size_t heads, size_t sq,
+                   size_t sk, size_t d, const uint8_t *mask, float *out, int nthreads) {
+    const long rows = (long)(heads * sq);
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nthreads > 1 ? nthreads : 1)
+#endif
+    {
+        float *scores = (float *)malloc((sk ? sk : 1) * sizeof(float));
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (long r = 0; r < rows; r++)
+            attention_row(q, k, v, heads, sq, sk, d, mask, out, (size_t)r / sq, (size_t)r % sq, scores);
+        free(scores);
+    }
+    (void)nthreads;
 }
 
 /* ---- activation quantization (build-defined) ----------------------------- */

@@ -132,6 +132,15 @@ void orc_residual_norm(float *h, const float *a, size_t rows, size_t dim, const 
 void orc_gate_residual(float *h, const float *a, size_t rows, size_t dim, const float *mods,
                        size_t gate);                                  /* lib.rs:390-400 */
 
+/* ---- attention: crates/lightx2v-cpu/src/lib.rs:155-203 -------------------- */
+/* q [heads, sq, d], k / v [heads, sk, d]; mask [sq, sk] (1 = allowed) or
+ * NULL; out [sq, heads*d].  scores = (q.k sequential f32) * (1/sqrtf(d)),
+ * forbidden pairs -inf; softmax_row: max fold, expf(s - m), sequential sum,
+ * multiply by 1/sum; out = sequential sum over keys of p * v.  nthreads > 1
+ * splits (head, query) rows over OpenMP threads, same per-row order. */
+void orc_attention(const float *q, const float *k, const float *v, size_t heads, size_t sq,
+                   size_t sk, size_t d, const uint8_t *mask, float *out, int nthreads);
+
 /* ---- element-wise maps of the scalar functions above over arrays ---------- */
 void orc_map_e4m3_ref(const float *v, size_t n, uint8_t *out);
 void orc_map_e4m3_canon(const float *v, size_t n, uint8_t *out);

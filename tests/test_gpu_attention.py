@@ -1,0 +1,164 @@
+"""attention / causal_attention (backend.rs:273-305) on the device against the
+oracle's restatement of the reference (crates/lightx2v-cpu/src/lib.rs:155-203).
+
+Tolerances: head_dim 64 / 128 run on the bf16 MFMA (q, k, v and the softmax
+weights P rounded to bf16, f32 accumulation and softmax): against the oracle
+on the same bf16-rounded q, k, v, rel-L2 <= 1e-2 and max-abs <= 2e-2 * max|y|
+(P's bf16 rounding is the dominant term; measured values are printed by the
+assertion on failure).  Other head sizes run the per-query f32 kernel:
+rel-L2 <= 1e-5 (only the summation order and exp2 differ).  Masks: fully
+masked tiles are skipped, mixed tiles read mask bytes; a query with no
+allowed key is NaN in both, sk = 0 gives zeros in both.
+"""
+
+import numpy as np
+import pytest
+
+import lightx2v_hip as H
+import oracle as O
+from helpers import assert_close, u32
+
+pytestmark = pytest.mark.gpu
+MFMA_TOL = (1e-2, 2e-2)
+ROWS_TOL = (1e-5, 1e-4)
+
+
+def _qkv(seed, heads, sq, sk, d):
+    rng = O.Rng(seed)
+    q = rng.normal(heads * sq * d).reshape(heads, sq, d).astype(np.float32)
+    k = rng.normal(heads * sk * d).reshape(heads, sk, d).astype(np.float32)
+    v = rng.normal(heads * sk * d).reshape(heads, sk, d).astype(np.float32)
+    return q, k, v
+
+
+def _up(be, a, dtype):
+    b = be.alloc(a.size, dtype)
+    be.write(b, a)
+    return b
+
+
+def _run(be, q, k, v, mask=None, dtype=H.DTYPE_F32, odtype=H.DTYPE_F32, resident=False):
+    heads, sq, d = q.shape
+    sk = k.shape[1]
+    qb, kb, vb = _up(be, q, dtype), _up(be, k, dtype), _up(be, v, dtype)
+    out = be.alloc(sq * heads * d, odtype)
+    if mask is None:
+        be.attention(qb, kb, vb, heads, sq, sk, d, out)
+    elif resident:
+        m = be.mask_upload(mask, sq, sk)
+        be.causal_attention(qb, kb, vb, heads, sq, sk, d, m, out)
+        m.free()
+    else:
+        be.causal_attention(qb, kb, vb, heads, sq, sk, d, mask, out)
+    return be.download(out).reshape(sq, heads * d)
+
+
+def _want(q, k, v, mask=None, bf16=True):
+    if bf16:
+        q, k, v = O.bf16_round(q), O.bf16_round(k), O.bf16_round(v)
+    return O.attention(q, k, v, mask)
+
+
+def _frame_causal(sq, sk, frame):
+    """MemRoPE-style block mask: query frame i sees key frames <= i (keys and
+    queries indexed in frames of `frame` tokens, the chunk's queries last)."""
+    qf = (np.arange(sq) + (sk - sq)) // frame
+    kf = np.arange(sk) // frame
+    return kf[None, :] <= qf[:, None]
+
+
+@pytest.mark.parametrize("heads,sq,sk,d", [(2, 128, 64, 128), (3, 77, 130, 128), (1, 300, 1000, 64),
+                                           (4, 256, 512, 128), (2, 1, 1, 128), (1, 129, 65, 64)])
+@pytest.mark.parametrize("dtype", [H.DTYPE_F32, H.DTYPE_BF16])
+def test_attention_mfma(be, heads, sq, sk, d, dtype):
+    q, k, v = _qkv(1000 + sq + sk, heads, sq, sk, d)
+    got = _run(be, q, k, v, dtype=dtype)
+    assert_close(got, _want(q, k, v), *MFMA_TOL, what=f"attention {heads}x{sq}x{sk}x{d}")
+
+
+@pytest.mark.parametrize("heads,sq,sk,d", [(2, 40, 33, 80), (1, 5, 7, 16), (3, 17, 100, 256)])
+def test_attention_other_head_dims(be, heads, sq, sk, d):
+    q, k, v = _qkv(2000 + d, heads, sq, sk, d)
+    got = _run(be, q, k, v)
+    assert_close(got, _want(q, k, v, bf16=False), *ROWS_TOL, what=f"attention d={d}")
+
+
+@pytest.mark.parametrize("d", [64, 128, 48])
+@pytest.mark.parametrize("kind", ["frames", "random", "keep_first"])
+def test_causal_attention(be, d, kind):
+    heads, sq, sk = 2, 200, 600
+    q, k, v = _qkv(3000 + d, heads, sq, sk, d)
+    if kind == "frames":
+        mask = _frame_causal(sq, sk, 100)
+    elif kind == "random":
+        mask = np.random.default_rng(5).random((sq, sk)) < 0.3
+        mask[:, 0] = True
+    else:  # one allowed key per query past the first
+        mask = np.zeros((sq, sk), bool)
+        mask[:, 0] = True
+        mask[np.arange(sq), (np.arange(sq) * 7) % sk] = True
+    got = _run(be, q, k, v, mask)
+    tol = MFMA_TOL if d in (64, 128) else ROWS_TOL
+    assert_close(got, _want(q, k, v, mask, bf16=d in (64, 128)), *tol, what=f"causal {kind} d={d}")
+    # the resident mask gives the same result, bit for bit
+    assert np.array_equal(u32(_run(be, q, k, v, mask, resident=True)), u32(got))
+
+
+def test_fully_masked_rows_and_no_keys(be):
+    heads, sq, sk, d = 1, 130, 70, 128
+    q, k, v = _qkv(4000, heads, sq, sk, d)
+    mask = np.ones((sq, sk), bool)
+    mask[5] = False
+    mask[129] = False
+    got = _run(be, q, k, v, mask)
+    want = _want(q, k, v, mask)
+    assert np.array_equal(np.isnan(got), np.isnan(want)) and np.isnan(got[5]).all() and np.isnan(got[129]).all()
+    ok = ~np.isnan(want).any(axis=1)
+    assert_close(got[ok], want[ok], *MFMA_TOL, what="partly masked")
+    # sk = 0: the reference's empty sums are 0
+    qb = _up(be, q, H.DTYPE_F32)
+    kb, vb = be.alloc(1, H.DTYPE_F32), be.alloc(1, H.DTYPE_F32)
+    out = be.alloc(sq * d, H.DTYPE_F32)
+    be.write(out, np.full(sq * d, 7.0, np.float32))
+    be.attention(qb, kb, vb, heads, sq, 0, d, out)
+    assert np.array_equal(be.download(out), np.zeros(sq * d, np.float32))
+
+
+def test_attention_bf16_out(be):
+    heads, sq, sk, d = 2, 96, 160, 128
+    q, k, v = _qkv(5000, heads, sq, sk, d)
+    y32 = _run(be, q, k, v, dtype=H.DTYPE_BF16)
+    y16 = _run(be, q, k, v, dtype=H.DTYPE_BF16, odtype=H.DTYPE_BF16)
+    assert np.array_equal(u32(y16), u32(O.bf16_round(y32)))
+
+
+def test_attention_wan_shape_sampled(be):
+    """12 heads x 128 (Wan2.1-1.3B), a 3-frame chunk of 1560-token frames
+    after one cached frame, frame-causal mask; 96 sampled query rows."""
+    heads, d, frame = 12, 128, 1560
+    sq, sk = 3 * frame, 4 * frame
+    q, k, v = _qkv(6000, heads, sq, sk, d)
+    mask = _frame_causal(sq, sk, frame)
+    got = _run(be, q, k, v, mask, dtype=H.DTYPE_BF16)
+    rows = np.linspace(0, sq - 1, 96).astype(int)
+    want = O.attention(O.bf16_round(q[:, rows]), O.bf16_round(k), O.bf16_round(v), mask[rows])
+    assert_close(got[rows], want, *MFMA_TOL, what="wan shape")
+
+
+def test_attention_errors(be):
+    heads, sq, sk, d = 1, 8, 8, 64
+    q, k, v = _qkv(7000, heads, sq, sk, d)
+    qb, kb, vb = _up(be, q, H.DTYPE_F32), _up(be, k, H.DTYPE_F32), _up(be, v, H.DTYPE_BF16)
+    out = be.alloc(sq * d, H.DTYPE_F32)
+    with pytest.raises(H.HipError):  # v in another dtype
+        be.attention(qb, kb, vb, heads, sq, sk, d, out)
+    vb = _up(be, v, H.DTYPE_F32)
+    with pytest.raises(H.HipError):  # k too short for sk
+        be.attention(qb, kb, vb, heads, sq, sk + 1, d, out)
+    with pytest.raises(H.HipError):  # out aliases q
+        be.attention(qb, kb, vb, heads, sq, sk, d, qb)
+    with pytest.raises(H.HipError):  # head_dim past 256
+        be.attention(qb, kb, vb, 1, 1, 1, 300, out)
+    m = be.mask_upload(np.ones((sq, sk), bool), sq, sk)
+    with pytest.raises(H.HipError):  # resident mask of another shape
+        be.causal_attention(qb, kb, vb, heads, sq - 1, sk, d, m, out)
