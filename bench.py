@@ -418,6 +418,38 @@ def main():
                      "tflops": round(2.0 * rows * n * k / (us * 1e-6) / 1e12, 1),
                      "pct_fp8_peak": round(2.0 * rows * n * k / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS * 100, 1)}
 
+    # ---- causal attention at the chunk's shape (not part of the linear metric) ----
+    # 12 heads x 128, the 3-frame chunk's 4680 queries against one cached
+    # 1560-token frame plus the chunk (6240 keys), frame-causal MemRoPE-style
+    # mask resident on the device (crates/lightx2v-model/src/dit.rs:655-668).
+    import numpy as np
+    heads, hd, frame = DIM // 128, 128, 1560
+    sk = M + frame
+    qf = (np.arange(M) + frame) // frame
+    kf = np.arange(sk) // frame
+    amask = kf[None, :] <= qf[:, None]
+    aq, ak, av = be.alloc(heads * M * hd), be.alloc(heads * sk * hd), be.alloc(heads * sk * hd)
+    for i, bb in enumerate((aq, ak, av)):
+        be.fill_normal(bb, 1600 + i, 1.0)
+    aout = be.alloc(M * heads * hd)
+    am = be.mask_upload(amask, M, sk)
+    be.causal_attention(aq, ak, av, heads, M, sk, hd, am, aout)
+    be.profile_region("attn", True)
+    for _ in range(20):
+        be.causal_attention(aq, ak, av, heads, M, sk, hd, am, aout)
+    be.profile_region("attn", False)
+    attn_us = be.profile_kernel("attn")[1] * 1e3 / 20
+    pairs = float(amask.sum()) * heads
+    attn = {"shape": f"{heads} heads x {hd}, sq {M}, sk {sk}, frame-causal mask",
+            "us": round(attn_us, 2),
+            "tflops_allowed_pairs": round(4.0 * hd * pairs / (attn_us * 1e-6) / 1e12, 1),
+            "pct_bf16_peak": round(4.0 * hd * pairs / (attn_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS * 100, 1),
+            "kernel": "k_attn_mfma (bf16 MFMA, online softmax)"}
+    log(f"bench: causal attention {attn_us:.1f} us ({attn['tflops_allowed_pairs']} TFLOP/s over allowed pairs)")
+    am.free()
+    for bb in (aq, ak, av, aout):
+        bb.free()
+
     # plain-copy calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
     cal_n = 64 << 20
     ca, cb = be.alloc(cal_n, H.DTYPE_F32), be.alloc(cal_n, H.DTYPE_F32)
@@ -477,6 +509,7 @@ def main():
         },
         "act_quant_ms_per_chunk": round(region["act_quant_chunk"], 3),
         "per_gemm": per,
+        "causal_attention": attn,
         "per_config": configs,
         "roofline": {
             "bound": "mfma",

@@ -27,9 +27,10 @@ namespace lx2v {
 
 namespace {
 
-constexpr int AQ = 128;  // queries per workgroup
+constexpr int AQ = 256;  // queries per workgroup (eight waves of 32: K / V tiles shared by 256 queries)
 constexpr int AK = 64;   // keys per tile
-constexpr int AT = 256;  // threads per workgroup (4 waves)
+constexpr int AT = 512;  // threads per workgroup
+constexpr int TROW = 2048;  // key tiles whose mask summary is staged in LDS (sk <= 131072)
 
 __device__ __forceinline__ float ld_f(const void *p, size_t i, int dt) {
     return dt == LX2V_DTYPE_BF16 ? bf16_bits_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
@@ -49,17 +50,26 @@ __device__ __forceinline__ u32x4 ld8_bf16(const void *p, size_t i) {
 template <int D, int DT, int ODT>
 __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, const void *__restrict__ K,
                                                   const void *__restrict__ V, int heads, int sq, int sk,
-                                                  const uint8_t *__restrict__ tiles, const uint8_t *__restrict__ mask,
+                                                  const uint8_t *__restrict__ tiles, const uint32_t *__restrict__ mbits,
                                                   float c, void *__restrict__ out) {
     constexpr int KSTR = D * 2 + 16;   // bytes per K row in LDS (padded: conflict-free fragment reads)
     constexpr int VSTR = AK * 2 + 16;  // bytes per V^T row (one d, 64 keys)
     constexpr int QS = D / 16;         // 16-wide d steps of S^T
     constexpr int DB = D / 32;         // 32-row d blocks of O^T
-    __shared__ __attribute__((aligned(16))) uint8_t ks[AK * KSTR];
-    __shared__ __attribute__((aligned(16))) uint8_t vt[D * VSTR];
+    // 16-byte K chunks and V chunk pairs per thread (the last round may be partial)
+    constexpr int KN = AK * D / 8, VN = AK * D / 16, KI = (KN + AT - 1) / AT, VI = (VN + AT - 1) / AT;
+    constexpr int KSZ = AK * KSTR, VSZ = D * VSTR;
+    // Two LDS buffers: tile t + 1 is written while tile t is read.
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (KSZ + VSZ)];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l32 = lane & 31, hf = lane >> 5;
-    const int head = blockIdx.y, qt = blockIdx.x, nkt = (sk + AK - 1) / AK;
+    // XCD-aware order: workgroups b, b + 8, ... run on one XCD, so give each
+    // XCD a contiguous range of (head, query tile) items -- the workgroups of
+    // a head then share its K / V in one L2.
+    const int nqt = (sq + AQ - 1) / AQ, items = nqt * heads, per_xcd = (items + 7) / 8;
+    const int b = blockIdx.x, item = (b % 8) * per_xcd + b / 8;
+    if (item >= items) return;
+    const int head = item / nqt, qt = item % nqt, nkt = (sk + AK - 1) / AK;
     const int q = qt * AQ + wv * 32 + l32;  // this lane's query
     const bool qin = q < sq;
     const size_t qbase = ((size_t)head * sq + (qin ? q : 0)) * D;
@@ -71,32 +81,83 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     for (int s = 0; s < QS; s++)
         qf[s] = __builtin_bit_cast(bf16x8, qin ? ld8_bf16<DT>(Q, qbase + 16 * s + 8 * hf) : (u32x4){});
 
+    // Q in registers before the loop: otherwise the first use of qf in every
+    // iteration waits for all loads in flight, the next tile's included.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+
     f32x16 o[DB];
 #pragma unroll
     for (int b = 0; b < DB; b++) o[b] = (f32x16){};
     float m = -INFINITY, lsum = 0.0f;
 
-    for (int kt = 0; kt < nkt; kt++) {
-        const int state = tiles ? tiles[(size_t)qt * nkt + kt] : 1;  // 0 none allowed, 1 all, 2 mixed
-        if (state == 0) continue;                                    // uniform over the workgroup
-        const int k0 = kt * AK;
-        __syncthreads();  // the previous tile's fragment reads are done
-        // K tile: 64 keys x D, 16-byte chunks; V^T: two keys x 8 d per item.
+    // This query tile's row of the mask summary, staged in LDS (a global
+    // load per tile would cost a memory latency per tile); rows longer than
+    // the stage are read from global memory.
+    // Longer rows skip the summary: every tile is then read as mixed.
+    __shared__ uint8_t trow[TROW];
+    const bool tlds = tiles && nkt <= TROW;
+    if (tlds)
+        for (int i = tid; i < nkt; i += AT) trow[i] = tiles[(size_t)qt * nkt + i];
+    __syncthreads();
+    auto tstate = [&](int kt) -> int { return !tiles ? 1 : (tlds ? (int)trow[kt] : 2); };
+    // The next key tile at or after kt with an allowed pair (uniform).
+    auto next_tile = [&](int kt) {
+        while (kt < nkt && tstate(kt) == 0) kt++;
+        return kt;
+    };
+    // Tile kt from global memory into registers: K as 16-byte chunks (key,
+    // chunk), V as chunk pairs of two consecutive keys (for V^T).  Buffer
+    // loads: keys past sk (and unused lanes, offset kOob) read zero, and
+    // every load is issued, so waits can count the loads in flight.
+    constexpr uint32_t ES = DT == LX2V_DTYPE_BF16 ? 2 : 4;
+    const auto ksrc = make_rsrc((const uint8_t *)K + kvbase * ES, (uint32_t)sk * D * ES);
+    const auto vsrc = make_rsrc((const uint8_t *)V + kvbase * ES, (uint32_t)sk * D * ES);
+    auto ld8 = [&](__amdgpu_buffer_rsrc_t r, uint32_t off, bool in) -> u32x4 {
+        if constexpr (DT == LX2V_DTYPE_BF16) {
+            return buffer_load_x4(r, in ? off * 2 : kOob);
+        } else {
+            const f32x4 a = __builtin_bit_cast(f32x4, buffer_load_x4(r, in ? off * 4 : kOob));
+            const f32x4 b = __builtin_bit_cast(f32x4, buffer_load_x4(r, in ? off * 4 + 16 : kOob));
+            return (u32x4){pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)};
+        }
+    };
+    u32x4 kr[KI], va[VI], vb[VI];
+    uint32_t mwn[2];  // mask bits of the loaded tile (mixed tiles; kOob reads 0 otherwise)
+    const uint32_t nw = ((uint32_t)sk + 31) / 32;
+    const auto msrc = make_rsrc(mbits, mbits ? (uint32_t)sq * nw * 4 : 0u);
+    auto gload = [&](int kt) {
+        const uint32_t k0 = (uint32_t)kt * AK;
+        const bool mixed = kt < nkt && tstate(kt) == 2 && qin;
 #pragma unroll
-        for (int it = 0; it < AK * D / 8 / AT; it++) {
+        for (int kb = 0; kb < 2; kb++)
+            mwn[kb] = buffer_load_x1(msrc, mixed ? ((uint32_t)q * nw + k0 / 32 + (uint32_t)kb) * 4 : kOob);
+#pragma unroll
+        for (int it = 0; it < KI; it++) {
             const int idx = it * AT + tid, key = idx / (D / 8), ch = idx % (D / 8);
-            const bool in = k0 + key < sk;
-            const u32x4 w = in ? ld8_bf16<DT>(K, kvbase + (size_t)(k0 + key) * D + 8 * ch) : (u32x4){};
-            *(u32x4 *)(ks + key * KSTR + ch * 16) = w;
+            kr[it] = ld8(ksrc, (k0 + key) * D + 8 * ch, idx < KN);
         }
 #pragma unroll
-        for (int it = 0; it < AK * D / 16 / AT; it++) {
-            const int idx = it * AT + tid, kp = idx / (D / 8), ch = idx % (D / 8);
-            const int key = 2 * kp;
-            const u32x4 a = k0 + key < sk ? ld8_bf16<DT>(V, kvbase + (size_t)(k0 + key) * D + 8 * ch) : (u32x4){};
-            const u32x4 b =
-                k0 + key + 1 < sk ? ld8_bf16<DT>(V, kvbase + (size_t)(k0 + key + 1) * D + 8 * ch) : (u32x4){};
-            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+        for (int it = 0; it < VI; it++) {
+            const int idx = it * AT + tid, key = 2 * (idx / (D / 8)), ch = idx % (D / 8);
+            va[it] = ld8(vsrc, (k0 + key) * D + 8 * ch, idx < VN);
+            vb[it] = ld8(vsrc, (k0 + key + 1) * D + 8 * ch, idx < VN);
+        }
+    };
+
+    // Registers into LDS buffer buf: K rows, and V transposed (one d per row).
+    auto lstore = [&](int buf) {
+        uint8_t *ks = lds + buf * (KSZ + VSZ), *vt = ks + KSZ;
+#pragma unroll
+        for (int it = 0; it < KI; it++) {
+            const int idx = it * AT + tid, key = idx / (D / 8), ch = idx % (D / 8);
+            if (idx < KN) *(u32x4 *)(ks + key * KSTR + ch * 16) = kr[it];
+        }
+#pragma unroll
+        for (int it = 0; it < VI; it++) {
+            const int idx = it * AT + tid, key = 2 * (idx / (D / 8)), ch = idx % (D / 8);
+            if (idx >= VN) continue;
+            const uint32_t av[4] = {va[it].x, va[it].y, va[it].z, va[it].w};
+            const uint32_t bv[4] = {vb[it].x, vb[it].y, vb[it].z, vb[it].w};
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const uint32_t lo = (e & 1) ? av[e / 2] >> 16 : av[e / 2] & 0xFFFFu;
@@ -104,7 +165,32 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                 *(uint32_t *)(vt + (8 * ch + e) * VSTR + key * 2) = lo | (hi << 16);
             }
         }
-        __syncthreads();
+    };
+
+    // Explicit vmcnt(0) after each lstore: the mask words were loaded before
+    // K / V and are complete once lstore has its operands, but the compiler
+    // cannot see that across the loop's back edge and would otherwise wait
+    // for the next tile's loads at their first use.
+    int kt = next_tile(0), buf = 0;
+    if (kt < nkt) {
+        gload(kt);
+        lstore(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    while (kt < nkt) {
+        const int state = tstate(kt);  // 1 all pairs allowed, 2 mixed
+        const int k0 = kt * AK, kn = next_tile(kt + 1);
+        // this tile's mask words, loaded with its K / V (already in registers)
+        const uint32_t mw[2] = {mwn[0], mwn[1]};
+        // The next tile's loads land while this tile is computed (kn = nkt:
+        // every load reads zero, unused).  The scheduling barriers keep them
+        // here: left alone, the compiler sinks them to their use after the
+        // MFMAs and nothing overlaps.
+        __builtin_amdgcn_sched_barrier(0);
+        gload(kn);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *ks = lds + buf * (KSZ + VSZ), *vt = ks + KSZ;
 
         // S^T = K Q^T for keys k0 + 32 kb + (8 g + 4 hf + r), r = 0..3 in registers 4 g + r.
         f32x16 st[2];
@@ -117,41 +203,62 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                 st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb], 0, 0, 0);
             }
         }
-        // scale (log2 domain) and mask; keys past sk are masked, and so is
-        // every key of a query past sq only through k < sk (its output is
-        // never stored)
+        // Scale into the log2 domain and mask.  A full tile with every pair
+        // allowed (uniform) takes no per-element test; otherwise keys past sk
+        // and, in mixed tiles, pairs whose mask bit is clear are -inf.
         float tmax = -INFINITY;
+        if (state == 1 && k0 + AK <= sk) {
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
+            for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * hf + (i % 4);
-                bool ok = key < sk;
-                if (state == 2 && ok && qin) ok = mask[(size_t)q * sk + key] != 0;
-                const float x = ok ? st[kb][i] * c : -INFINITY;
-                st[kb][i] = x;
-                tmax = fmaxf(tmax, x);
+                for (int i = 0; i < 16; i++) {
+                    st[kb][i] *= c;
+                    tmax = fmaxf(tmax, st[kb][i]);
+                }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+                // allowed keys of this 32-key block as bits (mask word, keys
+                // before sk), shifted so that register i tests a constant bit
+                const int left = sk - (k0 + 32 * kb);
+                uint32_t allow = state == 2 ? mw[kb] : ~0u;
+                allow &= left >= 32 ? ~0u : (left <= 0 ? 0u : (1u << left) - 1u);
+                allow >>= 4 * hf;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const bool ok = (allow >> (8 * (i / 4) + (i % 4))) & 1u;
+                    st[kb][i] = ok ? st[kb][i] * c : -INFINITY;
+                    tmax = fmaxf(tmax, st[kb][i]);
+                }
             }
+        }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         const float mn = fmaxf(m, tmax);
-        // no key allowed yet for this query: nothing to add
-        const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+        // With no key allowed yet (mn = -inf) every p is exp2(-inf) = 0 and o,
+        // lsum are still 0, so any finite reference works: use 0.  The raw
+        // v_exp_f32 flushes results below 2^-126 to 0 (no contribution a
+        // softmax sum in f32 could register).
+        const float mref = mn == -INFINITY ? 0.0f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m - mref);
         float psum = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float p = mn == -INFINITY ? 0.0f : exp2f(st[kb][i] - mn);
+                const float p = __builtin_amdgcn_exp2f(st[kb][i] - mref);
                 st[kb][i] = p;
                 psum += p;
             }
         psum += __shfl_xor(psum, 32, 64);
         lsum = lsum * alpha + psum;
         m = mn;
+        // rescale the output only where some query's max moved (uniform test)
+        if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-        for (int b = 0; b < DB; b++)
+            for (int b = 0; b < DB; b++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) o[b][i] *= alpha;
+                for (int i = 0; i < 16; i++) o[b][i] *= alpha;
+        }
 
         // O^T += V^T P^T, four 16-key steps: step (kb, t) takes registers
         // 8 t .. 8 t + 7 of st[kb], i.e. keys 32 kb + 16 t + 4 hf + 0..3 and
@@ -174,6 +281,12 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                     o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[b], 0, 0, 0);
                 }
             }
+        // the other buffer was last read before the previous barrier
+        if (kn < nkt) lstore(buf ^ 1);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        buf ^= 1;
+        kt = kn;
     }
 
     if (!qin) return;
@@ -269,9 +382,24 @@ __global__ __launch_bounds__(AT) void k_mask_tiles(const uint8_t *__restrict__ m
     if (lane == 0) tiles[t] = !wany ? 0 : (wall ? 1 : 2);
 }
 
+// Mask bits: word w of query q holds keys 32 w .. 32 w + 31 (bit = key % 32),
+// keys past sk clear.  One wave per (query, 64 keys).
+__global__ __launch_bounds__(AT) void k_mask_pack(const uint8_t *__restrict__ mask, int sq, int sk,
+                                                  uint32_t *__restrict__ bits) {
+    const int lane = threadIdx.x & 63;
+    const int nw = (sk + 31) / 32, nw2 = (nw + 1) / 2;
+    const size_t t = blockIdx.x * (size_t)(AT / 64) + (threadIdx.x >> 6);
+    if (t >= (size_t)sq * nw2) return;
+    const int q = (int)(t / nw2), key = (int)(t % nw2) * 64 + lane;
+    const bool a = key < sk && mask[(size_t)q * sk + key] != 0;
+    const uint64_t b = __ballot(a);
+    const int w = key / 32;
+    if ((lane & 31) == 0 && w < nw) bits[(size_t)q * nw + w] = (uint32_t)(lane ? b >> 32 : b);
+}
+
 template <int D, int DT>
 void attn_mfma_od(hipStream_t s, dim3 grid, const void *q, const void *k, const void *v, int heads, int sq, int sk,
-                  const uint8_t *tiles, const uint8_t *mask, float c, void *out, int odt) {
+                  const uint8_t *tiles, const uint32_t *mask, float c, void *out, int odt) {
     if (odt == LX2V_DTYPE_BF16)
         hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_BF16>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, tiles,
                            mask, c, out);
@@ -294,23 +422,34 @@ void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk,
 
 size_t mask_tile_count(size_t sq, size_t sk) { return ((sq + AQ - 1) / AQ) * ((sk + AK - 1) / AK); }
 
+size_t mask_word_count(size_t sq, size_t sk) { return sq * ((sk + 31) / 32); }
+
+void launch_mask_pack(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint32_t *bits) {
+    const size_t n = sq * (((sk + 31) / 32 + 1) / 2);
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_mask_pack, dim3((unsigned)((n + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, mask, (int)sq,
+                       (int)sk, bits);
+}
+
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
-                      size_t sk, size_t d, const uint8_t *mask, const uint8_t *tiles, void *out, int odt) {
+                      size_t sk, size_t d, const uint8_t *mask, const uint32_t *mbits, const uint8_t *tiles, void *out,
+                      int odt) {
     if (heads == 0 || sq == 0) return;
     const float c = 1.4426950408889634f / sqrtf((float)d);  // log2(e) / sqrt(d): softmax in base 2
     if (attention_mfma_supported(d)) {
-        const dim3 grid((unsigned)((sq + AQ - 1) / AQ), (unsigned)heads);
+        const size_t items = ((sq + AQ - 1) / AQ) * heads;
+        const dim3 grid((unsigned)(8 * ((items + 7) / 8)));
         const int hq = (int)heads, iq = (int)sq, ik = (int)sk;
         if (d == 128) {
             if (dt == LX2V_DTYPE_BF16)
-                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, tiles, mask, c, out, odt);
+                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, tiles, mbits, c, out, odt);
             else
-                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, tiles, mask, c, out, odt);
+                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, tiles, mbits, c, out, odt);
         } else {
             if (dt == LX2V_DTYPE_BF16)
-                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, tiles, mask, c, out, odt);
+                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, tiles, mbits, c, out, odt);
             else
-                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, tiles, mask, c, out, odt);
+                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, tiles, mbits, c, out, odt);
         }
         return;
     }

@@ -1003,7 +1003,8 @@ int lx2v_hip_gate_residual(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_bu
 // ---- attention ------------------------------------------------------------------
 
 struct lx2v_hip_mask {
-    uint8_t *bytes = nullptr;  // [sq, sk], then the tile summary
+    uint8_t *bytes = nullptr;  // [sq, sk], then the bits, then the tile summary
+    uint32_t *bits = nullptr;
     uint8_t *tiles = nullptr;
     size_t sq = 0, sk = 0;
 };
@@ -1021,6 +1022,8 @@ static int attn_check(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_b
     if (d == 0 || d > 256) return fail(LX2V_ERR_UNSUPPORTED, "attention: head_dim %zu (1..256)", d);
     if (sq >= (1u << 30) || sk >= (1u << 30) || heads >= (1u << 16))
         return fail(LX2V_ERR_BAD_SHAPE, "attention: %zu heads, sq %zu, sk %zu too large", heads, sq, sk);
+    if (sk * d * k->elem_bytes() >= (1ull << 31) || sq * ((sk + 31) / 32) * 4 >= (1ull << 31))
+        return fail(LX2V_ERR_BAD_SHAPE, "attention: one head's keys or the mask bits pass 2 GiB (sk %zu)", sk);
     const size_t nq = heads * sq * d, nk = heads * sk * d;
     if (q->len < nq || k->len < nk || v->len < nk || out->len < nq)
         return fail(LX2V_ERR_BAD_SHAPE, "attention: q %zu / k %zu / v %zu / out %zu elements, need %zu, %zu, %zu, %zu",
@@ -1033,32 +1036,38 @@ static int attn_check(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_b
 }
 
 static int attn_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
-                    size_t heads, size_t sq, size_t sk, size_t d, const uint8_t *mask, const uint8_t *tiles,
-                    lx2v_hip_buf *out) {
+                    size_t heads, size_t sq, size_t sk, size_t d, const lx2v_hip_mask *mask, lx2v_hip_buf *out) {
     if (!heads || !sq) return ok();
     return run(ctx, mask ? "causal_attention" : "attention", [&] {
-        launch_attention(ctx->stream, q->ptr, k->ptr, v->ptr, q->dtype, heads, sq, sk, d, mask, tiles, out->ptr,
-                         out->dtype);
+        launch_attention(ctx->stream, q->ptr, k->ptr, v->ptr, q->dtype, heads, sq, sk, d, mask ? mask->bytes : nullptr,
+                         mask ? mask->bits : nullptr, mask ? mask->tiles : nullptr, out->ptr, out->dtype);
     });
 }
 
 int lx2v_hip_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
                        size_t heads, size_t sq, size_t sk, size_t head_dim, lx2v_hip_buf *out) {
     if (int rc = attn_check(ctx, q, k, v, heads, sq, sk, head_dim, out)) return rc;
-    return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, nullptr, nullptr, out);
+    return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, nullptr, out);
 }
 
-// The mask bytes and their tile summary in device memory at `base`.
-static int mask_fill(lx2v_hip_ctx *ctx, const uint8_t *host, size_t sq, size_t sk, uint8_t *base, uint8_t **tiles) {
+// The mask bytes, bits and tile summary in device memory at `base` (mask_bytes).
+static size_t mask_bytes(size_t sq, size_t sk) {
+    return ((sq * sk + 255) & ~(size_t)255) + mask_word_count(sq, sk) * 4 + mask_tile_count(sq, sk);
+}
+
+static int mask_fill(lx2v_hip_ctx *ctx, const uint8_t *host, size_t sq, size_t sk, uint8_t *base, lx2v_hip_mask *m) {
     const size_t nb = sq * sk;
-    *tiles = base + ((nb + 255) & ~(size_t)255);
+    m->bytes = base;
+    m->bits = (uint32_t *)(base + ((nb + 255) & ~(size_t)255));
+    m->tiles = (uint8_t *)(m->bits + mask_word_count(sq, sk));
+    m->sq = sq;
+    m->sk = sk;
     HIP_TRY(hipMemcpyAsync(base, host, nb, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(mask)");
-    if (attention_mfma_supported(128))
-        return run(ctx, "mask_tiles", [&] { launch_mask_tiles(ctx->stream, base, sq, sk, *tiles); });
-    return ok();
+    return run(ctx, "mask_tiles", [&] {
+        launch_mask_pack(ctx->stream, base, sq, sk, m->bits);
+        launch_mask_tiles(ctx->stream, base, sq, sk, m->tiles);
+    });
 }
-
-static size_t mask_bytes(size_t sq, size_t sk) { return ((sq * sk + 255) & ~(size_t)255) + mask_tile_count(sq, sk); }
 
 int lx2v_hip_causal_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
                               size_t heads, size_t sq, size_t sk, size_t head_dim, const uint8_t *mask,
@@ -1066,12 +1075,12 @@ int lx2v_hip_causal_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx
     if (!mask) return lx2v_hip_attention(ctx, q, k, v, heads, sq, sk, head_dim, out);
     if (int rc = attn_check(ctx, q, k, v, heads, sq, sk, head_dim, out)) return rc;
     if (int rc = not_capturing(ctx, "causal_attention with a host mask")) return rc;
-    if (!heads || !sq || !sk) return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, nullptr, nullptr, out);  // sk = 0: zeros
+    if (!heads || !sq || !sk) return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, nullptr, out);  // sk = 0: zeros
     auto &mb = extras()[ctx].mask;
     if (int rc = ensure(ctx, &mb.ptr, &mb.bytes, mask_bytes(sq, sk), "mask alloc")) return rc;
-    uint8_t *tiles;
-    if (int rc = mask_fill(ctx, mask, sq, sk, (uint8_t *)mb.ptr, &tiles)) return rc;
-    if (int rc = attn_run(ctx, q, k, v, heads, sq, sk, head_dim, (const uint8_t *)mb.ptr, tiles, out)) return rc;
+    lx2v_hip_mask m;
+    if (int rc = mask_fill(ctx, mask, sq, sk, (uint8_t *)mb.ptr, &m)) return rc;
+    if (int rc = attn_run(ctx, q, k, v, heads, sq, sk, head_dim, &m, out)) return rc;
     // the host mask is the caller's again when the call returns
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(causal_attention)");
     return ok();
@@ -1087,12 +1096,14 @@ int lx2v_hip_mask_upload(lx2v_hip_ctx *ctx, const uint8_t *mask, size_t sq, size
     auto *m = new lx2v_hip_mask;
     m->sq = sq;
     m->sk = sk;
-    hipError_t e = hipMalloc((void **)&m->bytes, std::max<size_t>(mask_bytes(sq, sk), 4));
+    uint8_t *base = nullptr;
+    hipError_t e = hipMalloc((void **)&base, std::max<size_t>(mask_bytes(sq, sk), 4));
     if (e != hipSuccess) {
         delete m;
         return hip_fail(e, "hipMalloc(mask)");
     }
-    int rc = sq * sk ? mask_fill(ctx, mask, sq, sk, m->bytes, &m->tiles) : LX2V_OK;
+    m->bytes = base;
+    int rc = sq * sk ? mask_fill(ctx, mask, sq, sk, base, m) : LX2V_OK;
     if (!rc) {
         hipError_t e2 = hipStreamSynchronize(ctx->stream);
         if (e2 != hipSuccess) rc = hip_fail(e2, "mask_upload");
@@ -1123,8 +1134,7 @@ int lx2v_hip_attention_masked(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx
     if (int rc = attn_check(ctx, q, k, v, heads, sq, sk, head_dim, out)) return rc;
     if (mask && (mask->sq != sq || mask->sk != sk))
         return fail(LX2V_ERR_BAD_SHAPE, "attention: mask is %zux%zu, scores are %zux%zu", mask->sq, mask->sk, sq, sk);
-    return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, mask ? mask->bytes : nullptr, mask ? mask->tiles : nullptr,
-                    out);
+    return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, mask && sq * sk ? mask : nullptr, out);
 }
 
 int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std) {

@@ -155,11 +155,16 @@ void launch_gate_residual(hipStream_t s, void *h, const void *a, int dt, const f
 // out [sq, heads*d] = softmax(q k^T / sqrt(d), mask) v; q [heads, sq, d], k / v
 // [heads, sk, d] of dtype dt; mask [sq, sk] bytes or null; tiles its summary
 // (launch_mask_tiles, mask_tile_count entries) or null; out of dtype odt.
+// mbits: the mask as bits (launch_mask_pack, mask_word_count words), read by
+// the MFMA kernel in mixed tiles; the per-query kernel reads the bytes.
 bool attention_mfma_supported(size_t d);
 size_t mask_tile_count(size_t sq, size_t sk);
+size_t mask_word_count(size_t sq, size_t sk);
 void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint8_t *tiles);
+void launch_mask_pack(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint32_t *bits);
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
-                      size_t sk, size_t d, const uint8_t *mask, const uint8_t *tiles, void *out, int odt);
+                      size_t sk, size_t d, const uint8_t *mask, const uint32_t *mbits, const uint8_t *tiles, void *out,
+                      int odt);
 
 // ---- reference-exact load-time quantizers (k_quant.hip) ------------------------
 // Fp8E4M3::quantize with quant.rs's own encoder: raw codes, exponent wrap included.
