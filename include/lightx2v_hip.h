@@ -259,6 +259,57 @@ int lx2v_hip_attention_masked(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx
                               const lx2v_hip_buf *v, size_t heads, size_t sq, size_t sk,
                               size_t head_dim, const lx2v_hip_mask *mask, lx2v_hip_buf *out);
 
+/* ---- KV cache / MemRoPE (backend.rs:333-392) ---------------------------------
+ * One layer's cache: K and V rows of [heads, head_dim] in HBM (the context's
+ * activation dtype when the cache is made), with one temporal index and one
+ * slot kind per row on the host, as the reference's KvCache
+ * (crates/lightx2v-cpu/src/lib.rs:126-146).  K / V arguments are
+ * [heads, rows, head_dim], F32 or BF16.  The cache grows past its capacity
+ * as the reference's Vec does; growing, the update, kv and free are not
+ * allowed during graph capture. */
+typedef struct lx2v_hip_kv lx2v_hip_kv;
+/* SlotKind (crates/lightx2v-core/src/memrope.rs:31-37) */
+enum { LX2V_SLOT_SINK = 0, LX2V_SLOT_LONG_EMA = 1, LX2V_SLOT_SHORT_EMA = 2, LX2V_SLOT_RECENT = 3, LX2V_SLOT_NEW = 4 };
+/* The MemRopeConfig fields the update reads (config.rs:265-278); the new
+ * window is MemRopeConfig::new_frames() = 3 (config.rs:298-300). */
+typedef struct {
+    size_t cache_frames;
+    size_t sink_frames;
+    float ema_alpha_long;
+    float ema_alpha_short;
+} lx2v_hip_memrope_t;
+/* kv_cache_new (backend.rs:333-335) */
+int lx2v_hip_kv_cache_new(lx2v_hip_ctx *ctx, size_t heads, size_t head_dim, size_t capacity_tokens,
+                          lx2v_hip_kv **out);
+int lx2v_hip_kv_cache_free(lx2v_hip_ctx *ctx, lx2v_hip_kv *cache);
+/* kv_cache_append (backend.rs:337-349): rows appended as New. */
+int lx2v_hip_kv_cache_append(lx2v_hip_ctx *ctx, lx2v_hip_kv *cache, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                             size_t rows, const size_t *temporal);
+/* kv_cache_put (backend.rs:351-366): overwrite the block's own rows when the
+ * same temporal run is cached (EMA slots skipped), else append. */
+int lx2v_hip_kv_cache_put(lx2v_hip_ctx *ctx, lx2v_hip_kv *cache, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                          size_t rows, const size_t *temporal);
+/* kv_cache_len / kv_cache_temporal (backend.rs:368-372); kinds: the slot
+ * kind per row (the reference's pub KvCache::kinds, lib.rs:138-139). */
+int lx2v_hip_kv_cache_len(const lx2v_hip_kv *cache, size_t *rows);
+int lx2v_hip_kv_cache_temporal(const lx2v_hip_kv *cache, size_t *out, size_t cap);
+int lx2v_hip_kv_cache_kinds(const lx2v_hip_kv *cache, uint8_t *out, size_t cap);
+/* kv_cache_kv (backend.rs:374-375): new [heads, rows, head_dim] buffers in
+ * the cache's dtype.  _read writes into the caller's buffers instead. */
+int lx2v_hip_kv_cache_kv(lx2v_hip_ctx *ctx, const lx2v_hip_kv *cache, lx2v_hip_buf **k, lx2v_hip_buf **v);
+int lx2v_hip_kv_cache_read(lx2v_hip_ctx *ctx, const lx2v_hip_kv *cache, lx2v_hip_buf *k, lx2v_hip_buf *v);
+/* kv_cache_memrope_update (backend.rs:377-387): seed the zero EMA frames,
+ * graduate New -> Recent, fold the oldest Recent (else New) frame into the
+ * EMA slots and evict it while over cache_frames, mark the sinks. */
+int lx2v_hip_kv_cache_memrope_update(lx2v_hip_ctx *ctx, lx2v_hip_kv *cache, const lx2v_hip_memrope_t *cfg,
+                                     size_t frame_tokens);
+/* causal_attention over the whole cache in place (no reference counterpart:
+ * the reference copies the cache out with kv_cache_kv first, dit.rs:655-666).
+ * q [heads, sq, head_dim] in the cache's dtype; mask [sq, rows] resident or
+ * NULL. */
+int lx2v_hip_kv_cache_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_kv *cache, size_t heads,
+                                size_t sq, size_t head_dim, const lx2v_hip_mask *mask, lx2v_hip_buf *out);
+
 /* Synthetic data for benchmarks (Rng::normal, rng.rs:39-54, drawn per element
  * index on the device; values agree with the host Rng to libm ulps):
  * buf[i] = normal(seed)[i] * std. */

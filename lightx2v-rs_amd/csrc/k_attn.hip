@@ -49,7 +49,7 @@ __device__ __forceinline__ u32x4 ld8_bf16(const void *p, size_t i) {
 
 template <int D, int DT, int ODT>
 __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, const void *__restrict__ K,
-                                                  const void *__restrict__ V, int heads, int sq, int sk,
+                                                  const void *__restrict__ V, int heads, int sq, int sk, int kvs,
                                                   const uint8_t *__restrict__ tiles, const uint32_t *__restrict__ mbits,
                                                   float c, void *__restrict__ out) {
     constexpr int KSTR = D * 2 + 16;   // bytes per K row in LDS (padded: conflict-free fragment reads)
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     const int q = qt * AQ + wv * 32 + l32;  // this lane's query
     const bool qin = q < sq;
     const size_t qbase = ((size_t)head * sq + (qin ? q : 0)) * D;
-    const size_t kvbase = (size_t)head * sk * D;
+    const size_t kvbase = (size_t)head * kvs * D;  // kvs: rows between heads of K / V (>= sk)
 
     // Q^T fragments (B operand): d 16 s + 8 hf .. + 8 of this lane's query.
     bf16x8 qf[QS];
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
 // elements j, j + 64, ...; keys one at a time with an online softmax in f32.
 __global__ __launch_bounds__(AT) void k_attn_rows(const void *__restrict__ Q, const void *__restrict__ K,
                                                   const void *__restrict__ V, int dt, int heads, int sq, int sk,
-                                                  int d, const uint8_t *__restrict__ mask, float c,
+                                                  int kvs, int d, const uint8_t *__restrict__ mask, float c,
                                                   void *__restrict__ out, int odt) {
     const int lane = threadIdx.x & 63;
     const size_t row = blockIdx.x * (size_t)(AT / 64) + (threadIdx.x >> 6);  // head * sq + query
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(AT) void k_attn_rows(const void *__restrict__ Q, co
     float m = -INFINITY, lsum = 0.0f;
     for (int key = 0; key < sk; key++) {
         if (mask && !mask[(size_t)q * sk + key]) continue;
-        const size_t kb = ((size_t)head * sk + key) * d;
+        const size_t kb = ((size_t)head * kvs + key) * d;
         float s = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -399,13 +399,13 @@ __global__ __launch_bounds__(AT) void k_mask_pack(const uint8_t *__restrict__ ma
 
 template <int D, int DT>
 void attn_mfma_od(hipStream_t s, dim3 grid, const void *q, const void *k, const void *v, int heads, int sq, int sk,
-                  const uint8_t *tiles, const uint32_t *mask, float c, void *out, int odt) {
+                  int kvs, const uint8_t *tiles, const uint32_t *mask, float c, void *out, int odt) {
     if (odt == LX2V_DTYPE_BF16)
-        hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_BF16>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, tiles,
-                           mask, c, out);
+        hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_BF16>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
+                           tiles, mask, c, out);
     else
-        hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_F32>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, tiles,
-                           mask, c, out);
+        hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_F32>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
+                           tiles, mask, c, out);
 }
 
 }  // namespace
@@ -432,30 +432,30 @@ void launch_mask_pack(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, 
 }
 
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
-                      size_t sk, size_t d, const uint8_t *mask, const uint32_t *mbits, const uint8_t *tiles, void *out,
-                      int odt) {
+                      size_t sk, size_t kvs, size_t d, const uint8_t *mask, const uint32_t *mbits,
+                      const uint8_t *tiles, void *out, int odt) {
     if (heads == 0 || sq == 0) return;
     const float c = 1.4426950408889634f / sqrtf((float)d);  // log2(e) / sqrt(d): softmax in base 2
     if (attention_mfma_supported(d)) {
         const size_t items = ((sq + AQ - 1) / AQ) * heads;
         const dim3 grid((unsigned)(8 * ((items + 7) / 8)));
-        const int hq = (int)heads, iq = (int)sq, ik = (int)sk;
+        const int hq = (int)heads, iq = (int)sq, ik = (int)sk, is = (int)kvs;
         if (d == 128) {
             if (dt == LX2V_DTYPE_BF16)
-                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, tiles, mbits, c, out, odt);
+                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt);
             else
-                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, tiles, mbits, c, out, odt);
+                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt);
         } else {
             if (dt == LX2V_DTYPE_BF16)
-                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, tiles, mbits, c, out, odt);
+                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt);
             else
-                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, tiles, mbits, c, out, odt);
+                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt);
         }
         return;
     }
     const size_t rows = heads * sq;
     hipLaunchKernelGGL(k_attn_rows, dim3((unsigned)((rows + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, q, k, v, dt,
-                       (int)heads, (int)sq, (int)sk, (int)d, mask, c, out, odt);
+                       (int)heads, (int)sq, (int)sk, (int)kvs, (int)d, mask, c, out, odt);
 }
 
 }  // namespace lx2v

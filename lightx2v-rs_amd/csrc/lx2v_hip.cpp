@@ -97,6 +97,7 @@ int not_capturing(const lx2v_hip_ctx *ctx, const char *what) {
 struct CtxExtra {
     Stage stage;
     Stage mask;  // causal_attention's host mask, uploaded per call, and its tile summary
+    Stage kv_spare;  // the MemRoPE update's output layout, swapped with the cache it updates
 };
 
 }  // namespace
@@ -311,6 +312,7 @@ int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
     auto &x = extras()[ctx];
     if (x.stage.ptr) (void)hipFree(x.stage.ptr);
     if (x.mask.ptr) (void)hipFree(x.mask.ptr);
+    if (x.kv_spare.ptr) (void)hipFree(x.kv_spare.ptr);
     extras().erase(ctx);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -1039,8 +1041,9 @@ static int attn_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf
                     size_t heads, size_t sq, size_t sk, size_t d, const lx2v_hip_mask *mask, lx2v_hip_buf *out) {
     if (!heads || !sq) return ok();
     return run(ctx, mask ? "causal_attention" : "attention", [&] {
-        launch_attention(ctx->stream, q->ptr, k->ptr, v->ptr, q->dtype, heads, sq, sk, d, mask ? mask->bytes : nullptr,
-                         mask ? mask->bits : nullptr, mask ? mask->tiles : nullptr, out->ptr, out->dtype);
+        launch_attention(ctx->stream, q->ptr, k->ptr, v->ptr, q->dtype, heads, sq, sk, sk, d,
+                         mask ? mask->bytes : nullptr, mask ? mask->bits : nullptr, mask ? mask->tiles : nullptr,
+                         out->ptr, out->dtype);
     });
 }
 
@@ -1135,6 +1138,385 @@ int lx2v_hip_attention_masked(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx
     if (mask && (mask->sq != sq || mask->sk != sk))
         return fail(LX2V_ERR_BAD_SHAPE, "attention: mask is %zux%zu, scores are %zux%zu", mask->sq, mask->sk, sq, sk);
     return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, mask && sq * sk ? mask : nullptr, out);
+}
+
+// ---- KV cache / MemRoPE (backend.rs:333-392) ------------------------------------
+//
+// Device: K and V as [heads, cap, d] in one allocation (K first), the
+// context's activation dtype at creation.  Host: the temporal index and slot
+// kind of every row, as the reference's KvCache (crates/lightx2v-cpu/src/
+// lib.rs:126-146); every append / overwrite / evict decision is made on them.
+
+struct lx2v_hip_kv {
+    size_t heads = 0, d = 0, cap = 0;
+    int dtype = LX2V_DTYPE_F32;
+    void *buf = nullptr;  // [2][heads][cap][d]
+    size_t bytes = 0;
+    std::vector<size_t> temporal;
+    std::vector<uint8_t> kinds;
+    // the MemRoPE plan: pinned host staging, its device copy, and the event
+    // after which the staging may be rewritten
+    int *plan_host = nullptr, *plan_dev = nullptr;
+    size_t plan_cap = 0;
+    hipEvent_t plan_done = nullptr;
+    size_t eb() const { return dtype == LX2V_DTYPE_BF16 ? 2 : 4; }
+    void *k() const { return buf; }
+    void *v() const { return (uint8_t *)buf + heads * cap * d * eb(); }
+    size_t rows() const { return temporal.size(); }
+};
+
+namespace {
+
+size_t kv_cap_of(const lx2v_hip_kv *kv, size_t bytes) { return bytes / (2 * kv->heads * kv->d * kv->eb()); }
+
+// Reallocate for at least `need` rows per head, keeping the live rows.
+int kv_grow(lx2v_hip_ctx *ctx, lx2v_hip_kv *kv, size_t need) {
+    if (need <= kv->cap) return LX2V_OK;
+    if (int rc = not_capturing(ctx, "kv_cache growth")) return rc;
+    const size_t cap = std::max(need, kv->cap + kv->cap / 2), bytes = 2 * kv->heads * cap * kv->d * kv->eb();
+    void *nb = nullptr;
+    HIP_TRY(hipMalloc(&nb, bytes), "hipMalloc(kv_cache)");
+    if (kv->buf && kv->rows()) {
+        const size_t w = kv->rows() * kv->d * kv->eb();
+        hipError_t e = hipMemcpy2DAsync(nb, cap * kv->d * kv->eb(), kv->buf, kv->cap * kv->d * kv->eb(), w,
+                                        2 * kv->heads, hipMemcpyDeviceToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(nb);
+            return hip_fail(e, "kv_cache growth copy");
+        }
+    } else if (kv->buf) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream), "kv_cache growth");
+    }
+    if (kv->buf) (void)hipFree(kv->buf);
+    kv->buf = nb;
+    kv->bytes = bytes;
+    kv->cap = cap;
+    return LX2V_OK;
+}
+
+int kv_src_check(const lx2v_hip_kv *kv, const lx2v_hip_buf *k, const lx2v_hip_buf *v, size_t rows,
+                 const size_t *temporal) {
+    NEED(k, "k");
+    NEED(v, "v");
+    if (rows) NEED(temporal, "temporal");
+    if (!valid_dtype(k->dtype) || !valid_dtype(v->dtype))
+        return fail(LX2V_ERR_BAD_ARG, "kv_cache: k and v are F32 or BF16 buffers");
+    const size_t n = kv->heads * rows * kv->d;
+    if (k->len < n || v->len < n)
+        return fail(LX2V_ERR_BAD_SHAPE, "kv_cache: k %zu / v %zu elements, [%zu heads, %zu rows, %zu] needs %zu",
+                    k->len, v->len, kv->heads, rows, kv->d, n);
+    if ((kv->rows() + rows) * kv->d >= (1u << 31))
+        return fail(LX2V_ERR_BAD_SHAPE, "kv_cache: %zu + %zu rows of %zu pass 2^31 elements per head", kv->rows(), rows,
+                    kv->d);
+    return LX2V_OK;
+}
+
+// k, v [heads, rows, d] into cache rows [row0, row0 + rows).
+int kv_write_rows(lx2v_hip_ctx *ctx, lx2v_hip_kv *kv, const lx2v_hip_buf *k, const lx2v_hip_buf *v, size_t rows,
+                  size_t row0) {
+    return run(ctx, "kv_cache_put", [&] {
+        launch_kv_copy(ctx->stream, k->ptr, k->dtype, rows, 0, kv->k(), kv->dtype, kv->cap, row0, kv->heads, rows,
+                       kv->d);
+        launch_kv_copy(ctx->stream, v->ptr, v->dtype, rows, 0, kv->v(), kv->dtype, kv->cap, row0, kv->heads, rows,
+                       kv->d);
+    });
+}
+
+int kv_append(lx2v_hip_ctx *ctx, lx2v_hip_kv *kv, const lx2v_hip_buf *k, const lx2v_hip_buf *v, size_t rows,
+              const size_t *temporal) {
+    const size_t at = kv->rows();
+    if (int rc = kv_grow(ctx, kv, at + rows)) return rc;
+    if (int rc = kv_write_rows(ctx, kv, k, v, rows, at)) return rc;
+    kv->temporal.insert(kv->temporal.end(), temporal, temporal + rows);
+    kv->kinds.insert(kv->kinds.end(), rows, (uint8_t)LX2V_SLOT_NEW);  // lib.rs:640-642
+    return LX2V_OK;
+}
+
+}  // namespace
+
+int lx2v_hip_kv_cache_new(lx2v_hip_ctx *ctx, size_t heads, size_t head_dim, size_t capacity_tokens,
+                          lx2v_hip_kv **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (int rc = not_capturing(ctx, "kv_cache_new")) return rc;
+    if (!heads || !head_dim || heads >= (1u << 16) || head_dim > 256)
+        return fail(LX2V_ERR_BAD_SHAPE, "kv_cache_new: %zu heads of %zu (1..256)", heads, head_dim);
+    if (capacity_tokens * head_dim >= (1u << 31))
+        return fail(LX2V_ERR_BAD_SHAPE, "kv_cache_new: capacity %zu", capacity_tokens);
+    if (int rc = set_dev(ctx)) return rc;
+    auto *kv = new lx2v_hip_kv;
+    kv->heads = heads;
+    kv->d = head_dim;
+    kv->dtype = ctx->act_dtype;
+    hipError_t e = hipEventCreateWithFlags(&kv->plan_done, hipEventDisableTiming);
+    int rc = e == hipSuccess ? kv_grow(ctx, kv, std::max<size_t>(capacity_tokens, 1)) : hip_fail(e, "kv_cache_new");
+    if (rc) {
+        if (kv->plan_done) (void)hipEventDestroy(kv->plan_done);
+        delete kv;
+        return rc;
+    }
+    *out = kv;
+    return ok();
+}
+
+int lx2v_hip_kv_cache_free(lx2v_hip_ctx *ctx, lx2v_hip_kv *kv) {
+    NEED(ctx, "ctx");
+    if (!kv) return ok();
+    if (int rc = not_capturing(ctx, "kv_cache_free")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(kv_cache_free)");
+    if (kv->buf) (void)hipFree(kv->buf);
+    if (kv->plan_dev) (void)hipFree(kv->plan_dev);
+    if (kv->plan_host) (void)hipHostFree(kv->plan_host);
+    (void)hipEventDestroy(kv->plan_done);
+    delete kv;
+    return ok();
+}
+
+int lx2v_hip_kv_cache_append(lx2v_hip_ctx *ctx, lx2v_hip_kv *kv, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                             size_t rows, const size_t *temporal) {
+    NEED(ctx, "ctx");
+    NEED(kv, "cache");
+    if (int rc = kv_src_check(kv, k, v, rows, temporal)) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    if (int rc = kv_append(ctx, kv, k, v, rows, temporal)) return rc;
+    return ok();
+}
+
+int lx2v_hip_kv_cache_put(lx2v_hip_ctx *ctx, lx2v_hip_kv *kv, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
+                          size_t rows, const size_t *temporal) {
+    NEED(ctx, "ctx");
+    NEED(kv, "cache");
+    if (int rc = kv_src_check(kv, k, v, rows, temporal)) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    if (rows) {
+        // lib.rs:647-678: the first non-EMA row with temporal[0]; overwrite
+        // when the next `rows` rows carry exactly `temporal`.
+        const auto &T = kv->temporal;
+        for (size_t pos = 0; pos < T.size(); pos++) {
+            if (T[pos] != temporal[0] || kv->kinds[pos] == LX2V_SLOT_LONG_EMA || kv->kinds[pos] == LX2V_SLOT_SHORT_EMA)
+                continue;
+            bool same = pos + rows <= T.size();
+            for (size_t i = 0; same && i < rows; i++) same = T[pos + i] == temporal[i];
+            if (!same) break;
+            if (int rc = kv_write_rows(ctx, kv, k, v, rows, pos)) return rc;
+            return ok();
+        }
+    }
+    if (int rc = kv_append(ctx, kv, k, v, rows, temporal)) return rc;
+    return ok();
+}
+
+int lx2v_hip_kv_cache_len(const lx2v_hip_kv *kv, size_t *rows) {
+    NEED(kv, "cache");
+    NEED(rows, "rows");
+    *rows = kv->rows();
+    return ok();
+}
+
+int lx2v_hip_kv_cache_temporal(const lx2v_hip_kv *kv, size_t *out, size_t cap) {
+    NEED(kv, "cache");
+    if (cap < kv->rows()) return fail(LX2V_ERR_BAD_SHAPE, "kv_cache_temporal: room for %zu of %zu rows", cap, kv->rows());
+    if (kv->rows()) NEED(out, "out");
+    std::copy(kv->temporal.begin(), kv->temporal.end(), out);
+    return ok();
+}
+
+int lx2v_hip_kv_cache_kinds(const lx2v_hip_kv *kv, uint8_t *out, size_t cap) {
+    NEED(kv, "cache");
+    if (cap < kv->rows()) return fail(LX2V_ERR_BAD_SHAPE, "kv_cache_kinds: room for %zu of %zu rows", cap, kv->rows());
+    if (kv->rows()) NEED(out, "out");
+    std::copy(kv->kinds.begin(), kv->kinds.end(), out);
+    return ok();
+}
+
+int lx2v_hip_kv_cache_read(lx2v_hip_ctx *ctx, const lx2v_hip_kv *kv, lx2v_hip_buf *k, lx2v_hip_buf *v) {
+    NEED(ctx, "ctx");
+    NEED(kv, "cache");
+    NEED(k, "k");
+    NEED(v, "v");
+    const size_t rows = kv->rows(), n = kv->heads * rows * kv->d;
+    if (!valid_dtype(k->dtype) || !valid_dtype(v->dtype))
+        return fail(LX2V_ERR_BAD_ARG, "kv_cache_kv: k and v are F32 or BF16 buffers");
+    if (k->len < n || v->len < n)
+        return fail(LX2V_ERR_BAD_SHAPE, "kv_cache_kv: k %zu / v %zu elements, the cache holds %zu", k->len, v->len, n);
+    if (k->ptr == v->ptr && n) return fail(LX2V_ERR_ALIAS, "kv_cache_kv: k and v are one buffer");
+    if (int rc = set_dev(ctx)) return rc;
+    return run(ctx, "kv_cache_kv", [&] {
+        launch_kv_copy(ctx->stream, kv->k(), kv->dtype, kv->cap, 0, k->ptr, k->dtype, rows, 0, kv->heads, rows, kv->d);
+        launch_kv_copy(ctx->stream, kv->v(), kv->dtype, kv->cap, 0, v->ptr, v->dtype, rows, 0, kv->heads, rows, kv->d);
+    });
+}
+
+int lx2v_hip_kv_cache_kv(lx2v_hip_ctx *ctx, const lx2v_hip_kv *kv, lx2v_hip_buf **k, lx2v_hip_buf **v) {
+    NEED(ctx, "ctx");
+    NEED(kv, "cache");
+    NEED(k, "k");
+    NEED(v, "v");
+    if (int rc = not_capturing(ctx, "kv_cache_kv")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    const size_t n = kv->heads * kv->rows() * kv->d;
+    lx2v_hip_buf *kb = nullptr, *vb = nullptr;
+    if (int rc = alloc_buf(ctx, n, kv->dtype, &kb)) return rc;
+    int rc = alloc_buf(ctx, n, kv->dtype, &vb);
+    if (!rc) rc = lx2v_hip_kv_cache_read(ctx, kv, kb, vb);
+    if (rc) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(kb->ptr);
+        delete kb;
+        if (vb) {
+            (void)hipFree(vb->ptr);
+            delete vb;
+        }
+        return rc;
+    }
+    *k = kb;
+    *v = vb;
+    return ok();
+}
+
+int lx2v_hip_kv_cache_memrope_update(lx2v_hip_ctx *ctx, lx2v_hip_kv *kv, const lx2v_hip_memrope_t *cfg,
+                                     size_t frame_tokens) {
+    NEED(ctx, "ctx");
+    NEED(kv, "cache");
+    NEED(cfg, "cfg");
+    if (!frame_tokens || frame_tokens >= (1u << 24))
+        return fail(LX2V_ERR_BAD_SHAPE, "memrope_update: frame_tokens %zu", frame_tokens);
+    if (int rc = not_capturing(ctx, "kv_cache_memrope_update")) return rc;
+    if (int rc = set_dev(ctx)) return rc;
+    const size_t ft = frame_tokens;
+    // Simulate lib.rs:707-806 on the row metadata, carrying each row's source:
+    // an old row (>= 0), zeros (-1), or EMA slot s's output row o (-2 - (s ft + o)).
+    std::vector<size_t> T = kv->temporal;
+    std::vector<uint8_t> K = kv->kinds;
+    std::vector<int64_t> src(T.size());
+    for (size_t i = 0; i < src.size(); i++) src[i] = (int64_t)i;
+    auto frames = [&] { return T.size() / ft; };
+    if (frames() == 0) return ok();
+    auto first_frame = [&](uint8_t kind) -> int64_t {
+        for (size_t f = 0; f < frames(); f++)
+            if (K[f * ft] == kind) return (int64_t)f;
+        return -1;
+    };
+    // seed the zero EMA frames after the sinks: [sink, long, short] (lib.rs:728-752)
+    if (first_frame(LX2V_SLOT_LONG_EMA) < 0 && frames() > cfg->sink_frames) {
+        const size_t at = cfg->sink_frames * ft, t = T[std::min(at, T.size() - 1)];
+        for (uint8_t kind : {(uint8_t)LX2V_SLOT_SHORT_EMA, (uint8_t)LX2V_SLOT_LONG_EMA}) {
+            T.insert(T.begin() + at, ft, t);
+            K.insert(K.begin() + at, ft, kind);
+            src.insert(src.begin() + at, ft, (int64_t)-1);
+        }
+    }
+    // graduate New frames past the window to Recent (lib.rs:754-768; new_frames() = 3, config.rs:298-300)
+    {
+        std::vector<size_t> nf;
+        for (size_t f = 0; f < frames(); f++)
+            if (K[f * ft] == LX2V_SLOT_NEW) nf.push_back(f);
+        for (size_t i = 0; i + 3 < nf.size(); i++) std::fill(K.begin() + nf[i] * ft, K.begin() + (nf[i] + 1) * ft, (uint8_t)LX2V_SLOT_RECENT);
+    }
+    // fold and evict while over capacity (lib.rs:769-799)
+    const uint8_t slot_kind[2] = {LX2V_SLOT_LONG_EMA, LX2V_SLOT_SHORT_EMA};
+    std::vector<int64_t> init[2];
+    std::vector<std::vector<int64_t>> evs[2];
+    while (frames() > cfg->cache_frames) {
+        int64_t f = first_frame(LX2V_SLOT_RECENT);
+        if (f < 0) f = first_frame(LX2V_SLOT_NEW);
+        if (f < 0) break;
+        const size_t r0 = (size_t)f * ft;
+        for (int s = 0; s < 2; s++) {
+            const int64_t sf = first_frame(slot_kind[s]);
+            if (sf < 0) continue;
+            if (init[s].empty()) {  // the slot's rows before its first fold; from now on they are its output
+                init[s].assign(src.begin() + sf * ft, src.begin() + (sf + 1) * ft);
+                for (size_t o = 0; o < ft; o++) src[sf * ft + o] = -2 - (int64_t)(s * ft + o);
+            }
+            evs[s].emplace_back(src.begin() + r0, src.begin() + r0 + ft);
+        }
+        T.erase(T.begin() + r0, T.begin() + r0 + ft);
+        K.erase(K.begin() + r0, K.begin() + r0 + ft);
+        src.erase(src.begin() + r0, src.begin() + r0 + ft);
+    }
+    for (size_t f = 0; f < std::min<size_t>(cfg->sink_frames, frames()); f++)
+        std::fill(K.begin() + f * ft, K.begin() + (f + 1) * ft, (uint8_t)LX2V_SLOT_SINK);  // lib.rs:800-805
+
+    bool moved = src.size() != kv->rows();
+    for (size_t i = 0; !moved && i < src.size(); i++) moved = src[i] != (int64_t)i;
+    if (moved) {
+        // plan: map, then per slot its init rows and evicted rows
+        std::vector<int> plan(src.begin(), src.end());
+        int n_ev[2], init_at[2], ev_at[2];
+        float alpha[2] = {cfg->ema_alpha_long, cfg->ema_alpha_short};
+        for (int s = 0; s < 2; s++) {
+            n_ev[s] = (int)evs[s].size();
+            init_at[s] = (int)plan.size();
+            if (init[s].empty()) init[s].assign(ft, -1);
+            plan.insert(plan.end(), init[s].begin(), init[s].end());
+            ev_at[s] = (int)plan.size();
+            for (auto &e : evs[s]) plan.insert(plan.end(), e.begin(), e.end());
+        }
+        if (plan.size() >= (1u << 31)) return fail(LX2V_ERR_BAD_SHAPE, "memrope_update: plan too large");
+        if (plan.size() > kv->plan_cap) {
+            HIP_TRY(hipStreamSynchronize(ctx->stream), "memrope_update");
+            if (kv->plan_host) (void)hipHostFree(kv->plan_host);
+            if (kv->plan_dev) (void)hipFree(kv->plan_dev);
+            kv->plan_host = nullptr;
+            kv->plan_dev = nullptr;
+            kv->plan_cap = 0;
+            HIP_TRY(hipHostMalloc((void **)&kv->plan_host, plan.size() * sizeof(int)), "hipHostMalloc(memrope plan)");
+            HIP_TRY(hipMalloc((void **)&kv->plan_dev, plan.size() * sizeof(int)), "hipMalloc(memrope plan)");
+            kv->plan_cap = plan.size();
+        }
+        HIP_TRY(hipEventSynchronize(kv->plan_done), "memrope_update");  // the previous plan's copy has run
+        std::copy(plan.begin(), plan.end(), kv->plan_host);
+        HIP_TRY(hipMemcpyAsync(kv->plan_dev, kv->plan_host, plan.size() * sizeof(int), hipMemcpyHostToDevice,
+                               ctx->stream),
+                "hipMemcpyAsync(memrope plan)");
+        HIP_TRY(hipEventRecord(kv->plan_done, ctx->stream), "memrope_update");
+        // gather into the context's spare layout, then swap it with the cache's
+        auto &sp = extras()[ctx].kv_spare;
+        const size_t need = 2 * kv->heads * std::max(src.size(), kv->cap) * kv->d * kv->eb();
+        if (int rc = ensure(ctx, &sp.ptr, &sp.bytes, need, "kv_cache spare alloc")) return rc;
+        const size_t dcap = kv_cap_of(kv, sp.bytes), rows = src.size();
+        uint8_t *dst = (uint8_t *)sp.ptr;
+        if (int rc = run(ctx, "kv_cache_memrope_update", [&] {
+                launch_kv_remap(ctx->stream, kv->k(), kv->cap, dst, dcap, kv->dtype, kv->heads, rows, kv->d,
+                                kv->plan_dev, (int)ft, n_ev, init_at, ev_at, alpha);
+                launch_kv_remap(ctx->stream, kv->v(), kv->cap, dst + kv->heads * dcap * kv->d * kv->eb(), dcap,
+                                kv->dtype, kv->heads, rows, kv->d, kv->plan_dev, (int)ft, n_ev, init_at, ev_at, alpha);
+            }))
+            return rc;
+        std::swap(kv->buf, sp.ptr);
+        std::swap(kv->bytes, sp.bytes);
+        kv->cap = dcap;
+    }
+    kv->temporal = std::move(T);
+    kv->kinds = std::move(K);
+    return ok();
+}
+
+int lx2v_hip_kv_cache_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_kv *kv, size_t heads,
+                                size_t sq, size_t head_dim, const lx2v_hip_mask *mask, lx2v_hip_buf *out) {
+    NEED(kv, "cache");
+    if (heads != kv->heads || head_dim != kv->d)
+        return fail(LX2V_ERR_BAD_SHAPE, "kv_cache_attention: %zu heads of %zu, the cache holds %zu of %zu", heads,
+                    head_dim, kv->heads, kv->d);
+    const size_t sk = kv->rows();
+    lx2v_hip_buf kb, vb;  // views of the cache: [heads, cap, d]
+    kb.ptr = kv->k();
+    vb.ptr = kv->v();
+    kb.len = vb.len = kv->heads * kv->cap * kv->d;
+    kb.dtype = vb.dtype = kv->dtype;
+    if (int rc = attn_check(ctx, q, &kb, &vb, heads, sq, sk, head_dim, out)) return rc;
+    if (mask && (mask->sq != sq || mask->sk != sk))
+        return fail(LX2V_ERR_BAD_SHAPE, "kv_cache_attention: mask is %zux%zu, scores are %zux%zu", mask->sq, mask->sk,
+                    sq, sk);
+    if (!heads || !sq) return ok();
+    const lx2v_hip_mask *m = mask && sq * sk ? mask : nullptr;
+    return run(ctx, m ? "causal_attention" : "attention", [&] {
+        launch_attention(ctx->stream, q->ptr, kb.ptr, vb.ptr, q->dtype, heads, sq, sk, kv->cap, head_dim,
+                         m ? m->bytes : nullptr, m ? m->bits : nullptr, m ? m->tiles : nullptr, out->ptr, out->dtype);
+    });
 }
 
 int lx2v_hip_fill_normal(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf, uint64_t seed, float std) {

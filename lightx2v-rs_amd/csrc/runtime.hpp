@@ -153,7 +153,7 @@ void launch_gate_residual(hipStream_t s, void *h, const void *a, int dt, const f
 
 // ---- attention (k_attn.hip) -------------------------------------------------------
 // out [sq, heads*d] = softmax(q k^T / sqrt(d), mask) v; q [heads, sq, d], k / v
-// [heads, sk, d] of dtype dt; mask [sq, sk] bytes or null; tiles its summary
+// [heads, kvs, d] of dtype dt, keys 0 .. sk - 1 of each head used (kvs >= sk); mask [sq, sk] bytes or null; tiles its summary
 // (launch_mask_tiles, mask_tile_count entries) or null; out of dtype odt.
 // mbits: the mask as bits (launch_mask_pack, mask_word_count words), read by
 // the MFMA kernel in mixed tiles; the per-query kernel reads the bytes.
@@ -163,8 +163,19 @@ size_t mask_word_count(size_t sq, size_t sk);
 void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint8_t *tiles);
 void launch_mask_pack(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint32_t *bits);
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
-                      size_t sk, size_t d, const uint8_t *mask, const uint32_t *mbits, const uint8_t *tiles, void *out,
-                      int odt);
+                      size_t sk, size_t kvs, size_t d, const uint8_t *mask, const uint32_t *mbits,
+                      const uint8_t *tiles, void *out, int odt);
+
+// ---- KV cache (k_kv.hip) ---------------------------------------------------------
+// [heads, rows, d] from src (head stride sstride rows, first row srow0) to dst
+// (dstride, drow0), converting dtype sdt -> ddt (F32 / BF16).
+void launch_kv_copy(hipStream_t s, const void *src, int sdt, size_t sstride, size_t srow0, void *dst, int ddt,
+                    size_t dstride, size_t drow0, size_t heads, size_t rows, size_t d);
+// The MemRoPE update's gather: dst row r of every head from plan[r] (old row,
+// zeros, or an EMA slot row folded with the evicted rows; see k_kv.hip).
+void launch_kv_remap(hipStream_t s, const void *src, size_t sstride, void *dst, size_t dstride, int dt, size_t heads,
+                     size_t rows, size_t d, const int *plan, int ft, const int n_ev[2], const int init_at[2],
+                     const int ev_at[2], const float alpha[2]);
 
 // ---- reference-exact load-time quantizers (k_quant.hip) ------------------------
 // Fp8E4M3::quantize with quant.rs's own encoder: raw codes, exponent wrap included.

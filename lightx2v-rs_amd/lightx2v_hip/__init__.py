@@ -45,7 +45,10 @@ EXPORTS = [
     "lx2v_hip_quantize_q4", "lx2v_hip_quantize_fp8_ref", "lx2v_hip_weight_export",
     "lx2v_hip_layer_norm", "lx2v_hip_residual_norm", "lx2v_hip_gate_residual", "lx2v_hip_download_e4m3",
     "lx2v_hip_attention", "lx2v_hip_causal_attention", "lx2v_hip_mask_upload", "lx2v_hip_mask_free",
-    "lx2v_hip_attention_masked",
+    "lx2v_hip_attention_masked", "lx2v_hip_kv_cache_new", "lx2v_hip_kv_cache_free", "lx2v_hip_kv_cache_append",
+    "lx2v_hip_kv_cache_put", "lx2v_hip_kv_cache_len", "lx2v_hip_kv_cache_temporal", "lx2v_hip_kv_cache_kinds",
+    "lx2v_hip_kv_cache_kv", "lx2v_hip_kv_cache_read", "lx2v_hip_kv_cache_memrope_update",
+    "lx2v_hip_kv_cache_attention",
 ]
 
 
@@ -56,6 +59,20 @@ class HipError(RuntimeError):
 
 
 NORM_AFFINE, NORM_MOD = 0, 1
+
+# SlotKind (crates/lightx2v-core/src/memrope.rs:31-37)
+SLOT_SINK, SLOT_LONG_EMA, SLOT_SHORT_EMA, SLOT_RECENT, SLOT_NEW = range(5)
+
+
+class MemRopeConfig(ctypes.Structure):
+    """The MemRopeConfig fields the cache update reads (config.rs:265-295;
+    defaults = default_memrope())."""
+
+    _fields_ = [("cache_frames", ctypes.c_size_t), ("sink_frames", ctypes.c_size_t),
+                ("ema_alpha_long", ctypes.c_float), ("ema_alpha_short", ctypes.c_float)]
+
+    def __init__(self, cache_frames=12, sink_frames=3, ema_alpha_long=0.01, ema_alpha_short=0.1):
+        super().__init__(cache_frames, sink_frames, ema_alpha_long, ema_alpha_short)
 
 
 class _Norm(ctypes.Structure):
@@ -134,6 +151,17 @@ def _load():
         "lx2v_hip_mask_upload": (ip, [vp, vp, sz, sz, pp]),
         "lx2v_hip_mask_free": (ip, [vp, vp]),
         "lx2v_hip_attention_masked": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),
+        "lx2v_hip_kv_cache_new": (ip, [vp, sz, sz, sz, pp]),
+        "lx2v_hip_kv_cache_free": (ip, [vp, vp]),
+        "lx2v_hip_kv_cache_append": (ip, [vp, vp, vp, vp, sz, vp]),
+        "lx2v_hip_kv_cache_put": (ip, [vp, vp, vp, vp, sz, vp]),
+        "lx2v_hip_kv_cache_len": (ip, [vp, ctypes.POINTER(ctypes.c_size_t)]),
+        "lx2v_hip_kv_cache_temporal": (ip, [vp, vp, sz]),
+        "lx2v_hip_kv_cache_kinds": (ip, [vp, vp, sz]),
+        "lx2v_hip_kv_cache_kv": (ip, [vp, vp, pp, pp]),
+        "lx2v_hip_kv_cache_read": (ip, [vp, vp, vp, vp]),
+        "lx2v_hip_kv_cache_memrope_update": (ip, [vp, vp, ctypes.POINTER(MemRopeConfig), sz]),
+        "lx2v_hip_kv_cache_attention": (ip, [vp, vp, vp, sz, sz, sz, vp, vp]),
         "lx2v_hip_fill_normal": (ip, [vp, vp, ctypes.c_uint64, ctypes.c_float]),
         "lx2v_hip_linear": (ip, [vp, vp, sz, sz, vp, vp, ip, vp, sz]),
         "lx2v_hip_act_quant": (ip, [vp, vp, sz, sz, sz, vp, vp]),
@@ -250,6 +278,72 @@ class Mask:
             pass
 
 
+class KvCache:
+    """One layer's KV cache (the trait's ``KvCache``, backend.rs:333-392):
+    K / V rows in HBM, temporal index and slot kind per row on the host."""
+
+    def __init__(self, be: "HipBackend", h: int, heads: int, head_dim: int):
+        self._be, self.h, self.heads, self.head_dim = be, h, heads, head_dim
+
+    @staticmethod
+    def _temporal(temporal, rows: int) -> np.ndarray:
+        t = np.ascontiguousarray(temporal, np.uint64).ravel()
+        if t.size != rows:
+            raise HipError(ERR_BAD_SHAPE, f"{t.size} temporal indices for {rows} rows")
+        return t
+
+    def append(self, k: Buf, v: Buf, rows: int, temporal):
+        t = self._temporal(temporal, rows)
+        _check(lib.lx2v_hip_kv_cache_append(self._be.ctx, self.h, k.h, v.h, rows, _ptr(t)))
+
+    def put(self, k: Buf, v: Buf, rows: int, temporal):
+        t = self._temporal(temporal, rows)
+        _check(lib.lx2v_hip_kv_cache_put(self._be.ctx, self.h, k.h, v.h, rows, _ptr(t)))
+
+    def __len__(self) -> int:
+        n = ctypes.c_size_t(0)
+        _check(lib.lx2v_hip_kv_cache_len(self.h, ctypes.byref(n)))
+        return n.value
+
+    def temporal(self) -> list:
+        t = np.zeros(len(self), np.uint64)
+        _check(lib.lx2v_hip_kv_cache_temporal(self.h, _ptr(t), t.size))
+        return [int(x) for x in t]
+
+    def kinds(self) -> list:
+        k = np.zeros(len(self), np.uint8)
+        _check(lib.lx2v_hip_kv_cache_kinds(self.h, _ptr(k), k.size))
+        return [int(x) for x in k]
+
+    def kv(self):
+        """(K, V) as new [heads, rows, head_dim] buffers in the cache's dtype."""
+        kh, vh = ctypes.c_void_p(), ctypes.c_void_p()
+        _check(lib.lx2v_hip_kv_cache_kv(self._be.ctx, self.h, ctypes.byref(kh), ctypes.byref(vh)))
+        return Buf(self._be, kh.value), Buf(self._be, vh.value)
+
+    def read(self, k: Buf, v: Buf):
+        _check(lib.lx2v_hip_kv_cache_read(self._be.ctx, self.h, k.h, v.h))
+
+    def memrope_update(self, cfg: MemRopeConfig, frame_tokens: int):
+        _check(lib.lx2v_hip_kv_cache_memrope_update(self._be.ctx, self.h, ctypes.byref(cfg), frame_tokens))
+
+    def attention(self, q: Buf, sq: int, mask: Optional[Mask], out: Buf):
+        """causal_attention of q [heads, sq, d] over every cached row, in place."""
+        _check(lib.lx2v_hip_kv_cache_attention(self._be.ctx, q.h, self.h, self.heads, sq, self.head_dim,
+                                               mask.h if mask is not None else None, out.h))
+
+    def free(self):
+        if self.h and self._be.ctx:
+            lib.lx2v_hip_kv_cache_free(self._be.ctx, self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Graph:
     """A captured sequence of device work, replayed with one launch."""
 
@@ -278,6 +372,7 @@ class HipBackend:
         h = ctypes.c_void_p()
         _check(lib.lx2v_hip_create(device, ctypes.byref(h)))
         self.ctx = h.value
+        self.act_dtype = DTYPE_F32  # the context's default (lx2v_hip_create)
 
     @classmethod
     def try_new(cls, device: int = 0) -> Optional["HipBackend"]:
@@ -307,6 +402,7 @@ class HipBackend:
 
     def set_act_dtype(self, dtype: int):
         _check(lib.lx2v_hip_set_act_dtype(self.ctx, dtype))
+        self.act_dtype = dtype
 
     def set_fp8_act(self, mode: int):
         _check(lib.lx2v_hip_set_fp8_act(self.ctx, mode))
@@ -492,6 +588,12 @@ class HipBackend:
         h = ctypes.c_void_p()
         _check(lib.lx2v_hip_mask_upload(self.ctx, _ptr(m), sq, sk, ctypes.byref(h)))
         return Mask(self, h.value, sq, sk)
+
+    # ---- backend.rs:333-392: KV cache / MemRoPE ----
+    def kv_cache_new(self, heads: int, head_dim: int, capacity_tokens: int) -> KvCache:
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_kv_cache_new(self.ctx, heads, head_dim, capacity_tokens, ctypes.byref(h)))
+        return KvCache(self, h.value, heads, head_dim)
 
     def act_quant(self, x: Buf, x_row: int, rows: int, cols: int):
         q = np.empty((rows, cols), np.uint8)
