@@ -53,13 +53,12 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                                                   const uint8_t *__restrict__ tiles, const uint32_t *__restrict__ mbits,
                                                   float c, void *__restrict__ out) {
     constexpr int KSTR = D * 2 + 16;   // bytes per K row in LDS (padded: conflict-free fragment reads)
-    constexpr int VSTR = AK * 2 + 16;  // bytes per V^T row (one d, 64 keys)
+    constexpr int VSTR = AK * 2 + 8;   // bytes per V^T row (one d, 64 keys; 34 words: conflict-free 8-byte reads)
     constexpr int QS = D / 16;         // 16-wide d steps of S^T
     constexpr int DB = D / 32;         // 32-row d blocks of O^T
-    // 16-byte K chunks and V chunk pairs per thread (the last round may be partial)
     constexpr int KN = AK * D / 8, VN = AK * D / 16, KI = (KN + AT - 1) / AT, VI = (VN + AT - 1) / AT;
     constexpr int KSZ = AK * KSTR, VSZ = D * VSTR;
-    // Two LDS buffers: tile t + 1 is written while tile t is read.
+    // K of tiles t + 1 and t + 2, V of tiles t and t + 1: [K0 K1 V0 V1].
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (KSZ + VSZ)];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l32 = lane & 31, hf = lane >> 5;
@@ -88,12 +87,11 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     f32x16 o[DB];
 #pragma unroll
     for (int b = 0; b < DB; b++) o[b] = (f32x16){};
-    float m = -INFINITY, lsum = 0.0f;
+    float m = -INFINITY, lsum = 0.0f;  // running max (log2 domain, scaled) and sum
 
     // This query tile's row of the mask summary, staged in LDS (a global
     // load per tile would cost a memory latency per tile); rows longer than
-    // the stage are read from global memory.
-    // Longer rows skip the summary: every tile is then read as mixed.
+    // the stage skip the summary: every tile is then read as mixed.
     __shared__ uint8_t trow[TROW];
     const bool tlds = tiles && nkt <= TROW;
     if (tlds)
@@ -105,7 +103,8 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
         while (kt < nkt && tstate(kt) == 0) kt++;
         return kt;
     };
-    // Tile kt from global memory into registers: K as 16-byte chunks (key,
+
+    // Tiles from global memory into registers: K as 16-byte chunks (key,
     // chunk), V as chunk pairs of two consecutive keys (for V^T).  Buffer
     // loads: keys past sk (and unused lanes, offset kOob) read zero, and
     // every load is issued, so waits can count the loads in flight.
@@ -122,39 +121,47 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
         }
     };
     u32x4 kr[KI], va[VI], vb[VI];
-    uint32_t mwn[2];  // mask bits of the loaded tile (mixed tiles; kOob reads 0 otherwise)
+    uint32_t mwn[2];  // mask bits of the V tile loaded last (mixed tiles; kOob reads 0 otherwise)
     const uint32_t nw = ((uint32_t)sk + 31) / 32;
     const auto msrc = make_rsrc(mbits, mbits ? (uint32_t)sq * nw * 4 : 0u);
-    auto gload = [&](int kt) {
+    auto gload_k = [&](int kt) {
         const uint32_t k0 = (uint32_t)kt * AK;
-        const bool mixed = kt < nkt && tstate(kt) == 2 && qin;
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-            mwn[kb] = buffer_load_x1(msrc, mixed ? ((uint32_t)q * nw + k0 / 32 + (uint32_t)kb) * 4 : kOob);
 #pragma unroll
         for (int it = 0; it < KI; it++) {
             const int idx = it * AT + tid, key = idx / (D / 8), ch = idx % (D / 8);
             kr[it] = ld8(ksrc, (k0 + key) * D + 8 * ch, idx < KN);
         }
+    };
+    auto gload_v = [&](int kt) {
+        const uint32_t k0 = (uint32_t)kt * AK;
+        const bool mixed = kt < nkt && tstate(kt) == 2 && qin;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+            mwn[kb] = buffer_load_x1(msrc, mixed ? ((uint32_t)q * nw + k0 / 32 + (uint32_t)kb) * 4 : kOob);
+        // V item idx: key pair idx % 32 (keys 2 p, 2 p + 1), chunk idx / 32 --
+        // consecutive lanes take consecutive key pairs, so the transposed
+        // stores below hit consecutive LDS words
 #pragma unroll
         for (int it = 0; it < VI; it++) {
-            const int idx = it * AT + tid, key = 2 * (idx / (D / 8)), ch = idx % (D / 8);
+            const int idx = it * AT + tid, key = 2 * (idx % (AK / 2)), ch = idx / (AK / 2);
             va[it] = ld8(vsrc, (k0 + key) * D + 8 * ch, idx < VN);
             vb[it] = ld8(vsrc, (k0 + key + 1) * D + 8 * ch, idx < VN);
         }
     };
-
-    // Registers into LDS buffer buf: K rows, and V transposed (one d per row).
-    auto lstore = [&](int buf) {
-        uint8_t *ks = lds + buf * (KSZ + VSZ), *vt = ks + KSZ;
+    // Registers into LDS: K rows; V transposed (one d per row).
+    auto lstore_k = [&](int buf) {
+        uint8_t *ks = lds + buf * KSZ;
 #pragma unroll
         for (int it = 0; it < KI; it++) {
             const int idx = it * AT + tid, key = idx / (D / 8), ch = idx % (D / 8);
             if (idx < KN) *(u32x4 *)(ks + key * KSTR + ch * 16) = kr[it];
         }
+    };
+    auto lstore_v = [&](int buf) {
+        uint8_t *vt = lds + 2 * KSZ + buf * VSZ;
 #pragma unroll
         for (int it = 0; it < VI; it++) {
-            const int idx = it * AT + tid, key = 2 * (idx / (D / 8)), ch = idx % (D / 8);
+            const int idx = it * AT + tid, key = 2 * (idx % (AK / 2)), ch = idx / (AK / 2);
             if (idx >= VN) continue;
             const uint32_t av[4] = {va[it].x, va[it].y, va[it].z, va[it].w};
             const uint32_t bv[4] = {vb[it].x, vb[it].y, vb[it].z, vb[it].w};
@@ -166,93 +173,115 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
             }
         }
     };
+    // S^T = K Q^T for the 64 keys in K buffer kb: keys 32 j + (8 g + 4 hf + r),
+    // r = 0..3, in registers 4 g + r of st[j].
+    auto scores = [&](int kbuf, f32x16 *st) {
+        const uint8_t *ks = lds + kbuf * KSZ;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            st[j] = (f32x16){};
+#pragma unroll
+            for (int s = 0; s < QS; s++) {
+                const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + (32 * j + l32) * KSTR + (2 * s + hf) * 16));
+                st[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[j], 0, 0, 0);
+            }
+        }
+    };
 
-    // Explicit vmcnt(0) after each lstore: the mask words were loaded before
-    // K / V and are complete once lstore has its operands, but the compiler
-    // cannot see that across the loop's back edge and would otherwise wait
-    // for the next tile's loads at their first use.
-    int kt = next_tile(0), buf = 0;
+    // Mask tile kt's scores in place: a full tile with every pair allowed is
+    // left alone; otherwise keys past sk and, in mixed tiles, pairs whose
+    // mask bit is clear become -inf.  mwk: the tile's two mask words.
+    auto apply_mask = [&](f32x16 *st, int kt, const uint32_t *mwk) {
+        const int state = tstate(kt), k0 = kt * AK;
+        if (state == 1 && k0 + AK <= sk) return;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            // allowed keys of this 32-key block as bits (mask word, keys
+            // before sk), shifted so that register i tests a constant bit
+            const int left = sk - (k0 + 32 * j);
+            uint32_t allow = state == 2 ? mwk[j] : ~0u;
+            allow &= left >= 32 ? ~0u : (left <= 0 ? 0u : (1u << left) - 1u);
+            allow >>= 4 * hf;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const bool ok = (allow >> (8 * (i / 4) + (i % 4))) & 1u;
+                st[j][i] = ok ? st[j][i] : -INFINITY;
+            }
+        }
+    };
+
+    // Software pipeline: while tile t's softmax and O^T += V^T P^T run, the
+    // scores of tile t + 1 are computed (its K is already in LDS) and the K of
+    // tile t + 2 and V of t + 1 are loaded.  The MFMAs of S(t + 1) and the
+    // softmax of t are independent, so the matrix cores and the vector ALUs
+    // of a SIMD work at once.  Explicit vmcnt(0) after each store: the mask
+    // words were loaded before V and are complete once V is, but the
+    // compiler cannot see that across the loop's back edge.
+    int kt = next_tile(0);
+    int kn = kt < nkt ? next_tile(kt + 1) : nkt;
+    f32x16 sc[2];  // scores of tile kt (raw q.k)
+    uint32_t mw[2] = {0u, 0u};
     if (kt < nkt) {
-        gload(kt);
-        lstore(0);
+        gload_k(kt);
+        gload_v(kt);
+        lstore_k(0);
+        lstore_v(0);
+        mw[0] = mwn[0];
+        mw[1] = mwn[1];
+        gload_k(kn);
+        lstore_k(1);
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
+    if (kt < nkt) {
+        scores(0, sc);
+        apply_mask(sc, kt, mw);
+    }
+    __syncthreads();  // K buffer 0 is rewritten at the end of the first iteration
+    int kbi = 1, vbi = 0;  // K buffer holding K(kn); V buffer holding V(kt)
+    const float tau = 8.0f;  // rescale O only when a query's max grows by more than 2^8
     while (kt < nkt) {
-        const int state = tstate(kt);  // 1 all pairs allowed, 2 mixed
-        const int k0 = kt * AK, kn = next_tile(kt + 1);
-        // this tile's mask words, loaded with its K / V (already in registers)
-        const uint32_t mw[2] = {mwn[0], mwn[1]};
-        // The next tile's loads land while this tile is computed (kn = nkt:
-        // every load reads zero, unused).  The scheduling barriers keep them
-        // here: left alone, the compiler sinks them to their use after the
-        // MFMAs and nothing overlaps.
+        const int knn = kn < nkt ? next_tile(kn + 1) : nkt;
+        // loads for the stores at the end of this iteration (kOob when past the last tile)
         __builtin_amdgcn_sched_barrier(0);
-        gload(kn);
+        gload_k(knn);
+        gload_v(kn);
         __builtin_amdgcn_sched_barrier(0);
-        const uint8_t *ks = lds + buf * (KSZ + VSZ), *vt = ks + KSZ;
 
-        // S^T = K Q^T for keys k0 + 32 kb + (8 g + 4 hf + r), r = 0..3 in registers 4 g + r.
-        f32x16 st[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            st[kb] = (f32x16){};
-#pragma unroll
-            for (int s = 0; s < QS; s++) {
-                const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + (32 * kb + l32) * KSTR + (2 * s + hf) * 16));
-                st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb], 0, 0, 0);
-            }
-        }
-        // Scale into the log2 domain and mask.  A full tile with every pair
-        // allowed (uniform) takes no per-element test; otherwise keys past sk
-        // and, in mixed tiles, pairs whose mask bit is clear are -inf.
+        // S(kn), unconditionally (past the last tile it reads a stale buffer
+        // and is not used): a branch here would keep these MFMAs from being
+        // interleaved with the softmax below.
+        f32x16 sn[2];
+        scores(kbi, sn);
+
+        // tile kt's scores were masked when they were computed
         float tmax = -INFINITY;
-        if (state == 1 && k0 + AK <= sk) {
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    st[kb][i] *= c;
-                    tmax = fmaxf(tmax, st[kb][i]);
-                }
-        } else {
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-                // allowed keys of this 32-key block as bits (mask word, keys
-                // before sk), shifted so that register i tests a constant bit
-                const int left = sk - (k0 + 32 * kb);
-                uint32_t allow = state == 2 ? mw[kb] : ~0u;
-                allow &= left >= 32 ? ~0u : (left <= 0 ? 0u : (1u << left) - 1u);
-                allow >>= 4 * hf;
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const bool ok = (allow >> (8 * (i / 4) + (i % 4))) & 1u;
-                    st[kb][i] = ok ? st[kb][i] * c : -INFINITY;
-                    tmax = fmaxf(tmax, st[kb][i]);
-                }
-            }
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mn = fmaxf(m, tmax);
-        // With no key allowed yet (mn = -inf) every p is exp2(-inf) = 0 and o,
-        // lsum are still 0, so any finite reference works: use 0.  The raw
-        // v_exp_f32 flushes results below 2^-126 to 0 (no contribution a
-        // softmax sum in f32 could register).
+            for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, sc[j][i]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * c;
+        // The reference point moves only when the tile's max passes it by more
+        // than tau: p = 2^(s c - m) <= 2^tau in between, exact in f32, and O
+        // is rescaled far less often.  With no key allowed yet (m = -inf) any
+        // finite reference works: use 0.  The raw v_exp_f32 flushes results
+        // below 2^-126 to 0 (no contribution a softmax sum in f32 could
+        // register).
+        const float mn = tmax > m + tau ? tmax : m;
         const float mref = mn == -INFINITY ? 0.0f : mn;
         const float alpha = __builtin_amdgcn_exp2f(m - mref);
         float psum = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float p = __builtin_amdgcn_exp2f(st[kb][i] - mref);
-                st[kb][i] = p;
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][i], c, -mref));
+                sc[j][i] = p;
                 psum += p;
             }
         psum += __shfl_xor(psum, 32, 64);
         lsum = lsum * alpha + psum;
         m = mn;
-        // rescale the output only where some query's max moved (uniform test)
         if (__ballot(alpha != 1.0f)) {
 #pragma unroll
             for (int b = 0; b < DB; b++)
@@ -260,18 +289,19 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                 for (int i = 0; i < 16; i++) o[b][i] *= alpha;
         }
 
-        // O^T += V^T P^T, four 16-key steps: step (kb, t) takes registers
-        // 8 t .. 8 t + 7 of st[kb], i.e. keys 32 kb + 16 t + 4 hf + 0..3 and
-        // 32 kb + 16 t + 8 + 4 hf + 0..3, and V^T in the same key order.
+        // O^T += V^T P^T, four 16-key steps: step (j, t) takes registers
+        // 8 t .. 8 t + 7 of sc[j], i.e. keys 32 j + 16 t + 4 hf + 0..3 and
+        // 32 j + 16 t + 8 + 4 hf + 0..3, and V^T in the same key order.
+        const uint8_t *vt = lds + 2 * KSZ + vbi * VSZ;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-                const f32x16 &sp = st[kb];
+                const f32x16 &sp = sc[j];
                 const u32x4 pw = (u32x4){pack_bf16x2(sp[8 * t + 0], sp[8 * t + 1]), pack_bf16x2(sp[8 * t + 2], sp[8 * t + 3]),
                                          pack_bf16x2(sp[8 * t + 4], sp[8 * t + 5]), pack_bf16x2(sp[8 * t + 6], sp[8 * t + 7])};
                 const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
-                const int kk = 32 * kb + 16 * t + 4 * hf;
+                const int kk = 32 * j + 16 * t + 4 * hf;
 #pragma unroll
                 for (int b = 0; b < DB; b++) {
                     const uint8_t *row = vt + (32 * b + l32) * VSTR;
@@ -281,12 +311,21 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                     o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[b], 0, 0, 0);
                 }
             }
-        // the other buffer was last read before the previous barrier
-        if (kn < nkt) lstore(buf ^ 1);
+        // K(kt) and V of the previous tile were last read before the previous
+        // barrier (stores past the last tile write zeros, unused)
+        lstore_k(kbi ^ 1);
+        lstore_v(vbi ^ 1);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        mw[0] = mwn[0];
+        mw[1] = mwn[1];
+        if (kn < nkt) apply_mask(sn, kn, mw);
         __syncthreads();
-        buf ^= 1;
+        sc[0] = sn[0];
+        sc[1] = sn[1];
+        kbi ^= 1;
+        vbi ^= 1;
         kt = kn;
+        kn = knn;
     }
 
     if (!qin) return;
