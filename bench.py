@@ -450,6 +450,62 @@ def main():
     for bb in (aq, ak, av, aout):
         bb.free()
 
+    # ---- KV cache at steady state (not part of the linear metric) ----
+    # One layer's MemRoPE cache after 6 chunks (12 frames of 1560 tokens, bf16,
+    # K / V [heads, cap, 128]): the re-run steps' put (overwrite in place) and
+    # update (nothing moves), the chunk's first step (append + seed / evict
+    # gather), and attention of the chunk over the cache in place with the
+    # DiT's mask (key temporal <= query temporal, dit.rs:636-668).
+    rows = M
+    cfg = H.MemRopeConfig()
+    kvc = be.kv_cache_new(heads, hd, 12 * frame)
+    kb_, vb_ = be.alloc(heads * rows * hd), be.alloc(heads * rows * hd)
+    be.fill_normal(kb_, 1700, 1.0)
+    be.fill_normal(vb_, 1701, 1.0)
+    temporal = [np.array([c * 3 + i // frame for i in range(rows)], np.uint64) for c in range(40)]
+    for c in range(6):
+        kvc.put(kb_, vb_, rows, temporal[c])
+        kvc.memrope_update(cfg, frame)
+    be.sync()
+    tq = temporal[5].astype(np.int64)
+    kmask = np.array(kvc.temporal())[None, :] <= tq[:, None]
+    km = be.mask_upload(kmask, rows, len(kvc))
+    qb_, ob_ = be.alloc(heads * rows * hd), be.alloc(rows * heads * hd)
+    be.fill_normal(qb_, 1702, 1.0)
+    kvc.attention(qb_, rows, km, ob_)
+
+    def region_us(name, fn, n):
+        be.sync()
+        be.profile_region(name, True)
+        for _ in range(n):
+            fn()
+        be.profile_region(name, False)
+        return be.profile_kernel(name)[1] * 1e3 / n
+
+    kv_attn_us = region_us("kv_attn", lambda: kvc.attention(qb_, rows, km, ob_), 10)
+    put_us = region_us("kv_put", lambda: (kvc.put(kb_, vb_, rows, temporal[5]), kvc.memrope_update(cfg, frame)), 10)
+    nxt = [6]
+
+    def first_step():
+        kvc.put(kb_, vb_, rows, temporal[nxt[0]])
+        kvc.memrope_update(cfg, frame)
+        nxt[0] += 1
+
+    evict_us = region_us("kv_evict", first_step, 5)
+    kpairs = float(kmask.sum()) * heads
+    kv = {"shape": f"{heads} heads x {hd}, {len(kvc)} cached rows (12 frames of {frame}), chunk of {rows} queries, bf16",
+          "attention_in_place_us": round(kv_attn_us, 2),
+          "attention_tflops_allowed_pairs": round(4.0 * hd * kpairs / (kv_attn_us * 1e-6) / 1e12, 1),
+          "put_and_update_rerun_step_us": round(put_us, 2),
+          "put_and_update_first_step_us": round(evict_us, 2),
+          "kernels": "k_kv_copy, k_kv_remap (HBM), k_attn_mfma"}
+    log(f"bench: kv cache attention {kv_attn_us:.1f} us, re-run put+update {put_us:.1f} us, "
+        f"first step {evict_us:.1f} us")
+    km.free()
+    kvc.free()
+    for bb in (kb_, vb_, qb_, ob_):
+        bb.free()
+
     # plain-copy calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
     cal_n = 64 << 20
     ca, cb = be.alloc(cal_n, H.DTYPE_F32), be.alloc(cal_n, H.DTYPE_F32)
@@ -510,6 +566,7 @@ def main():
         "act_quant_ms_per_chunk": round(region["act_quant_chunk"], 3),
         "per_gemm": per,
         "causal_attention": attn,
+        "kv_cache": kv,
         "per_config": configs,
         "roofline": {
             "bound": "mfma",
