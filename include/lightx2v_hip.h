@@ -254,6 +254,13 @@ int lx2v_hip_causal_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx
 typedef struct lx2v_hip_mask lx2v_hip_mask;
 int lx2v_hip_mask_upload(lx2v_hip_ctx *ctx, const uint8_t *mask, size_t sq, size_t sk,
                          lx2v_hip_mask **out);
+/* The MemRoPE block mask built on the device from temporal indices: pair
+ * (i, j) allowed iff tk[j] <= tq[i], the mask dit.rs:643-653 builds on the
+ * host from the chunk's token temporal indices and kv_cache_temporal (no
+ * reference counterpart: it replaces the [sq, sk] byte array's host build
+ * and upload, 87.6 MB per step at the Wan shape, with 8 (sq + sk) bytes). */
+int lx2v_hip_mask_temporal(lx2v_hip_ctx *ctx, const size_t *tq, size_t sq, const size_t *tk, size_t sk,
+                           lx2v_hip_mask **out);
 int lx2v_hip_mask_free(lx2v_hip_ctx *ctx, lx2v_hip_mask *mask);
 int lx2v_hip_attention_masked(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k,
                               const lx2v_hip_buf *v, size_t heads, size_t sq, size_t sk,

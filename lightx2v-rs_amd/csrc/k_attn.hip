@@ -436,6 +436,70 @@ __global__ __launch_bounds__(AT) void k_mask_pack(const uint8_t *__restrict__ ma
     if ((lane & 31) == 0 && w < nw) bits[(size_t)q * nw + w] = (uint32_t)(lane ? b >> 32 : b);
 }
 
+// The MemRoPE block mask from temporal indices (dit.rs:643-653): pair
+// (q, k) is allowed iff tk[k] <= tq[q].  Bytes: 16 per thread; bits: a thread
+// per 32-key word; tile summary: a wave per tile from the min / max of the
+// tile's query and key indices (all allowed iff max tk <= min tq, none iff
+// min tk > max tq).
+__global__ __launch_bounds__(AT) void k_mask_temporal_bytes(const uint64_t *__restrict__ tq, const uint64_t *__restrict__ tk,
+                                                            int sq, int sk, uint8_t *__restrict__ mask) {
+    const size_t n = (size_t)sq * sk;
+    for (size_t i0 = (blockIdx.x * (size_t)AT + threadIdx.x) * 16; i0 < n; i0 += (size_t)gridDim.x * AT * 16) {
+        uint8_t v[16];
+        size_t q = i0 / sk, k = i0 % sk;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            v[e] = i0 + e < n ? (uint8_t)(tk[k] <= tq[q]) : 0;
+            if (++k == (size_t)sk) k = 0, q++;
+        }
+        if (i0 + 16 <= n && (((uintptr_t)(mask + i0)) & 15) == 0) {
+            *(u32x4 *)(mask + i0) = *(const u32x4 *)v;
+        } else {
+            for (int e = 0; e < 16 && i0 + e < n; e++) mask[i0 + e] = v[e];
+        }
+    }
+}
+
+__global__ __launch_bounds__(AT) void k_mask_temporal_bits(const uint64_t *__restrict__ tq, const uint64_t *__restrict__ tk,
+                                                           int sq, int sk, uint32_t *__restrict__ bits) {
+    const int nw = (sk + 31) / 32;
+    const size_t n = (size_t)sq * nw;
+    for (size_t t = blockIdx.x * (size_t)AT + threadIdx.x; t < n; t += (size_t)gridDim.x * AT) {
+        const int q = (int)(t / nw), w = (int)(t % nw);
+        const uint64_t tqv = tq[q];
+        uint32_t b = 0;
+        for (int e = 0; e < 32; e++) {
+            const int k = 32 * w + e;
+            if (k < sk && tk[k] <= tqv) b |= 1u << e;
+        }
+        bits[t] = b;
+    }
+}
+
+__global__ __launch_bounds__(AT) void k_mask_temporal_tiles(const uint64_t *__restrict__ tq, const uint64_t *__restrict__ tk,
+                                                            int sq, int sk, int nqt, int nkt, uint8_t *__restrict__ tiles) {
+    const int lane = threadIdx.x & 63;
+    const size_t t = blockIdx.x * (size_t)(AT / 64) + (threadIdx.x >> 6);
+    if (t >= (size_t)nqt * nkt) return;
+    const int qt = (int)(t / nkt), kt = (int)(t % nkt);
+    uint64_t qmin = ~0ull, qmax = 0, kmin = ~0ull, kmax = 0;
+    for (int i = lane; i < AQ; i += 64) {
+        const int q = qt * AQ + i;
+        if (q < sq) qmin = min(qmin, tq[q]), qmax = max(qmax, tq[q]);
+    }
+    {
+        const int k = kt * AK + lane;
+        if (k < sk) kmin = tk[k], kmax = tk[k];
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        qmin = min(qmin, (uint64_t)__shfl_xor((unsigned long long)qmin, o, 64));
+        qmax = max(qmax, (uint64_t)__shfl_xor((unsigned long long)qmax, o, 64));
+        kmin = min(kmin, (uint64_t)__shfl_xor((unsigned long long)kmin, o, 64));
+        kmax = max(kmax, (uint64_t)__shfl_xor((unsigned long long)kmax, o, 64));
+    }
+    if (lane == 0) tiles[t] = kmin > qmax ? 0 : (kmax <= qmin ? 1 : 2);
+}
+
 template <int D, int DT>
 void attn_mfma_od(hipStream_t s, dim3 grid, const void *q, const void *k, const void *v, int heads, int sq, int sk,
                   int kvs, const uint8_t *tiles, const uint32_t *mask, float c, void *out, int odt) {
@@ -457,6 +521,20 @@ void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk,
     if (n == 0) return;
     hipLaunchKernelGGL(k_mask_tiles, dim3((unsigned)((n + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, mask, (int)sq,
                        (int)sk, nqt, nkt, tiles);
+}
+
+void launch_mask_temporal(hipStream_t s, const uint64_t *tq, size_t sq, const uint64_t *tk, size_t sk, uint8_t *mask,
+                          uint32_t *bits, uint8_t *tiles) {
+    if (sq == 0 || sk == 0) return;
+    const size_t nb = sq * sk, nw = sq * ((sk + 31) / 32);
+    hipLaunchKernelGGL(k_mask_temporal_bytes, dim3((unsigned)std::min<size_t>((nb / 16 + AT) / AT, 16384)), dim3(AT), 0,
+                       s, tq, tk, (int)sq, (int)sk, mask);
+    hipLaunchKernelGGL(k_mask_temporal_bits, dim3((unsigned)std::min<size_t>((nw + AT - 1) / AT, 16384)), dim3(AT), 0,
+                       s, tq, tk, (int)sq, (int)sk, bits);
+    const int nqt = (int)((sq + AQ - 1) / AQ), nkt = (int)((sk + AK - 1) / AK);
+    const size_t n = (size_t)nqt * nkt;
+    hipLaunchKernelGGL(k_mask_temporal_tiles, dim3((unsigned)((n + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, tq, tk,
+                       (int)sq, (int)sk, nqt, nkt, tiles);
 }
 
 size_t mask_tile_count(size_t sq, size_t sk) { return ((sq + AQ - 1) / AQ) * ((sk + AK - 1) / AK); }

@@ -75,35 +75,80 @@ struct RemapArgs {
     float alpha[2];
 };
 
-// One thread per (row, element) of head blockIdx.y.
-template <int DT>
+// V consecutive elements at element index i (16 B for F32, 8 B for BF16
+// when V = 4; i is a multiple of V).
+template <int DT, int V>
+__device__ __forceinline__ void kv_ldv(const void *p, size_t i, float (&x)[V]) {
+    if constexpr (V == 4 && DT == LX2V_DTYPE_F32) {
+        const f32x4 a = *(const f32x4 *)((const float *)p + i);
+        x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w;
+    } else if constexpr (V == 4) {
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t a = *(const u32x2_t *)((const uint16_t *)p + i);
+        x[0] = __uint_as_float(a.x << 16), x[1] = __uint_as_float(a.x & 0xFFFF0000u);
+        x[2] = __uint_as_float(a.y << 16), x[3] = __uint_as_float(a.y & 0xFFFF0000u);
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; e++) x[e] = kv_ld<DT>(p, i + e);
+    }
+}
+
+template <int DT, int V>
+__device__ __forceinline__ void kv_stv(void *p, size_t i, const float (&x)[V]) {
+    if constexpr (V == 4 && DT == LX2V_DTYPE_F32) {
+        *(f32x4 *)((float *)p + i) = (f32x4){x[0], x[1], x[2], x[3]};
+    } else if constexpr (V == 4) {
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        *(u32x2_t *)((uint16_t *)p + i) =
+            (u32x2_t){f32_to_bf16_bits(x[0]) | ((uint32_t)f32_to_bf16_bits(x[1]) << 16),
+                      f32_to_bf16_bits(x[2]) | ((uint32_t)f32_to_bf16_bits(x[3]) << 16)};
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; e++) kv_st<DT>(p, i + e, x[e]);
+    }
+}
+
+// One thread per (row, group of V elements) of head blockIdx.y.
+template <int DT, int V>
 __global__ __launch_bounds__(KT) void k_kv_remap(const void *__restrict__ src, size_t sstride,
                                                  void *__restrict__ dst, size_t dstride, uint32_t rows, uint32_t d,
                                                  const int *__restrict__ plan, RemapArgs a) {
-    const uint32_t n = rows * d;
+    const uint32_t per_row = d / V, n = rows * per_row;
     const size_t h = blockIdx.y;
     for (uint32_t t = blockIdx.x * KT + threadIdx.x; t < n; t += gridDim.x * KT) {
-        const uint32_t j = t % d, r = t / d;
+        const uint32_t j = (t % per_row) * V, r = t / per_row;
         const size_t sh = h * sstride * d + j;  // (head, element) base in the old layout
         const int m = plan[r];
-        float x;
+        float x[V];
         if (m >= 0) {
-            x = kv_ld<DT>(src, sh + (size_t)m * d);
+            kv_ldv<DT, V>(src, sh + (size_t)m * d, x);
         } else if (m == -1) {
-            x = 0.0f;
+#pragma unroll
+            for (int e = 0; e < V; e++) x[e] = 0.0f;
         } else {
             const int c = -m - 2, s = c / a.ft, o = c % a.ft;
             const int i0 = plan[a.init_at[s] + o];
-            float e = i0 >= 0 ? kv_ld<DT>(src, sh + (size_t)i0 * d) : 0.0f;
+            if (i0 >= 0) {
+                kv_ldv<DT, V>(src, sh + (size_t)i0 * d, x);
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; e++) x[e] = 0.0f;
+            }
             const float al = a.alpha[s], keep = 1.0f - al;
             for (int i = 0; i < a.n_ev[s]; i++) {
                 const int ri = plan[a.ev_at[s] + i * a.ft + o];
-                const float f = ri >= 0 ? kv_ld<DT>(src, sh + (size_t)ri * d) : 0.0f;
-                e = keep * e + al * f;
+                float f[V];
+                if (ri >= 0) {
+                    kv_ldv<DT, V>(src, sh + (size_t)ri * d, f);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; e++) f[e] = 0.0f;
+                }
+#pragma unroll
+                for (int e = 0; e < V; e++) x[e] = keep * x[e] + al * f[e];
             }
-            x = e;
         }
-        kv_st<DT>(dst, (h * dstride + r) * d + j, x);
+        kv_stv<DT, V>(dst, (h * dstride + r) * d + j, x);
     }
 }
 
@@ -153,12 +198,23 @@ void launch_kv_remap(hipStream_t s, const void *src, size_t sstride, void *dst, 
         a.ev_at[i] = ev_at[i];
         a.alpha[i] = alpha[i];
     }
-    if (dt == LX2V_DTYPE_BF16)
-        hipLaunchKernelGGL(k_kv_remap<LX2V_DTYPE_BF16>, grid_for(rows * d, heads), dim3(KT), 0, s, src, sstride, dst,
-                           dstride, (uint32_t)rows, (uint32_t)d, plan, a);
-    else
-        hipLaunchKernelGGL(k_kv_remap<LX2V_DTYPE_F32>, grid_for(rows * d, heads), dim3(KT), 0, s, src, sstride, dst,
-                           dstride, (uint32_t)rows, (uint32_t)d, plan, a);
+    const bool v4 = d % 4 == 0;
+    const dim3 g = grid_for(v4 ? rows * d / 4 : rows * d, heads);
+    if (dt == LX2V_DTYPE_BF16) {
+        if (v4)
+            hipLaunchKernelGGL((k_kv_remap<LX2V_DTYPE_BF16, 4>), g, dim3(KT), 0, s, src, sstride, dst, dstride,
+                               (uint32_t)rows, (uint32_t)d, plan, a);
+        else
+            hipLaunchKernelGGL((k_kv_remap<LX2V_DTYPE_BF16, 1>), g, dim3(KT), 0, s, src, sstride, dst, dstride,
+                               (uint32_t)rows, (uint32_t)d, plan, a);
+    } else {
+        if (v4)
+            hipLaunchKernelGGL((k_kv_remap<LX2V_DTYPE_F32, 4>), g, dim3(KT), 0, s, src, sstride, dst, dstride,
+                               (uint32_t)rows, (uint32_t)d, plan, a);
+        else
+            hipLaunchKernelGGL((k_kv_remap<LX2V_DTYPE_F32, 1>), g, dim3(KT), 0, s, src, sstride, dst, dstride,
+                               (uint32_t)rows, (uint32_t)d, plan, a);
+    }
 }
 
 }  // namespace lx2v

@@ -1120,6 +1120,53 @@ int lx2v_hip_mask_upload(lx2v_hip_ctx *ctx, const uint8_t *mask, size_t sq, size
     return ok();
 }
 
+int lx2v_hip_mask_temporal(lx2v_hip_ctx *ctx, const size_t *tq, size_t sq, const size_t *tk, size_t sk,
+                           lx2v_hip_mask **out) {
+    NEED(ctx, "ctx");
+    NEED(out, "out");
+    if (sq) NEED(tq, "tq");
+    if (sk) NEED(tk, "tk");
+    if (int rc = not_capturing(ctx, "mask_temporal")) return rc;
+    if (sq >= (1u << 30) || sk >= (1u << 30) || sq * sk >= (1ull << 40))
+        return fail(LX2V_ERR_BAD_SHAPE, "mask %zux%zu too large", sq, sk);
+    if (int rc = set_dev(ctx)) return rc;
+    auto *m = new lx2v_hip_mask;
+    m->sq = sq;
+    m->sk = sk;
+    // [bytes | bits | tiles] as mask_fill lays them out, then tq and tk
+    const size_t nb = sq * sk, body = mask_bytes(sq, sk), toff = (body + 255) & ~(size_t)255;
+    uint8_t *base = nullptr;
+    hipError_t e = hipMalloc((void **)&base, std::max<size_t>(toff + (sq + sk) * 8, 4));
+    if (e != hipSuccess) {
+        delete m;
+        return hip_fail(e, "hipMalloc(mask)");
+    }
+    m->bytes = base;
+    m->bits = (uint32_t *)(base + ((nb + 255) & ~(size_t)255));
+    m->tiles = (uint8_t *)(m->bits + mask_word_count(sq, sk));
+    uint64_t *dq = (uint64_t *)(base + toff), *dk = dq + sq;
+    int rc = LX2V_OK;
+    static_assert(sizeof(size_t) == sizeof(uint64_t), "temporal indices are 64-bit");
+    if (sq) e = hipMemcpyAsync(dq, tq, sq * 8, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && sk) e = hipMemcpyAsync(dk, tk, sk * 8, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "mask_temporal upload");
+    if (!rc)
+        rc = run(ctx, "mask_temporal", [&] {
+            launch_mask_temporal(ctx->stream, dq, sq, dk, sk, m->bytes, m->bits, m->tiles);
+        });
+    if (!rc) {
+        hipError_t e2 = hipStreamSynchronize(ctx->stream);  // tq / tk are the caller's again
+        if (e2 != hipSuccess) rc = hip_fail(e2, "mask_temporal");
+    }
+    if (rc) {
+        (void)hipFree(base);
+        delete m;
+        return rc;
+    }
+    *out = m;
+    return ok();
+}
+
 int lx2v_hip_mask_free(lx2v_hip_ctx *ctx, lx2v_hip_mask *m) {
     NEED(ctx, "ctx");
     if (!m) return ok();

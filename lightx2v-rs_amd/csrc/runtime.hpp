@@ -162,6 +162,9 @@ size_t mask_tile_count(size_t sq, size_t sk);
 size_t mask_word_count(size_t sq, size_t sk);
 void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint8_t *tiles);
 void launch_mask_pack(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint32_t *bits);
+// All three forms of the mask "tk[k] <= tq[q]" from temporal indices.
+void launch_mask_temporal(hipStream_t s, const uint64_t *tq, size_t sq, const uint64_t *tk, size_t sk, uint8_t *mask,
+                          uint32_t *bits, uint8_t *tiles);
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
                       size_t sk, size_t kvs, size_t d, const uint8_t *mask, const uint32_t *mbits,
                       const uint8_t *tiles, void *out, int odt);

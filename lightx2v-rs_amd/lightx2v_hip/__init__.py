@@ -48,7 +48,7 @@ EXPORTS = [
     "lx2v_hip_attention_masked", "lx2v_hip_kv_cache_new", "lx2v_hip_kv_cache_free", "lx2v_hip_kv_cache_append",
     "lx2v_hip_kv_cache_put", "lx2v_hip_kv_cache_len", "lx2v_hip_kv_cache_temporal", "lx2v_hip_kv_cache_kinds",
     "lx2v_hip_kv_cache_kv", "lx2v_hip_kv_cache_read", "lx2v_hip_kv_cache_memrope_update",
-    "lx2v_hip_kv_cache_attention",
+    "lx2v_hip_kv_cache_attention", "lx2v_hip_mask_temporal",
 ]
 
 
@@ -150,6 +150,7 @@ def _load():
         "lx2v_hip_causal_attention": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),
         "lx2v_hip_mask_upload": (ip, [vp, vp, sz, sz, pp]),
         "lx2v_hip_mask_free": (ip, [vp, vp]),
+        "lx2v_hip_mask_temporal": (ip, [vp, vp, sz, vp, sz, pp]),
         "lx2v_hip_attention_masked": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),
         "lx2v_hip_kv_cache_new": (ip, [vp, sz, sz, sz, pp]),
         "lx2v_hip_kv_cache_free": (ip, [vp, vp]),
@@ -588,6 +589,14 @@ class HipBackend:
         h = ctypes.c_void_p()
         _check(lib.lx2v_hip_mask_upload(self.ctx, _ptr(m), sq, sk, ctypes.byref(h)))
         return Mask(self, h.value, sq, sk)
+
+    def mask_temporal(self, tq, tk) -> Mask:
+        """Resident mask "tk[j] <= tq[i]" built on the device (dit.rs:643-653)."""
+        q = np.ascontiguousarray(tq, np.uint64).ravel()
+        k = np.ascontiguousarray(tk, np.uint64).ravel()
+        h = ctypes.c_void_p()
+        _check(lib.lx2v_hip_mask_temporal(self.ctx, _ptr(q), q.size, _ptr(k), k.size, ctypes.byref(h)))
+        return Mask(self, h.value, q.size, k.size)
 
     # ---- backend.rs:333-392: KV cache / MemRoPE ----
     def kv_cache_new(self, heads: int, head_dim: int, capacity_tokens: int) -> KvCache:

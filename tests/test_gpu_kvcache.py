@@ -158,11 +158,40 @@ def test_attention_reads_the_cache_in_place(be, hd):
     kb, vb = c.kv()
     be.causal_attention(qb, kb, vb, heads, sq, sk, hd, m, o2)
     assert np.array_equal(u32(be.download(o1)), u32(be.download(o2)))
+    # the same mask built on the device from the temporal indices
+    mt = be.mask_temporal(tq, c.temporal())
+    o3 = be.alloc(sq * heads * hd, H.DTYPE_F32)
+    c.attention(qb, sq, mt, o3)
+    assert np.array_equal(u32(be.download(o3)), u32(be.download(o2)))
+    mt.free()
     # dense (no mask) as well
     c.attention(qb, sq, None, o1)
     be.attention(qb, kb, vb, heads, sq, sk, hd, o2)
     assert np.array_equal(u32(be.download(o1)), u32(be.download(o2)))
     m.free()
+
+
+@pytest.mark.parametrize("hd", [128, 48])
+def test_mask_temporal_matches_host_mask(be, hd):
+    """Random (unsorted, repeated) temporal indices, ragged sizes: the device-built
+    mask gives the same attention as the host-built one, bit for bit."""
+    rng = np.random.default_rng(hd + 1)
+    heads, sq, sk = 2, 300, 777
+    tq = rng.integers(0, 40, sq)
+    tk = rng.integers(0, 40, sk)
+    tk[5] = 0  # every query has an allowed key
+    mask = tk[None, :] <= tq[:, None]
+    q = O.bf16_round(rng.standard_normal((heads, sq, hd)).astype(np.float32))
+    k = O.bf16_round(rng.standard_normal((heads, sk, hd)).astype(np.float32))
+    v = O.bf16_round(rng.standard_normal((heads, sk, hd)).astype(np.float32))
+    qb, kb, vb = (_up(be, a, H.DTYPE_BF16) for a in (q, k, v))
+    o1, o2 = be.alloc(sq * heads * hd, H.DTYPE_F32), be.alloc(sq * heads * hd, H.DTYPE_F32)
+    m1, m2 = be.mask_upload(mask, sq, sk), be.mask_temporal(tq, tk)
+    be.causal_attention(qb, kb, vb, heads, sq, sk, hd, m1, o1)
+    be.causal_attention(qb, kb, vb, heads, sq, sk, hd, m2, o2)
+    assert np.array_equal(u32(be.download(o1)), u32(be.download(o2)))
+    m1.free()
+    m2.free()
 
 
 def test_wan_shape(be):
