@@ -469,7 +469,15 @@ def main():
     be.sync()
     tq = temporal[5].astype(np.int64)
     kmask = np.array(kvc.temporal())[None, :] <= tq[:, None]
-    km = be.mask_upload(kmask, rows, len(kvc))
+    # the step's mask, built on the device from the temporal indices (the
+    # reference builds the [sq, sk] bools on the host, dit.rs:643-653)
+    be.sync()
+    t0 = time.perf_counter()
+    km = be.mask_temporal(temporal[5], kvc.temporal())
+    mask_ms = (time.perf_counter() - t0) * 1e3
+    t0 = time.perf_counter()
+    be.mask_upload(kmask, rows, len(kvc)).free()
+    upload_ms = (time.perf_counter() - t0) * 1e3
     qb_, ob_ = be.alloc(heads * rows * hd), be.alloc(rows * heads * hd)
     be.fill_normal(qb_, 1702, 1.0)
     kvc.attention(qb_, rows, km, ob_)
@@ -498,6 +506,7 @@ def main():
           "attention_tflops_allowed_pairs": round(4.0 * hd * kpairs / (kv_attn_us * 1e-6) / 1e12, 1),
           "put_and_update_rerun_step_us": round(put_us, 2),
           "put_and_update_first_step_us": round(evict_us, 2),
+          "step_mask_ms": {"device_from_temporal": round(mask_ms, 3), "host_bools_uploaded": round(upload_ms, 3)},
           "kernels": "k_kv_copy, k_kv_remap (HBM), k_attn_mfma"}
     log(f"bench: kv cache attention {kv_attn_us:.1f} us, re-run put+update {put_us:.1f} us, "
         f"first step {evict_us:.1f} us")
