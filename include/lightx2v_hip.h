@@ -226,6 +226,16 @@ int lx2v_hip_layer_norm(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t rows, s
 int lx2v_hip_residual_norm(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_buf *a, size_t rows,
                            size_t dim, const lx2v_hip_buf *mods, int has_gate, size_t gate,
                            const lx2v_hip_norm_t *norm, float eps, lx2v_hip_buf *normed);
+/* linear followed by gate_residual in one call: h[h_row + r] += act(x W^T +
+ * b)[r] * mods[gate] for r < rows (no reference counterpart: dit.rs runs
+ * `linear` into a temporary, then `gate_residual`, after the attention O,
+ * cross-attention O and FFN-down projections).  Results equal that pair's
+ * with the temporary in h's dtype, bit for bit.  On the FP8 e4m3 path the
+ * add rides in the GEMM's epilogue (no temporary is written); elsewhere the
+ * pair runs as two launches. */
+int lx2v_hip_linear_residual(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                             const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act, lx2v_hip_buf *h,
+                             size_t h_row, const lx2v_hip_buf *mods, size_t gate);
 /* In place on h: h += a * mods[gate] (backend.rs:243-252). */
 int lx2v_hip_gate_residual(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_buf *a, size_t rows,
                            size_t dim, const lx2v_hip_buf *mods, size_t gate);

@@ -102,6 +102,10 @@ constexpr int stage_swz() {
 struct MxOut {
     uint8_t *scales = nullptr;
     int rows = 0;
+    // Residual mode (bf16 / f32 output only): Y holds the residual stream h
+    // and the tile is added in, Y[m][n] = Y[m][n] + y[m][n] * gate[n], with
+    // y as the plain epilogue would have stored it.
+    const float *gate = nullptr;
 };
 
 // Stage 1 of the staged epilogue for one wave: its accumulators, scaled by
@@ -212,9 +216,22 @@ __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const fl
     }
 }
 
+// h + y * g for one staged element, the product and the sum rounded apart
+// (no contraction): the result of storing y, then h += y * g in f32.
+template <typename TY>
+__device__ __forceinline__ TY residual1(TY h, TY y, float g) {
+#pragma clang fp contract(off)
+    if constexpr (sizeof(TY) == 2) {
+        const float r = bf16_bits_to_f32(h) + bf16_bits_to_f32(y) * g;
+        return f32_to_bf16_bits(r);
+    } else {
+        return h + y * g;
+    }
+}
+
 template <int R, int BN, int NT, typename TY>
 __device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m0, int n0, int M, int N,
-                                              TY *__restrict__ Y) {
+                                              TY *__restrict__ Y, const float *__restrict__ gate = nullptr) {
     constexpr int EB = sizeof(TY), RB = BN * EB, CPR = RB / 16, EPC = 16 / EB, SWZ = stage_swz<BN, TY>();
     static_assert((R * CPR) % NT == 0, "staging tile must split evenly over the block");
     const bool vec = N % EPC == 0;
@@ -223,8 +240,14 @@ __device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m
         const int idx = it * NT + tid, r = idx / CPR, c = idx % CPR;
         const int m = m0 + r, n = n0 + c * EPC;
         if (m >= M || n >= N) continue;
-        const u32x4 v = *(const u32x4 *)(stg + r * RB + ((c ^ (r & (SWZ - 1))) << 4));
+        u32x4 v = *(const u32x4 *)(stg + r * RB + ((c ^ (r & (SWZ - 1))) << 4));
         TY *yp = Y + (size_t)m * N + n;
+        if (gate) {  // residual mode (uniform)
+            TY *e = (TY *)&v;
+#pragma unroll
+            for (int q = 0; q < EPC; q++)
+                if (n + q < N) e[q] = residual1<TY>(yp[q], e[q], gate[n + q]);
+        }
         if (vec) {
             *(u32x4 *)yp = v;
         } else {
@@ -259,7 +282,10 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uin
         if (wr < (p + 1) * R && wr + 32 * TM > p * R)
             acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, R, wr, wc, lane, act, mx, m0, n0, M, N);
         __syncthreads();
-        lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y);
+        if constexpr (sizeof(TY) == 1)
+            lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y);
+        else
+            lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
     }
 }
 

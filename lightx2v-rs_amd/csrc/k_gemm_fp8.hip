@@ -259,7 +259,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                                                                    int act, int tiles_m, int tiles_n,
                                                                    const uint8_t *__restrict__ amx,
                                                                    uint32_t amx_len, int amx_rows,
-                                                                   uint8_t *__restrict__ ymx, int ymx_rows) {
+                                                                   uint8_t *__restrict__ ymx, int ymx_rows,
+                                                                   const float *__restrict__ gate) {
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -465,6 +466,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     MxOut mx;
     mx.scales = ymx;
     mx.rows = ymx_rows;
+    mx.gate = gate;
     staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N,
                                                           act, Y, mx);
 }
@@ -494,7 +496,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
                                                        const float *__restrict__ sb,
                                                        const float *__restrict__ bias,
                                                        TY *__restrict__ Y, int M, int N, int K, int act,
-                                                       int tiles_m, int tiles_n) {
+                                                       int tiles_m, int tiles_n, const float *__restrict__ gate) {
     constexpr int BM = 256;
     static_assert(GM * GN == 4, "four waves per group");
     constexpr int WM = BM / 2 / GM, WN = BN / GN, TM = WM / 32, TN = WN / 32, KK = BKB / 64;
@@ -609,21 +611,23 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
     }
     if (grp == 0) __builtin_amdgcn_s_barrier();
     ops.park(sc, tid, m0, n0, M, N, sa, sb);
+    MxOut mx;
+    mx.gate = gate;
     staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY>(acc, smem, sc, grp * (BM / 2) + wm * WM, wn * WN, tid, lane,
-                                                        m0, n0, M, N, act, Y);
+                                                        m0, n0, M, N, act, Y, mx);
 }
 
 template <int BN, int GM, int GN, int BKB, int NS>
 void launch_pp(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
-               const float *bias, int act, void *y, int y_dtype, int M, int N, int K) {
+               const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const float *gate) {
     int tiles_m = (M + 255) / 256, tiles_n = (N + BN - 1) / BN;
     dim3 grid(tiles_m * tiles_n), block(512);
     if (y_dtype == LX2V_DTYPE_BF16)
         hipLaunchKernelGGL((k_gemm_fp8_pp<BN, GM, GN, BKB, NS, uint16_t>), grid, block, 0, s, a, sa, b, sb, bias,
-                           (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
+                           (uint16_t *)y, M, N, K, act, tiles_m, tiles_n, gate);
     else
         hipLaunchKernelGGL((k_gemm_fp8_pp<BN, GM, GN, BKB, NS, float>), grid, block, 0, s, a, sa, b, sb, bias,
-                           (float *)y, M, N, K, act, tiles_m, tiles_n);
+                           (float *)y, M, N, K, act, tiles_m, tiles_n, gate);
 }
 
 template <int BM, int BN>
@@ -650,7 +654,7 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
     const int arows = (int)mx.a_rows, yrows = (int)mx.y_rows;
 #define LX2V_DMA(AMV, T)                                                                                         \
     hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, AMV, T>), grid, block, 0, s, a, sa, b, sb, \
-                       bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y, yrows)
+                       bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y, yrows, mx.gate)
     if constexpr (MXIN) {
         if (mx.a) {
             if (y_dtype == LX2V_DTYPE_BF16)
@@ -706,7 +710,7 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 4:
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
-        default: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        default: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx.gate); break;
     }
 }
 

@@ -98,6 +98,7 @@ struct CtxExtra {
     Stage stage;
     Stage mask;  // causal_attention's host mask, uploaded per call, and its tile summary
     Stage kv_spare;  // the MemRoPE update's output layout, swapped with the cache it updates
+    Stage resid;     // linear_residual's output where the add cannot ride in the GEMM
 };
 
 }  // namespace
@@ -313,6 +314,7 @@ int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
     if (x.stage.ptr) (void)hipFree(x.stage.ptr);
     if (x.mask.ptr) (void)hipFree(x.mask.ptr);
     if (x.kv_spare.ptr) (void)hipFree(x.kv_spare.ptr);
+    if (x.resid.ptr) (void)hipFree(x.resid.ptr);
     extras().erase(ctx);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -1783,9 +1785,10 @@ static int act_quant_into_ws(lx2v_hip_ctx *ctx, const void *x, int dtype, size_t
     return run(ctx, "act_quant_e4m3", [&] { launch_act_quant(ctx->stream, x, dtype, rows, cols, *q, *s); });
 }
 
-int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
-                    const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y,
-                    size_t y_row) {
+// gate: residual mode (only where linear_fusable says so): y is the
+// residual stream, y[r] += out[r] * gate.
+static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows, const lx2v_hip_weight *w,
+                      const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y, size_t y_row, const float *gate) {
     NEED(ctx, "ctx");
     NEED(x, "x");
     NEED(w, "weight");
@@ -1863,6 +1866,7 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
             mx.y = y->mxs + 4 * y_row;
             mx.y_rows = y->srows;
         }
+        mx.gate = gate;
         if (w->group == K && gemm_fp8_supported(rows, N, K)) {
             const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx);
             if (int rc = run(ctx, "gemm_fp8_e4m3", [&] {
@@ -1915,6 +1919,56 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
         }))
         return rc;
     return ok();
+}
+
+int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                    const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y,
+                    size_t y_row) {
+    return linear_run(ctx, x, x_row, rows, w, bias, act, y, y_row, nullptr);
+}
+
+// The residual add can ride in the GEMM's epilogue: FP8 weight with one scale
+// per channel on the e4m3 path, a bf16 / f32 output, and a direct-to-LDS or
+// ping-pong configuration (K % 128 == 0).
+static bool linear_fusable(const lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t rows, const lx2v_hip_weight *w,
+                           const lx2v_hip_buf *h) {
+    const size_t N = w->rows, K = w->cols;
+    if (w->fmt != LX2V_WFMT_FP8 || h->quantized() || w->group != K || !gemm_fp8_supported(rows, N, K)) return false;
+    if (!(ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized())) return false;
+    const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3;
+    return plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx).kernel >= 0;
+}
+
+int lx2v_hip_linear_residual(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                             const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act, lx2v_hip_buf *h,
+                             size_t h_row, const lx2v_hip_buf *mods, size_t gate) {
+    NEED(ctx, "ctx");
+    NEED(x, "x");
+    NEED(w, "weight");
+    NEED(h, "h");
+    if (h->quantized()) return fail(LX2V_ERR_BAD_ARG, "linear_residual: h is an F32 or BF16 buffer");
+    const size_t N = w->rows;
+    if (h_row + rows < h_row || (h_row + rows) * N > h->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "h has %zu elements, rows [%zu,+%zu) x %zu need %zu", h->len, h_row, rows, N,
+                    (h_row + rows) * N);
+    if (mods && overlap(mods->ptr, mods->bytes(), (char *)h->ptr + h_row * N * h->elem_bytes(), rows * N * h->elem_bytes()))
+        return fail(LX2V_ERR_ALIAS, "linear_residual: h overlaps mods");
+    if (!rows) return ok();
+    if (int rc = set_dev(ctx)) return rc;
+    const float *g = nullptr;  // slot 2 of the staging: linear's bias conversion uses slot 0
+    if (int rc = param_f32(ctx, mods, gate * N, N, 2, &g, "mods (gate)")) return rc;
+    if (linear_fusable(ctx, x, rows, w, h)) return linear_run(ctx, x, x_row, rows, w, bias, act, h, h_row, g);
+    // Elsewhere: the linear into a workspace of h's dtype, then the add.
+    auto &st = extras()[ctx].resid;
+    if (int rc = ensure(ctx, &st.ptr, &st.bytes, rows * N * h->elem_bytes(), "residual workspace alloc")) return rc;
+    lx2v_hip_buf yb;
+    yb.ptr = st.ptr;
+    yb.len = rows * N;
+    yb.dtype = h->dtype;
+    if (int rc = linear_run(ctx, x, x_row, rows, w, bias, act, &yb, 0, nullptr)) return rc;
+    return run(ctx, "gate_residual", [&] {
+        launch_gate_residual(ctx->stream, (char *)h->ptr + h_row * N * h->elem_bytes(), yb.ptr, h->dtype, g, rows, N);
+    });
 }
 
 int lx2v_hip_act_quant(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows, size_t cols,

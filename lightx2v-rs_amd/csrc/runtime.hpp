@@ -218,6 +218,10 @@ struct Fp8Mx {
     size_t a_len = 0, a_rows = 0;
     uint8_t *y = nullptr;
     size_t y_rows = 0;
+    // Residual mode (y_dtype BF16 / F32, the direct-to-LDS and ping-pong
+    // kernels only): y is the residual stream h, updated in place,
+    // h[m][n] += out[m][n] * gate[n] with out as the plain store would write it.
+    const float *gate = nullptr;
 };
 bool gemm_fp8_supported(size_t M, size_t N, size_t K);
 Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in);

@@ -48,7 +48,7 @@ EXPORTS = [
     "lx2v_hip_attention_masked", "lx2v_hip_kv_cache_new", "lx2v_hip_kv_cache_free", "lx2v_hip_kv_cache_append",
     "lx2v_hip_kv_cache_put", "lx2v_hip_kv_cache_len", "lx2v_hip_kv_cache_temporal", "lx2v_hip_kv_cache_kinds",
     "lx2v_hip_kv_cache_kv", "lx2v_hip_kv_cache_read", "lx2v_hip_kv_cache_memrope_update",
-    "lx2v_hip_kv_cache_attention", "lx2v_hip_mask_temporal",
+    "lx2v_hip_kv_cache_attention", "lx2v_hip_mask_temporal", "lx2v_hip_linear_residual",
 ]
 
 
@@ -165,6 +165,7 @@ def _load():
         "lx2v_hip_kv_cache_attention": (ip, [vp, vp, vp, sz, sz, sz, vp, vp]),
         "lx2v_hip_fill_normal": (ip, [vp, vp, ctypes.c_uint64, ctypes.c_float]),
         "lx2v_hip_linear": (ip, [vp, vp, sz, sz, vp, vp, ip, vp, sz]),
+        "lx2v_hip_linear_residual": (ip, [vp, vp, sz, sz, vp, vp, ip, vp, sz, vp, sz]),
         "lx2v_hip_act_quant": (ip, [vp, vp, sz, sz, sz, vp, vp]),
         "lx2v_hip_sync": (ip, [vp]),
         "lx2v_hip_profile_enable": (ip, [vp, ip]),
@@ -545,6 +546,12 @@ class HipBackend:
                y: Buf, y_row: int):
         _check(lib.lx2v_hip_linear(self.ctx, x.h, x_row, rows, w.h, bias.h if bias else None, act, y.h,
                                    y_row))
+
+    def linear_residual(self, x: Buf, x_row: int, rows: int, w: Weight, bias: Optional[Buf], act: int, h: Buf,
+                        h_row: int, mods: Buf, gate: int):
+        """h[h_row + r] += act(x W^T + b)[r] * mods[gate]: linear then gate_residual, fused on the FP8 path."""
+        _check(lib.lx2v_hip_linear_residual(self.ctx, x.h, x_row, rows, w.h, bias.h if bias else None, act, h.h,
+                                            h_row, mods.h, gate))
 
     # ---- backend.rs:214-252: the norms around the linears ----
     def layer_norm(self, x: Buf, rows: int, dim: int, norm: NormKind, mods: Optional[Buf], eps: float, out: Buf):
