@@ -308,7 +308,8 @@ def main():
     # cross Q; cross O -> residual_norm (mod) -> FFN up -> FFN down ->
     # gate_residual, per layer with its own modulation table.  "unfused":
     # the norms write bf16 and each linear quantizes its input per token;
-    # "fused": the norms write the e4m3 input directly (no quantize pass).
+    # "fused": the norms write the e4m3 input directly (no quantize pass) and
+    # FFN down adds its gated output into h in its epilogue (linear_residual).
     NK = H.NormKind
     h = be.alloc(M * DIM)
     be.fill_normal(h, 1201, 1.0)
@@ -339,8 +340,11 @@ def main():
                     be.linear(acts["x_o2"], 0, M, *lw["o2"], 0, outs["o2"], 0)
                     be.residual_norm(h, outs["o2"], M, DIM, md, None, NK.mod(4, 3), 1e-6, xin)
                     be.linear(xin, 0, M, *lw["ffn1"], 1, ffn_mx, 0)
-                    be.linear(ffn_mx, 0, M, *lw["ffn2"], 0, outs["ffn2"], 0)
-                    be.gate_residual(h, outs["ffn2"], M, DIM, md, 5)
+                    if fused:  # the gate-residual add in FFN down's epilogue
+                        be.linear_residual(ffn_mx, 0, M, *lw["ffn2"], 0, h, 0, md, 5)
+                    else:
+                        be.linear(ffn_mx, 0, M, *lw["ffn2"], 0, outs["ffn2"], 0)
+                        be.gate_residual(h, outs["ffn2"], M, DIM, md, 5)
         return run
 
     block = {}
@@ -570,7 +574,7 @@ def main():
             "unfused": block["unfused"], "fused": block["fused"],
             "what": "the chunk's 840 linears plus their producers and consumers (layer_norm, 2 residual_norm, "
                     "gate_residual per layer-step; attention excluded); fused = the norms write the FP8 "
-                    "linears' e4m3 inputs in the same pass",
+                    "linears' e4m3 inputs in the same pass and FFN down's epilogue does the gate-residual add",
         },
         "act_quant_ms_per_chunk": round(region["act_quant_chunk"], 3),
         "per_gemm": per,

@@ -229,24 +229,66 @@ __device__ __forceinline__ TY residual1(TY h, TY y, float g) {
     }
 }
 
-template <int R, int BN, int NT, typename TY>
+template <int R, int BN, int NT, typename TY, bool RES = true>
 __device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m0, int n0, int M, int N,
-                                              TY *__restrict__ Y, const float *__restrict__ gate = nullptr) {
+                                              TY *__restrict__ Y, const float *__restrict__ gate_arg = nullptr) {
+    const float *gate = RES ? gate_arg : nullptr;
     constexpr int EB = sizeof(TY), RB = BN * EB, CPR = RB / 16, EPC = 16 / EB, SWZ = stage_swz<BN, TY>();
+    constexpr int IT = R * CPR / NT;
     static_assert((R * CPR) % NT == 0, "staging tile must split evenly over the block");
     const bool vec = N % EPC == 0;
+    // Residual mode (uniform): every read of h and of the gate row for this
+    // pass is issued before the first use, so their latencies overlap.
+    // A thread's chunk column is the same in every iteration (NT is a
+    // multiple of the chunks per row), so its gate values are read once.
+    static_assert(NT % CPR == 0, "a thread keeps one chunk column");
+    u32x4 hv[RES ? IT : 1];
+    float gv[EPC];
+    if constexpr (RES) {
+        if (gate) {
+            const int n = n0 + (tid % CPR) * EPC;
 #pragma unroll
-    for (int it = 0; it < R * CPR / NT; it++) {
+            for (int q = 0; q < EPC; q++) gv[q] = 0.0f;
+            if (n + EPC <= N && (((uintptr_t)(gate + n)) & 15) == 0) {
+#pragma unroll
+                for (int q = 0; q < EPC; q += 4) {
+                    const f32x4 g4 = *(const f32x4 *)(gate + n + q);
+                    gv[q] = g4.x, gv[q + 1] = g4.y, gv[q + 2] = g4.z, gv[q + 3] = g4.w;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < EPC; q++)
+                    if (n + q < N) gv[q] = gate[n + q];
+            }
+#pragma unroll
+            for (int it = 0; it < IT; it++) {
+                const int idx = it * NT + tid, r = idx / CPR, m = m0 + r;
+                hv[it] = (u32x4){};
+                if (m >= M || n >= N) continue;
+                const TY *yp = Y + (size_t)m * N + n;
+                if (vec) {
+                    hv[it] = *(const u32x4 *)yp;
+                } else {
+                    TY *he = (TY *)&hv[it];
+#pragma unroll
+                    for (int q = 0; q < EPC; q++)
+                        if (n + q < N) he[q] = yp[q];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
         const int idx = it * NT + tid, r = idx / CPR, c = idx % CPR;
         const int m = m0 + r, n = n0 + c * EPC;
         if (m >= M || n >= N) continue;
         u32x4 v = *(const u32x4 *)(stg + r * RB + ((c ^ (r & (SWZ - 1))) << 4));
         TY *yp = Y + (size_t)m * N + n;
-        if (gate) {  // residual mode (uniform)
+        if (RES && gate) {
             TY *e = (TY *)&v;
+            const TY *he = (const TY *)&hv[RES ? it : 0];
 #pragma unroll
-            for (int q = 0; q < EPC; q++)
-                if (n + q < N) e[q] = residual1<TY>(yp[q], e[q], gate[n + q]);
+            for (int q = 0; q < EPC; q++) e[q] = residual1<TY>(he[q], e[q], gv[q]);
         }
         if (vec) {
             *(u32x4 *)yp = v;
@@ -267,7 +309,7 @@ constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
 // for every wave's last fragment reads before reusing the ring; the
 // operands in sc (TileOps) must be parked before the call.  The wave owns
 // tile rows [wr, wr + 32 TM) and columns [wc, wc + 32 TN).
-template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY>
+template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY, bool RES = true>
 __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, const float *sc, int wr,
                                                 int wc, int tid, int lane, int m0, int n0, int M, int N, int act,
                                                 TY *__restrict__ Y, MxOut mx = MxOut()) {
@@ -282,10 +324,10 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uin
         if (wr < (p + 1) * R && wr + 32 * TM > p * R)
             acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, R, wr, wc, lane, act, mx, m0, n0, M, N);
         __syncthreads();
-        if constexpr (sizeof(TY) == 1)
-            lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y);
+        if constexpr (sizeof(TY) == 1 || !RES)
+            lds_to_global<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y);
         else
-            lds_to_global<R, BN, NT, TY>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
+            lds_to_global<R, BN, NT, TY, true>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
     }
 }
 

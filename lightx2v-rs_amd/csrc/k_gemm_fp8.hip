@@ -496,7 +496,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
                                                        const float *__restrict__ sb,
                                                        const float *__restrict__ bias,
                                                        TY *__restrict__ Y, int M, int N, int K, int act,
-                                                       int tiles_m, int tiles_n, const float *__restrict__ gate) {
+                                                       int tiles_m, int tiles_n) {
     constexpr int BM = 256;
     static_assert(GM * GN == 4, "four waves per group");
     constexpr int WM = BM / 2 / GM, WN = BN / GN, TM = WM / 32, TN = WN / 32, KK = BKB / 64;
@@ -611,23 +611,22 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
     }
     if (grp == 0) __builtin_amdgcn_s_barrier();
     ops.park(sc, tid, m0, n0, M, N, sa, sb);
-    MxOut mx;
-    mx.gate = gate;
-    staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY>(acc, smem, sc, grp * (BM / 2) + wm * WM, wn * WN, tid, lane,
-                                                        m0, n0, M, N, act, Y, mx);
+    // no residual mode here: its prefetch registers would spill this tile
+    staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY, false>(acc, smem, sc, grp * (BM / 2) + wm * WM, wn * WN, tid,
+                                                               lane, m0, n0, M, N, act, Y);
 }
 
 template <int BN, int GM, int GN, int BKB, int NS>
 void launch_pp(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
-               const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const float *gate) {
+               const float *bias, int act, void *y, int y_dtype, int M, int N, int K) {
     int tiles_m = (M + 255) / 256, tiles_n = (N + BN - 1) / BN;
     dim3 grid(tiles_m * tiles_n), block(512);
     if (y_dtype == LX2V_DTYPE_BF16)
         hipLaunchKernelGGL((k_gemm_fp8_pp<BN, GM, GN, BKB, NS, uint16_t>), grid, block, 0, s, a, sa, b, sb, bias,
-                           (uint16_t *)y, M, N, K, act, tiles_m, tiles_n, gate);
+                           (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
     else
         hipLaunchKernelGGL((k_gemm_fp8_pp<BN, GM, GN, BKB, NS, float>), grid, block, 0, s, a, sa, b, sb, bias,
-                           (float *)y, M, N, K, act, tiles_m, tiles_n, gate);
+                           (float *)y, M, N, K, act, tiles_m, tiles_n);
 }
 
 template <int BM, int BN>
@@ -710,7 +709,7 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 4:
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
-        default: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx.gate); break;
+        default: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
     }
 }
 
@@ -725,6 +724,8 @@ int forced_cfg() {
 }
 
 }  // namespace
+
+bool gemm_fp8_residual_ok(const Fp8Plan &p) { return p.kernel >= 0 && p.kernel != 5; }
 
 bool gemm_fp8_supported(size_t M, size_t N, size_t K) {
     // 32-bit buffer offsets (the out-of-range offset 2^31 must stay past

@@ -1928,15 +1928,15 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
 }
 
 // The residual add can ride in the GEMM's epilogue: FP8 weight with one scale
-// per channel on the e4m3 path, a bf16 / f32 output, and a direct-to-LDS or
-// ping-pong configuration (K % 128 == 0).
+// per channel on the e4m3 path, a bf16 / f32 output, and a direct-to-LDS
+// configuration (K % 128 == 0; not the 256 x 256 ping-pong tile).
 static bool linear_fusable(const lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t rows, const lx2v_hip_weight *w,
                            const lx2v_hip_buf *h) {
     const size_t N = w->rows, K = w->cols;
     if (w->fmt != LX2V_WFMT_FP8 || h->quantized() || w->group != K || !gemm_fp8_supported(rows, N, K)) return false;
     if (!(ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized())) return false;
     const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3;
-    return plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx).kernel >= 0;
+    return gemm_fp8_residual_ok(plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx));
 }
 
 int lx2v_hip_linear_residual(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,

@@ -218,12 +218,14 @@ struct Fp8Mx {
     size_t a_len = 0, a_rows = 0;
     uint8_t *y = nullptr;
     size_t y_rows = 0;
-    // Residual mode (y_dtype BF16 / F32, the direct-to-LDS and ping-pong
-    // kernels only): y is the residual stream h, updated in place,
+    // Residual mode (y_dtype BF16 / F32, plans with gemm_fp8_residual_ok):
+    // y is the residual stream h, updated in place,
     // h[m][n] += out[m][n] * gate[n] with out as the plain store would write it.
     const float *gate = nullptr;
 };
 bool gemm_fp8_supported(size_t M, size_t N, size_t K);
+// Whether the plan's kernel takes Fp8Mx::gate (the residual epilogue).
+bool gemm_fp8_residual_ok(const Fp8Plan &p);
 Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in);
 void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t *a, const float *a_scale,
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
