@@ -437,42 +437,44 @@ __global__ __launch_bounds__(AT) void k_mask_pack(const uint8_t *__restrict__ ma
 }
 
 // The MemRoPE block mask from temporal indices (dit.rs:643-653): pair
-// (q, k) is allowed iff tk[k] <= tq[q].  Bytes: 16 per thread; bits: a thread
-// per 32-key word; tile summary: a wave per tile from the min / max of the
-// tile's query and key indices (all allowed iff max tk <= min tq, none iff
-// min tk > max tq).
+// (q, k) is allowed iff tk[k] <= tq[q].  Bytes: a thread per 16 keys of a
+// query row (rows from blockIdx.y); bits: a wave per 64-key block and 64
+// queries, one ballot per query; tile summary: a wave per tile from the
+// min / max of the tile's query and key indices (all allowed iff
+// max tk <= min tq, none iff min tk > max tq).
 __global__ __launch_bounds__(AT) void k_mask_temporal_bytes(const uint64_t *__restrict__ tq, const uint64_t *__restrict__ tk,
                                                             int sq, int sk, uint8_t *__restrict__ mask) {
-    const size_t n = (size_t)sq * sk;
-    for (size_t i0 = (blockIdx.x * (size_t)AT + threadIdx.x) * 16; i0 < n; i0 += (size_t)gridDim.x * AT * 16) {
-        uint8_t v[16];
-        size_t q = i0 / sk, k = i0 % sk;
+    const int chunks = (sk + 15) / 16;
+    for (int q = blockIdx.y; q < sq; q += gridDim.y) {
+        const uint64_t tqv = tq[q];
+        uint8_t *row = mask + (size_t)q * sk;
+        for (int c = blockIdx.x * AT + threadIdx.x; c < chunks; c += gridDim.x * AT) {
+            const int k0 = 16 * c;
+            uint8_t v[16];
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            v[e] = i0 + e < n ? (uint8_t)(tk[k] <= tq[q]) : 0;
-            if (++k == (size_t)sk) k = 0, q++;
-        }
-        if (i0 + 16 <= n && (((uintptr_t)(mask + i0)) & 15) == 0) {
-            *(u32x4 *)(mask + i0) = *(const u32x4 *)v;
-        } else {
-            for (int e = 0; e < 16 && i0 + e < n; e++) mask[i0 + e] = v[e];
+            for (int e = 0; e < 16; e++) v[e] = k0 + e < sk ? (uint8_t)(tk[k0 + e] <= tqv) : 0;
+            if (k0 + 16 <= sk && (((uintptr_t)(row + k0)) & 15) == 0) {
+                *(u32x4 *)(row + k0) = *(const u32x4 *)v;
+            } else {
+                for (int e = 0; e < 16 && k0 + e < sk; e++) row[k0 + e] = v[e];
+            }
         }
     }
 }
 
 __global__ __launch_bounds__(AT) void k_mask_temporal_bits(const uint64_t *__restrict__ tq, const uint64_t *__restrict__ tk,
                                                            int sq, int sk, uint32_t *__restrict__ bits) {
-    const int nw = (sk + 31) / 32;
-    const size_t n = (size_t)sq * nw;
-    for (size_t t = blockIdx.x * (size_t)AT + threadIdx.x; t < n; t += (size_t)gridDim.x * AT) {
-        const int q = (int)(t / nw), w = (int)(t % nw);
-        const uint64_t tqv = tq[q];
-        uint32_t b = 0;
-        for (int e = 0; e < 32; e++) {
-            const int k = 32 * w + e;
-            if (k < sk && tk[k] <= tqv) b |= 1u << e;
-        }
-        bits[t] = b;
+    const int lane = threadIdx.x & 63, nw = (sk + 31) / 32, nkb = (sk + 63) / 64;
+    const size_t wave = blockIdx.x * (size_t)(AT / 64) + (threadIdx.x >> 6);
+    const int kb = (int)(wave % nkb), qg = (int)(wave / nkb);
+    if (qg * 64 >= sq) return;
+    const int k = 64 * kb + lane;
+    const uint64_t tkv = k < sk ? tk[k] : ~0ull;  // keys past sk: never allowed
+    const int q1 = min(qg * 64 + 64, sq);
+    for (int q = qg * 64; q < q1; q++) {
+        const uint64_t b = __ballot(k < sk && tkv <= tq[q]);
+        const int w = 2 * kb + (lane >> 5);
+        if ((lane & 31) == 0 && w < nw) bits[(size_t)q * nw + w] = (uint32_t)(lane ? b >> 32 : b);
     }
 }
 
@@ -526,11 +528,13 @@ void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk,
 void launch_mask_temporal(hipStream_t s, const uint64_t *tq, size_t sq, const uint64_t *tk, size_t sk, uint8_t *mask,
                           uint32_t *bits, uint8_t *tiles) {
     if (sq == 0 || sk == 0) return;
-    const size_t nb = sq * sk, nw = sq * ((sk + 31) / 32);
-    hipLaunchKernelGGL(k_mask_temporal_bytes, dim3((unsigned)std::min<size_t>((nb / 16 + AT) / AT, 16384)), dim3(AT), 0,
-                       s, tq, tk, (int)sq, (int)sk, mask);
-    hipLaunchKernelGGL(k_mask_temporal_bits, dim3((unsigned)std::min<size_t>((nw + AT - 1) / AT, 16384)), dim3(AT), 0,
-                       s, tq, tk, (int)sq, (int)sk, bits);
+    const size_t chunks = (sk + 15) / 16;
+    hipLaunchKernelGGL(k_mask_temporal_bytes,
+                       dim3((unsigned)((chunks + AT - 1) / AT), (unsigned)std::min<size_t>(sq, 65535)), dim3(AT), 0, s,
+                       tq, tk, (int)sq, (int)sk, mask);
+    const size_t waves = ((sk + 63) / 64) * ((sq + 63) / 64);
+    hipLaunchKernelGGL(k_mask_temporal_bits, dim3((unsigned)((waves + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, tq, tk,
+                       (int)sq, (int)sk, bits);
     const int nqt = (int)((sq + AQ - 1) / AQ), nkt = (int)((sk + AK - 1) / AK);
     const size_t n = (size_t)nqt * nkt;
     hipLaunchKernelGGL(k_mask_temporal_tiles, dim3((unsigned)((n + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, tq, tk,
