@@ -437,26 +437,27 @@ __global__ __launch_bounds__(AT) void k_mask_pack(const uint8_t *__restrict__ ma
 }
 
 // The MemRoPE block mask from temporal indices (dit.rs:643-653): pair
-// (q, k) is allowed iff tk[k] <= tq[q].  Bytes: a thread per 16 keys of a
+// (q, k) is allowed iff tk[k] <= tq[q].  Bytes: a thread per 4 keys of a
 // query row (rows from blockIdx.y); bits: a wave per 64-key block and 64
 // queries, one ballot per query; tile summary: a wave per tile from the
 // min / max of the tile's query and key indices (all allowed iff
 // max tk <= min tq, none iff min tk > max tq).
 __global__ __launch_bounds__(AT) void k_mask_temporal_bytes(const uint64_t *__restrict__ tq, const uint64_t *__restrict__ tk,
                                                             int sq, int sk, uint8_t *__restrict__ mask) {
-    const int chunks = (sk + 15) / 16;
+    const int chunks = (sk + 3) / 4;
     for (int q = blockIdx.y; q < sq; q += gridDim.y) {
         const uint64_t tqv = tq[q];
         uint8_t *row = mask + (size_t)q * sk;
         for (int c = blockIdx.x * AT + threadIdx.x; c < chunks; c += gridDim.x * AT) {
-            const int k0 = 16 * c;
-            uint8_t v[16];
+            const int k0 = 4 * c;
+            uint32_t v = 0;
 #pragma unroll
-            for (int e = 0; e < 16; e++) v[e] = k0 + e < sk ? (uint8_t)(tk[k0 + e] <= tqv) : 0;
-            if (k0 + 16 <= sk && (((uintptr_t)(row + k0)) & 15) == 0) {
-                *(u32x4 *)(row + k0) = *(const u32x4 *)v;
+            for (int e = 0; e < 4; e++)
+                if (k0 + e < sk && tk[k0 + e] <= tqv) v |= 1u << (8 * e);
+            if (k0 + 4 <= sk && (((uintptr_t)(row + k0)) & 3) == 0) {
+                *(uint32_t *)(row + k0) = v;
             } else {
-                for (int e = 0; e < 16 && k0 + e < sk; e++) row[k0 + e] = v[e];
+                for (int e = 0; e < 4 && k0 + e < sk; e++) row[k0 + e] = (uint8_t)(v >> (8 * e));
             }
         }
     }
@@ -528,7 +529,7 @@ void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk,
 void launch_mask_temporal(hipStream_t s, const uint64_t *tq, size_t sq, const uint64_t *tk, size_t sk, uint8_t *mask,
                           uint32_t *bits, uint8_t *tiles) {
     if (sq == 0 || sk == 0) return;
-    const size_t chunks = (sk + 15) / 16;
+    const size_t chunks = (sk + 3) / 4;
     hipLaunchKernelGGL(k_mask_temporal_bytes,
                        dim3((unsigned)((chunks + AT - 1) / AT), (unsigned)std::min<size_t>(sq, 65535)), dim3(AT), 0, s,
                        tq, tk, (int)sq, (int)sk, mask);
