@@ -400,22 +400,24 @@ __global__ __launch_bounds__(AT) void k_attn_rows(const void *__restrict__ Q, co
     }
 }
 
-// Mask summary per (128-query, 64-key) tile: 0 no pair allowed, 1 every
-// pair allowed, 2 mixed.  One wave per tile; pairs past sq / sk ignored.
-__global__ __launch_bounds__(AT) void k_mask_tiles(const uint8_t *__restrict__ mask, int sq, int sk, int nqt, int nkt,
-                                                   uint8_t *__restrict__ tiles) {
-    const int lane = threadIdx.x & 63;
+// Mask summary per (256-query, 64-key) tile: 0 no pair allowed, 1 every
+// pair allowed, 2 mixed; pairs past sq / sk ignored.  From the packed bits
+// (launch_mask_pack's words): a wave per tile reads its 256 queries' two
+// words (2 KB, where the bytes would be 16 KB).
+__global__ __launch_bounds__(AT) void k_mask_tiles_bits(const uint32_t *__restrict__ bits, int sq, int sk, int nqt,
+                                                        int nkt, uint8_t *__restrict__ tiles) {
+    const int lane = threadIdx.x & 63, nw = (sk + 31) / 32;
     const size_t t = blockIdx.x * (size_t)(AT / 64) + (threadIdx.x >> 6);
     if (t >= (size_t)nqt * nkt) return;
     const int qt = (int)(t / nkt), kt = (int)(t % nkt);
     bool any = false, all = true;
-    for (int i = lane; i < AQ * AK; i += 64) {
-        const int q = qt * AQ + i / AK, k = kt * AK + i % AK;
-        if (q < sq && k < sk) {
-            const bool a = mask[(size_t)q * sk + k] != 0;
-            any |= a;
-            all &= a;
-        }
+    for (int i = lane; i < 2 * AQ; i += 64) {
+        const int q = qt * AQ + i / 2, j = i % 2, left = sk - (kt * AK + 32 * j);
+        if (q >= sq || left <= 0) continue;
+        const uint32_t vm = left >= 32 ? ~0u : (1u << left) - 1u;
+        const uint32_t w = bits[(size_t)q * nw + 2 * kt + j] & vm;
+        any |= w != 0;
+        all &= w == vm;
     }
     const bool wany = __ballot(any) != 0, wall = __ballot(!all) == 0;
     if (lane == 0) tiles[t] = !wany ? 0 : (wall ? 1 : 2);
@@ -518,12 +520,12 @@ void attn_mfma_od(hipStream_t s, dim3 grid, const void *q, const void *k, const 
 
 bool attention_mfma_supported(size_t d) { return d == 64 || d == 128; }
 
-void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint8_t *tiles) {
+void launch_mask_tiles_bits(hipStream_t s, const uint32_t *bits, size_t sq, size_t sk, uint8_t *tiles) {
     const int nqt = (int)((sq + AQ - 1) / AQ), nkt = (int)((sk + AK - 1) / AK);
     const size_t n = (size_t)nqt * nkt;
     if (n == 0) return;
-    hipLaunchKernelGGL(k_mask_tiles, dim3((unsigned)((n + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, mask, (int)sq,
-                       (int)sk, nqt, nkt, tiles);
+    hipLaunchKernelGGL(k_mask_tiles_bits, dim3((unsigned)((n + AT / 64 - 1) / (AT / 64))), dim3(AT), 0, s, bits,
+                       (int)sq, (int)sk, nqt, nkt, tiles);
 }
 
 void launch_mask_temporal(hipStream_t s, const uint64_t *tq, size_t sq, const uint64_t *tk, size_t sk, uint8_t *mask,

@@ -1070,7 +1070,7 @@ static int mask_fill(lx2v_hip_ctx *ctx, const uint8_t *host, size_t sq, size_t s
     HIP_TRY(hipMemcpyAsync(base, host, nb, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(mask)");
     return run(ctx, "mask_tiles", [&] {
         launch_mask_pack(ctx->stream, base, sq, sk, m->bits);
-        launch_mask_tiles(ctx->stream, base, sq, sk, m->tiles);
+        launch_mask_tiles_bits(ctx->stream, m->bits, sq, sk, m->tiles);
     });
 }
 

@@ -154,14 +154,16 @@ void launch_gate_residual(hipStream_t s, void *h, const void *a, int dt, const f
 // ---- attention (k_attn.hip) -------------------------------------------------------
 // out [sq, heads*d] = softmax(q k^T / sqrt(d), mask) v; q [heads, sq, d], k / v
 // [heads, kvs, d] of dtype dt, keys 0 .. sk - 1 of each head used (kvs >= sk); mask [sq, sk] bytes or null; tiles its summary
-// (launch_mask_tiles, mask_tile_count entries) or null; out of dtype odt.
+// (launch_mask_tiles_bits or launch_mask_temporal, mask_tile_count entries) or
+// null; out of dtype odt.
 // mbits: the mask as bits (launch_mask_pack, mask_word_count words), read by
 // the MFMA kernel in mixed tiles; the per-query kernel reads the bytes.
 bool attention_mfma_supported(size_t d);
 size_t mask_tile_count(size_t sq, size_t sk);
 size_t mask_word_count(size_t sq, size_t sk);
-void launch_mask_tiles(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint8_t *tiles);
 void launch_mask_pack(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, uint32_t *bits);
+// The tile summary from the packed bits (launch_mask_pack's output).
+void launch_mask_tiles_bits(hipStream_t s, const uint32_t *bits, size_t sq, size_t sk, uint8_t *tiles);
 // All three forms of the mask "tk[k] <= tq[q]" from temporal indices.
 void launch_mask_temporal(hipStream_t s, const uint64_t *tq, size_t sq, const uint64_t *tk, size_t sk, uint8_t *mask,
                           uint32_t *bits, uint8_t *tiles);
