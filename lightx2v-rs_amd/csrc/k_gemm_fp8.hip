@@ -249,7 +249,15 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8(const uint8_t *__restrict__
 // byte 0 (the byte the MFMA's scale operand reads); the weight's scale
 // operand is 2^0.  TY = uint8_t writes MX e4m3 output (codes to Y, scales
 // to ymx).
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC, int AM, typename TY>
+//
+// Grouped weight scales (GS = 1): one scale per 128 columns of K per channel
+// (Fp8E4M3 with group 128, quant.rs:21, 425-429), BKB = 128 so that a stage
+// is exactly one scale group.  Wave 0 adds one DMA per stage: the stage's
+// BN channel scales from the stage-major copy (row 2 kt of gsc, N floats a
+// row).  Each stage's two MFMAs per block run into a fresh partial sum,
+// which is then folded in, acc += part * s[n, kt]; sb is then null (1 in the
+// epilogue) and sa still scales each token.
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC, int AM, int GS, typename TY>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint8_t *__restrict__ A,
                                                                    const float *__restrict__ sa,
                                                                    const uint8_t *__restrict__ B,
@@ -260,7 +268,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                                                                    const uint8_t *__restrict__ amx,
                                                                    uint32_t amx_len, int amx_rows,
                                                                    uint8_t *__restrict__ ymx, int ymx_rows,
-                                                                   const float *__restrict__ gate) {
+                                                                   const float *__restrict__ gate,
+                                                                   const float *__restrict__ gsc) {
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -276,8 +285,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     static_assert(((BM * BKB) & AMASK) == 0 && ((BN * BKB) & BMASK) == 0, "tile regions are powers of two");
     static_assert(ALD * RPI * NW == BM && BLD * RPI * NW == BN, "tile rows must split over the waves");
     using Ops = TileOps<BM, BN, 64 * NW>;
-    constexpr int ASL = AM ? 1024 : 16;  // per-stage LDS for A's block scales (BM rows x 4 bytes)
+    // per-stage LDS for A's block scales (BM rows x 4 bytes) or the weight's
+    // group scales (BN floats): a whole wave's 16-byte DMA (lanes whose
+    // offset is out of range still write their zeros)
+    constexpr int ASL = (AM || GS) ? 1024 : 16;
     static_assert(!AM || BM * 4 <= ASL, "A scale slot");
+    static_assert(!GS || (BKB == 128 && !AM && BN * 4 <= 64 * 16), "grouped scales: one 128-column group per stage");
+    constexpr bool XS = AM || GS;  // wave 0 issues one more load per stage
     static_assert(NS >= 2 && OCC * (NS * STAGE + Ops::NV * 4 + NS * ASL) <= 160 * 1024, "LDS for OCC workgroups per CU");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
     __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
@@ -300,8 +314,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // (readfirstlane: the saturating length would otherwise be computed on
     // the VALU and take the descriptor out of SGPRs)
     const auto rs_src = make_rsrc(
-        AM ? amx + 4 * m0 : A,
-        __builtin_amdgcn_readfirstlane(AM ? (amx_len > 4u * m0 ? amx_len - 4u * (uint32_t)m0 : 0u) : 0u));
+        AM ? amx + 4 * m0 : (GS ? (const uint8_t *)(gsc + n0) : A),
+        __builtin_amdgcn_readfirstlane(
+            AM ? (amx_len > 4u * m0 ? amx_len - 4u * (uint32_t)m0 : 0u)
+               : (GS ? ((uint32_t)(2 * KT) * (uint32_t)N - (uint32_t)n0) * 4u : 0u)));
 
     // Load i of this wave covers tile rows [(i NW + wid) RPI, +RPI); lane l
     // fills slot l % CPR of row l / CPR.
@@ -328,8 +344,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             dma16(rb_src, sbuf + (BM + ((n - ALD) * NW + wid_u) * RPI) * BKB,
                   in ? b_off[n >= ALD ? n - ALD : 0] + k0 : kOob);
     };
-    // Wave 0's MX scale load of stage kt (slot buf).
+    // Wave 0's MX scale load of stage kt (slot buf), or its group-scale load.
     auto issue_scales = [&](int kt, int buf) {
+        if constexpr (GS) {
+            // lane l: channels n0 + 4 l .. + 3 of stage kt's group; past the
+            // last channel the next row (or zeros at the end) is read, for
+            // channels that are never stored
+            if (wid_u == 0) {
+                const bool ok = kt < KT && lane < BN / 4;
+                dma16(rs_src, asl + buf * ASL, ok ? (uint32_t)(2 * kt) * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
+            }
+        }
         if constexpr (AM) {
             const bool in = kt < KT;
             // First in the stage's issue order: issued after the A / B
@@ -361,6 +386,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // its first MFMAs -- issued back to back right after the barrier, the
     // loads held both waves of a SIMD off the MFMA pipe (7-9% at one
     // workgroup per CU).  dkt < 0: no loads.
+    f32x16 part[GS ? TN : 1][GS ? TM : 1];  // grouped scales: this stage's partial sums
     auto compute = [&](int buf, int stage, int dkt, int dbuf) {
         const uint8_t *s = smem + buf * STAGE;
         uint32_t sraw[AM ? TM : 1];
@@ -424,8 +450,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                 for (int j = 0; j < TN; j++)
 #pragma unroll
                     for (int i = 0; i < TM; i++) {
-                        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                            bf[j], af[i], acc[j][i], 0, 0, 0, 0, 0, 0);
+                        if constexpr (GS)
+                            part[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                                bf[j], af[i], kk == 0 ? (f32x16){} : part[j][i], 0, 0, 0, 0, 0, 0);
+                        else
+                            acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                                bf[j], af[i], acc[j][i], 0, 0, 0, 0, 0, 0);
                         const int n = kk * TN * TM + j * TM + i;
                         if (n < ALD + BLD && dkt >= 0) {
                             __builtin_amdgcn_sched_barrier(0);
@@ -433,6 +463,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                             __builtin_amdgcn_sched_barrier(0);
                         }
                     }
+            }
+        }
+        if constexpr (GS) {
+            // acc += part * s[n, stage]: lane l's register 4 g + q of block j
+            // is channel wn WN + 32 j + 8 g + 4 (l / 32) + q of the tile
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                f32x4 g4[4];
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    g4[g] = *(const f32x4 *)(asl + buf * ASL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            acc[j][i][4 * g + q] = __builtin_fmaf(part[j][i][4 * g + q], g4[g][q], acc[j][i][4 * g + q]);
             }
         }
     };
@@ -450,13 +498,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 #pragma unroll
         for (int j = 0; j < NS; j++) {
             if (kt + j < KT) {
-                if (AM && wid_u == 0)  // wave 0 also loads each stage's A scales
+                if (XS && wid_u == 0)  // wave 0 also loads each stage's A or group scales
                     wait_vmcnt<(NS - 2) * (LPS + 1)>();
                 else
                     wait_vmcnt<(NS - 2) * LPS>();
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (AM) issue_scales(kt + j + NS - 1, (j + NS - 1) % NS);
+                if constexpr (XS) issue_scales(kt + j + NS - 1, (j + NS - 1) % NS);
                 compute(j, kt + j, kt + j + NS - 1, (j + NS - 1) % NS);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -644,16 +692,30 @@ void launch_cfg(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
 
 // MXOUT / MXIN: also instantiate the MX-output / MX-activation kernels (only
 // for the configurations the planner offers such shapes to).
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC = 1, bool MXOUT = false, bool MXIN = false>
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC = 1, bool MXOUT = false, bool MXIN = false,
+          bool GSC = false>
 void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
                 const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
     int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
     const uint32_t alen = (uint32_t)mx.a_len;
     const int arows = (int)mx.a_rows, yrows = (int)mx.y_rows;
-#define LX2V_DMA(AMV, T)                                                                                         \
-    hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, AMV, T>), grid, block, 0, s, a, sa, b, sb, \
-                       bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y, yrows, mx.gate)
+#define LX2V_DMA_G(AMV, GSV, T)                                                                              \
+    hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, AMV, GSV, T>), grid, block, 0, s, a, sa, b, \
+                       GSV ? nullptr : sb, bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y,  \
+                       yrows, mx.gate, mx.wgs)
+#define LX2V_DMA(AMV, T) LX2V_DMA_G(AMV, 0, T)
+    if constexpr (GSC) {
+        if (mx.wgs) {
+            if (y_dtype == LX2V_DTYPE_BF16)
+                LX2V_DMA_G(0, 1, uint16_t);
+            else if (y_dtype == LX2V_DTYPE_F32)
+                LX2V_DMA_G(0, 1, float);
+            else if constexpr (MXOUT)
+                LX2V_DMA_G(0, 1, uint8_t);
+            return;
+        }
+    }
     if constexpr (MXIN) {
         if (mx.a) {
             if (y_dtype == LX2V_DTYPE_BF16)
@@ -676,6 +738,7 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
     else
         LX2V_DMA(0, float);
 #undef LX2V_DMA
+#undef LX2V_DMA_G
 }
 
 
@@ -699,9 +762,13 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
                     const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
     switch (idx) {
         case 0:
-            launch_dma<256, 128, 4, 2, 128, 3, 1, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
+            launch_dma<256, 128, 4, 2, 128, 3, 1, true, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K,
+                                                                    mx);
             break;
-        case 1: launch_dma<128, 256, 2, 4, 128, 3>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
+        case 1:
+            launch_dma<128, 256, 2, 4, 128, 3, 1, false, false, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K,
+                                                                      mx);
+            break;
         case 2: launch_dma<256, 128, 4, 2, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
         case 3:
             launch_dma<128, 128, 2, 2, 64, 3, 3, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
@@ -726,6 +793,11 @@ int forced_cfg() {
 }  // namespace
 
 bool gemm_fp8_residual_ok(const Fp8Plan &p) { return p.kernel >= 0 && p.kernel != 5; }
+
+bool gemm_fp8_grouped_supported(size_t M, size_t N, size_t K, size_t group) {
+    return group == 128 && K % 128 == 0 && N % 4 == 0 && gemm_fp8_supported(M, N, K) &&
+           (K / 64) * N * 4 < (1ull << 31);
+}
 
 bool gemm_fp8_supported(size_t M, size_t N, size_t K) {
     // 32-bit buffer offsets (the out-of-range offset 2^31 must stay past
@@ -754,24 +826,49 @@ constexpr CfgCost kAuto[] = {
     {3, 0.606, 0.44, 4.59},   // 128 x 128, three per CU
     {5, 1.121, 14.77, 0.0},   // 256 x 256 ping-pong
 };
+// Grouped weight scales (128-byte stages only): the two one-per-CU tiles,
+// with the per-CU costs of their per-channel versions.
+constexpr CfgCost kGroupedAuto[] = {
+    {0, 0.625, 8.16, 0.21},  // 256 x 128
+    {1, 0.625, 8.16, 0.21},  // 128 x 256
+};
 
 // The configurations with MX-activation / MX-output kernels.  The 128 x 256
 // two-per-CU tile takes no MX activations: their scale handling needs more
 // than the 128 VGPRs two workgroups per CU leave a wave.
 bool mx_capable(int idx, bool mx_in) { return idx == 0 || idx == 3 || (idx == 4 && !mx_in); }
+// The configurations built with grouped weight scales (128-byte stages, one
+// workgroup per CU: the partial sums need the registers); MX output on the
+// 256 x 128 tile only, no MX activations.
+bool grouped_capable(int idx, bool mx, bool mx_in) { return !mx_in && (idx == 0 || (idx == 1 && !mx)); }
 
-Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in) {
+Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped) {
     Fp8Plan p;
     if (K % 128 != 0) return p;  // the register-staged kernel
     const int nd = (int)(sizeof(kDma) / sizeof(kDma[0]));
     const int forced = forced_cfg();
-    if (forced >= 0 && forced < nd && (!mx || mx_capable(forced, mx_in))) {
+    auto ok = [&](int idx) {
+        return grouped ? grouped_capable(idx, mx, mx_in) : (!mx || mx_capable(idx, mx_in));
+    };
+    if (forced >= 0 && forced < nd && ok(forced)) {
         p.kernel = forced;
         return p;
     }
     double best = 0.0;
+    for (const CfgCost &c : kGroupedAuto) {
+        if (!grouped || !ok(c.idx)) continue;
+        const DmaCfg &d = kDma[c.idx];
+        const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
+        const double rounds = (double)((tiles + num_cu - 1) / num_cu);
+        const double t = rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us) + c.fixed_us;
+        if (p.kernel < 0 || t < best * 0.9999) {
+            best = t;
+            p.kernel = c.idx;
+        }
+    }
+    if (grouped) return p;
     for (const CfgCost &c : kAuto) {
-        if (mx && !mx_capable(c.idx, mx_in)) continue;
+        if (!ok(c.idx)) continue;
         const DmaCfg &d = kDma[c.idx];
         const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
         const double rounds = (double)((tiles + num_cu - 1) / num_cu);

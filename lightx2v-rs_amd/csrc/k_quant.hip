@@ -14,6 +14,7 @@
 #include <float.h>
 
 #include "device_common.hpp"
+#include "powf_arm.hpp"
 #include "runtime.hpp"
 
 namespace lx2v {
@@ -78,11 +79,9 @@ __device__ __forceinline__ float q4_code(float v, float is, float z) {
     return fminf(fmaxf(r, 0.0f), 15.0f);
 }
 
-// f32::powf(a, y) for a > 0: a^y in double, rounded once to f32.  glibc's
-// powf (what the Rust calls) returns the same f32 except for ~0.06% of
-// arguments, where it is one ulp away (host sweep of every f32 in [1e-9,
-// 100] at y = 0.7 - 1).
-__device__ __forceinline__ float powf_dbl(float a, float y) { return (float)pow((double)a, (double)y); }
+// f32::powf(a, y) for a > 0 as glibc computes it (powf_arm.hpp: bit-identical
+// to the libm on every positive f32 at y = 0.7 - 1).
+__device__ __forceinline__ float powf_ref(float a, float y) { return powf_arm::powf_pos(a, y); }
 
 __global__ __launch_bounds__(kQThreads) void k_quantize_q4_ref(const float *__restrict__ src, size_t ngroups,
                                                                size_t group, int hqq, uint8_t *__restrict__ packed,
@@ -113,7 +112,7 @@ __global__ __launch_bounds__(kQThreads) void k_quantize_q4_ref(const float *__re
                 float sh = 0.0f;
                 if (a > 0.0f) {
                     const float sg = __builtin_signbit(e) ? -1.0f : 1.0f;  // f32::signum
-                    sh = sg * fmaxf(a - powf_dbl(a, pm1) / beta, 0.0f);
+                    sh = sg * fmaxf(a - powf_ref(a, pm1) / beta, 0.0f);
                 }
                 zsum += c - (v - sh) * is;
             }

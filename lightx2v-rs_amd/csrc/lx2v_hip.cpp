@@ -51,12 +51,6 @@ int ok() {
 
 bool valid_dtype(int d) { return d == LX2V_DTYPE_F32 || d == LX2V_DTYPE_BF16; }
 
-// Device-side staging owned by the context for boundary conversions.
-struct Stage {
-    void *ptr = nullptr;
-    size_t bytes = 0;
-};
-
 int ensure(lx2v_hip_ctx *ctx, void **ptr, size_t *have, size_t need, const char *what) {
     if (*have >= need) return LX2V_OK;
     if (ctx->capturing)
@@ -93,23 +87,7 @@ int not_capturing(const lx2v_hip_ctx *ctx, const char *what) {
     return LX2V_OK;
 }
 
-// Context-owned staging buffer (one per context, grown on demand).
-struct CtxExtra {
-    Stage stage;
-    Stage mask;  // causal_attention's host mask, uploaded per call, and its tile summary
-    Stage kv_spare;  // the MemRoPE update's output layout, swapped with the cache it updates
-    Stage resid;     // linear_residual's output where the add cannot ride in the GEMM
-};
-
 }  // namespace
-
-// Staging lives beside the context's workspace; stored in a side table keyed
-// by context so runtime.hpp stays free of it.
-#include <unordered_map>
-static std::unordered_map<const lx2v_hip_ctx *, CtxExtra> &extras() {
-    static std::unordered_map<const lx2v_hip_ctx *, CtxExtra> m;
-    return m;
-}
 
 namespace lx2v {
 
@@ -166,7 +144,7 @@ int run(lx2v_hip_ctx *ctx, const char *name, F &&fn) {
 }
 
 int stage_for(lx2v_hip_ctx *ctx, size_t bytes, void **out) {
-    auto &st = extras()[ctx].stage;
+    auto &st = ctx->stage;
     int rc = ensure(ctx, &st.ptr, &st.bytes, bytes, "staging alloc");
     if (rc) return rc;
     *out = st.ptr;
@@ -291,7 +269,6 @@ int lx2v_hip_create(int device, lx2v_hip_ctx **out) {
     }
     const char *pv = getenv("LIGHTX2V_PROFILE");
     ctx->prof.on = pv && strcmp(pv, "0") != 0;
-    extras()[ctx];
     *out = ctx;
     return ok();
 }
@@ -310,12 +287,8 @@ int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
     for (auto e : ctx->prof.pool) (void)hipEventDestroy(e);
     for (auto &r : ctx->prof.open_regions) (void)hipEventDestroy(r.second);
     if (ctx->ws) (void)hipFree(ctx->ws);
-    auto &x = extras()[ctx];
-    if (x.stage.ptr) (void)hipFree(x.stage.ptr);
-    if (x.mask.ptr) (void)hipFree(x.mask.ptr);
-    if (x.kv_spare.ptr) (void)hipFree(x.kv_spare.ptr);
-    if (x.resid.ptr) (void)hipFree(x.resid.ptr);
-    extras().erase(ctx);
+    for (lx2v::Stage *x : {&ctx->stage, &ctx->mask, &ctx->kv_spare, &ctx->resid})
+        if (x->ptr) (void)hipFree(x->ptr);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return ok();
@@ -1081,7 +1054,7 @@ int lx2v_hip_causal_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx
     if (int rc = attn_check(ctx, q, k, v, heads, sq, sk, head_dim, out)) return rc;
     if (int rc = not_capturing(ctx, "causal_attention with a host mask")) return rc;
     if (!heads || !sq || !sk) return attn_run(ctx, q, k, v, heads, sq, sk, head_dim, nullptr, out);  // sk = 0: zeros
-    auto &mb = extras()[ctx].mask;
+    auto &mb = ctx->mask;
     if (int rc = ensure(ctx, &mb.ptr, &mb.bytes, mask_bytes(sq, sk), "mask alloc")) return rc;
     lx2v_hip_mask m;
     if (int rc = mask_fill(ctx, mask, sq, sk, (uint8_t *)mb.ptr, &m)) return rc;
@@ -1523,7 +1496,7 @@ int lx2v_hip_kv_cache_memrope_update(lx2v_hip_ctx *ctx, lx2v_hip_kv *kv, const l
                 "hipMemcpyAsync(memrope plan)");
         HIP_TRY(hipEventRecord(kv->plan_done, ctx->stream), "memrope_update");
         // gather into the context's spare layout, then swap it with the cache's
-        auto &sp = extras()[ctx].kv_spare;
+        auto &sp = ctx->kv_spare;
         const size_t need = 2 * kv->heads * std::max(src.size(), kv->cap) * kv->d * kv->eb();
         if (int rc = ensure(ctx, &sp.ptr, &sp.bytes, need, "kv_cache spare alloc")) return rc;
         const size_t dcap = kv_cap_of(kv, sp.bytes), rows = src.size();
@@ -1811,11 +1784,15 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     }
     const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3, y_mx = y->dtype == LX2V_DTYPE_MXE4M3;
     if (y_mx && y->cols != N) return fail(LX2V_ERR_BAD_SHAPE, "MXE4M3 y has %zu cols, weight has %zu rows", y->cols, N);
-    if ((x_mx || y_mx) && (w->fmt != LX2V_WFMT_FP8 || w->group != K || K % 128 || !gemm_fp8_supported(rows, N, K) ||
-                           (x_mx && x_row % 16)))
+    // FP8 weights the fp8 MFMA takes: one scale per channel, or per 128 columns.
+    const bool fp8_grouped = w->fmt == LX2V_WFMT_FP8 && w->group != K && w->sscale && !x_mx &&
+                             gemm_fp8_grouped_supported(rows, N, K, w->group);
+    const bool fp8_mfma = w->fmt == LX2V_WFMT_FP8 && (w->group == K ? gemm_fp8_supported(rows, N, K) : fp8_grouped);
+    if ((x_mx || y_mx) && (!fp8_mfma || K % 128 || (x_mx && (w->group != K || x_row % 16))))
         return fail(LX2V_ERR_UNSUPPORTED,
-                    "MXE4M3 operands need an FP8 weight with one scale per channel, cols %% 128 == 0 and an MX "
-                    "input row offset %% 16 == 0 (weight %zux%zu group %zu, x_row %zu)",
+                    "MXE4M3 operands need an FP8 weight with cols %% 128 == 0 and one scale per channel (or, for an "
+                    "MX output only, per 128 columns), and an MX input row offset %% 16 == 0 (weight %zux%zu group "
+                    "%zu, x_row %zu)",
                     N, K, w->group, x_row);
     const char *xp = (const char *)x->ptr + x_row * K * x->elem_bytes();
     char *yp = (char *)y->ptr + y_row * N * y->elem_bytes();
@@ -1843,7 +1820,15 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         }
     }
 
-    if (w->fmt == LX2V_WFMT_FP8 && (ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized() || y_mx)) {
+    // The e4m3 path: quantized activations, MX output, or (per-token e4m3
+    // mode) an FP8 weight the fp8 MFMA takes or no bf16 GEMM tiles (the
+    // scalar kernel on e4m3 activations).  FP8 weights with other groups
+    // that the bf16 GEMM takes run it below (the weight dequantized to bf16
+    // in its loader, bf16 activations).
+    const bool w16_ok = gemm_w16_dma_supported(w, rows) ||
+                        (gemm_w16_supported(w) && rows * K * x->elem_bytes() < (1ull << 31));
+    if (w->fmt == LX2V_WFMT_FP8 &&
+        (x->quantized() || y_mx || (ctx->fp8_act == LX2V_FP8_ACT_E4M3 && (fp8_mfma || !w16_ok)))) {
         const uint8_t *q;
         const float *s = nullptr;
         Fp8Mx mx;
@@ -1867,9 +1852,18 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
             mx.y_rows = y->srows;
         }
         mx.gate = gate;
-        if (w->group == K && gemm_fp8_supported(rows, N, K)) {
-            const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx);
-            if (int rc = run(ctx, "gemm_fp8_e4m3", [&] {
+        if (fp8_mfma) {
+            if (fp8_grouped) mx.wgs = w->sscale;
+            const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx, fp8_grouped);
+            if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1)  // the tiles built with grouped scales
+                return fail(LX2V_ERR_UNSUPPORTED, "no grouped-scale fp8 kernel for configuration %d", plan.kernel);
+            // Profile name: the kernel configuration and the operand forms,
+            // e.g. "gemm_fp8_e4m3.c0.g128.mxout".
+            char pname[64];
+            char cfg[8] = "creg";  // the register-staged kernel (K % 128 != 0)
+            if (plan.kernel >= 0) snprintf(cfg, sizeof cfg, "c%d", plan.kernel);
+            snprintf(pname, sizeof pname, "gemm_fp8_e4m3.%s%s%s%s%s", cfg, fp8_grouped ? ".g128" : "", x_mx ? ".mxin" : "", y_mx ? ".mxout" : "", gate ? ".res" : "");
+            if (int rc = run(ctx, pname, [&] {
                     launch_gemm_fp8(ctx->stream, ctx->num_cu, plan, q, s, (const uint8_t *)w->codes, w->scales, bp,
                                     act, yp, y->dtype, rows, N, K, mx);
                 }))
@@ -1933,10 +1927,12 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
 static bool linear_fusable(const lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t rows, const lx2v_hip_weight *w,
                            const lx2v_hip_buf *h) {
     const size_t N = w->rows, K = w->cols;
-    if (w->fmt != LX2V_WFMT_FP8 || h->quantized() || w->group != K || !gemm_fp8_supported(rows, N, K)) return false;
-    if (!(ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized())) return false;
     const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3;
-    return gemm_fp8_residual_ok(plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx));
+    const bool grouped = w->group != K;
+    if (w->fmt != LX2V_WFMT_FP8 || h->quantized() || !gemm_fp8_supported(rows, N, K)) return false;
+    if (grouped && !(w->sscale && !x_mx && gemm_fp8_grouped_supported(rows, N, K, w->group))) return false;
+    if (!(ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized())) return false;
+    return gemm_fp8_residual_ok(plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx, grouped));
 }
 
 int lx2v_hip_linear_residual(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
@@ -1959,7 +1955,7 @@ int lx2v_hip_linear_residual(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_
     if (int rc = param_f32(ctx, mods, gate * N, N, 2, &g, "mods (gate)")) return rc;
     if (linear_fusable(ctx, x, rows, w, h)) return linear_run(ctx, x, x_row, rows, w, bias, act, h, h_row, g);
     // Elsewhere: the linear into a workspace of h's dtype, then the add.
-    auto &st = extras()[ctx].resid;
+    auto &st = ctx->resid;
     if (int rc = ensure(ctx, &st.ptr, &st.bytes, rows * N * h->elem_bytes(), "residual workspace alloc")) return rc;
     lx2v_hip_buf yb;
     yb.ptr = st.ptr;

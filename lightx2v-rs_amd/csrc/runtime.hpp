@@ -73,8 +73,17 @@ struct Profiler {
     std::map<std::string, hipEvent_t> open_regions;            // lx2v_hip_profile_region
 };
 
+// Device memory a context owns for one purpose, grown on demand.
+struct Stage {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
 }  // namespace lx2v
 
+// Everything a context mutates lives in it: two contexts driven from two
+// threads share no host state (the only process-wide state is each thread's
+// last-error string).
 struct lx2v_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -89,6 +98,10 @@ struct lx2v_hip_ctx {
     // Stream capture in progress (lx2v_hip_graph_begin): nothing may
     // allocate, free or synchronise until lx2v_hip_graph_end.
     bool capturing = false;
+    lx2v::Stage stage;     // boundary conversions (bias, parameters)
+    lx2v::Stage mask;      // causal_attention's host mask, uploaded per call, and its tile summary
+    lx2v::Stage kv_spare;  // the MemRoPE update's output layout, swapped with the cache it updates
+    lx2v::Stage resid;     // linear_residual's output where the add cannot ride in the GEMM
 };
 
 namespace lx2v {
@@ -224,11 +237,17 @@ struct Fp8Mx {
     // y is the residual stream h, updated in place,
     // h[m][n] += out[m][n] * gate[n] with out as the plain store would write it.
     const float *gate = nullptr;
+    // Grouped weight scales (a plan made with grouped = true): the weight's
+    // stage-major scale copy (lx2v_hip_weight::sscale, group 128); b_scale
+    // is then ignored.
+    const float *wgs = nullptr;
 };
 bool gemm_fp8_supported(size_t M, size_t N, size_t K);
+// Group-128 FP8 weights on the fp8 MFMA (needs the stage-major scale copy).
+bool gemm_fp8_grouped_supported(size_t M, size_t N, size_t K, size_t group);
 // Whether the plan's kernel takes Fp8Mx::gate (the residual epilogue).
 bool gemm_fp8_residual_ok(const Fp8Plan &p);
-Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in);
+Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped = false);
 void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t *a, const float *a_scale,
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
                      int y_dtype, size_t M, size_t N, size_t K, const Fp8Mx &mx);

@@ -675,6 +675,15 @@ class HipBackend:
     def profile_region(self, name: str, begin: bool):
         _check(lib.lx2v_hip_profile_region(self.ctx, name.encode(), int(begin)))
 
+    def profile_stats(self) -> dict:
+        """{kernel name: (calls, total_ms)} from profile_report()."""
+        out = {}
+        for line in (self.profile_report() or "").splitlines():
+            f = line.split()
+            if len(f) == 5 and f[4].endswith("%") and f[1].isdigit():
+                out[f[0]] = (int(f[1]), float(f[2]))
+        return out
+
     def profile_kernel(self, name: str):
         c = ctypes.c_uint64(0)
         t = ctypes.c_double(0.0)

@@ -1,0 +1,132 @@
+"""The benchmark chunk's GEMMs at their own shapes (config 4: the Wan2.1-1.3B
+block-linear set for one 3-frame chunk, crates/lightx2v-model/src/dit.rs:
+602-759), called the way bench.py calls them: bf16 activation buffers,
+FP8 per-channel weights, the planner's kernel configuration for each shape.
+
+Per call site: every output row computed; a sample of rows (first and last
+tiles included) against the oracle on the same e4m3 operands (FP8_TIGHT,
+f32 output); the bf16 output equal to the f32 output rounded, bit for bit;
+and the kernel configuration that ran, read from the profile report, equal
+to the one the bench's chunk uses.  The FFN pair runs as in the bench: FFN
+up with GELU writes MX e4m3 (checked bit for bit against the standalone MX
+quantizer of its f32 output), FFN down reads it (against the oracle on the
+decoded MX input), and the chain against the plain f32 oracle (4e-2).
+
+The same shapes with group-128 weights (the reference's FP8 default) run
+the grouped tiles.
+"""
+
+import numpy as np
+import pytest
+
+import lightx2v_hip as H
+import oracle as O
+from helpers import FP8_TIGHT, assert_close, normal, oracle_w8a8, u32
+
+pytestmark = pytest.mark.gpu
+
+DIM, FFN, TEXT, M = 1536, 8960, 512, 4680
+
+# (name, rows, K, N, act, configuration the planner picks on 256 CUs)
+SITES = [
+    ("qkv", M, DIM, 3 * DIM, H.ACT_NONE, "c2"),
+    ("o", M, DIM, DIM, H.ACT_NONE, "c0"),
+    ("kv2", TEXT, DIM, 2 * DIM, H.ACT_NONE, "c3"),
+]
+
+
+def _pick(rows, seed):
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([np.arange(32), np.arange(rows - 32, rows),
+                                     rng.choice(rows, 64, replace=False)]))
+
+
+def _bf16_buf(be, x):
+    be.set_act_dtype(H.DTYPE_BF16)
+    try:
+        return be.upload(x)
+    finally:
+        be.set_act_dtype(H.DTYPE_F32)
+
+
+def _profiled(be, fn):
+    be.profile_reset()
+    be.profile_enable(True)
+    try:
+        fn()
+        st = be.profile_stats()
+    finally:
+        be.profile_enable(False)
+        be.profile_reset()
+    return {k for k in st if k.startswith("gemm")}
+
+
+@pytest.mark.parametrize("name,rows,K,N,act,cfg", SITES)
+@pytest.mark.parametrize("group", ["channel", 128])
+def test_call_site(be, name, rows, K, N, act, cfg, group):
+    g = K if group == "channel" else 128
+    x = O.bf16_round(normal(1001 + N, rows * K).reshape(rows, K))
+    wf = normal(1002 + N, N * K, 0.02).reshape(N, K)
+    q, s = O.fp8_quantize(wf, N, K, g, True)
+    b = normal(1003 + N, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, g)
+    xb, bb = _bf16_buf(be, x), be.upload(b)
+    y16 = be.alloc(rows * N, H.DTYPE_BF16)
+    y32 = be.alloc(rows * N, H.DTYPE_F32)
+    ks = _profiled(be, lambda: be.linear(xb, 0, rows, w, bb, act, y16, 0))
+    want_cfg = f"gemm_fp8_e4m3.{cfg}" if group == "channel" else None
+    if want_cfg:
+        assert ks == {want_cfg}, ks
+    else:
+        assert len(ks) == 1 and next(iter(ks)).endswith(".g128"), ks
+    be.linear(xb, 0, rows, w, bb, act, y32, 0)
+    got32 = be.download(y32).reshape(rows, N)
+    got16 = be.download(y16).reshape(rows, N)
+    assert np.all(np.isfinite(got32))
+    assert np.array_equal(u32(got16), u32(O.bf16_round(got32))), "bf16 output = f32 output rounded"
+    p = _pick(rows, N)
+    assert_close(got32[p], oracle_w8a8(x[p], q, s, g, b, act), *FP8_TIGHT, what=f"{name} g{g} vs oracle")
+
+
+@pytest.mark.parametrize("group", ["channel", 128])
+def test_ffn_pair_mx_handoff(be, group):
+    """FFN up 4680x1536->8960 (GELU, MX output) -> FFN down 4680x8960->1536
+    (MX input), as the bench chains them."""
+    g1 = DIM if group == "channel" else 128
+    x = O.bf16_round(normal(1101, M * DIM).reshape(M, DIM))
+    w1f = normal(1102, FFN * DIM, 0.02).reshape(FFN, DIM)
+    w2f = normal(1103, DIM * FFN, 0.02).reshape(DIM, FFN)
+    q1, s1 = O.fp8_quantize(w1f, FFN, DIM, g1, True)
+    q2, s2 = O.fp8_quantize(w2f, DIM, FFN, FFN, True)  # MX input needs per-channel scales
+    b1, b2 = normal(1104, FFN, 0.01), normal(1105, DIM, 0.01)
+    w1, w2 = be.weight_fp8(q1, s1, FFN, DIM, g1), be.weight_fp8(q2, s2, DIM, FFN, FFN)
+    xb, bb1, bb2 = _bf16_buf(be, x), be.upload(b1), be.upload(b2)
+    h = be.alloc_mx(M, FFN)
+    y = be.alloc(M * DIM, H.DTYPE_F32)
+    ks = _profiled(be, lambda: (be.linear(xb, 0, M, w1, bb1, H.ACT_GELU_TANH, h, 0),
+                                be.linear(h, 0, M, w2, bb2, H.ACT_NONE, y, 0)))
+    if group == "channel":
+        assert ks == {"gemm_fp8_e4m3.c4.mxout", "gemm_fp8_e4m3.c0.mxin"}, ks
+    else:
+        assert ks == {"gemm_fp8_e4m3.c0.g128.mxout", "gemm_fp8_e4m3.c0.mxin"}, ks
+    # FFN up: MX output == MX quantizer of the same GEMM's f32 output, whole tensor
+    h32 = be.alloc(M * FFN, H.DTYPE_F32)
+    be.linear(xb, 0, M, w1, bb1, H.ACT_GELU_TANH, h32, 0)
+    ref = be.alloc_mx(M, FFN)
+    be.quantize_mx(h32, 0, M, ref)
+    qa, sa = be.download_mx(h, M, FFN)
+    qb, sb = be.download_mx(ref, M, FFN)
+    assert np.array_equal(qa, qb) and np.array_equal(sa, sb)
+    p = _pick(M, 7)
+    hf32 = be.download(h32).reshape(M, FFN)
+    assert_close(hf32[p], oracle_w8a8(x[p], q1, s1, g1, b1, 1), *FP8_TIGHT, what="FFN up vs oracle")
+    del hf32
+    # FFN down on the decoded MX input
+    hd = be.download(h).reshape(M, FFN)[p]
+    got = be.download(y).reshape(M, DIM)[p]
+    w2d = O.fp8_dequantize(q2, s2, DIM, FFN, FFN)
+    assert_close(got, O.linear(hd, w2d, b2, 0, nthreads=8), *FP8_TIGHT, what="FFN down on MX input vs oracle")
+    # the chain against the plain f32 oracle
+    w1d = O.fp8_dequantize(q1, s1, FFN, DIM, g1)
+    hf = O.linear(x[p], w1d, b1, 1, nthreads=8)
+    assert_close(got, O.linear(hf, w2d, b2, 0, nthreads=8), 4e-2, 0.3, what="FFN chain vs f32 oracle")

@@ -137,6 +137,81 @@ def test_fp8_reference_quantizer_codes(be):
     assert_close(y[:, ok], want[:, ok], *FP8_TIGHT, what="fp8 reference-encoder codes")
 
 
+def _kernels(be, fn):
+    """The profile names of the kernels fn() launches."""
+    be.profile_reset()
+    be.profile_enable(True)
+    try:
+        out = fn()
+        st = be.profile_stats()
+    finally:
+        be.profile_enable(False)
+        be.profile_reset()
+    return out, set(st)
+
+
+# (M, K, N): the 256x128 and 128x256 grouped tiles, ragged M / N, one-row,
+# and the Wan chunk's O shape
+G128_SHAPES = [(130, 512, 200), (77, 256, 132), (300, 1536, 1536), (1, 128, 64), (513, 512, 2056),
+               (260, 1024, 1540)]
+
+
+@pytest.mark.parametrize("M,K,N", G128_SHAPES)
+def test_fp8_g128_mfma_vs_oracle(be, M, K, N):
+    """Group-128 FP8 (the reference default, FP8_GROUP, quant.rs:21, 425-429)
+    on the fp8 MFMA: each 128-column stage's partial sum is scaled by its
+    group's scale.  Against the oracle on the same e4m3 activations, with a
+    heavy-tailed column block so the groups' scales differ by 20x."""
+    x = normal(15 + M, M * K).reshape(M, K)
+    wf = normal(16 + N, N * K, 0.02).reshape(N, K)
+    wf[:, 128:256 if K > 128 else 128] *= np.float32(20.0)
+    q, s = O.fp8_quantize(wf, N, K, 128, True)
+    b = normal(17, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, 128)
+    y, ks = _kernels(be, lambda: run_linear(be, x, w, b, H.ACT_GELU_TANH))
+    if K > 128:  # (at K = 128 one group per channel: the per-channel tiles)
+        assert any(k.startswith("gemm_fp8_e4m3.c") and k.endswith(".g128") for k in ks), ks
+    assert "gemm_generic" not in ks
+    assert_close(y, oracle_w8a8(x, q, s, 128, b, 1), *FP8_TIGHT, what="fp8 g128 MFMA vs oracle")
+    # bf16 output: the f32 output rounded, bit for bit
+    y16 = run_linear(be, x, w, b, H.ACT_GELU_TANH, y_dtype=H.DTYPE_BF16)
+    assert np.array_equal(u32(y16), u32(O.bf16_round(y)))
+
+
+def test_fp8_g128_reference_contract(be):
+    """The reference's own FP8 weights (its encoder, group 128, exponent-0
+    codes included) against the unmodified contract: the oracle's linear
+    with weight(&q.dequantize()) (backend.rs:179-188) on the same e4m3
+    activations.  Canonicalizing the exponent-0 codes moves each such
+    weight by <= 7 * 2^-12 * s, inside the fp8 tolerance."""
+    M, K, N = 192, 1536, 512
+    x = normal(18, M * K).reshape(M, K)
+    wf = normal(19, N * K, 0.02).reshape(N, K)
+    q, s = O.fp8_quantize(wf, N, K, 128, False)
+    w = be.weight_fp8(q, s, N, K, 128)
+    assert w.info()["canonicalized"] > 0
+    y = run_linear(be, x, w, None, H.ACT_NONE)
+    nan_cols = np.any((q & 0x7F) == 0x7F, axis=1)
+    assert np.array_equal(np.isnan(y).any(0), nan_cols)
+    want = oracle_w8a8(x, q, s, 128, None, 0)
+    ok = ~nan_cols
+    assert_close(y[:, ok], want[:, ok], *FP8_TIGHT, what="fp8 g128, reference codes, unmodified contract")
+
+
+@pytest.mark.parametrize("group", [64, 256])
+def test_fp8_other_groups_bf16_mfma(be, group):
+    """FP8 groups other than 128 and cols: the bf16 GEMM (weight dequantized
+    to bf16 in its loader, bf16 activations) rather than the scalar kernel."""
+    M, K, N = 150, 1024, 320
+    x = normal(20 + group, M * K).reshape(M, K)
+    _, q, s = fp8_weight(21 + group, N, K, group)
+    w = be.weight_fp8(q, s, N, K, group)
+    y, ks = _kernels(be, lambda: run_linear(be, x, w, None, H.ACT_NONE))
+    assert "gemm_w16_fp8" in ks and "gemm_generic" not in ks, ks
+    wd = O.fp8_dequantize(q, s, N, K, group)
+    assert_close(y, oracle_w16(x, wd, None, 0), *W16_TIGHT, what=f"fp8 g{group} on the bf16 MFMA")
+
+
 def test_fp8_grouped_paths(be):
     """Group-128 FP8 (the reference default, quant.rs:21): e4m3 activations
     and the bf16-activation mode."""
@@ -254,11 +329,12 @@ def test_profile_report_names_kernels(be):
     try:
         run_linear(be, normal(61, M * K).reshape(M, K), w, None, H.ACT_NONE)
         rep = be.profile_report()
-        calls, ms = be.profile_kernel("gemm_fp8_e4m3")
+        st = be.profile_stats()
     finally:
         be.profile_enable(False)
-    assert rep and "gemm_fp8_e4m3" in rep and "act_quant_e4m3" in rep
-    assert calls == 1 and ms > 0
+    assert rep and "act_quant_e4m3" in rep
+    gemm = [k for k in st if k.startswith("gemm_fp8_e4m3.")]  # named by configuration
+    assert len(gemm) == 1 and st[gemm[0]][0] == 1 and st[gemm[0]][1] > 0
 
 
 def test_cpp_check_harness(be):

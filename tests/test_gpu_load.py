@@ -113,27 +113,21 @@ def test_quantize_q4_rtn_bit_exact(be, group):
 
 @pytest.mark.parametrize("group", [32, 64])
 def test_quantize_q4_hqq_matches_oracle(be, group):
-    """HQQ's powf: the device takes a^-0.3 in double and rounds once; glibc's
-    powf is one ulp off that for ~0.06% of arguments, which can move a zero
-    point's last bits.  Stated bar: >= 99.9% of groups bit-identical (codes,
-    scale, zero), and the rest no worse in round-trip error than 1.001x."""
+    """HQQ (quant.rs:248-281) on the device: the shrink's a^-0.3 is glibc's
+    powf restated (csrc/powf_arm.hpp, bit-identical to the libm on every
+    positive f32 at this exponent, tests/test_powf_arm.py), so codes, scales
+    and zero points equal the oracle's (which calls the libm) in every
+    group, including a heavy-tailed row."""
     rows, cols = 128, 2048
     w = _normal(51, rows * cols, 0.02).reshape(rows, cols)
     w[3, ::7] *= np.float32(20.0)
     wq = be.quantize_q4(_dev_f32(be, w), rows, cols, group, True)
     c, s, z = O.q4_quantize(w, rows, cols, group, True)
     e = be.weight_export(wq)
-    got_c = O.q4_unpack(e["q"], rows * cols).reshape(-1, group)
-    same = (np.all(got_c == c.reshape(-1, group), axis=1) & (u32(e["scales"]).ravel() == u32(s).ravel())
-            & (u32(e["zeros"]).ravel() == u32(z).ravel()))
-    assert same.mean() >= 0.999, f"{(~same).sum()} of {same.size} groups differ"
-    assert np.array_equal(u32(e["scales"]), u32(s))  # the scale does not depend on HQQ
-    d_dev = be.dequantize(wq).reshape(-1, group)
-    d_ref = O.q4_dequantize(c, s, z, rows, cols, group).reshape(-1, group)
-    wg = w.reshape(-1, group)
-    err_dev = np.abs(d_dev - wg).mean(axis=1)
-    err_ref = np.abs(d_ref - wg).mean(axis=1)
-    assert np.all(err_dev[~same] <= err_ref[~same] * 1.001 + 1e-12)
+    assert np.array_equal(O.q4_unpack(e["q"], rows * cols), c.ravel())
+    assert np.array_equal(u32(e["scales"]), u32(s))
+    assert np.array_equal(u32(e["zeros"]), u32(z))
+    assert np.array_equal(u32(be.dequantize(wq)), u32(O.q4_dequantize(c, s, z, rows, cols, group)))
 
 
 def test_quantize_q4_rejects_odd_group(be):

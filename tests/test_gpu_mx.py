@@ -63,7 +63,7 @@ def test_quantize_mx_bit_exact(be, rows, cols, x_row, xdt):
 MX_SHAPES = [(300, 1536, 640), (77, 256, 160), (3000, 512, 2048), (2100, 2048, 2048), (1000, 1536, 8960)]
 
 
-@pytest.mark.parametrize("M,K,N", MX_SHAPES)
+@pytest.mark.parametrize("M,K,N", MX_SHAPES + [(4680, 8960, 1536)])  # + the chunk's FFN down
 def test_linear_mx_input_vs_oracle(be, M, K, N):
     x = normal(11 + M, M * K).reshape(M, K)
     _, q, s = fp8_weight(12 + N, N, K, K)
@@ -73,15 +73,19 @@ def test_linear_mx_input_vs_oracle(be, M, K, N):
     xb = _upload(be, x, H.DTYPE_F32)
     xq = be.alloc_mx(M + 16, K)
     be.quantize_mx(xb, 0, M, xq)
-    rows = min(M, 256)
+    # every row from offset 16 (or 0) through the GEMM; the oracle on a
+    # sample of rows that includes the first and last tiles' rows
+    r0 = 16 if M > 64 else 0
+    rows = M - r0
     y = be.alloc((rows + 3) * N)
-    be.linear(xq, 16 if M > rows + 16 else 0, rows, w, bb, H.ACT_NONE, y, 3)
-    r0 = 16 if M > rows + 16 else 0
-    qx, sx = O.act_quant_mx(x)
-    xd = O.dequant_mx(qx, sx)[r0:r0 + rows]
-    want = O.linear(xd, O.fp8_dequantize(q, s, N, K, K), b, 0, nthreads=8)
+    be.linear(xq, r0, rows, w, bb, H.ACT_NONE, y, 3)
     got = be.download(y).reshape(rows + 3, N)[3:]
-    assert_close(got, want, *FP8_TIGHT, what="MX-input fp8 GEMM vs oracle")
+    pick = np.unique(np.concatenate([np.arange(min(rows, 40)), np.arange(max(0, rows - 40), rows),
+                                     np.random.default_rng(M).choice(rows, min(rows, 64), replace=False)]))
+    qx, sx = O.act_quant_mx(x)
+    xd = O.dequant_mx(qx, sx)[r0:][pick]
+    want = O.linear(xd, O.fp8_dequantize(q, s, N, K, K), b, 0, nthreads=8)
+    assert_close(got[pick], want, *FP8_TIGHT, what="MX-input fp8 GEMM vs oracle")
 
 
 @pytest.mark.parametrize("M,K,N", MX_SHAPES + [(4680, 1536, 8960)])
@@ -110,6 +114,27 @@ def test_linear_mx_output_is_quantized_f32_output(be, M, K, N, act, xmx):
     q1, s1 = be.download_mx(ymx, M + 5, N)
     q2, s2 = be.download_mx(ref, M, N)
     assert np.array_equal(q1[5:], q2) and np.array_equal(s1[:, 5:], s2)
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 512, 640), (4680, 1536, 8960)])
+def test_linear_mx_output_g128(be, M, K, N):
+    """Group-128 FP8 weights writing MX output (the 256x128 grouped tile):
+    codes and scales equal quantize_mx of the f32 output, bit for bit."""
+    x = normal(24 + M, M * K).reshape(M, K)
+    _, q, s = fp8_weight(25 + N, N, K, 128)
+    b = normal(26, N, 0.1)
+    w = be.weight_fp8(q, s, N, K, 128)
+    bb = be.upload(b)
+    xb = _upload(be, x, H.DTYPE_BF16)
+    y32 = be.alloc(M * N)
+    be.linear(xb, 0, M, w, bb, H.ACT_GELU_TANH, y32, 0)
+    ymx = be.alloc_mx(M, N)
+    be.linear(xb, 0, M, w, bb, H.ACT_GELU_TANH, ymx, 0)
+    ref = be.alloc_mx(M, N)
+    be.quantize_mx(y32, 0, M, ref)
+    q1, s1 = be.download_mx(ymx, M, N)
+    q2, s2 = be.download_mx(ref, M, N)
+    assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
 
 
 def test_mx_ffn_chain(be):
@@ -191,11 +216,15 @@ def test_mx_errors(be):
     with pytest.raises(H.HipError) as e:
         be.linear(xq, 0, M, w8, None, H.ACT_NONE, y, 0)
     assert e.value.status == H.ERR_UNSUPPORTED
-    _, qg, sg = fp8_weight(54, N, K, 128)  # grouped scales: no MX GEMM
+    _, qg, sg = fp8_weight(54, N, K, 128)  # grouped scales: no MX input
     wg = be.weight_fp8(qg, sg, N, K, 128)
-    ymx = be.alloc_mx(M, N)
     with pytest.raises(H.HipError) as e:
-        be.linear(xb, 0, M, wg, None, H.ACT_NONE, ymx, 0)
+        be.linear(xq, 0, M, wg, None, H.ACT_NONE, y, 0)
+    assert e.value.status == H.ERR_UNSUPPORTED
+    _, qg, sg = fp8_weight(55, N, K, 64)  # group 64: no MX output
+    wg = be.weight_fp8(qg, sg, N, K, 64)
+    with pytest.raises(H.HipError) as e:
+        be.linear(xb, 0, M, wg, None, H.ACT_NONE, be.alloc_mx(M, N), 0)
     assert e.value.status == H.ERR_UNSUPPORTED
     with pytest.raises(H.HipError) as e:
         be.write(xq, np.zeros(4, np.float32))
