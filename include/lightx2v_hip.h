@@ -240,6 +240,20 @@ int lx2v_hip_linear_residual(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_
 int lx2v_hip_gate_residual(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_buf *a, size_t rows,
                            size_t dim, const lx2v_hip_buf *mods, size_t gate);
 
+/* Backend::head_split (backend.rs:255-273; CPU lib.rs:406-455): columns
+ * [col_off, col_off + heads*head_dim) of `rows` rows of width src_stride ->
+ * out as [heads, rows, head_dim].  rms_w ([heads*head_dim], or NULL): RMS-
+ * normalised across all heads first, x * (1 / sqrt(mean(x^2) + eps)) * w.
+ * rope_cos / rope_sin ([rows, head_dim/2] each, both or neither): each
+ * head's interleaved pairs (2i, 2i+1) rotated, (a c - b s, a s + b c).
+ * src / out F32 or BF16 (out's dtype is the output's); rms_w and the tables
+ * F32 or BF16.  out must not overlap src.  The mean of squares is a lane
+ * reduction (the reference folds it sequentially: rel. 1e-7 differences);
+ * every other operation rounds as the reference's. */
+int lx2v_hip_head_split(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows, size_t src_stride, size_t col_off,
+                        size_t heads, size_t head_dim, const lx2v_hip_buf *rms_w, const lx2v_hip_buf *rope_cos,
+                        const lx2v_hip_buf *rope_sin, float eps, lx2v_hip_buf *out);
+
 /* ---- attention (backend.rs:273-305) -----------------------------------------
  * q [heads, sq, head_dim], k / v [heads, sk, head_dim] (F32 or BF16, one
  * dtype); out [sq, heads*head_dim] (F32 or BF16), heads merged.  Scores

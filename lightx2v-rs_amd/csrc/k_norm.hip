@@ -357,6 +357,155 @@ void norm_launch_od(hipStream_t s, const NormArgs &p, int od) {
     }
 }
 
+// ---- head_split (crates/lightx2v-cpu/src/lib.rs:406-455) -----------------------------
+//
+// Columns [col_off, col_off + heads hd) of each row -> out [heads, rows, hd],
+// optionally RMS-normalised across all heads (x * inv * w, inv = 1 /
+// sqrt(mean(x^2) + eps)) and rotated by RoPE (interleaved pairs, cos / sin
+// [rows, hd / 2]).  One wave per row; lane l holds the 8-column chunks l,
+// l + 64, ... of the row in registers (hd % 8 == 0, so a chunk lies in one
+// head and holds 4 whole pairs).  The mean of squares is a lane reduction;
+// every other operation rounds as the reference's (no contraction).
+
+struct HeadSplitArgs {
+    const void *src;
+    size_t rows, stride, col_off, heads, hd;
+    const void *w;      // [heads hd] or null
+    const void *cs;     // cos [rows, hd / 2] or null (then sn is null too)
+    const void *sn;
+    int wdt, rdt;       // dtype of w, of cos / sin (F32 or BF16)
+    float eps;
+    void *out;
+};
+
+__device__ __forceinline__ float ld_param(const void *p, int dt, size_t i) {
+    return dt == LX2V_DTYPE_BF16 ? bf16_bits_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+}
+
+template <int DT, int OD, int T>
+__global__ __launch_bounds__(kNThreads) void k_head_split(HeadSplitArgs p) {
+    constexpr int R = DT == LX2V_DTYPE_BF16 ? 1 : 2;  // 16-byte words per input chunk
+    constexpr int EB = DT == LX2V_DTYPE_BF16 ? 2 : 4;
+    const int lane = threadIdx.x & 63;
+    const size_t row = blockIdx.x * (size_t)(kNThreads / 64) + (threadIdx.x >> 6);
+    if (row >= p.rows) return;  // wave-uniform
+    const size_t d = p.heads * p.hd;
+    const int nch = (int)(d / 8);
+    const u32x4 *xr = (const u32x4 *)((const char *)p.src + (row * p.stride + p.col_off) * EB);
+    float v[T][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const int c = lane + 64 * t;
+        u32x4 raw[R];
+#pragma unroll
+        for (int h = 0; h < R; h++) raw[h] = c < nch ? xr[(size_t)c * R + h] : (u32x4){};
+        unpack8<DT>(raw, v[t]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss += v[t][e] * v[t][e];
+    }
+    if (p.w) {
+        const float ms = wave_sum(ss) / (float)d;
+        const float inv = 1.0f / sqrtf(ms + p.eps);
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const int c = lane + 64 * t;
+            if (c >= nch) continue;
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[t][e] = v[t][e] * inv * ld_param(p.w, p.wdt, (size_t)c * 8 + e);
+        }
+    }
+    const size_t hh = p.hd / 2;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const int c = lane + 64 * t;
+        if (c >= nch) continue;
+        const size_t col = (size_t)c * 8, h = col / p.hd, j = col % p.hd;
+        if (p.cs) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const size_t i = row * hh + j / 2 + e;
+                const float cv = ld_param(p.cs, p.rdt, i), sv = ld_param(p.sn, p.rdt, i);
+                const float a = v[t][2 * e], b = v[t][2 * e + 1];
+                v[t][2 * e] = a * cv - b * sv;
+                v[t][2 * e + 1] = a * sv + b * cv;
+            }
+        }
+        u32x4 w[2];
+        pack8(v[t], w, OD);
+        u32x4 *o = (u32x4 *)((char *)p.out + ((h * p.rows + row) * p.hd + j) * (OD == LX2V_DTYPE_BF16 ? 2 : 4));
+        o[0] = w[0];
+        if (OD == LX2V_DTYPE_F32) o[1] = w[1];
+    }
+}
+
+// Any head size (and rows too wide for the register kernel): one wave per
+// row, columns strided over the lanes, the row read twice.
+template <int DT, int OD>
+__global__ __launch_bounds__(kNThreads) void k_head_split_any(HeadSplitArgs p) {
+    const int lane = threadIdx.x & 63;
+    const size_t row = blockIdx.x * (size_t)(kNThreads / 64) + (threadIdx.x >> 6);
+    if (row >= p.rows) return;
+    const size_t d = p.heads * p.hd, base = row * p.stride + p.col_off;
+    auto ld = [&](size_t col) {
+        return DT == LX2V_DTYPE_BF16 ? bf16_bits_to_f32(((const uint16_t *)p.src)[base + col])
+                                     : ((const float *)p.src)[base + col];
+    };
+    float inv = 1.0f;
+    if (p.w) {
+        float ss = 0.0f;
+        for (size_t col = lane; col < d; col += 64) {
+            const float x = ld(col);
+            ss += x * x;
+        }
+        inv = 1.0f / sqrtf(wave_sum(ss) / (float)d + p.eps);
+    }
+    auto val = [&](size_t col) { return p.w ? ld(col) * inv * ld_param(p.w, p.wdt, col) : ld(col); };
+    auto st = [&](size_t col, float x) {
+        const size_t h = col / p.hd, j = col % p.hd, o = (h * p.rows + row) * p.hd + j;
+        if (OD == LX2V_DTYPE_BF16)
+            ((uint16_t *)p.out)[o] = f32_to_bf16_bits(x);
+        else
+            ((float *)p.out)[o] = x;
+    };
+    const size_t hh = p.hd / 2;
+    // lane-strided over pairs of each head (an odd head's last element alone)
+    const size_t per = hh + (p.hd & 1);
+    for (size_t u = lane; u < p.heads * per; u += 64) {
+        const size_t h = u / per, i = u % per, col = h * p.hd + 2 * i;
+        if (i == hh) {  // odd hd: the unpaired last element
+            st(col, val(col));
+            continue;
+        }
+        const float a = val(col), b = val(col + 1);
+        if (p.cs) {
+            const float cv = ld_param(p.cs, p.rdt, row * hh + i), sv = ld_param(p.sn, p.rdt, row * hh + i);
+            st(col, a * cv - b * sv);
+            st(col + 1, a * sv + b * cv);
+        } else {
+            st(col, a);
+            st(col + 1, b);
+        }
+    }
+}
+
+template <int DT, int OD>
+void head_split_launch(hipStream_t s, const HeadSplitArgs &p) {
+    const dim3 block(kNThreads), grid((unsigned)((p.rows + kNThreads / 64 - 1) / (kNThreads / 64)));
+    const size_t d = p.heads * p.hd, per = (d / 8 + 63) / 64;
+    const bool vec = p.hd % 8 == 0 && p.stride % 8 == 0 && p.col_off % 8 == 0 && per <= 12;
+    if (!vec)
+        hipLaunchKernelGGL((k_head_split_any<DT, OD>), grid, block, 0, s, p);
+    else if (per <= 2)
+        hipLaunchKernelGGL((k_head_split<DT, OD, 2>), grid, block, 0, s, p);
+    else if (per <= 4)
+        hipLaunchKernelGGL((k_head_split<DT, OD, 4>), grid, block, 0, s, p);
+    else if (per <= 8)
+        hipLaunchKernelGGL((k_head_split<DT, OD, 8>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((k_head_split<DT, OD, 12>), grid, block, 0, s, p);
+}
+
 }  // namespace
 
 void launch_norm(hipStream_t s, void *x, const void *a, int dt, const float *gate, const float *pm, const float *pa,
@@ -388,6 +537,24 @@ void launch_norm(hipStream_t s, void *x, const void *a, int dt, const float *gat
             norm_launch_od<LX2V_DTYPE_F32, true>(s, p, od);
         else
             norm_launch_od<LX2V_DTYPE_F32, false>(s, p, od);
+    }
+}
+
+void launch_head_split(hipStream_t s, const void *src, int dt, size_t rows, size_t stride, size_t col_off,
+                       size_t heads, size_t hd, const void *w, int wdt, const void *cs, const void *sn, int rdt,
+                       float eps, void *out, int od) {
+    if (rows == 0 || heads * hd == 0) return;
+    HeadSplitArgs p{src, rows, stride, col_off, heads, hd, w, cs, sn, wdt, rdt, eps, out};
+    if (dt == LX2V_DTYPE_BF16) {
+        if (od == LX2V_DTYPE_BF16)
+            head_split_launch<LX2V_DTYPE_BF16, LX2V_DTYPE_BF16>(s, p);
+        else
+            head_split_launch<LX2V_DTYPE_BF16, LX2V_DTYPE_F32>(s, p);
+    } else {
+        if (od == LX2V_DTYPE_BF16)
+            head_split_launch<LX2V_DTYPE_F32, LX2V_DTYPE_BF16>(s, p);
+        else
+            head_split_launch<LX2V_DTYPE_F32, LX2V_DTYPE_F32>(s, p);
     }
 }
 

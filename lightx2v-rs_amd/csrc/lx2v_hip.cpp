@@ -977,6 +977,44 @@ int lx2v_hip_gate_residual(lx2v_hip_ctx *ctx, lx2v_hip_buf *h, const lx2v_hip_bu
                [&] { launch_gate_residual(ctx->stream, h->ptr, a->ptr, h->dtype, g, rows, dim); });
 }
 
+// Backend::head_split (backend.rs:255-273).
+int lx2v_hip_head_split(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows, size_t src_stride, size_t col_off,
+                        size_t heads, size_t head_dim, const lx2v_hip_buf *rms_w, const lx2v_hip_buf *rope_cos,
+                        const lx2v_hip_buf *rope_sin, float eps, lx2v_hip_buf *out) {
+    NEED(ctx, "ctx");
+    NEED(src, "src");
+    NEED(out, "out");
+    if (src->quantized() || out->quantized() || (rms_w && rms_w->quantized()) ||
+        (rope_cos && rope_cos->quantized()) || (rope_sin && rope_sin->quantized()))
+        return fail(LX2V_ERR_BAD_ARG, "head_split: F32 or BF16 buffers only");
+    if (!rope_cos != !rope_sin) return fail(LX2V_ERR_BAD_ARG, "head_split: rope_cos and rope_sin go together");
+    const size_t d = heads * head_dim;
+    if (!rows || !d) return ok();
+    if (col_off + d < col_off || col_off + d > src_stride)
+        return fail(LX2V_ERR_BAD_SHAPE, "head_split: columns [%zu, +%zu) outside a row of %zu", col_off, d, src_stride);
+    if ((rows - 1) * src_stride + col_off + d > src->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "head_split: src has %zu elements, %zu rows of stride %zu need %zu", src->len,
+                    rows, src_stride, (rows - 1) * src_stride + col_off + d);
+    if (rows * d > out->len)
+        return fail(LX2V_ERR_BAD_SHAPE, "head_split: out has %zu elements, needs %zu", out->len, rows * d);
+    if (rms_w && rms_w->len < d)
+        return fail(LX2V_ERR_BAD_SHAPE, "head_split: rms_w has %zu elements, needs %zu", rms_w->len, d);
+    if (rope_cos && (rope_cos->len < rows * (head_dim / 2) || rope_sin->len < rows * (head_dim / 2)))
+        return fail(LX2V_ERR_BAD_SHAPE, "head_split: rope tables need %zu elements each", rows * (head_dim / 2));
+    if (overlap(out->ptr, rows * d * out->elem_bytes(), src->ptr, src->bytes()))
+        return fail(LX2V_ERR_ALIAS, "head_split: out overlaps src");
+    for (const lx2v_hip_buf *b : {rms_w, rope_cos, rope_sin})
+        if (b && overlap(out->ptr, rows * d * out->elem_bytes(), b->ptr, b->bytes()))
+            return fail(LX2V_ERR_ALIAS, "head_split: out overlaps a parameter");
+    if (int rc = set_dev(ctx)) return rc;
+    return run(ctx, "head_split", [&] {
+        launch_head_split(ctx->stream, src->ptr, src->dtype, rows, src_stride, col_off, heads, head_dim,
+                          rms_w ? rms_w->ptr : nullptr, rms_w ? rms_w->dtype : LX2V_DTYPE_F32,
+                          rope_cos ? rope_cos->ptr : nullptr, rope_sin ? rope_sin->ptr : nullptr,
+                          rope_cos ? rope_cos->dtype : LX2V_DTYPE_F32, eps, out->ptr, out->dtype);
+    });
+}
+
 // ---- attention ------------------------------------------------------------------
 
 struct lx2v_hip_mask {

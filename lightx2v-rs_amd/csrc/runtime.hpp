@@ -164,6 +164,14 @@ void launch_norm(hipStream_t s, void *x, const void *a, int dt, const float *gat
 // h += a * g[column] over rows x dim (h, a of dtype dt).
 void launch_gate_residual(hipStream_t s, void *h, const void *a, int dt, const float *g, size_t rows, size_t dim);
 
+// Backend::head_split: columns [col_off, col_off + heads hd) of rows x stride
+// src (dtype dt) -> out [heads, rows, hd] (dtype od), optionally RMS-normed
+// across heads with w [heads hd] (dtype wdt) and RoPE-rotated with cs / sn
+// [rows, hd / 2] (dtype rdt); null = skip.
+void launch_head_split(hipStream_t s, const void *src, int dt, size_t rows, size_t stride, size_t col_off,
+                       size_t heads, size_t hd, const void *w, int wdt, const void *cs, const void *sn, int rdt,
+                       float eps, void *out, int od);
+
 // ---- attention (k_attn.hip) -------------------------------------------------------
 // out [sq, heads*d] = softmax(q k^T / sqrt(d), mask) v; q [heads, sq, d], k / v
 // [heads, kvs, d] of dtype dt, keys 0 .. sk - 1 of each head used (kvs >= sk); mask [sq, sk] bytes or null; tiles its summary

@@ -48,7 +48,7 @@ EXPORTS = [
     "lx2v_hip_attention_masked", "lx2v_hip_kv_cache_new", "lx2v_hip_kv_cache_free", "lx2v_hip_kv_cache_append",
     "lx2v_hip_kv_cache_put", "lx2v_hip_kv_cache_len", "lx2v_hip_kv_cache_temporal", "lx2v_hip_kv_cache_kinds",
     "lx2v_hip_kv_cache_kv", "lx2v_hip_kv_cache_read", "lx2v_hip_kv_cache_memrope_update",
-    "lx2v_hip_kv_cache_attention", "lx2v_hip_mask_temporal", "lx2v_hip_linear_residual",
+    "lx2v_hip_kv_cache_attention", "lx2v_hip_mask_temporal", "lx2v_hip_linear_residual", "lx2v_hip_head_split",
 ]
 
 
@@ -146,6 +146,7 @@ def _load():
         "lx2v_hip_residual_norm": (ip, [vp, vp, vp, sz, sz, vp, ip, sz, ctypes.POINTER(_Norm), ctypes.c_float,
                                         vp]),
         "lx2v_hip_gate_residual": (ip, [vp, vp, vp, sz, sz, vp, sz]),
+        "lx2v_hip_head_split": (ip, [vp, vp, sz, sz, sz, sz, sz, vp, vp, vp, ctypes.c_float, vp]),
         "lx2v_hip_attention": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp]),
         "lx2v_hip_causal_attention": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),
         "lx2v_hip_mask_upload": (ip, [vp, vp, sz, sz, pp]),
@@ -573,6 +574,14 @@ class HipBackend:
         _check(lib.lx2v_hip_gate_residual(self.ctx, h.h, a.h, rows, dim, mods.h, gate))
 
     # ---- backend.rs:273-305: attention ----
+    def head_split(self, src: Buf, rows: int, src_stride: int, col_off: int, heads: int, head_dim: int,
+                   rms_w: Optional[Buf], rope: Optional[tuple], eps: float, out: Buf):
+        """Backend::head_split: rope = (cos, sin) buffers or None."""
+        c, s = rope if rope is not None else (None, None)
+        _check(lib.lx2v_hip_head_split(self.ctx, src.h, rows, src_stride, col_off, heads, head_dim,
+                                       rms_w.h if rms_w is not None else None, c.h if c is not None else None,
+                                       s.h if s is not None else None, ctypes.c_float(eps), out.h))
+
     def attention(self, q: Buf, k: Buf, v: Buf, heads: int, sq: int, sk: int, head_dim: int, out: Buf):
         """q [heads, sq, d], k / v [heads, sk, d] -> out [sq, heads * d]."""
         _check(lib.lx2v_hip_attention(self.ctx, q.h, k.h, v.h, heads, sq, sk, head_dim, out.h))

@@ -339,6 +339,26 @@ def gate_residual(h: np.ndarray, a: np.ndarray, mods, gate: int) -> np.ndarray:
     return h
 
 
+def head_split(src: np.ndarray, col_off: int, heads: int, head_dim: int, rms_w=None, rope=None,
+               eps: float = 1e-6, f64: bool = False) -> np.ndarray:
+    """crates/lightx2v-cpu/src/lib.rs:406-455: src [rows, stride] -> [heads,
+    rows, head_dim]; rms_w [heads * head_dim] or None; rope (cos, sin), each
+    [rows, head_dim / 2], or None.  f64=True: the same in double (a pin)."""
+    src = np.ascontiguousarray(src, np.float32)
+    rows, stride = src.shape
+    assert col_off + heads * head_dim <= stride
+    w = None if rms_w is None else np.ascontiguousarray(rms_w, np.float32)
+    c = s = None
+    if rope is not None:
+        c, s = (np.ascontiguousarray(t, np.float32) for t in rope)
+        assert c.size == rows * (head_dim // 2) and s.size == c.size
+    out = np.empty((heads, rows, head_dim), np.float64 if f64 else np.float32)
+    fn = lib().orc_head_split_f64 if f64 else lib().orc_head_split
+    fn(_p(src, _f32p), _sz(rows), _sz(stride), _sz(col_off), _sz(heads), _sz(head_dim), _fp(w), _fp(c), _fp(s),
+       ctypes.c_float(eps), _p(out, _f64p if f64 else _f32p))
+    return out
+
+
 def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask=None, nthreads: int = 8) -> np.ndarray:
     """crates/lightx2v-cpu/src/lib.rs:155-203: q [heads, sq, d], k / v [heads,
     sk, d], mask [sq, sk] bool or None -> out [sq, heads * d]."""

@@ -441,6 +441,73 @@ void orc_gate_residual(float *h, const float *a, size_t rows, size_t dim, const 
         for (size_t j = 0; j < dim; j++) h[r * dim + j] += a[r * dim + j] * mods[gate * dim + j];
 }
 
+/* ---- head split ----------------------------------------------------------- */
+
+/* crates/lightx2v-cpu/src/lib.rs:406-455: columns [col_off, col_off + heads*hd)
+ * of each of `rows` rows (row stride src_stride) -> out [heads, rows, hd];
+ * with rms_w: x * inv * w[j], inv = 1 / sqrt(mean(x^2) + eps), the mean a
+ * sequential f32 fold of the squares; with cos / sin ([rows, hd/2]): each
+ * head's interleaved pairs (2i, 2i+1) rotated, a*c - b*s and a*s + b*c. */
+void orc_head_split(const float *src, size_t rows, size_t src_stride, size_t col_off, size_t heads, size_t hd,
+                    const float *rms_w, const float *cos_t, const float *sin_t, float eps, float *out) {
+    const size_t d = heads * hd;
+    float *tmp = (float *)malloc(d * sizeof(float));
+    for (size_t r = 0; r < rows; r++) {
+        const float *row = src + r * src_stride + col_off;
+        if (rms_w) {
+            float ss = 0.0f;
+            for (size_t j = 0; j < d; j++) ss += row[j] * row[j];
+            const float ms = ss / (float)d;
+            const float inv = 1.0f / sqrtf(ms + eps);
+            for (size_t j = 0; j < d; j++) tmp[j] = row[j] * inv * rms_w[j];
+        } else {
+            for (size_t j = 0; j < d; j++) tmp[j] = row[j];
+        }
+        if (cos_t && sin_t) {
+            for (size_t h = 0; h < heads; h++)
+                for (size_t i = 0; i < hd / 2; i++) {
+                    const float a = tmp[h * hd + 2 * i], b = tmp[h * hd + 2 * i + 1];
+                    const float c = cos_t[r * (hd / 2) + i], s = sin_t[r * (hd / 2) + i];
+                    tmp[h * hd + 2 * i] = a * c - b * s;
+                    tmp[h * hd + 2 * i + 1] = a * s + b * c;
+                }
+        }
+        for (size_t h = 0; h < heads; h++)
+            for (size_t j = 0; j < hd; j++) out[(h * rows + r) * hd + j] = tmp[h * hd + j];
+    }
+    free(tmp);
+}
+
+/* The same in f64 throughout (test pin: the f32 restatement must sit
+ * within f32 rounding of it). */
+void orc_head_split_f64(const float *src, size_t rows, size_t src_stride, size_t col_off, size_t heads, size_t hd,
+                        const float *rms_w, const float *cos_t, const float *sin_t, float eps, double *out) {
+    const size_t d = heads * hd;
+    double *tmp = (double *)malloc(d * sizeof(double));
+    for (size_t r = 0; r < rows; r++) {
+        const float *row = src + r * src_stride + col_off;
+        double inv = 1.0;
+        if (rms_w) {
+            double ss = 0.0;
+            for (size_t j = 0; j < d; j++) ss += (double)row[j] * row[j];
+            inv = 1.0 / sqrt(ss / (double)d + (double)eps);
+        }
+        for (size_t j = 0; j < d; j++) tmp[j] = rms_w ? (double)row[j] * inv * rms_w[j] : (double)row[j];
+        if (cos_t && sin_t) {
+            for (size_t h = 0; h < heads; h++)
+                for (size_t i = 0; i < hd / 2; i++) {
+                    const double a = tmp[h * hd + 2 * i], b = tmp[h * hd + 2 * i + 1];
+                    const double c = cos_t[r * (hd / 2) + i], s = sin_t[r * (hd / 2) + i];
+                    tmp[h * hd + 2 * i] = a * c - b * s;
+                    tmp[h * hd + 2 * i + 1] = a * s + b * c;
+                }
+        }
+        for (size_t h = 0; h < heads; h++)
+            for (size_t j = 0; j < hd; j++) out[(h * rows + r) * hd + j] = tmp[h * hd + j];
+    }
+    free(tmp);
+}
+
 /* ---- attention ------------------------------------------------------------ */
 
 static void attention_row(const float *q, const float *k, const float *v, size_t heads, size_t sq,

@@ -129,6 +129,10 @@ void orc_residual_norm(float *h, const float *a, size_t rows, size_t dim, const 
                        long gate, int kind, const float *w, const float *b, size_t scale,
                        size_t shift, float eps, float *normed);       /* lib.rs:363-388 */
 /* h += a * mods[gate*dim + j]. */
+void orc_head_split(const float *src, size_t rows, size_t src_stride, size_t col_off, size_t heads, size_t hd,
+                    const float *rms_w, const float *cos_t, const float *sin_t, float eps, float *out);
+void orc_head_split_f64(const float *src, size_t rows, size_t src_stride, size_t col_off, size_t heads, size_t hd,
+                        const float *rms_w, const float *cos_t, const float *sin_t, float eps, double *out);
 void orc_gate_residual(float *h, const float *a, size_t rows, size_t dim, const float *mods,
                        size_t gate);                                  /* lib.rs:390-400 */
 
