@@ -73,7 +73,7 @@ def per_config(be, H):
     import numpy as np
     out = {}
 
-    def weight(kind, n, k, std, seed, heavy=False):
+    def weight(kind, n, k, std, seed, heavy=False, group=None):
         tmp = be.alloc(n * k, H.DTYPE_F32)
         be.fill_normal(tmp, seed, std)
         if heavy:  # 1% of the weight's K columns x20 (columns k % 100 == 37)
@@ -83,7 +83,7 @@ def per_config(be, H):
             be.set_act_dtype(H.DTYPE_F32)
             tmp = be.upload(w.ravel())
         if kind == "fp8":
-            w = be.quantize_fp8(tmp, n, k, k)
+            w = be.quantize_fp8(tmp, n, k, group or k)
         elif kind == "q8":
             w = be.quantize_q8(tmp, n, k, 32)
         else:
@@ -91,7 +91,14 @@ def per_config(be, H):
         tmp.free()
         return w
 
-    def time_linear(name, x, rows, k, w, n, act, xdt, ydt, peak, path):
+    def alg_bytes(rows, n, k, xdt, ydt, kind, group):
+        """|X| + |W codes| + |scales (+ zeros)| + |bias| + |Y|, each once at its dtype."""
+        eb = {H.DTYPE_F32: 4, H.DTYPE_BF16: 2}
+        codes = n * k // 2 if kind == "q4" else n * k
+        scales = n * (k // group) * 4 * (2 if kind == "q4" else 1)
+        return rows * k * eb[xdt] + codes + scales + n * 4 + rows * n * eb[ydt]
+
+    def time_linear(name, x, rows, k, w, n, act, xdt, ydt, peak, path, kind="fp8", group=None):
         be.set_act_dtype(ydt)
         y = be.alloc(rows * n)
         b = be.alloc(n, H.DTYPE_F32)
@@ -107,13 +114,23 @@ def per_config(be, H):
             be.linear(x, 0, rows, w, b, act, y, 0)
         be.profile_region("c_" + name, False)
         us = be.profile_kernel("c_" + name)[1] * 1e3 / 30
-        tf = 2.0 * rows * n * k / (us * 1e-6) / 1e12
+        fl = 2.0 * rows * n * k
+        tf = fl / (us * 1e-6) / 1e12
+        nb = alg_bytes(rows, n, k, xdt, ydt, kind, group or k)
+        ai = fl / nb
+        bound = min(peak, ai * HBM_GBS / 1e3)  # TFLOP/s: the MFMA peak or AI x 8 TB/s
         out[name] = {"shape": f"{rows}x{k}->{n}", "us_per_linear": round(us, 2), "tflops": round(tf, 1),
-                     "peak_tflops": peak, "pct_peak": round(100.0 * tf / peak, 1), "path": path}
+                     "peak_tflops": peak, "pct_peak": round(100.0 * tf / peak, 1),
+                     "alg_bytes": nb, "ai_flop_per_byte": round(ai, 1),
+                     "bound": "hbm" if bound < peak else "mfma", "bound_tflops": round(bound, 1),
+                     "us_at_bound": round(fl / (bound * 1e12) * 1e6, 2), "pct_bound": round(100.0 * tf / bound, 1),
+                     "hbm_gbs": round(nb / (us * 1e-6) / 1e9, 1), "path": path}
         y.free()
         b.free()
 
     fp8_path = "per-token e4m3 activations (quantized inside linear) x FP8 weight, fp8 MFMA"
+    fp8_g128_path = ("per-token e4m3 activations x FP8 weight with one scale per 128 columns, fp8 MFMA (each "
+                     "128-column stage's partial sums scaled by the group's scale)")
     # config 1: FP8 self-attn Q projection, f32 activations in and out
     be.set_act_dtype(H.DTYPE_F32)
     x = be.alloc(M * DIM)
@@ -121,14 +138,29 @@ def per_config(be, H):
     w = weight("fp8", DIM, DIM, 0.02, 1002)
     time_linear("cfg1_fp8_q_proj_f32", x, M, DIM, w, DIM, 0, H.DTYPE_F32, H.DTYPE_F32, PEAK_FP8_TFLOPS, fp8_path)
     w.free()
+    # the same with group-128 scales (the reference's FP8 default, quant.rs:21)
+    w = weight("fp8", DIM, DIM, 0.02, 1002, group=128)
+    time_linear("cfg1_fp8_g128_q_proj_f32", x, M, DIM, w, DIM, 0, H.DTYPE_F32, H.DTYPE_F32, PEAK_FP8_TFLOPS,
+                fp8_g128_path, group=128)
+    w.free()
     x.free()
+    # config 4's seven GEMMs with group-128 weights, bf16 activations in and out
+    for name, rows, n, k, act, _ in GEMMS:
+        be.set_act_dtype(H.DTYPE_BF16)
+        x = be.alloc(rows * k)
+        be.fill_normal(x, 1041, 1.0)
+        w = weight("fp8", n, k, 0.02, 1042 + n + k, group=128)
+        time_linear(f"cfg4_g128_{name}", x, rows, k, w, n, act, H.DTYPE_BF16, H.DTYPE_BF16, PEAK_FP8_TFLOPS,
+                    fp8_g128_path, group=128)
+        w.free()
+        x.free()
     # config 2: Q8 (per-32 scales) FFN up + GELU, bf16 activations
     be.set_act_dtype(H.DTYPE_BF16)
     x = be.alloc(M * DIM)
     be.fill_normal(x, 1011, 1.0)
     w = weight("q8", FFN, DIM, 0.02, 1012)
     time_linear("cfg2_q8_ffn_up_gelu", x, M, DIM, w, FFN, 1, H.DTYPE_BF16, H.DTYPE_BF16, PEAK_BF16_TFLOPS,
-                "bf16 activations x Q8 weight dequantized to bf16 inside the GEMM, bf16 MFMA")
+                "bf16 activations x Q8 weight dequantized to bf16 inside the GEMM, bf16 MFMA", kind="q8", group=32)
     w.free()
     x.free()
     # config 3: Q4 (symmetric, per-32 scales) FFN down, input = GELU of N(0,1); plain and heavy-tailed
@@ -145,7 +177,7 @@ def per_config(be, H):
         w = weight("q4", DIM, FFN, 0.02, 1022, heavy=heavy)
         time_linear("cfg3_q4_ffn_down" + ("_heavy_tailed" if heavy else ""), x, M, FFN, w, DIM, 0,
                     H.DTYPE_BF16, H.DTYPE_BF16, PEAK_BF16_TFLOPS,
-                    "bf16 activations x Q4 weight dequantized to bf16 inside the GEMM, bf16 MFMA")
+                    "bf16 activations x Q4 weight dequantized to bf16 inside the GEMM, bf16 MFMA", kind="q4", group=32)
         w.free()
     x.free()
     # config 5: Wan2.2-TI2V-5B shapes in FP8, M = 2640 and 880
@@ -165,23 +197,28 @@ def per_config(be, H):
 
 
 def cpu_baseline(seconds_target=12.0):
-    """The CPU oracle (crates/lightx2v-cpu/src/lib.rs:296-326 restated,
-    row-parallel OpenMP with the reference's per-element operation order)
-    on a row sample of one layer-step's 7 FP8 GEMMs (weights dequantized as
-    the oracle's weight_fp8 does)."""
+    """The CPU oracle (crates/lightx2v-cpu/src/lib.rs:296-326 restated: a
+    sequential f32 acc += x*w per output, then bias, then GELU) on a row
+    sample of one layer-step's 7 FP8 GEMMs (weights dequantized as the
+    oracle's weight_fp8 does), timed twice in this run: on one thread (the
+    reference's CpuBackend is single-threaded, lib.rs:107-149) and with
+    OpenMP over output rows on every host core this process may use
+    (bit-identical outputs).  Each leg runs about seconds_target / 2."""
     import numpy as np
 
     import oracle as O
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    threads = max(1, min(16, threads))
+    nproc = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = max(1, min(affinity, int(omp))) if omp and omp.isdigit() else affinity
     ws = {}
     for i, (name, rows, n, k, act, _) in enumerate(GEMMS):
         wf = O.Rng(1002 + i).normal(n * k).reshape(n, k) * np.float32(0.02)
         q, s = O.fp8_quantize(wf, n, k, k, True)
         ws[name] = (O.fp8_dequantize(q, s, n, k, k), O.Rng(1003 + i).normal(n) * np.float32(0.01))
 
-    def run(sample_rows):
+    def run(sample_rows, nt):
         fl = 0.0
         t = 0.0
         for name, rows, n, k, act, _ in GEMMS:
@@ -189,21 +226,36 @@ def cpu_baseline(seconds_target=12.0):
             x = O.Rng(1001).normal(r * k).reshape(r, k)
             wd, b = ws[name]
             t0 = time.perf_counter()
-            O.linear(x, wd, b, act, nthreads=threads)
+            O.linear(x, wd, b, act, nthreads=nt)
             t += time.perf_counter() - t0
             fl += 2.0 * r * n * k
         return fl, t
 
-    fl, t = run(4)
-    rows = int(max(8, min(M, 4 * seconds_target / max(t, 1e-3))))
-    fl, t = run(rows)
+    def leg(nt):
+        fl, t = run(max(1, nt), nt)
+        rows = int(max(nt, min(M, max(1, nt) * (seconds_target / 2) / max(t, 1e-3))))
+        fl, t = run(rows, nt)
+        return fl / t / 1e12, rows, fl, t
+
+    v1, r1, f1, t1 = leg(1)
+    vn, rn, fn, tn = leg(threads)
+    step_flops = flops_of(GEMMS) * LAYERS * DMD
     return {
-        "value": fl / t / 1e12,
+        "value": vn,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle linear (sequential f32, OpenMP over rows) on {rows} rows of each of one "
-                   f"layer-step's 7 FP8 GEMMs (weights dequantized), {fl / 1e9:.1f} GFLOP in {t:.1f} s"),
+        "sample": (f"oracle linear (sequential f32 per output, OpenMP over rows) on {rn} rows of each of one "
+                   f"layer-step's 7 FP8 GEMMs (weights dequantized): {fn / 1e9:.1f} GFLOP in {tn:.1f} s on "
+                   f"{threads} threads (host nproc {nproc}, {affinity} usable by this process)"),
+        "single_thread": {
+            "value": v1, "cores": 1,
+            "sample": f"the same on {r1} rows per GEMM, one thread: {f1 / 1e9:.2f} GFLOP in {t1:.1f} s",
+        },
+        "chunk_s_extrapolated": {"single_thread": step_flops / (v1 * 1e12), "all_cores": step_flops / (vn * 1e12),
+                                 "what": "the chunk's 47.4 TFLOP at the sampled rates (an extrapolation)"},
+        "nproc": nproc,
+        "affinity": affinity,
     }
 
 
@@ -213,7 +265,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline: both legs together")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config linears")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eagerly only (rocprofv3 cannot trace hipGraphLaunch here)")
@@ -241,18 +293,22 @@ def main():
     ffn_mx = be.alloc_mx(M, FFN)  # FFN up -> FFN down in MX e4m3
     acts["y_ffn1"] = outs["ffn1"]
     tmp = be.alloc(FFN * DIM, H.DTYPE_F32)
-    layers = []
-    for l in range(LAYERS):
-        lw = {}
-        for j, (name, rows, n, k, act, _) in enumerate(GEMMS):
-            seed = 10_000 * (l + 1) + 10 * j
-            be.fill_normal(tmp, seed, 0.02)
-            w = be.quantize_fp8(tmp, n, k, k)
-            b = be.alloc(n, H.DTYPE_F32)
-            be.fill_normal(b, seed + 1, 0.01)
-            lw[name] = (w, b)
-        layers.append(lw)
-    tmp.free()
+
+    def make_layers(group):
+        out = []
+        for l in range(LAYERS):
+            lw = {}
+            for j, (name, rows, n, k, act, _) in enumerate(GEMMS):
+                seed = 10_000 * (l + 1) + 10 * j
+                be.fill_normal(tmp, seed, 0.02)
+                w = be.quantize_fp8(tmp, n, k, group or k)
+                b = be.alloc(n, H.DTYPE_F32)
+                be.fill_normal(b, seed + 1, 0.01)
+                lw[name] = (w, b)
+            out.append(lw)
+        return out
+
+    layers = make_layers(None)
     be.sync()
     wbytes = sum(w.info()["device_bytes"] for lw in layers for w, _ in lw.values())
     log(f"bench: setup {time.perf_counter() - t0:.1f} s, {wbytes / 1e9:.2f} GB FP8 weights resident")
@@ -300,6 +356,25 @@ def main():
     # the same chunk with the FFN hand-off in bf16 (per-token e4m3 inside FFN down)
     ms_bf16_handoff = timed(chunk(False), args.steps, args.warmup)
     log(f"bench: bf16 FFN hand-off (eager) {ms_bf16_handoff:.2f} ms/chunk")
+    # the chunk with group-128 weights (the reference's FP8 format, quant.rs:21;
+    # FFN up -> down in bf16: MX input takes per-channel weights only), eager
+    g128 = make_layers(128)
+
+    def chunk_g128():
+        for _ in range(DMD):
+            for lw in g128:
+                for name, rows, n, k, act, src in GEMMS:
+                    w, b = lw[name]
+                    be.linear(acts[src], 0, rows, w, b, act, outs[name], 0)
+
+    ms_g128 = timed(chunk_g128, args.steps, args.warmup)
+    log(f"bench: group-128 weights (eager) {ms_g128:.2f} ms/chunk")
+    for lw in g128:
+        for w, b in lw.values():
+            w.free()
+            b.free()
+    del g128
+    tmp.free()
     value = step_flops / ms / 1e9
 
     # ---- the block's linear path with its producers and consumers ---------------
@@ -315,8 +390,22 @@ def main():
     be.fill_normal(h, 1201, 1.0)
     normed = be.alloc(M * DIM)
     xq_blk = be.alloc_e4m3(M, DIM)
+    # head_split's outputs and parameters: q / k / v of the chunk and the
+    # text, [heads, rows, 128] bf16; RMS weights per layer; RoPE tables
+    # [M, 64] (dit.rs:612-641, 705, 477-489)
+    HD = 128
+    hq, hk, hv = (be.alloc(M * DIM) for _ in range(3))
+    hk2, hv2 = be.alloc(TEXT * DIM), be.alloc(TEXT * DIM)
+    rcos, rsin = be.alloc(M * HD // 2, H.DTYPE_F32), be.alloc(M * HD // 2, H.DTYPE_F32)
+    be.fill_normal(rcos, 1601, 0.7)
+    be.fill_normal(rsin, 1602, 0.7)
+    lrms = []
     lmods, lnw = [], []
     for l in range(LAYERS):
+        rw = [be.alloc(DIM, H.DTYPE_F32) for _ in range(4)]  # norm_q1, norm_k1, norm_q2, norm_k2
+        for i, b in enumerate(rw):
+            be.fill_normal(b, 1700 + 4 * l + i, 0.1)
+        lrms.append(rw)
         md = be.alloc(6 * DIM, H.DTYPE_F32)
         be.fill_normal(md, 1300 + l, 0.1)
         nw, nb = be.alloc(DIM, H.DTYPE_F32), be.alloc(DIM, H.DTYPE_F32)
@@ -331,12 +420,19 @@ def main():
             for _ in range(DMD):
                 for l, lw in enumerate(layers):
                     md, (nw, nb) = lmods[l], lnw[l]
+                    nq1, nk1, nq2, nk2 = lrms[l]
                     be.layer_norm(h, M, DIM, NK.mod(1, 0), md, 1e-6, xin)
                     be.linear(xin, 0, M, *lw["qkv"], 0, outs["qkv"], 0)
+                    be.head_split(outs["qkv"], M, 3 * DIM, 0, DIM // HD, HD, nq1, (rcos, rsin), 1e-6, hq)
+                    be.head_split(outs["qkv"], M, 3 * DIM, DIM, DIM // HD, HD, nk1, (rcos, rsin), 1e-6, hk)
+                    be.head_split(outs["qkv"], M, 3 * DIM, 2 * DIM, DIM // HD, HD, None, None, 1e-6, hv)
                     be.linear(acts["x_o"], 0, M, *lw["o"], 0, outs["o"], 0)
                     be.residual_norm(h, outs["o"], M, DIM, md, 2, NK.affine(nw, nb), 1e-6, xin)
                     be.linear(xin, 0, M, *lw["q2"], 0, outs["q2"], 0)
+                    be.head_split(outs["q2"], M, DIM, 0, DIM // HD, HD, nq2, None, 1e-6, hq)
                     be.linear(acts["x_text"], 0, TEXT, *lw["kv2"], 0, outs["kv2"], 0)
+                    be.head_split(outs["kv2"], TEXT, 2 * DIM, 0, DIM // HD, HD, nk2, None, 1e-6, hk2)
+                    be.head_split(outs["kv2"], TEXT, 2 * DIM, DIM, DIM // HD, HD, None, None, 1e-6, hv2)
                     be.linear(acts["x_o2"], 0, M, *lw["o2"], 0, outs["o2"], 0)
                     be.residual_norm(h, outs["o2"], M, DIM, md, None, NK.mod(4, 3), 1e-6, xin)
                     be.linear(xin, 0, M, *lw["ffn1"], 1, ffn_mx, 0)
@@ -397,6 +493,12 @@ def main():
         _, t = be.profile_kernel(name)
         region[name] = t / reps
     gemm_ms = region["gemm_fp8_chunk"]
+    # algorithmic bytes of the chunk's GEMMs as run here: e4m3 X (MX for FFN
+    # down, + its scale bytes), e4m3 W + f32 channel scales, f32 bias, bf16 Y
+    # (MX e4m3 + scales for FFN up), averaged per launch
+    alg_per_launch = sum(r * k + (r * k // 32 if nm == "ffn2" else r * 4) + n * k + n * 8 +
+                         (r * n + r * n // 32 if nm == "ffn1" else 2 * r * n)
+                         for nm, r, n, k, _, _ in GEMMS) / len(GEMMS)
     achieved = step_flops / gemm_ms / 1e9
     log(f"bench: GEMM-only {gemm_ms:.2f} ms/chunk ({gemm_ms * 1e3 / n_linear:.2f} us/launch, "
         f"{achieved:.1f} TFLOP/s); act quant {region['act_quant_chunk']:.2f} ms/chunk")
@@ -421,6 +523,20 @@ def main():
         per[name] = {"shape": f"{rows}x{k}->{n}", "gemm_us": round(us, 2), "act_quant_us": round(uq, 2),
                      "tflops": round(2.0 * rows * n * k / (us * 1e-6) / 1e12, 1),
                      "pct_fp8_peak": round(2.0 * rows * n * k / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS * 100, 1)}
+
+    # ---- head_split at the chunk's q (RMS + RoPE), 20 calls in a region ----
+    be.head_split(outs["qkv"], M, 3 * DIM, 0, DIM // HD, HD, lrms[0][0], (rcos, rsin), 1e-6, hq)
+    be.profile_region("hsplit", True)
+    for _ in range(20):
+        be.head_split(outs["qkv"], M, 3 * DIM, 0, DIM // HD, HD, lrms[0][0], (rcos, rsin), 1e-6, hq)
+    be.profile_region("hsplit", False)
+    hs_us = be.profile_kernel("hsplit")[1] * 1e3 / 20
+    hs_bytes = M * DIM * 2 * 2 + M * HD // 2 * 4 * 2 + DIM * 4
+    head_split = {"shape": f"q of the chunk's QKV: {M} rows x {DIM} of {3 * DIM}, RMS + RoPE, bf16 -> "
+                           f"[{DIM // HD}, {M}, {HD}]", "us": round(hs_us, 2), "alg_bytes": hs_bytes,
+                  "hbm_gbs": round(hs_bytes / (hs_us * 1e-6) / 1e9, 1),
+                  "pct_hbm": round(100.0 * hs_bytes / (hs_us * 1e-6) / 1e9 / HBM_GBS, 1)}
+    log(f"bench: head_split {hs_us:.1f} us ({head_split['hbm_gbs']} GB/s)")
 
     # ---- causal attention at the chunk's shape (not part of the linear metric) ----
     # 12 heads x 128, the 3-frame chunk's 4680 queries against one cached
@@ -569,15 +685,18 @@ def main():
         "ms_per_chunk_eager": round(ms_eager, 3),
         "ms_per_chunk_graph": round(ms_graph, 3) if ms_graph else None,
         "ms_per_chunk_bf16_ffn_handoff": round(ms_bf16_handoff, 3),
+        "ms_per_chunk_g128_weights": round(ms_g128, 3),
         "gemm_only_ms_per_chunk": round(gemm_ms, 3),
         "block_path_ms_per_chunk": {
             "unfused": block["unfused"], "fused": block["fused"],
             "what": "the chunk's 840 linears plus their producers and consumers (layer_norm, 2 residual_norm, "
-                    "gate_residual per layer-step; attention excluded); fused = the norms write the FP8 "
-                    "linears' e4m3 inputs in the same pass and FFN down's epilogue does the gate-residual add",
+                    "6 head_split (q / k RMS + RoPE, v; cross q; text k / v), gate_residual per layer-step; "
+                    "attention and the KV cache excluded); fused = the norms write the FP8 linears' e4m3 inputs "
+                    "in the same pass and FFN down's epilogue does the gate-residual add",
         },
         "act_quant_ms_per_chunk": round(region["act_quant_chunk"], 3),
         "per_gemm": per,
+        "head_split": head_split,
         "causal_attention": attn,
         "kv_cache": kv,
         "per_config": configs,
@@ -590,6 +709,8 @@ def main():
             "traffic": traffic,
             "kernel": "fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma: 256x128, 128x256 and 128x128 tiles)",
             "avg_launch_us": round(gemm_ms * 1e3 / n_linear, 2),
+            "hbm_gbs": round(traffic / (gemm_ms * 1e-3 / n_linear) / 1e9, 1) if traffic else None,
+            "alg_bytes_per_launch": round(alg_per_launch),
             "launches_per_step": n_linear,
         },
         "cpu_baseline": cpu,

@@ -382,6 +382,35 @@ __device__ __forceinline__ float ld_param(const void *p, int dt, size_t i) {
     return dt == LX2V_DTYPE_BF16 ? bf16_bits_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
 }
 
+// Parameters i .. i + N - 1 (N = 4 or 8, i a multiple of N) in one or two
+// vector loads.
+template <int N>
+__device__ __forceinline__ void ld_params(const void *p, int dt, size_t i, float (&o)[N]) {
+    if (dt == LX2V_DTYPE_BF16) {
+        const uint32_t *q = (const uint32_t *)((const uint16_t *)p + i);
+        uint32_t u[N / 2];
+        if constexpr (N == 8) {
+            const u32x4 t = *(const u32x4 *)q;
+            u[0] = t.x, u[1] = t.y, u[2] = t.z, u[3] = t.w;
+        } else {
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+            const u32x2_t t = *(const u32x2_t *)q;
+            u[0] = t.x, u[1] = t.y;
+        }
+#pragma unroll
+        for (int e = 0; e < N / 2; e++) {
+            o[2 * e] = bf16_bits_to_f32(u[e] & 0xFFFFu);
+            o[2 * e + 1] = bf16_bits_to_f32(u[e] >> 16);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < N; e += 4) {
+            const f32x4 t = *(const f32x4 *)((const float *)p + i + e);
+            o[e] = t.x, o[e + 1] = t.y, o[e + 2] = t.z, o[e + 3] = t.w;
+        }
+    }
+}
+
 template <int DT, int OD, int T>
 __global__ __launch_bounds__(kNThreads) void k_head_split(HeadSplitArgs p) {
     constexpr int R = DT == LX2V_DTYPE_BF16 ? 1 : 2;  // 16-byte words per input chunk
@@ -411,8 +440,10 @@ __global__ __launch_bounds__(kNThreads) void k_head_split(HeadSplitArgs p) {
         for (int t = 0; t < T; t++) {
             const int c = lane + 64 * t;
             if (c >= nch) continue;
+            float wv[8];
+            ld_params<8>(p.w, p.wdt, (size_t)c * 8, wv);
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[t][e] = v[t][e] * inv * ld_param(p.w, p.wdt, (size_t)c * 8 + e);
+            for (int e = 0; e < 8; e++) v[t][e] = v[t][e] * inv * wv[e];
         }
     }
     const size_t hh = p.hd / 2;
@@ -422,13 +453,14 @@ __global__ __launch_bounds__(kNThreads) void k_head_split(HeadSplitArgs p) {
         if (c >= nch) continue;
         const size_t col = (size_t)c * 8, h = col / p.hd, j = col % p.hd;
         if (p.cs) {
+            float cv[4], sv[4];
+            ld_params<4>(p.cs, p.rdt, row * hh + j / 2, cv);
+            ld_params<4>(p.sn, p.rdt, row * hh + j / 2, sv);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const size_t i = row * hh + j / 2 + e;
-                const float cv = ld_param(p.cs, p.rdt, i), sv = ld_param(p.sn, p.rdt, i);
                 const float a = v[t][2 * e], b = v[t][2 * e + 1];
-                v[t][2 * e] = a * cv - b * sv;
-                v[t][2 * e + 1] = a * sv + b * cv;
+                v[t][2 * e] = a * cv[e] - b * sv[e];
+                v[t][2 * e + 1] = a * sv[e] + b * cv[e];
             }
         }
         u32x4 w[2];
