@@ -397,6 +397,22 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
                     const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act,
                     lx2v_hip_buf *y, size_t y_row);
 
+/* No counterpart in the reference: lx2v_hip_linear for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, kernels and results as
+ * lx2v_hip_linear, bit for bit; its workspaces (the per-token e4m3
+ * activations and row scales, a bf16 bias's f32 copy, f32 activations' bf16
+ * copy) live in a device array of 48 MiB per device instead of the
+ * context's, so it calls no hipMalloc / hipFree and records no profiler
+ * events.  A call needing more (roughly rows * cols > 48 MiB with f32 / bf16
+ * activations) fails with LX2V_ERR_UNSUPPORTED and a message; pre-quantized
+ * E4M3 / MXE4M3 activations need none.  Every call on one device shares the
+ * array, which keeps the last call's contents: calls that overlap on one
+ * device (two streams, two contexts, two threads) race. */
+int lx2v_hip_linear_noalloc(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                            const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act,
+                            lx2v_hip_buf *y, size_t y_row);
+
 /* Test hook: the per-token e4m3 activation quantization linear applies to
  * x rows [x_row, x_row + rows) of width cols (FP8_ACT_E4M3), copied to host:
  * q [rows, cols] codes, s [rows] scales. */

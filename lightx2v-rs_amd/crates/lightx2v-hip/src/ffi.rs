@@ -415,6 +415,17 @@ extern "C" {
         y: *mut RawBuf,
         y_row: usize,
     ) -> c_int;
+    pub fn lx2v_hip_linear_noalloc(
+        ctx: *mut Ctx,
+        x: *const RawBuf,
+        x_row: usize,
+        rows: usize,
+        w: *const RawWeight,
+        bias: *const RawBuf,
+        act: c_int,
+        y: *mut RawBuf,
+        y_row: usize,
+    ) -> c_int;
     pub fn lx2v_hip_act_quant(
         ctx: *mut Ctx,
         x: *const RawBuf,

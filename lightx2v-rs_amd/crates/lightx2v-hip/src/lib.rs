@@ -561,6 +561,36 @@ impl HipBackend {
         });
     }
 
+    /// `linear` with no allocation (its workspaces in the library's 48 MiB
+    /// per-device scratch): for callers under graph capture or in loops that
+    /// must not allocate.  Calls that overlap on one device race.
+    #[allow(clippy::too_many_arguments)]
+    pub fn linear_noalloc(
+        &self,
+        x: &HipBuf,
+        x_row: usize,
+        rows: usize,
+        w: &HipWeight,
+        bias: Option<&HipBuf>,
+        act: Act,
+        y: &HipBuf,
+        y_row: usize,
+    ) {
+        check(unsafe {
+            ffi::lx2v_hip_linear_noalloc(
+                self.c(),
+                x.raw,
+                x_row,
+                rows,
+                w.raw,
+                Self::opt(bias),
+                Self::act(act),
+                y.raw,
+                y_row,
+            )
+        });
+    }
+
     /// Profile every kernel launch with HIP events (the CPU backend's
     /// LIGHTX2V_PROFILE switch is honoured at creation too).
     pub fn profile_enable(&self, on: bool) {

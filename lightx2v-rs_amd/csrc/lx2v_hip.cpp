@@ -258,6 +258,9 @@ int lx2v_hip_create(int device, lx2v_hip_ctx **out) {
         return fail(LX2V_ERR_NO_DEVICE, "device %d is %s, this build targets gfx950", device,
                     prop.gcnArchName);
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    // The no-alloc entry point's scratch on this device (once per device;
+    // a failure is reported by that entry point, not here).
+    (void)scratch_setup(device);
     auto *ctx = new lx2v_hip_ctx;
     ctx->device = device;
     ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
@@ -1798,8 +1801,12 @@ static int act_quant_into_ws(lx2v_hip_ctx *ctx, const void *x, int dtype, size_t
 
 // gate: residual mode (only where linear_fusable says so): y is the
 // residual stream, y[r] += out[r] * gate.
+// scr: the no-alloc variant -- every workspace comes from this device
+// memory (bias staging first, then the activations' e4m3 codes and row
+// scales or their bf16 copy), and the call fails cleanly if it is too small.
 static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows, const lx2v_hip_weight *w,
-                      const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y, size_t y_row, const float *gate) {
+                      const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y, size_t y_row, const float *gate,
+                      const lx2v::Scratch *scr = nullptr) {
     NEED(ctx, "ctx");
     NEED(x, "x");
     NEED(w, "weight");
@@ -1840,23 +1847,6 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     if (bias && overlap(yp, rows * N * y->elem_bytes(), bias->ptr, N * bias->elem_bytes()))
         return fail(LX2V_ERR_ALIAS, "linear output overlaps its bias");
     if (!rows) return ok();
-    if (int rc = set_dev(ctx)) return rc;
-
-    // The epilogue reads an f32 bias.
-    const float *bp = nullptr;
-    if (bias) {
-        if (bias->dtype == LX2V_DTYPE_F32) {
-            bp = (const float *)bias->ptr;
-        } else {
-            void *st;
-            if (int rc = stage_for(ctx, N * 4, &st)) return rc;
-            if (int rc = run(ctx, "convert", [&] {
-                    launch_convert(ctx->stream, bias->ptr, LX2V_DTYPE_BF16, st, LX2V_DTYPE_F32, N);
-                }))
-                return rc;
-            bp = (const float *)st;
-        }
-    }
 
     // The e4m3 path: quantized activations, MX output, or (per-token e4m3
     // mode) an FP8 weight the fp8 MFMA takes or no bf16 GEMM tiles (the
@@ -1865,8 +1855,38 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     // in its loader, bf16 activations).
     const bool w16_ok = gemm_w16_dma_supported(w, rows) ||
                         (gemm_w16_supported(w) && rows * K * x->elem_bytes() < (1ull << 31));
-    if (w->fmt == LX2V_WFMT_FP8 &&
-        (x->quantized() || y_mx || (ctx->fp8_act == LX2V_FP8_ACT_E4M3 && (fp8_mfma || !w16_ok)))) {
+    const bool e4m3_path = w->fmt == LX2V_WFMT_FP8 &&
+                           (x->quantized() || y_mx || (ctx->fp8_act == LX2V_FP8_ACT_E4M3 && (fp8_mfma || !w16_ok)));
+    // Scratch layout (no-alloc variant): [f32 bias][e4m3 codes][f32 row scales]
+    // or [f32 bias][bf16 activations], each piece 256-byte aligned.
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t s_bias = bias && bias->dtype != LX2V_DTYPE_F32 ? al(N * 4) : 0;
+    const size_t s_act = e4m3_path ? (x->quantized() ? 0 : al(rows * K) + al(rows * 4))
+                                   : (gemm_w16_dma_supported(w, rows) && x->dtype == LX2V_DTYPE_F32 ? al(rows * K * 2) : 0);
+    if (scr && s_bias + s_act > scr->bytes)
+        return fail(LX2V_ERR_UNSUPPORTED,
+                    "linear_noalloc: this call needs %zu bytes of scratch (rows %zu x cols %zu), the maximum is %zu",
+                    s_bias + s_act, rows, K, scr->bytes);
+    if (int rc = set_dev(ctx)) return rc;
+
+    // The epilogue reads an f32 bias.
+    const float *bp = nullptr;
+    if (bias) {
+        if (bias->dtype == LX2V_DTYPE_F32) {
+            bp = (const float *)bias->ptr;
+        } else {
+            void *st = scr ? (void *)scr->ptr : nullptr;
+            if (!scr)
+                if (int rc = stage_for(ctx, N * 4, &st)) return rc;
+            if (int rc = run(ctx, "convert", [&] {
+                    launch_convert(ctx->stream, bias->ptr, LX2V_DTYPE_BF16, st, LX2V_DTYPE_F32, N);
+                }))
+                return rc;
+            bp = (const float *)st;
+        }
+    }
+
+    if (e4m3_path) {
         const uint8_t *q;
         const float *s = nullptr;
         Fp8Mx mx;
@@ -1878,6 +1898,13 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
             mx.a = x->mxs + 4 * x_row;
             mx.a_rows = x->srows;
             mx.a_len = x->srows * 4 * (K / 128) - 4 * x_row;
+        } else if (scr) {
+            uint8_t *wq = scr->ptr + s_bias;
+            float *ws = (float *)(wq + al(rows * K));
+            if (int rc = run(ctx, "act_quant_e4m3", [&] { launch_act_quant(ctx->stream, xp, x->dtype, rows, K, wq, ws); }))
+                return rc;
+            q = wq;
+            s = ws;
         } else {
             uint8_t *wq;
             float *ws;
@@ -1922,12 +1949,16 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         // rounded (RNE, as the register-staged loader would) into the workspace.
         const uint16_t *xb = (const uint16_t *)xp;
         if (x->dtype == LX2V_DTYPE_F32) {
-            if (int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, rows * K * 2, "workspace alloc")) return rc;
+            void *dst = scr ? (void *)(scr->ptr + s_bias) : nullptr;
+            if (!scr) {
+                if (int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, rows * K * 2, "workspace alloc")) return rc;
+                dst = ctx->ws;
+            }
             if (int rc = run(ctx, "convert", [&] {
-                    launch_convert(ctx->stream, xp, LX2V_DTYPE_F32, ctx->ws, LX2V_DTYPE_BF16, rows * K);
+                    launch_convert(ctx->stream, xp, LX2V_DTYPE_F32, dst, LX2V_DTYPE_BF16, rows * K);
                 }))
                 return rc;
-            xb = (const uint16_t *)ctx->ws;
+            xb = (const uint16_t *)dst;
         }
         const int cfg = plan_gemm_w16_dma(ctx->num_cu, rows, N);
         if (int rc = run(ctx, name, [&] {
@@ -1957,6 +1988,25 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
                     const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y,
                     size_t y_row) {
     return linear_run(ctx, x, x_row, rows, w, bias, act, y, y_row, nullptr);
+}
+
+// No counterpart in the reference: `linear` for callers that cannot
+// allocate.  The workspaces come from the device scratch array of
+// lx2v_scratch.hip (kScratchBytes per device, resolved at create); no
+// hipMalloc / hipFree, no profiler events.
+int lx2v_hip_linear_noalloc(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
+                            const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y,
+                            size_t y_row) {
+    NEED(ctx, "ctx");
+    hipError_t e = hipSuccess;
+    void *p = scratch_ptr(ctx->device, &e);
+    if (!p) return hip_fail(e == hipSuccess ? hipErrorNotInitialized : e, "linear_noalloc: device scratch");
+    const lx2v::Scratch scr{(uint8_t *)p, kScratchBytes};
+    const bool prof = ctx->prof.on;
+    ctx->prof.on = false;  // no event creation inside this call
+    const int rc = linear_run(ctx, x, x_row, rows, w, bias, act, y, y_row, nullptr, &scr);
+    ctx->prof.on = prof;
+    return rc;
 }
 
 // The residual add can ride in the GEMM's epilogue: FP8 weight with one scale

@@ -81,9 +81,26 @@ struct Stage {
 
 }  // namespace lx2v
 
+namespace lx2v {
+
+// Device scratch of lx2v_hip_linear_noalloc (lx2v_scratch.hip): a
+// file-scope device array of kScratchBytes per device, its address resolved
+// by scratch_setup (called by lx2v_hip_create with the device current) and
+// read back with scratch_ptr (null + the error if setup failed or never ran).
+constexpr size_t kScratchBytes = size_t(48) << 20;
+struct Scratch {
+    uint8_t *ptr;
+    size_t bytes;
+};
+hipError_t scratch_setup(int device);
+void *scratch_ptr(int device, hipError_t *err);
+
+}  // namespace lx2v
+
 // Everything a context mutates lives in it: two contexts driven from two
 // threads share no host state (the only process-wide state is each thread's
-// last-error string).
+// last-error string and the per-device scratch addresses, resolved once
+// under a lock).
 struct lx2v_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;

@@ -49,6 +49,7 @@ EXPORTS = [
     "lx2v_hip_kv_cache_put", "lx2v_hip_kv_cache_len", "lx2v_hip_kv_cache_temporal", "lx2v_hip_kv_cache_kinds",
     "lx2v_hip_kv_cache_kv", "lx2v_hip_kv_cache_read", "lx2v_hip_kv_cache_memrope_update",
     "lx2v_hip_kv_cache_attention", "lx2v_hip_mask_temporal", "lx2v_hip_linear_residual", "lx2v_hip_head_split",
+    "lx2v_hip_linear_noalloc",
 ]
 
 
@@ -147,6 +148,7 @@ def _load():
                                         vp]),
         "lx2v_hip_gate_residual": (ip, [vp, vp, vp, sz, sz, vp, sz]),
         "lx2v_hip_head_split": (ip, [vp, vp, sz, sz, sz, sz, sz, vp, vp, vp, ctypes.c_float, vp]),
+        "lx2v_hip_linear_noalloc": (ip, [vp, vp, sz, sz, vp, vp, ip, vp, sz]),
         "lx2v_hip_attention": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp]),
         "lx2v_hip_causal_attention": (ip, [vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),
         "lx2v_hip_mask_upload": (ip, [vp, vp, sz, sz, pp]),
@@ -547,6 +549,12 @@ class HipBackend:
                y: Buf, y_row: int):
         _check(lib.lx2v_hip_linear(self.ctx, x.h, x_row, rows, w.h, bias.h if bias else None, act, y.h,
                                    y_row))
+
+    def linear_noalloc(self, x: Buf, x_row: int, rows: int, w: Weight, bias: Optional[Buf], act: int, y: Buf,
+                       y_row: int):
+        """lx2v_hip_linear_noalloc: linear with its workspaces in the device scratch."""
+        _check(lib.lx2v_hip_linear_noalloc(self.ctx, x.h, x_row, rows, w.h, bias.h if bias is not None else None,
+                                           act, y.h, y_row))
 
     def linear_residual(self, x: Buf, x_row: int, rows: int, w: Weight, bias: Optional[Buf], act: int, h: Buf,
                         h_row: int, mods: Buf, gate: int):
