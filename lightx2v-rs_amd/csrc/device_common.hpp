@@ -248,7 +248,13 @@ __device__ __forceinline__ uint32_t buffer_load_x1(__amdgpu_buffer_rsrc_t r, uin
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
 
-// Offset that is always out of range (reads as zero).
+// Offset that is always out of range (reads as zero; a store there is dropped).
 constexpr uint32_t kOob = 0x80000000u;
+
+// 16-byte vector store through a buffer descriptor: offsets >= num_bytes are
+// dropped by the hardware range check.
+__device__ __forceinline__ void buffer_store_x4(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, 0);
+}
 
 }  // namespace lx2v

@@ -116,10 +116,13 @@ struct MxOut {
 // row (one j of one lane pair l, l + 32) gets the scale 2^k of mx_exponent
 // over its 32 values; the codes go to the staging tile and the scale byte
 // straight to global memory (tile origin m0, n0).
-template <int BM, int BN, int TM, int TN, typename TY>
+//
+// ACT (compile time, so the per-element code is branch-free): GELU or none.
+// ALLROWS: the pass covers the whole tile (every block of the wave is in it).
+template <int BM, int BN, int TM, int TN, typename TY, int ACT, bool ALLROWS>
 __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const float *sc, uint8_t *stg, int rloc,
-                                           int R, int wr, int wc, int lane, int act, MxOut mx, int m0, int n0,
-                                           int M, int N) {
+                                           int R, int wr, int wc, int lane, MxOut mx, int m0, int n0, int M,
+                                           int N) {
     constexpr int EB = sizeof(TY), RB = BN * EB, SWZ = stage_swz<BN, TY>();
     static_assert(RB >= 128 && (RB & (RB - 1)) == 0, "staging row must be a power of two >= 128 bytes");
     const int l32 = lane & 31, hf = lane >> 5;
@@ -144,7 +147,7 @@ __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const fl
             col_ops(j, s4, b4);
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                if (rloc + i * 32 < 0 || rloc + i * 32 >= R) continue;
+                if (!ALLROWS && (rloc + i * 32 < 0 || rloc + i * 32 >= R)) continue;
                 float v[16];
                 float amax = 0.0f;
 #pragma unroll
@@ -152,7 +155,7 @@ __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const fl
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         float t = acc[j][i][4 * g + q] * sam[i] * s4[g][q] + b4[g][q];
-                        if (act == LX2V_ACT_GELU_TANH) t = gelu_tanh_fast(t);
+                        if constexpr (ACT == LX2V_ACT_GELU_TANH) t = gelu_tanh_fast(t);
                         v[4 * g + q] = t;
                         amax = fmaxf(amax, fabsf(t));
                     }
@@ -194,12 +197,12 @@ __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const fl
             const int cb = c * EB;  // byte column in the row
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                if (rloc + i * 32 < 0 || rloc + i * 32 >= R) continue;
+                if (!ALLROWS && (rloc + i * 32 < 0 || rloc + i * 32 >= R)) continue;
                 float v[4];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     v[q] = acc[j][i][4 * g + q] * sam[i] * s4[q] + b4[q];
-                    if (act == LX2V_ACT_GELU_TANH) v[q] = gelu_tanh_fast(v[q]);
+                    if constexpr (ACT == LX2V_ACT_GELU_TANH) v[q] = gelu_tanh_fast(v[q]);
                 }
                 const int r = rloc + i * 32 + l32;
                 uint8_t *p = stg + r * RB + ((((cb >> 4) ^ (r & (SWZ - 1)))) << 4) + (cb & 15);
@@ -301,6 +304,59 @@ __device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m
     }
 }
 
+// Whole-tile store of a staged pass (R rows x BN) for tiles whose columns
+// all lie inside N, N a multiple of the 16-byte chunk's elements and M * N *
+// sizeof(TY) < 2^31: every LDS read is issued first, then every store, through
+// a descriptor of Y that drops rows past M -- no branches and no waits between
+// the stores.  RES (residual mode): h's chunks and the gate are loaded first
+// and h + y * gate stored.
+template <int R, int BN, int NT, typename TY, bool RES>
+__device__ __forceinline__ void lds_to_global_fast(const uint8_t *stg, int tid, int m0, int n0, int M, int N,
+                                                   TY *__restrict__ Y, const float *__restrict__ gate) {
+    constexpr int EB = sizeof(TY), RB = BN * EB, CPR = RB / 16, EPC = 16 / EB, SWZ = stage_swz<BN, TY>();
+    constexpr int IT = R * CPR / NT;
+    // chunks read from LDS ahead of their stores, four at a time (the
+    // two-workgroup-per-CU tiles have no registers for more)
+    constexpr int BATCH = IT < 4 ? IT : 4;
+    static_assert((R * CPR) % NT == 0 && NT % CPR == 0 && IT % BATCH == 0, "staging tile must split evenly");
+    const auto ry = make_rsrc(Y, (uint32_t)M * (uint32_t)N * EB);
+    const int c = tid % CPR, n = n0 + c * EPC;
+    auto off = [&](int it) {
+        const int m = m0 + (it * NT + tid) / CPR;
+        return m < M ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * EB : kOob;
+    };
+    u32x4 hv[RES ? IT : 1];
+    float gv[RES ? EPC : 1];
+    if constexpr (RES) {
+#pragma unroll
+        for (int it = 0; it < IT; it++) hv[it] = buffer_load_x4(ry, off(it));
+#pragma unroll
+        for (int q = 0; q < EPC; q += 4) {
+            const f32x4 g4 = *(const f32x4 *)(gate + n + q);
+            gv[q] = g4.x, gv[q + 1] = g4.y, gv[q + 2] = g4.z, gv[q + 3] = g4.w;
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < IT; b += BATCH) {
+        u32x4 v[BATCH];
+#pragma unroll
+        for (int k = 0; k < BATCH; k++) {
+            const int r = ((b + k) * NT + tid) / CPR;
+            v[k] = *(const u32x4 *)(stg + r * RB + ((c ^ (r & (SWZ - 1))) << 4));
+        }
+#pragma unroll
+        for (int k = 0; k < BATCH; k++) {
+            if constexpr (RES) {
+                TY *e = (TY *)&v[k];
+                const TY *he = (const TY *)&hv[b + k];
+#pragma unroll
+                for (int q = 0; q < EPC; q++) e[q] = residual1<TY>(he[q], e[q], gv[q]);
+            }
+            buffer_store_x4(v[k], ry, off(b + k));
+        }
+    }
+}
+
 constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
 
 // The staged epilogue of a BM x BN block tile through SMEM bytes of LDS,
@@ -309,25 +365,61 @@ constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
 // for every wave's last fragment reads before reusing the ring; the
 // operands in sc (TileOps) must be parked before the call.  The wave owns
 // tile rows [wr, wr + 32 TM) and columns [wc, wc + 32 TN).
-template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY, bool RES = true>
+//
+// ACT: the activation, fixed at compile time (LX2V_ACT_*), or -1 to take
+// `act` at run time (two copies of the staging code in the kernel: more
+// registers).
+//
+// WAIT0 = false: the caller's loads into `smem` are known complete (only a
+// barrier is taken first), so loads still in flight elsewhere -- the next
+// tile's stages of a persistent kernel -- keep flying through the epilogue.
+template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY, bool RES = true, int ACT = -1,
+          bool WAIT0 = true>
 __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, const float *sc, int wr,
                                                 int wc, int tid, int lane, int m0, int n0, int M, int N, int act,
                                                 TY *__restrict__ Y, MxOut mx = MxOut()) {
     constexpr int RB = BN * (int)sizeof(TY);
     constexpr int R = pow2_floor(SMEM / RB < BM ? SMEM / RB : BM);
     static_assert(BM % R == 0 && R % 32 == 0, "passes of whole 32-row blocks");
-    wait_vmcnt<0>();
+    if constexpr (WAIT0) wait_vmcnt<0>();
     __syncthreads();
+    constexpr int EPC = 16 / (int)sizeof(TY);
+    // Uniform per workgroup: the branch-free store path applies (bf16 and
+    // MX output; with f32 output its registers would spill the 128 x 128
+    // three-per-CU tile).
+    const bool fast = sizeof(TY) != 4 && n0 + BN <= N && N % EPC == 0 && (uint64_t)M * (uint64_t)N * sizeof(TY) < (1ull << 31) &&
+                      (((uintptr_t)mx.gate) & 15) == 0;
 #pragma unroll
     for (int p = 0; p < BM / R; p++) {
         if (p) __syncthreads();
-        if (wr < (p + 1) * R && wr + 32 * TM > p * R)
-            acc_to_lds<BM, BN, TM, TN, TY>(acc, sc, smem, wr - p * R, R, wr, wc, lane, act, mx, m0, n0, M, N);
+        if (wr < (p + 1) * R && wr + 32 * TM > p * R) {
+            if constexpr (ACT >= 0)
+                acc_to_lds<BM, BN, TM, TN, TY, ACT, R == BM>(acc, sc, smem, wr - p * R, R, wr, wc, lane, mx, m0, n0,
+                                                             M, N);
+            else if (act == LX2V_ACT_GELU_TANH)
+                acc_to_lds<BM, BN, TM, TN, TY, LX2V_ACT_GELU_TANH, R == BM>(acc, sc, smem, wr - p * R, R, wr, wc,
+                                                                            lane, mx, m0, n0, M, N);
+            else
+                acc_to_lds<BM, BN, TM, TN, TY, LX2V_ACT_NONE, R == BM>(acc, sc, smem, wr - p * R, R, wr, wc, lane,
+                                                                       mx, m0, n0, M, N);
+        }
         __syncthreads();
-        if constexpr (sizeof(TY) == 1 || !RES)
-            lds_to_global<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y);
-        else
-            lds_to_global<R, BN, NT, TY, true>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
+        if constexpr (sizeof(TY) == 1 || !RES) {
+            if (fast)
+                lds_to_global_fast<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y, nullptr);
+            else
+                lds_to_global<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y);
+        } else if (mx.gate) {
+            if (fast)
+                lds_to_global_fast<R, BN, NT, TY, true>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
+            else
+                lds_to_global<R, BN, NT, TY, true>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
+        } else {
+            if (fast)
+                lds_to_global_fast<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y, nullptr);
+            else
+                lds_to_global<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y);
+        }
     }
 }
 

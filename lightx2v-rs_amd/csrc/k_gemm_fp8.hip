@@ -257,7 +257,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8(const uint8_t *__restrict__
 // row).  Each stage's two MFMAs per block run into a fresh partial sum,
 // which is then folded in, acc += part * s[n, kt]; sb is then null (1 in the
 // epilogue) and sa still scales each token.
-template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC, int AM, int GS, typename TY>
+//
+// ACT: the epilogue activation (LX2V_ACT_*), a template parameter so that the
+// epilogue holds one copy of its staging code.
+template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC, int AM, int GS, int ACT, typename TY>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint8_t *__restrict__ A,
                                                                    const float *__restrict__ sa,
                                                                    const uint8_t *__restrict__ B,
@@ -515,8 +518,250 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     mx.scales = ymx;
     mx.rows = ymx_rows;
     mx.gate = gate;
-    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N,
-                                                          act, Y, mx);
+    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY, true, ACT>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0,
+                                                                     n0, M, N, act, Y, mx);
+}
+
+// ---- persistent direct-to-LDS kernel ---------------------------------------------
+//
+// k_gemm_fp8_dma's 256 x 128 tile (8 waves of 64 x 64 sub-tiles, 128-byte
+// stages in a 3-stage ring, per-token e4m3 activations) as one workgroup per
+// CU that walks a list of tiles: pass i of workgroup w computes tile
+// xcd_tile(w + i G) for a grid of G workgroups, G a multiple of 8, so every
+// tile of a workgroup lies in its XCD's band.  The ring runs on across
+// tiles: while a tile's last two stages are contracted, the next tile's
+// first two are already loading, and the epilogue stages its outputs
+// through the slot the last stage freed.  A tile's token scales, channel
+// scales and bias travel into LDS by DMA too (issued with its first stage),
+// so no compiler-tracked load is ever waited for -- such a wait would also
+// wait for the next tile's stages.  Null scales read a table of ones.
+//
+// Constraints (checked by the host): K % 128 == 0 and K >= 256; no MX
+// activations, no residual mode.  GS: group-128 weight scales (wave 0 adds
+// the stage's BN scales to each stage, as in k_gemm_fp8_dma).
+
+__device__ const float k_ones[256] = {
+#define LX2V_1x16 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f
+    LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16,
+    LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16, LX2V_1x16
+#undef LX2V_1x16
+};
+
+template <int GS, int ACT, typename TY>
+__global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restrict__ A, const float *__restrict__ sa,
+                                                       const uint8_t *__restrict__ B, const float *__restrict__ sb,
+                                                       const float *__restrict__ bias, TY *__restrict__ Y, int M,
+                                                       int N, int K, int act, int tiles_m, int tiles_n,
+                                                       uint8_t *__restrict__ ymx, int ymx_rows,
+                                                       const float *__restrict__ gsc) {
+    constexpr int BM = 256, BN = 128, WGM = 4, WGN = 2, BKB = 128, NS = 3;
+    constexpr int NW = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int CPR = BKB / 16, RPI = 64 / CPR;
+    constexpr int ALD = BM / RPI / NW, BLD = BN / RPI / NW;
+    constexpr int STAGE = (BM + BN) * BKB;
+    constexpr uint32_t AMASK = BM * BKB - 1, BMASK = BN * BKB - 1;
+    constexpr int GSL = 1024;  // per-stage slot for the group scales (a whole wave's DMA)
+    constexpr int NV = BM + 2 * BN;
+    static_assert(NS * STAGE + NV * 4 + 1024 + (GS ? NS * GSL : 0) <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    // [BM token scales][BN channel scales][BN bias] + a 1 KB pad that the
+    // partial DMAs of the last region never reach (lane-masked)
+    __shared__ __attribute__((aligned(16))) float sc[NV + 256];
+    __shared__ __attribute__((aligned(16))) uint8_t gsl[GS ? NS * GSL : 16];
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int wid_u = __builtin_amdgcn_readfirstlane(wid);
+    const int G = gridDim.x, w = blockIdx.x, ntiles = tiles_m * tiles_n;
+    const int my_n = w < ntiles ? (ntiles - w + G - 1) / G : 0;
+    if (my_n == 0) return;  // (uniform) no tile: no descriptor may be built
+    const int KT = K / BKB;
+    auto tile_of = [&](int i, int *m0, int *n0) {
+        int tm, tn;
+        xcd_tile(w + i * G, ntiles, tiles_m, tiles_n, &tm, &tn);
+        *m0 = tm * BM;
+        *n0 = tn * BN;
+    };
+
+    // Issue side: the (pass, stage) whose loads go out next, and its tile's
+    // descriptors.
+    int is_i = 0, is_kt = 0, is_m0 = 0, is_n0 = 0;
+    tile_of(0, &is_m0, &is_n0);
+    __amdgpu_buffer_rsrc_t ra_src, rb_src, rg_src;
+    auto set_issue_tile = [&]() {
+        ra_src = make_rsrc(A + (size_t)is_m0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(M - is_m0) * (uint32_t)K));
+        rb_src = make_rsrc(B + (size_t)is_n0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(N - is_n0) * (uint32_t)K));
+        if constexpr (GS)
+            rg_src = make_rsrc(gsc + is_n0, __builtin_amdgcn_readfirstlane(
+                                                ((uint32_t)(2 * KT) * (uint32_t)N - (uint32_t)is_n0) * 4u));
+    };
+    set_issue_tile();
+
+    const uint32_t lrow = (uint32_t)lane / CPR, lslot = (uint32_t)lane % CPR;
+    uint32_t a_off[ALD], b_off[BLD];
+#pragma unroll
+    for (int i = 0; i < ALD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * RPI + lrow;
+        a_off[i] = row * (uint32_t)K + dma_slot<BKB>(row, lslot) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < BLD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * RPI + lrow;
+        b_off[i] = row * (uint32_t)K + dma_slot<BKB>(BM + row, lslot) * 16;
+    }
+    // Load n of this wave's share of the issue stage into slot buf.
+    auto piece = [&](int n, int buf) {
+        const bool in = is_i < my_n;
+        const uint32_t k0 = (uint32_t)is_kt * BKB;
+        uint8_t *sbuf = smem + buf * STAGE;
+        if (n < ALD)
+            dma16(ra_src, sbuf + (n * NW + wid_u) * RPI * BKB, in ? a_off[n < ALD ? n : 0] + k0 : kOob);
+        else
+            dma16(rb_src, sbuf + (BM + ((n - ALD) * NW + wid_u) * RPI) * BKB,
+                  in ? b_off[n >= ALD ? n - ALD : 0] + k0 : kOob);
+    };
+    auto issue_scales = [&](int buf) {
+        if constexpr (GS) {
+            if (wid_u == 0) {
+                const bool ok = is_i < my_n && lane < BN / 4;
+                dma16(rg_src, gsl + buf * GSL, ok ? (uint32_t)(2 * is_kt) * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
+            }
+        }
+    };
+    auto advance_issue = [&]() {
+        if (++is_kt == KT) {
+            is_kt = 0;
+            if (++is_i < my_n) {
+                tile_of(is_i, &is_m0, &is_n0);
+                set_issue_tile();
+            }
+        }
+    };
+    // The tile's epilogue operands into sc (wave 1: token scales, wave 2:
+    // channel scales, wave 3: bias; lanes past the region masked off).
+    // A null scale reads the ones table; a null bias reads nothing (zeros).
+    auto issue_ops = [&](int m0, int n0) {
+        if (wid_u == 1) {
+            const auto r = sa ? make_rsrc(sa + m0, __builtin_amdgcn_readfirstlane((uint32_t)(M - m0) * 4u))
+                              : make_rsrc(k_ones, 1024u);
+            dma16(r, (uint8_t *)sc, (uint32_t)lane * 16u);
+        } else if (wid_u == 2) {
+            const auto r = sb ? make_rsrc(sb + n0, __builtin_amdgcn_readfirstlane((uint32_t)(N - n0) * 4u))
+                              : make_rsrc(k_ones, 1024u);
+            if (lane < BN / 4) dma16(r, (uint8_t *)(sc + BM), (uint32_t)lane * 16u);
+        } else if (wid_u == 3) {
+            const auto r = bias ? make_rsrc(bias + n0, __builtin_amdgcn_readfirstlane((uint32_t)(N - n0) * 4u))
+                                : make_rsrc(k_ones, 0u);
+            if (lane < BN / 4) dma16(r, (uint8_t *)(sc + BM + BN), (uint32_t)lane * 16u);
+        }
+    };
+    constexpr int LPS = ALD + BLD;
+
+    f32x16 acc[TN][TM];
+    f32x16 part[GS ? TN : 1][GS ? TM : 1];
+    const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
+    auto compute = [&](int buf, bool do_issue, int dbuf) {
+        const uint8_t *st = smem + buf * STAGE;
+#pragma unroll
+        for (int kk = 0; kk < BKB / 64; kk++) {
+            i32x8 af[TM], bf[TN];
+            const uint32_t c0 = kk * 4 + fhalf, c1 = c0 + 1;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const uint32_t row = wm * WM + i * 32 + frow;
+                u32x4 lo = *(const u32x4 *)(st + ((row * BKB + (dma_slot<BKB>(row, c0) << 4)) & AMASK));
+                u32x4 hi = *(const u32x4 *)(st + ((row * BKB + (dma_slot<BKB>(row, c1) << 4)) & AMASK));
+                af[i] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint32_t row = BM + wn * WN + j * 32 + frow;
+                const uint32_t rb = row - BM;
+                u32x4 lo = *(const u32x4 *)(st + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c0) << 4)) & BMASK));
+                u32x4 hi = *(const u32x4 *)(st + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c1) << 4)) & BMASK));
+                bf[j] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    if constexpr (GS)
+                        part[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            bf[j], af[i], kk == 0 ? (f32x16){} : part[j][i], 0, 0, 0, 0, 0, 0);
+                    else
+                        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[j][i], 0, 0, 0,
+                                                                                    0, 0, 0);
+                    const int n = kk * TN * TM + j * TM + i;
+                    if (n < LPS && do_issue) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        piece(n, dbuf);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+        }
+        if constexpr (GS) {
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                f32x4 g4[4];
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    g4[g] = *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            acc[j][i][4 * g + q] = __builtin_fmaf(part[j][i][4 * g + q], g4[g][q], acc[j][i][4 * g + q]);
+            }
+        }
+    };
+    static_assert((BKB / 64) * TN * TM >= LPS, "a stage's loads interleave with its MFMAs");
+
+    // Prologue: the first NS - 1 stages of the walk.
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++) {
+        issue_scales(st);
+#pragma unroll
+        for (int n = 0; n < LPS; n++) piece(n, st);
+        advance_issue();
+    }
+    int s = 0;  // global stage index of this workgroup's walk
+    for (int i = 0; i < my_n; i++) {
+        int m0, n0;
+        tile_of(i, &m0, &n0);
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int ii = 0; ii < TM; ii++) acc[j][ii] = (f32x16){};
+        for (int kt = 0; kt < KT; kt++, s++) {
+            // Stage s complete for this wave (stages s + 1 .. s + NS - 2 may
+            // still fly); the barrier publishes every wave's part and frees
+            // the slot the issue below refills.
+            if (GS && wid_u == 0)
+                wait_vmcnt<(NS - 2) * (LPS + 1)>();
+            else
+                wait_vmcnt<(NS - 2) * LPS>();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt == 0) issue_ops(m0, n0);  // after the barrier: the last epilogue is done with sc
+            const int buf = s % NS, dbuf = (s + NS - 1) % NS;
+            issue_scales(dbuf);
+            compute(buf, true, dbuf);
+            advance_issue();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // The ops DMA went out with stage s - KT, before the ring loads that
+        // every later wait covered (KT >= 2).
+        MxOut mx;
+        mx.scales = ymx;
+        mx.rows = ymx_rows;
+        staged_epilogue<BM, BN, 64 * NW, STAGE, TM, TN, TY, false, ACT, false>(
+            acc, smem + ((s - 1) % NS) * STAGE, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N, act, Y, mx);
+    }
+    wait_vmcnt<0>();  // the walk's trailing loads (zeros) land before the workgroup ends
 }
 
 // ---- ping-pong kernel: two wave groups alternate MFMA and LDS phases ---------------
@@ -700,10 +945,17 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
     dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
     const uint32_t alen = (uint32_t)mx.a_len;
     const int arows = (int)mx.a_rows, yrows = (int)mx.y_rows;
-#define LX2V_DMA_G(AMV, GSV, T)                                                                              \
-    hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, AMV, GSV, T>), grid, block, 0, s, a, sa, b, \
-                       GSV ? nullptr : sb, bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y,  \
+#define LX2V_DMA_A(AMV, GSV, ACTV, T)                                                                           \
+    hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, AMV, GSV, ACTV, T>), grid, block, 0, s, a, sa, \
+                       b, GSV ? nullptr : sb, bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y, \
                        yrows, mx.gate, mx.wgs)
+#define LX2V_DMA_G(AMV, GSV, T)                       \
+    do {                                              \
+        if (act == LX2V_ACT_GELU_TANH)                \
+            LX2V_DMA_A(AMV, GSV, LX2V_ACT_GELU_TANH, T); \
+        else                                          \
+            LX2V_DMA_A(AMV, GSV, LX2V_ACT_NONE, T);      \
+    } while (0)
 #define LX2V_DMA(AMV, T) LX2V_DMA_G(AMV, 0, T)
     if constexpr (GSC) {
         if (mx.wgs) {
@@ -739,8 +991,46 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
         LX2V_DMA(0, float);
 #undef LX2V_DMA
 #undef LX2V_DMA_G
+#undef LX2V_DMA_A
 }
 
+
+// The persistent 256 x 128 kernel: a grid of one workgroup per CU (a
+// multiple of 8, at most the tile count) walking the tiles.
+void launch_pt(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
+               const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
+    const int tiles_m = (M + 255) / 256, tiles_n = (N + 127) / 128, nt = tiles_m * tiles_n;
+    int g = nt < num_cu ? nt : num_cu;
+    g = g >= 8 ? g / 8 * 8 : g;
+    const dim3 grid(g), block(512);
+    const int yr = (int)mx.y_rows;
+#define LX2V_PT(GSV, ACTV, T)                                                                                      \
+    hipLaunchKernelGGL((k_gemm_fp8_pt<GSV, ACTV, T>), grid, block, 0, s, a, sa, b, GSV ? nullptr : sb, bias, (T *)y, \
+                       M, N, K, act, tiles_m, tiles_n, mx.y, yr, mx.wgs)
+#define LX2V_PT_T(GSV, T)                          \
+    do {                                           \
+        if (act == LX2V_ACT_GELU_TANH)             \
+            LX2V_PT(GSV, LX2V_ACT_GELU_TANH, T);   \
+        else                                       \
+            LX2V_PT(GSV, LX2V_ACT_NONE, T);        \
+    } while (0)
+#define LX2V_PT_Y(GSV)                                \
+    do {                                              \
+        if (y_dtype == LX2V_DTYPE_BF16)               \
+            LX2V_PT_T(GSV, uint16_t);                 \
+        else if (y_dtype == LX2V_DTYPE_F32)           \
+            LX2V_PT_T(GSV, float);                    \
+        else                                          \
+            LX2V_PT_T(GSV, uint8_t);                  \
+    } while (0)
+    if (mx.wgs)
+        LX2V_PT_Y(1);
+    else
+        LX2V_PT_Y(0);
+#undef LX2V_PT_Y
+#undef LX2V_PT_T
+#undef LX2V_PT
+}
 
 // Direct-to-LDS configurations: tile (activation rows x channels), wave
 // grid, K bytes per stage, stages.
@@ -756,6 +1046,8 @@ constexpr DmaCfg kDma[] = {
     {128, 256, 2, 4, 64, 3},   // 4: two per CU
     // ping-pong (k_gemm_fp8_pp); wgm x wgn = one group's waves
     {256, 256, 1, 4, 64, 4},   // 5
+    // persistent 256 x 128 (k_gemm_fp8_pt)
+    {256, 128, 4, 2, 128, 3},  // 6
 };
 
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
@@ -776,7 +1068,8 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
         case 4:
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
-        default: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 5: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        default: break;  // 6: launch_pt (needs the CU count)
     }
 }
 
@@ -792,7 +1085,7 @@ int forced_cfg() {
 
 }  // namespace
 
-bool gemm_fp8_residual_ok(const Fp8Plan &p) { return p.kernel >= 0 && p.kernel != 5; }
+bool gemm_fp8_residual_ok(const Fp8Plan &p) { return p.kernel >= 0 && p.kernel != 5 && p.kernel != 6; }
 
 bool gemm_fp8_grouped_supported(size_t M, size_t N, size_t K, size_t group) {
     return group == 128 && K % 128 == 0 && N % 4 == 0 && gemm_fp8_supported(M, N, K) &&
@@ -836,11 +1129,13 @@ constexpr CfgCost kGroupedAuto[] = {
 // The configurations with MX-activation / MX-output kernels.  The 128 x 256
 // two-per-CU tile takes no MX activations: their scale handling needs more
 // than the 128 VGPRs two workgroups per CU leave a wave.
-bool mx_capable(int idx, bool mx_in) { return idx == 0 || idx == 3 || (idx == 4 && !mx_in); }
+bool mx_capable(int idx, bool mx_in) { return idx == 0 || idx == 3 || ((idx == 4 || idx == 6) && !mx_in); }
 // The configurations built with grouped weight scales (128-byte stages, one
 // workgroup per CU: the partial sums need the registers); MX output on the
 // 256 x 128 tile only, no MX activations.
-bool grouped_capable(int idx, bool mx, bool mx_in) { return !mx_in && (idx == 0 || (idx == 1 && !mx)); }
+bool grouped_capable(int idx, bool mx, bool mx_in) {
+    return !mx_in && (idx == 0 || idx == 6 || (idx == 1 && !mx));
+}
 
 Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped) {
     Fp8Plan p;
@@ -850,7 +1145,7 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
     auto ok = [&](int idx) {
         return grouped ? grouped_capable(idx, mx, mx_in) : (!mx || mx_capable(idx, mx_in));
     };
-    if (forced >= 0 && forced < nd && ok(forced)) {
+    if (forced >= 0 && forced < nd && ok(forced) && (forced != 6 || K >= 256)) {
         p.kernel = forced;
         return p;
     }
@@ -885,6 +1180,10 @@ void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t 
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
                      int y_dtype, size_t M, size_t N, size_t K, const Fp8Mx &mx) {
     int m = (int)M, n = (int)N, k = (int)K;
+    if (p.kernel == 6) {
+        launch_pt(s, num_cu, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k, mx);
+        return;
+    }
     if (p.kernel >= 0) {
         launch_dma_idx(p.kernel, s, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k, mx);
         return;

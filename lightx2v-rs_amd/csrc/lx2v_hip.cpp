@@ -1920,7 +1920,7 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         if (fp8_mfma) {
             if (fp8_grouped) mx.wgs = w->sscale;
             const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx, fp8_grouped);
-            if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1)  // the tiles built with grouped scales
+            if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1 && plan.kernel != 6)  // built with grouped scales
                 return fail(LX2V_ERR_UNSUPPORTED, "no grouped-scale fp8 kernel for configuration %d", plan.kernel);
             // Profile name: the kernel configuration and the operand forms,
             // e.g. "gemm_fp8_e4m3.c0.g128.mxout".
