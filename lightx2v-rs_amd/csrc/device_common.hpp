@@ -7,6 +7,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "../../include/lightx2v_hip.h"
 
 namespace lx2v {
@@ -144,6 +147,15 @@ __device__ __forceinline__ uint32_t e4m3_canon_encode(float v) {
 // the hardware pack conversion, round to nearest even.  An exhaustive sweep
 // of every f32 in [-448, 448] on gfx950 found it bit-identical to
 // e4m3_ocp_encode, the rule the oracle restates.
+// Without the clamp: every finite value scaled by mx_inv(mx_exponent(amax))
+// lies within +-448 already (mx_exponent's bound); infinities and NaNs
+// become NaN codes instead of +-448.
+__device__ __forceinline__ uint32_t quant4_nc(const float *v, float inv) {
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, r, true);
+    return (uint32_t)r;
+}
+
 __device__ __forceinline__ uint32_t quant4(const float *v, float inv) {
     float t[4];
 #pragma unroll
@@ -178,10 +190,12 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // u = sqrt(2/pi) (x + 0.044715 x^3), on the hardware exp2 and reciprocal
 // (a few ulp; the oracle's own 1 + tanhf(u) loses more than that to
 // cancellation for u < 0).  Limits: x -> -inf gives -0, x -> +inf gives x.
+// The exponent -2 log2(e) u is evaluated as x (k0 + k1 x^2), the constants
+// folded (seven VALU operations in all, two of them transcendental).
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
-    const float c = 0.7978845608028654f;
-    float u = c * (x + 0.044715f * x * x * x);
-    float e = __builtin_amdgcn_exp2f(u * -2.8853900817779268f);  // -2 log2(e)
+    constexpr float k0 = -2.8853900817779268f * 0.7978845608028654f;  // -2 log2(e) sqrt(2/pi)
+    constexpr float k1 = k0 * 0.044715f;
+    const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(x * x, k1, k0));
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
@@ -255,6 +269,34 @@ constexpr uint32_t kOob = 0x80000000u;
 // dropped by the hardware range check.
 __device__ __forceinline__ void buffer_store_x4(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void buffer_store_b8(uint8_t v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b8(v, r, (int)off, 0, 0);
+}
+
+// v_permlane32_swap: lanes 32..63 of x trade places with lanes 0..31 of y.
+// Applied to x = y = v it hands lane l the value of lane l ^ 32 in one of
+// the two results (see max_pair32).
+__device__ __forceinline__ void swap32(uint32_t &x, uint32_t &y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+    x = r[0];
+    y = r[1];
+}
+// max(v, v of lane l ^ 32) in every lane.
+__device__ __forceinline__ float max_pair32(float v) {
+    uint32_t x = __float_as_uint(v), y = x;
+    swap32(x, y);
+    return fmaxf(__uint_as_float(x), __uint_as_float(y));
+}
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N - 1.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
 }  // namespace lx2v

@@ -25,6 +25,19 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, ui
                  : "memory");
 }
 
+// The same load given the LDS byte address (kernels that take it once from
+// the __shared__ array itself, not through a generic pointer).
+__device__ __forceinline__ void dma16_at(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voff) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(base), "v"(voff), "s"(r)
+                 : "memory");
+}
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T *p) {
+    typedef __attribute__((address_space(3))) uint8_t *lds_ptr;
+    return (uint32_t)(uintptr_t)(lds_ptr)(uint8_t *)p;
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.

@@ -527,8 +527,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 // k_gemm_fp8_dma's 256 x 128 tile (8 waves of 64 x 64 sub-tiles, 128-byte
 // stages in a 3-stage ring, per-token e4m3 activations) as one workgroup per
 // CU that walks a list of tiles: pass i of workgroup w computes tile
-// xcd_tile(w + i G) for a grid of G workgroups, G a multiple of 8, so every
-// tile of a workgroup lies in its XCD's band.  The ring runs on across
+// xcd_tile(w + i G) for a grid of G = min(tiles, CUs) workgroups, G a
+// multiple of 8 whenever the tiles outnumber the CUs, so every tile of a
+// workgroup lies in its XCD's band.  The ring runs on across
 // tiles: while a tile's last two stages are contracted, the next tile's
 // first two are already loading, and the epilogue stages its outputs
 // through the slot the last stage freed.  A tile's token scales, channel
@@ -764,6 +765,337 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
     wait_vmcnt<0>();  // the walk's trailing loads (zeros) land before the workgroup ends
 }
 
+// ---- persistent kernel with the epilogue folded into the next tile ----------------
+//
+// The persistent 256 x 128 walk of k_gemm_fp8_pt (3-stage DMA ring running
+// on across tiles, epilogue operands by DMA, a grid of min(tiles, CUs)
+// workgroups) with two accumulator sets, one per tile parity: while tile t
+// + 1's first EP stages are contracted into one set, each wave finishes
+// tile t from the other -- token scale, channel scale, bias, GELU, bf16
+// rounding or MX e4m3 quantization -- one 32 x 32 block per stage (two
+// stages with GELU), its VALU work placed between the stage's MFMAs so
+// that it issues while the matrix core runs.  The tile's operands sit in
+// the LDS slot of its parity, so the next tile's DMA does not overwrite them.
+//
+// The results go straight from registers to memory.  Lanes l and l + 32
+// hold one token's channels 8g + 0..3 and 8g + 4..7 (g = 0..3); one
+// v_permlane32_swap per register pair leaves lane l with a contiguous half
+// of the 32 channels and lane l + 32 with the other, so each 16-byte store
+// of a lane pairs with its neighbour's into one 32-byte piece of the row
+// (bf16: two stores per block; MX: one 16-byte store of codes and the
+// block's scale byte).
+//
+// vmcnt accounting: every stage issues LPS ring loads, and the stage that
+// finishes a block issues PST stores after them (the first tile, which has
+// no predecessor, stores to an out-of-range offset so that every count
+// holds); the wait for stage s leaves in flight what was issued after its
+// loads: the next stage's loads and the stores of the two stages between.
+//
+// Constraints (host): K % 128 == 0, K / 128 >= EP + 2, N % 128 == 0,
+// M N sizeof(TY) < 2^31; bf16 or MX e4m3 output; per-token activations and
+// per-channel weight scales; no residual mode.
+template <int ACT, typename TY>
+__global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restrict__ A, const float *__restrict__ sa,
+                                                       const uint8_t *__restrict__ B, const float *__restrict__ sb,
+                                                       const float *__restrict__ bias, TY *__restrict__ Y, int M,
+                                                       int N, int K, int tiles_m, int tiles_n,
+                                                       uint8_t *__restrict__ ymx, int ymx_rows) {
+    constexpr int BM = 256, BN = 128, WGN = 2, BKB = 128, NS = 3;
+    constexpr int NW = 8, WM = 64, WN = 64, TM = 2, TN = 2;
+    constexpr int CPR = BKB / 16, RPI = 64 / CPR;
+    constexpr int ALD = BM / RPI / NW, BLD = BN / RPI / NW, LPS = ALD + BLD;
+    constexpr int STAGE = (BM + BN) * BKB;
+    constexpr uint32_t AMASK = BM * BKB - 1, BMASK = BN * BKB - 1;
+    constexpr int NV = BM + 2 * BN;
+    constexpr int EB = sizeof(TY);
+    static_assert(EB == 1 || EB == 2, "bf16 or MX e4m3 output");
+    constexpr bool GELU = ACT == LX2V_ACT_GELU_TANH;
+    constexpr int NSLOT = 2 * TN * TM;  // MFMA slots per stage
+    // A finished block's epilogue spans two stages (16 slots).  Its 16
+    // values (channel group g = e / 4) are computed four per slot at slots
+    // 1, 2, 9, 10, or with GELU one per slot (slot e), so that no slot's
+    // VALU work outlasts an MFMA by much.  bf16: channels 0..15 of the
+    // block are swapped and stored in its first stage, 16..31 in its
+    // second (one store per stage); MX: codes and scale byte in the second.
+    constexpr int SPB = 2;
+    constexpr int EP = TM * TN * SPB;  // stages that carry the epilogue
+    constexpr int qF01 = GELU ? 7 : 3, qS01 = GELU ? 7 : 6;    // bf16, first half
+    constexpr int qF23 = GELU ? 15 : 11, qS23 = GELU ? 15 : 14;  // bf16 second half; MX quantize + store
+    static_assert(qS01 % NSLOT >= LPS && qS23 % NSLOT >= LPS, "a block's stores follow its stage's loads");
+    // vector-memory stores issued by peeled stage kt
+    constexpr auto pst = [](int kt) { return kt < 0 || kt >= EP ? 0 : (EB == 2 ? 1 : (kt % 2 == 1 ? 2 : 0)); };
+    static_assert(NS * STAGE + (2 * NV + 256) * 4 <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    // Per parity: [BM token scales][BN channel scales][BN bias], then a pad.
+    __shared__ __attribute__((aligned(16))) float sc[2 * NV + 256];
+
+    const uint32_t smem_at = lds_addr(smem), sc_at = lds_addr(sc);
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int wid_u = __builtin_amdgcn_readfirstlane(wid);
+    const int G = gridDim.x, w = blockIdx.x, ntiles = tiles_m * tiles_n;
+    const int my_n = w < ntiles ? (ntiles - w + G - 1) / G : 0;
+    if (my_n == 0) return;  // (uniform) no tile: no descriptor may be built
+    const int KT = K / BKB;
+    auto tile_of = [&](int i, int *m0, int *n0) {
+        int tm, tn;
+        xcd_tile(w + i * G, ntiles, tiles_m, tiles_n, &tm, &tn);
+        *m0 = tm * BM;
+        *n0 = tn * BN;
+    };
+
+    // Issue side: the (pass, stage) whose loads go out next.
+    int is_i = 0, is_kt = 0, is_m0 = 0, is_n0 = 0;
+    tile_of(0, &is_m0, &is_n0);
+    __amdgpu_buffer_rsrc_t ra_src, rb_src;
+    auto set_issue_tile = [&]() {
+        ra_src = make_rsrc(A + (size_t)is_m0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(M - is_m0) * (uint32_t)K));
+        rb_src = make_rsrc(B + (size_t)is_n0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(N - is_n0) * (uint32_t)K));
+    };
+    set_issue_tile();
+    const uint32_t lrow = (uint32_t)lane / CPR, lslot = (uint32_t)lane % CPR;
+    uint32_t a_off[ALD], b_off[BLD];
+#pragma unroll
+    for (int i = 0; i < ALD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * RPI + lrow;
+        a_off[i] = row * (uint32_t)K + dma_slot<BKB>(row, lslot) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < BLD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * RPI + lrow;
+        b_off[i] = row * (uint32_t)K + dma_slot<BKB>(BM + row, lslot) * 16;
+    }
+    auto piece = [&](int n, int buf) {
+        const bool in = is_i < my_n;
+        const uint32_t k0 = (uint32_t)is_kt * BKB;
+        const uint32_t sbuf = smem_at + (uint32_t)(buf * STAGE);
+        if (n < ALD)
+            dma16_at(ra_src, sbuf + (n * NW + wid_u) * RPI * BKB, in ? a_off[n < ALD ? n : 0] + k0 : kOob);
+        else
+            dma16_at(rb_src, sbuf + (BM + ((n - ALD) * NW + wid_u) * RPI) * BKB,
+                     in ? b_off[n >= ALD ? n - ALD : 0] + k0 : kOob);
+    };
+    auto advance_issue = [&]() {
+        if (++is_kt == KT) {
+            is_kt = 0;
+            if (++is_i < my_n) {
+                tile_of(is_i, &is_m0, &is_n0);
+                set_issue_tile();
+            }
+        }
+    };
+    // A tile's epilogue operands into its parity's slot (wave 1: token
+    // scales, wave 2: channel scales, wave 3: bias).
+    auto issue_ops = [&](int m0, int n0, uint32_t dst) {
+        if (wid_u == 1) {
+            const auto r = sa ? make_rsrc(sa + m0, __builtin_amdgcn_readfirstlane((uint32_t)(M - m0) * 4u))
+                              : make_rsrc(k_ones, 1024u);
+            dma16_at(r, dst, (uint32_t)lane * 16u);
+        } else if (wid_u == 2) {
+            const auto r = sb ? make_rsrc(sb + n0, __builtin_amdgcn_readfirstlane((uint32_t)(N - n0) * 4u))
+                              : make_rsrc(k_ones, 1024u);
+            if (lane < BN / 4) dma16_at(r, dst + BM * 4, (uint32_t)lane * 16u);
+        } else if (wid_u == 3) {
+            const auto r = bias ? make_rsrc(bias + n0, __builtin_amdgcn_readfirstlane((uint32_t)(N - n0) * 4u))
+                                : make_rsrc(k_ones, 0u);
+            if (lane < BN / 4) dma16_at(r, dst + (BM + BN) * 4, (uint32_t)lane * 16u);
+        }
+    };
+
+    // ---- epilogue steps of one 32 x 32 block (jb, ib) of a finished tile ----
+    const auto ry = make_rsrc(Y, (uint32_t)M * (uint32_t)N * EB);
+    const auto rmx = make_rsrc(ymx, EB == 1 ? ((uint32_t)(N / 128 - 1) * (uint32_t)ymx_rows + (uint32_t)M) * 4u : 0u);
+    const int l32 = lane & 31, hf = lane >> 5;
+    struct Epi {
+        float tsc, amax;
+        f32x4 cs[4], bs[4];
+        float v[16];
+        uint32_t w[8];
+        int kx;
+    };
+    auto epi_step = [&](auto Q, auto BLK, Epi &e, const f32x16 (&pv)[TN][TM], const float *scp, int pm0, int pn0,
+                        bool live) {
+        constexpr int q = decltype(Q)::value, blk = decltype(BLK)::value;
+        constexpr int jb = blk / TM, ib = blk % TM;
+        // the values this slot computes: [e0, e0 + ne)
+        constexpr int e0 = GELU ? q : (q == 1 ? 0 : q == 2 ? 4 : q == 9 ? 8 : 12);
+        constexpr int ne = GELU ? 1 : (q == 1 || q == 2 || q == 9 || q == 10 ? 4 : 0);
+        const int cb = wn * WN + jb * 32;  // the block's first tile column
+        auto ops = [&](int g) {
+            const int c = cb + 8 * g + 4 * hf;
+            e.cs[g] = *(const f32x4 *)(scp + BM + c);
+            e.bs[g] = *(const f32x4 *)(scp + BM + BN + c);
+        };
+        if constexpr (q == 0) {
+            e.tsc = scp[wm * WM + ib * 32 + l32];
+            e.amax = 0.0f;
+            ops(0);
+            ops(1);
+        }
+        static_for<ne>([&](auto K_) {
+            constexpr int el = e0 + decltype(K_)::value, g = el / 4, k = el % 4;
+            if constexpr (k == 0 && g + 2 < 4) ops(g + 2);  // two groups ahead
+            float t = pv[jb][ib][el] * e.tsc * e.cs[g][k] + e.bs[g][k];
+            if constexpr (GELU) t = gelu_tanh_fast(t);
+            e.v[el] = t;
+            if constexpr (EB == 2) {
+                if constexpr (el % 2 == 1) e.w[el / 2] = pack_bf16x2(e.v[el - 1], t);
+            } else {
+                e.amax = fmaxf(e.amax, fabsf(t));
+            }
+        });
+        const int m = pm0 + wm * WM + ib * 32 + l32, n = pn0 + cb;
+        const bool in = live && m < M;
+        const uint32_t row = (uint32_t)m * (uint32_t)N + (uint32_t)n;
+        if constexpr (EB == 2) {
+            // swap lanes l / l + 32 so that lane l holds channels 0..7 (16..23)
+            // in w0..w3 (w4..w7) and lane l + 32 channels 8..15 (24..31)
+            if constexpr (q == qF01) {
+                swap32(e.w[0], e.w[2]);
+                swap32(e.w[1], e.w[3]);
+            }
+            if constexpr (q == qS01)
+                buffer_store_x4((u32x4){e.w[0], e.w[1], e.w[2], e.w[3]}, ry,
+                                in ? (row + 8u * (uint32_t)hf) * 2u : kOob);
+            if constexpr (q == qF23) {
+                swap32(e.w[4], e.w[6]);
+                swap32(e.w[5], e.w[7]);
+            }
+            if constexpr (q == qS23)
+                buffer_store_x4((u32x4){e.w[4], e.w[5], e.w[6], e.w[7]}, ry,
+                                in ? (row + 16u + 8u * (uint32_t)hf) * 2u : kOob);
+        } else {
+            if constexpr (q == qF23) {
+                const float amax = max_pair32(e.amax);
+                e.kx = mx_exponent(amax);
+                const float inv = mx_inv(e.kx);
+#pragma unroll
+                for (int g = 0; g < 4; g++) e.w[g] = quant4_nc(e.v + 4 * g, inv);
+                // lane l: channels 0..15 as w0, w2, w1, w3; lane l + 32: 16..31
+                swap32(e.w[0], e.w[2]);
+                swap32(e.w[1], e.w[3]);
+            }
+            if constexpr (q == qS23) {
+                buffer_store_x4((u32x4){e.w[0], e.w[2], e.w[1], e.w[3]}, ry, in ? row + 16u * (uint32_t)hf : kOob);
+                buffer_store_b8((uint8_t)(e.kx + 127), rmx,
+                                in && hf == 0 ? (uint32_t)mx_sidx((size_t)m, (size_t)(n / 32), (size_t)ymx_rows)
+                                              : kOob);
+            }
+        }
+    };
+
+    // ---- one stage: MFMAs into ac, the issue stage's loads and the
+    // epilogue slots between them ----
+    const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
+    auto stage = [&](auto FIRST, f32x16 (&ac)[TN][TM], int buf, int dbuf, auto &&slot) {
+        const uint8_t *st = smem + buf * STAGE;
+        static_for<BKB / 64>([&](auto KK) {
+            constexpr int kk = decltype(KK)::value;
+            i32x8 af[TM], bf[TN];
+            const uint32_t c0 = kk * 4 + fhalf, c1 = c0 + 1;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const uint32_t row = wm * WM + i * 32 + frow;
+                u32x4 lo = *(const u32x4 *)(st + ((row * BKB + (dma_slot<BKB>(row, c0) << 4)) & AMASK));
+                u32x4 hi = *(const u32x4 *)(st + ((row * BKB + (dma_slot<BKB>(row, c1) << 4)) & AMASK));
+                af[i] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint32_t row = BM + wn * WN + j * 32 + frow;
+                const uint32_t rb = row - BM;
+                u32x4 lo = *(const u32x4 *)(st + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c0) << 4)) & BMASK));
+                u32x4 hi = *(const u32x4 *)(st + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c1) << 4)) & BMASK));
+                bf[j] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
+            static_for<TN * TM>([&](auto JI) {
+                constexpr int j = decltype(JI)::value / TM, i = decltype(JI)::value % TM;
+                constexpr int n = kk * TN * TM + j * TM + i;
+                if constexpr (decltype(FIRST)::value && kk == 0)
+                    ac[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], (f32x16){}, 0, 0, 0, 0,
+                                                                               0, 0);
+                else
+                    ac[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], ac[j][i], 0, 0, 0, 0,
+                                                                               0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (n < LPS) piece(n, dbuf);
+                slot(std::integral_constant<int, n>{});
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
+    };
+    static_assert(NSLOT >= LPS, "a stage's loads interleave with its MFMAs");
+
+
+    f32x16 acc[2][TN][TM];
+    Epi e;
+    // Prologue: the first NS - 1 stages of the walk.
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++) {
+#pragma unroll
+        for (int n = 0; n < LPS; n++) piece(n, st);
+        advance_issue();
+    }
+    int s = 0;  // global stage index of this workgroup's walk
+    auto tile = [&](auto P, int i) {
+        constexpr int p = decltype(P)::value;
+        int m0, n0, pm0 = 0, pn0 = 0;
+        tile_of(i, &m0, &n0);
+        if (i > 0) tile_of(i - 1, &pm0, &pn0);
+        const bool live = i > 0;
+        const float *scp = sc + (p ^ 1) * NV;
+        static_for<EP + 2>([&](auto KT_) {
+            constexpr int kt = decltype(KT_)::value;
+            // Stage s complete for this wave; then the barrier publishes
+            // every wave's part and frees the slot the issue refills.
+            wait_vmcnt<LPS + pst(kt - 1) + pst(kt - 2)>();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kt == 0) issue_ops(m0, n0, sc_at + p * NV * 4);
+            const int buf = s % NS, dbuf = (s + NS - 1) % NS;
+            auto slot = [&](auto NN) {
+                if constexpr (kt < EP) {
+                    constexpr int q = (kt % SPB) * NSLOT + decltype(NN)::value;
+                    epi_step(std::integral_constant<int, q>{}, std::integral_constant<int, kt / SPB>{}, e,
+                             acc[p ^ 1], scp, pm0, pn0, live);
+                }
+            };
+            stage(std::integral_constant<bool, kt == 0>{}, acc[p], buf, dbuf, slot);
+            advance_issue();
+            s++;
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        for (int kt = EP + 2; kt < KT; kt++, s++) {
+            wait_vmcnt<LPS>();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            const int buf = s % NS, dbuf = (s + NS - 1) % NS;
+            stage(std::false_type{}, acc[p], buf, dbuf, [](auto) {});
+            advance_issue();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    for (int i = 0; i < my_n; i += 2) {
+        tile(std::integral_constant<int, 0>{}, i);
+        if (i + 1 < my_n) tile(std::integral_constant<int, 1>{}, i + 1);
+    }
+    // The last tile's epilogue (its operands' DMA went out with its first
+    // stage, before ring loads that later waits covered).
+    auto last = [&](auto P) {
+        constexpr int p = decltype(P)::value;
+        int m0, n0;
+        tile_of(my_n - 1, &m0, &n0);
+        static_for<TN * TM>([&](auto BLK) {
+            static_for<NSLOT * SPB>([&](auto Q) { epi_step(Q, BLK, e, acc[p], sc + p * NV, m0, n0, true); });
+        });
+    };
+    if (my_n & 1)
+        last(std::integral_constant<int, 0>{});
+    else
+        last(std::integral_constant<int, 1>{});
+    wait_vmcnt<0>();  // the walk's trailing loads (zeros) land before the workgroup ends
+}
+
 // ---- ping-pong kernel: two wave groups alternate MFMA and LDS phases ---------------
 //
 // Measured on gfx950: a ds_read_b128 costs its own wave ~25 MFMA cycles of
@@ -995,13 +1327,13 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
 }
 
 
-// The persistent 256 x 128 kernel: a grid of one workgroup per CU (a
-// multiple of 8, at most the tile count) walking the tiles.
+// The persistent 256 x 128 kernel: min(tiles, CUs) workgroups (a multiple
+// of 8 whenever the tiles outnumber the CUs) walking the tiles.
 void launch_pt(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
                const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 127) / 128, nt = tiles_m * tiles_n;
     int g = nt < num_cu ? nt : num_cu;
-    g = g >= 8 ? g / 8 * 8 : g;
+    if (g < nt && g >= 8) g = g / 8 * 8;
     const dim3 grid(g), block(512);
     const int yr = (int)mx.y_rows;
 #define LX2V_PT(GSV, ACTV, T)                                                                                      \
@@ -1032,6 +1364,32 @@ void launch_pt(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, con
 #undef LX2V_PT
 }
 
+// The persistent kernel with the overlapped epilogue: min(tiles, CUs)
+// workgroups (a multiple of 8 whenever the tiles outnumber the CUs).
+void launch_ov(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
+               const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
+    const int tiles_m = (M + 255) / 256, tiles_n = N / 128, nt = tiles_m * tiles_n;
+    int g = nt < num_cu ? nt : num_cu;
+    if (g < nt && g >= 8) g = g / 8 * 8;
+    const dim3 grid(g), block(512);
+    const int yr = (int)mx.y_rows;
+#define LX2V_OV(ACTV, T)                                                                                      \
+    hipLaunchKernelGGL((k_gemm_fp8_ov<ACTV, T>), grid, block, 0, s, a, sa, b, sb, bias, (T *)y, M, N, K, tiles_m, \
+                       tiles_n, mx.y, yr)
+    if (y_dtype == LX2V_DTYPE_BF16) {
+        if (act == LX2V_ACT_GELU_TANH)
+            LX2V_OV(LX2V_ACT_GELU_TANH, uint16_t);
+        else
+            LX2V_OV(LX2V_ACT_NONE, uint16_t);
+    } else {
+        if (act == LX2V_ACT_GELU_TANH)
+            LX2V_OV(LX2V_ACT_GELU_TANH, uint8_t);
+        else
+            LX2V_OV(LX2V_ACT_NONE, uint8_t);
+    }
+#undef LX2V_OV
+}
+
 // Direct-to-LDS configurations: tile (activation rows x channels), wave
 // grid, K bytes per stage, stages.
 struct DmaCfg {
@@ -1048,6 +1406,8 @@ constexpr DmaCfg kDma[] = {
     {256, 256, 1, 4, 64, 4},   // 5
     // persistent 256 x 128 (k_gemm_fp8_pt)
     {256, 128, 4, 2, 128, 3},  // 6
+    // persistent 256 x 128, epilogue overlapped with the next tile (k_gemm_fp8_ov)
+    {256, 128, 4, 2, 128, 3},  // 7
 };
 
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
@@ -1069,7 +1429,7 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
         case 5: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        default: break;  // 6: launch_pt (needs the CU count)
+        default: break;  // 6, 7: launch_pt / launch_ov (need the CU count)
     }
 }
 
@@ -1085,7 +1445,7 @@ int forced_cfg() {
 
 }  // namespace
 
-bool gemm_fp8_residual_ok(const Fp8Plan &p) { return p.kernel >= 0 && p.kernel != 5 && p.kernel != 6; }
+bool gemm_fp8_residual_ok(const Fp8Plan &p) { return p.kernel >= 0 && p.kernel != 5 && p.kernel != 6 && p.kernel != 7; }
 
 bool gemm_fp8_grouped_supported(size_t M, size_t N, size_t K, size_t group) {
     return group == 128 && K % 128 == 0 && N % 4 == 0 && gemm_fp8_supported(M, N, K) &&
@@ -1108,22 +1468,34 @@ bool gemm_fp8_supported(size_t M, size_t N, size_t K) {
 // but hide most of each workgroup's prologue and epilogue behind another's
 // K loop; the 256 x 256 ping-pong tile has the cheapest K loop per unit of
 // work and the most expensive rounds.
+//
+// The persistent kernels (6, 7) are offered only to shapes of two or more
+// rounds: with one tile per workgroup there is nothing to overlap, and they
+// measured no faster than the one-shot tiles there.  Their costs are per
+// pass of a workgroup over its tiles (the same rounds count), measured on
+// the Wan shapes: 7 (epilogue folded into the next tile) at 256 x 128 x
+// 1536 tiles -- FFN up 6 passes 75 us, QKV 3 passes 38 us; 6 (grouped
+// scales) at QKV 45 us and FFN up 84 us.
 struct CfgCost {
     int idx;
     double per_stage_us, per_round_us, fixed_us;
+    bool persistent;
 };
 constexpr CfgCost kAuto[] = {
-    {0, 0.625, 8.16, 0.21},   // 256 x 128, one workgroup per CU
-    {2, 0.826, 4.21, 2.44},   // 256 x 128, two per CU
-    {4, 0.926, 2.43, 4.47},   // 128 x 256, two per CU
-    {3, 0.606, 0.44, 4.59},   // 128 x 128, three per CU
-    {5, 1.121, 14.77, 0.0},   // 256 x 256 ping-pong
+    {0, 0.625, 8.16, 0.21, false},  // 256 x 128, one workgroup per CU
+    {2, 0.826, 4.21, 2.44, false},  // 256 x 128, two per CU
+    {4, 0.926, 2.43, 4.47, false},  // 128 x 256, two per CU
+    {3, 0.606, 0.44, 4.59, false},  // 128 x 128, three per CU
+    {5, 1.121, 14.77, 0.0, false},  // 256 x 256 ping-pong
+    {7, 0.80, 2.70, 0.80, true},    // 256 x 128 persistent, overlapped epilogue
 };
 // Grouped weight scales (128-byte stages only): the two one-per-CU tiles,
-// with the per-CU costs of their per-channel versions.
+// with the per-CU costs of their per-channel versions, and the persistent
+// 256 x 128 tile.
 constexpr CfgCost kGroupedAuto[] = {
-    {0, 0.625, 8.16, 0.21},  // 256 x 128
-    {1, 0.625, 8.16, 0.21},  // 128 x 256
+    {0, 0.625, 8.16, 0.21, false},  // 256 x 128
+    {1, 0.625, 8.16, 0.21, false},  // 128 x 256
+    {6, 0.80, 3.50, 4.00, true},    // 256 x 128 persistent
 };
 
 // The configurations with MX-activation / MX-output kernels.  The 128 x 256
@@ -1136,13 +1508,26 @@ bool mx_capable(int idx, bool mx_in) { return idx == 0 || idx == 3 || ((idx == 4
 bool grouped_capable(int idx, bool mx, bool mx_in) {
     return !mx_in && (idx == 0 || idx == 6 || (idx == 1 && !mx));
 }
+// The overlapped-epilogue kernel (k_gemm_fp8_ov): per-token activations and
+// per-channel weight scales, bf16 or MX e4m3 output, whole 128-channel
+// tiles, and enough stages to carry the previous tile's epilogue (4, or 8
+// with GELU) plus the two the ring runs ahead.
+bool ov_capable(size_t M, size_t N, size_t K, bool mx_in, bool grouped, int y_dtype, int act, bool residual) {
+    const size_t eb = y_dtype == LX2V_DTYPE_BF16 ? 2 : (y_dtype == LX2V_DTYPE_MXE4M3 ? 1 : 0);
+    const size_t ep = act == LX2V_ACT_GELU_TANH ? 8 : 4;
+    return eb && !mx_in && !grouped && !residual && N % 128 == 0 && K % 128 == 0 && K / 128 >= ep + 2 &&
+           M * N * eb < (1ull << 31);
+}
 
-Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped) {
+Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped, int y_dtype,
+                      int act, bool residual) {
     Fp8Plan p;
     if (K % 128 != 0) return p;  // the register-staged kernel
     const int nd = (int)(sizeof(kDma) / sizeof(kDma[0]));
     const int forced = forced_cfg();
     auto ok = [&](int idx) {
+        if (residual && (idx == 5 || idx == 6)) return false;
+        if (idx == 7) return ov_capable(M, N, K, mx_in, grouped, y_dtype, act, residual);
         return grouped ? grouped_capable(idx, mx, mx_in) : (!mx || mx_capable(idx, mx_in));
     };
     if (forced >= 0 && forced < nd && ok(forced) && (forced != 6 || K >= 256)) {
@@ -1150,29 +1535,23 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
         return p;
     }
     double best = 0.0;
-    for (const CfgCost &c : kGroupedAuto) {
-        if (!grouped || !ok(c.idx)) continue;
+    auto consider = [&](const CfgCost &c) {
+        if (!ok(c.idx)) return;
         const DmaCfg &d = kDma[c.idx];
         const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
-        const double rounds = (double)((tiles + num_cu - 1) / num_cu);
-        const double t = rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us) + c.fixed_us;
-        if (p.kernel < 0 || t < best * 0.9999) {
-            best = t;
-            p.kernel = c.idx;
-        }
-    }
-    if (grouped) return p;
-    for (const CfgCost &c : kAuto) {
-        if (!ok(c.idx)) continue;
-        const DmaCfg &d = kDma[c.idx];
-        const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
-        const double rounds = (double)((tiles + num_cu - 1) / num_cu);
-        const double t = rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us) + c.fixed_us;
+        const size_t rounds = (tiles + num_cu - 1) / num_cu;
+        if (c.persistent && (rounds < 2 || K / 128 < 2)) return;
+        const double t = (double)rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us) + c.fixed_us;
         if (p.kernel < 0 || t < best * 0.9999) {  // ties keep the earlier
             best = t;
             p.kernel = c.idx;
         }
+    };
+    if (grouped) {
+        for (const CfgCost &c : kGroupedAuto) consider(c);
+        return p;
     }
+    for (const CfgCost &c : kAuto) consider(c);
     return p;
 }
 
@@ -1182,6 +1561,10 @@ void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t 
     int m = (int)M, n = (int)N, k = (int)K;
     if (p.kernel == 6) {
         launch_pt(s, num_cu, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k, mx);
+        return;
+    }
+    if (p.kernel == 7) {
+        launch_ov(s, num_cu, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k, mx);
         return;
     }
     if (p.kernel >= 0) {

@@ -1919,7 +1919,8 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         mx.gate = gate;
         if (fp8_mfma) {
             if (fp8_grouped) mx.wgs = w->sscale;
-            const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx, fp8_grouped);
+            const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx, fp8_grouped, y->dtype, act,
+                                               gate != nullptr);
             if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1 && plan.kernel != 6)  // built with grouped scales
                 return fail(LX2V_ERR_UNSUPPORTED, "no grouped-scale fp8 kernel for configuration %d", plan.kernel);
             // Profile name: the kernel configuration and the operand forms,
@@ -2020,7 +2021,7 @@ static bool linear_fusable(const lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_
     if (w->fmt != LX2V_WFMT_FP8 || h->quantized() || !gemm_fp8_supported(rows, N, K)) return false;
     if (grouped && !(w->sscale && !x_mx && gemm_fp8_grouped_supported(rows, N, K, w->group))) return false;
     if (!(ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized())) return false;
-    return gemm_fp8_residual_ok(plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx, grouped));
+    return gemm_fp8_residual_ok(plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx, grouped, h->dtype, LX2V_ACT_NONE, true));
 }
 
 int lx2v_hip_linear_residual(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,

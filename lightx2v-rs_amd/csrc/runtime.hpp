@@ -272,7 +272,10 @@ bool gemm_fp8_supported(size_t M, size_t N, size_t K);
 bool gemm_fp8_grouped_supported(size_t M, size_t N, size_t K, size_t group);
 // Whether the plan's kernel takes Fp8Mx::gate (the residual epilogue).
 bool gemm_fp8_residual_ok(const Fp8Plan &p);
-Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped = false);
+// y_dtype / act / residual: the launch's output form (some configurations
+// cover only bf16 / MX output, and the residual epilogue only some).
+Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped = false,
+                      int y_dtype = LX2V_DTYPE_BF16, int act = LX2V_ACT_NONE, bool residual = false);
 void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t *a, const float *a_scale,
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
                      int y_dtype, size_t M, size_t N, size_t K, const Fp8Mx &mx);
