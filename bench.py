@@ -82,7 +82,9 @@ def per_config(be, H):
             tmp.free()
             be.set_act_dtype(H.DTYPE_F32)
             tmp = be.upload(w.ravel())
-        if kind == "fp8":
+        if kind == "native":
+            w = be.weight(be.download(tmp), n, k)
+        elif kind == "fp8":
             w = be.quantize_fp8(tmp, n, k, group or k)
         elif kind == "q8":
             w = be.quantize_q8(tmp, n, k, 32)
@@ -94,8 +96,8 @@ def per_config(be, H):
     def alg_bytes(rows, n, k, xdt, ydt, kind, group):
         """|X| + |W codes| + |scales (+ zeros)| + |bias| + |Y|, each once at its dtype."""
         eb = {H.DTYPE_F32: 4, H.DTYPE_BF16: 2}
-        codes = n * k // 2 if kind == "q4" else n * k
-        scales = n * (k // group) * 4 * (2 if kind == "q4" else 1)
+        codes = n * k // 2 if kind == "q4" else (n * k * 2 if kind == "native" else n * k)
+        scales = 0 if kind == "native" else n * (k // group) * 4 * (2 if kind == "q4" else 1)
         return rows * k * eb[xdt] + codes + scales + n * 4 + rows * n * eb[ydt]
 
     def time_linear(name, x, rows, k, w, n, act, xdt, ydt, peak, path, kind="fp8", group=None):
@@ -192,6 +194,19 @@ def per_config(be, H):
                         PEAK_FP8_TFLOPS, fp8_path)
             w.free()
             x.free()
+    # native f32 weights (Backend::weight) at Wan2.1-1.3B's non-block linears: patch_embed, proj_out and
+    # the text MLP (dit.rs:540-561, 772-781, 450-469), through the weights' bf16 copy on the bf16 MFMA
+    native_path = "bf16 activations x the native f32 weight's bf16 copy, bf16 MFMA"
+    for nm, rows, n, k, act in (("patch_embed", M, DIM, 64, 0), ("proj_out", M, 64, DIM, 0),
+                                ("text_mlp1", TEXT, DIM, 4096, 1), ("text_mlp2", TEXT, DIM, DIM, 0)):
+        be.set_act_dtype(H.DTYPE_BF16)
+        x = be.alloc(rows * k)
+        be.fill_normal(x, 1051 + k, 1.0)
+        w = weight("native", n, k, 0.02, 1052 + n + k)
+        time_linear(f"native_{nm}", x, rows, k, w, n, act, H.DTYPE_BF16, H.DTYPE_BF16, PEAK_BF16_TFLOPS,
+                    native_path, kind="native")
+        w.free()
+        x.free()
     be.set_act_dtype(H.DTYPE_BF16)
     return out
 

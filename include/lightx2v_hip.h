@@ -72,6 +72,16 @@ enum { LX2V_WFMT_F32 = 0, LX2V_WFMT_Q8 = 1, LX2V_WFMT_Q4 = 2, LX2V_WFMT_FP8 = 3 
  *  FP8_ACT_BF16: bf16 activations, weights dequantized to bf16, bf16 MFMA. */
 enum { LX2V_FP8_ACT_E4M3 = 0, LX2V_FP8_ACT_BF16 = 1 };
 
+/* How linear contracts a native f32 weight (lx2v_hip_weight_f32).
+ *  NATIVE_BF16: the weight's bf16 copy (RNE, made at upload) times bf16
+ *    activations on the bf16 MFMA, f32 accumulation -- for cols % 64 == 0
+ *    (default).  The products carry the two bf16 roundings (relative 2^-9
+ *    each); the reference's wgpu backend rounds such weights to f16 the same
+ *    way (crates/lightx2v-wgpu/src/lib.rs:877-905).
+ *  NATIVE_F32: f32 operands and f32 arithmetic (the scalar kernel), the CPU
+ *    reference's own precision (crates/lightx2v-cpu/src/lib.rs:296-326). */
+enum { LX2V_NATIVE_BF16 = 0, LX2V_NATIVE_F32 = 1 };
+
 /* ---- errors / context --------------------------------------------------- */
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -93,6 +103,9 @@ int lx2v_hip_name(const lx2v_hip_ctx *ctx, char *out, size_t cap);
 int lx2v_hip_set_act_dtype(lx2v_hip_ctx *ctx, int dtype);
 /* LX2V_FP8_ACT_* used by lx2v_hip_linear for FP8 weights. */
 int lx2v_hip_set_fp8_act(lx2v_hip_ctx *ctx, int mode);
+/* LX2V_NATIVE_* used by lx2v_hip_linear for native f32 weights (no
+ * reference counterpart: the reference picks its precision per backend). */
+int lx2v_hip_set_native_mode(lx2v_hip_ctx *ctx, int mode);
 
 /* ---- buffers (backend.rs:160-177) -------------------------------------- */
 
@@ -116,7 +129,9 @@ int lx2v_hip_buf_free(lx2v_hip_ctx *ctx, lx2v_hip_buf *buf);
 
 /* ---- weights (backend.rs:178-188) -------------------------------------- */
 
-/* Backend::weight (backend.rs:178): native f32 [rows, cols] row-major. */
+/* Backend::weight (backend.rs:178): native f32 [rows, cols] row-major.
+ * With cols % 64 == 0 the weight also keeps a bf16 copy (2 bytes per
+ * element) for the bf16 MFMA (LX2V_NATIVE_BF16). */
 int lx2v_hip_weight_f32(lx2v_hip_ctx *ctx, const float *data, size_t rows, size_t cols,
                         lx2v_hip_weight **out);
 /* Backend::weight_q8 (backend.rs:179-182) over quant.rs:142-151's Q8:

@@ -59,6 +59,8 @@ pub const WFMT_FP8: c_int = 3;
 
 pub const FP8_ACT_E4M3: c_int = 0;
 pub const FP8_ACT_BF16: c_int = 1;
+pub const NATIVE_BF16: c_int = 0;
+pub const NATIVE_F32: c_int = 1;
 
 pub const NORM_AFFINE: c_int = 0;
 pub const NORM_MOD: c_int = 1;
@@ -107,6 +109,7 @@ extern "C" {
     pub fn lx2v_hip_name(ctx: *const Ctx, out: *mut c_char, cap: usize) -> c_int;
     pub fn lx2v_hip_set_act_dtype(ctx: *mut Ctx, dtype: c_int) -> c_int;
     pub fn lx2v_hip_set_fp8_act(ctx: *mut Ctx, mode: c_int) -> c_int;
+    pub fn lx2v_hip_set_native_mode(ctx: *mut Ctx, mode: c_int) -> c_int;
 
     // ---- buffers
     pub fn lx2v_hip_alloc(ctx: *mut Ctx, len: usize, out: *mut *mut RawBuf) -> c_int;

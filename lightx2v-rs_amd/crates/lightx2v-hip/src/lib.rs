@@ -591,6 +591,13 @@ impl HipBackend {
         });
     }
 
+    /// Native f32 weights on the bf16 MFMA through their bf16 copy
+    /// (default), or in f32 like the CPU reference (`exact_f32 = true`).
+    pub fn set_native_f32(&self, exact_f32: bool) {
+        let mode = if exact_f32 { ffi::NATIVE_F32 } else { ffi::NATIVE_BF16 };
+        check(unsafe { ffi::lx2v_hip_set_native_mode(self.c(), mode) });
+    }
+
     /// Profile every kernel launch with HIP events (the CPU backend's
     /// LIGHTX2V_PROFILE switch is honoured at creation too).
     pub fn profile_enable(&self, on: bool) {

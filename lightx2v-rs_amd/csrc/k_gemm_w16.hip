@@ -340,16 +340,6 @@ void launch_tile(hipStream_t s, const void *x, int x_dtype, const lx2v_hip_weigh
 constexpr int BKE = 64;        // K elements per stage
 constexpr int XRB = BKE * 2;   // bytes per LDS tile row (bf16)
 
-// f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}).
-template <class F, int... I>
-__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-    static_for_seq(f, std::make_integer_sequence<int, N>{});
-}
-
 // 16 consecutive K elements of one weight row, as 8 packed bf16 pairs
 // (element 2i low), each rounded from the reference's f32 dequantization
 // (quant.rs:183-191, 279-289, 432-440): c = 16 code bytes (Q8, FP8) or 8
@@ -685,6 +675,149 @@ int forced_w16_cfg() {
     return v;
 }
 
+// ---- bf16 x bf16: native f32 weights rounded to bf16 at upload ------------------
+//
+// Backend::weight's f32 weights (WeightQuant::Native, quant.rs:28-30) on
+// the bf16 MFMA: the weight's bf16 copy (RNE from f32, made once at upload)
+// and the bf16 activations both travel HBM -> LDS by the 16-byte
+// buffer_load ... lds into an NS-stage ring of 64-element K stages, laid
+// out and read like k_gemm_w16_dma's activation tiles; four 32x32x16 MFMAs
+// per block per stage; the staged epilogue adds the bias and applies GELU.
+template <int BM, int BN, int WGM, int WGN, int NS, typename TY>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_bf16_dma(const uint16_t *__restrict__ X,
+                                                                  const uint16_t *__restrict__ W,
+                                                                  const float *__restrict__ bias,
+                                                                  TY *__restrict__ Y, int M, int N, int K, int act,
+                                                                  int tiles_m, int tiles_n) {
+    constexpr int NW = WGM * WGN, NT = 64 * NW;
+    constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+    constexpr int XS = BM * XRB, WS = BN * XRB, STAGE = XS + WS;
+    constexpr int ALD = BM / 8 / NW, BLD = BN / 8 / NW, LPS = ALD + BLD;
+    using Ops = TileOps<BM, BN, NT>;
+    static_assert(ALD * 8 * NW == BM && BLD * 8 * NW == BN, "tile rows must split over the waves");
+    static_assert(NS >= 2 && (NS - 2) * LPS < 64, "vmcnt range");
+    static_assert(NS * STAGE + Ops::NV * 4 <= 160 * 1024, "LDS");
+    static_assert((XS & (XS - 1)) == 0 && (WS & (WS - 1)) == 0, "slot sizes are powers of two");
+    static_assert(4 * TN * TM >= LPS, "a stage's loads interleave with its MFMAs");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int wid_u = __builtin_amdgcn_readfirstlane(wid);
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = K / BKE;
+    Ops ops;
+    ops.load(tid, m0, n0, M, N, nullptr, nullptr, bias);
+
+    // Rows past either matrix read zero: they feed outputs that are never stored.
+    const auto rx = make_rsrc(X + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K * 2u);
+    const auto rw = make_rsrc(W + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K * 2u);
+    // Load i of this wave covers tile rows [(i NW + wid) 8, +8); lane l
+    // fills slot l % 8 of row l / 8 with the chunk the swizzle puts there.
+    const uint32_t lrow = (uint32_t)lane / 8u, lslot = (uint32_t)lane % 8u;
+    uint32_t x_off[ALD], w_off[BLD];
+#pragma unroll
+    for (int i = 0; i < ALD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * 8u + lrow;
+        x_off[i] = row * (uint32_t)K * 2u + dma_slot<XRB>(row, lslot) * 16u;
+    }
+#pragma unroll
+    for (int i = 0; i < BLD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * 8u + lrow;
+        w_off[i] = row * (uint32_t)K * 2u + dma_slot<XRB>(row, lslot) * 16u;
+    }
+    auto piece = [&](int n, int kt, int buf) {
+        const bool in = kt < KT;
+        uint8_t *sb = smem + buf * STAGE;
+        if (n < ALD)
+            dma16(rx, sb + (n * NW + wid_u) * 1024, in ? x_off[n < ALD ? n : 0] + (uint32_t)kt * XRB : kOob);
+        else
+            dma16(rw, sb + XS + ((n - ALD) * NW + wid_u) * 1024,
+                  in ? w_off[n >= ALD ? n - ALD : 0] + (uint32_t)kt * XRB : kOob);
+    };
+
+    f32x16 acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
+    // One stage's MFMAs from slot buf, the loads of stage dkt (slot dbuf)
+    // one after each of its first MFMAs.  Lanes 0..31 supply K elements
+    // 8 c .. 8 c + 7 of their row, lanes 32..63 the next 8 (chunk 2 kk + h).
+    const uint32_t frow = lane & 31, fhalf = lane >> 5;
+    auto compute = [&](int buf, int dkt, int dbuf) {
+        const uint8_t *xs = smem + buf * STAGE, *ws = xs + XS;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const uint32_t c = (uint32_t)kk * 2u + fhalf;
+            u32x4 xf[TM], wf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const uint32_t row = (uint32_t)(wm * WM + i * 32) + frow;
+                xf[i] = *(const u32x4 *)(xs + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (XS - 1)));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint32_t row = (uint32_t)(wn * WN + j * 32) + frow;
+                wf[j] = *(const u32x4 *)(ws + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (WS - 1)));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[j]),
+                                                                      __builtin_bit_cast(bf16x8, xf[i]), acc[j][i],
+                                                                      0, 0, 0);
+                    const int n = (kk * TN + j) * TM + i;
+                    if (n < LPS) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        piece(n, dkt, dbuf);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+        }
+    };
+    // Entering stage kt: stages kt .. kt + NS - 2 are in flight, so waiting
+    // until NS - 2 stages' loads remain leaves stage kt complete for this
+    // wave; the barrier publishes every wave's part and retires the reads
+    // of stage kt - 1, whose slot this stage's loads refill.
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++)
+#pragma unroll
+        for (int n = 0; n < LPS; n++) piece(n, st, st);
+    for (int kt = 0; kt < KT; kt += NS) {
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            if (kt + j < KT) {
+                wait_vmcnt<(NS - 2) * LPS>();
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                compute(j, kt + j + NS - 1, (j + NS - 1) % NS);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    ops.park(sc, tid, m0, n0, M, N, nullptr, nullptr);
+    staged_epilogue<BM, BN, NT, NS * STAGE, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N,
+                                                       act, Y);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS>
+void launch_bf16_cfg(hipStream_t s, const uint16_t *x, const uint16_t *w, const float *bias, int act, void *y,
+                     int y_dtype, int M, int N, int K) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
+    if (y_dtype == LX2V_DTYPE_BF16)
+        hipLaunchKernelGGL((k_gemm_bf16_dma<BM, BN, WGM, WGN, NS, uint16_t>), grid, block, 0, s, x, w, bias,
+                           (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((k_gemm_bf16_dma<BM, BN, WGM, WGN, NS, float>), grid, block, 0, s, x, w, bias, (float *)y,
+                           M, N, K, act, tiles_m, tiles_n);
+}
+
 }  // namespace
 
 bool gemm_w16_supported(const lx2v_hip_weight *w) {
@@ -753,6 +886,39 @@ int plan_gemm_w16_dma(int num_cu, size_t M, size_t N) {
 void launch_gemm_w16_dma(hipStream_t s, int cfg, const uint16_t *x, const lx2v_hip_weight *w, const float *bias,
                          int act, void *y, int y_dtype, size_t M) {
     launch_dma_idx(cfg, s, x, w, bias, act, y, y_dtype, (int)M);
+}
+
+bool gemm_bf16_supported(size_t M, size_t N, size_t K) {
+    return M > 0 && N > 0 && K >= BKE && K % BKE == 0 && M * K * 2 < (1ull << 31) && N * K * 2 < (1ull << 31) &&
+           M < (1u << 30) && N < (1u << 30);
+}
+
+// 256 x 128 (8 waves), 128 x 256 (8 waves) or 128 x 128 (4 waves): the one
+// that leaves the fewest idle tile slots over the rounds the grid takes, the
+// larger tile on ties.
+void launch_gemm_bf16(hipStream_t s, int num_cu, const uint16_t *x, const uint16_t *w, const float *bias, int act,
+                      void *y, int y_dtype, size_t M, size_t N, size_t K) {
+    struct Cfg {
+        int bm, bn;
+    };
+    const Cfg cfgs[] = {{256, 128}, {128, 256}, {128, 128}};
+    double best = -1.0;
+    int pick = 0;
+    for (int i = 0; i < 3; i++) {
+        const size_t tiles = ((M + cfgs[i].bm - 1) / cfgs[i].bm) * ((N + cfgs[i].bn - 1) / cfgs[i].bn);
+        const size_t rounds = (tiles + num_cu - 1) / num_cu;
+        const double eff = (double)M * N / ((double)rounds * num_cu * cfgs[i].bm * cfgs[i].bn);
+        if (eff > best * 1.0001) {
+            best = eff;
+            pick = i;
+        }
+    }
+    const int m = (int)M, n = (int)N, k = (int)K;
+    switch (pick) {
+        case 0: launch_bf16_cfg<256, 128, 4, 2, 3>(s, x, w, bias, act, y, y_dtype, m, n, k); break;
+        case 1: launch_bf16_cfg<128, 256, 2, 4, 3>(s, x, w, bias, act, y, y_dtype, m, n, k); break;
+        default: launch_bf16_cfg<128, 128, 2, 2, 3>(s, x, w, bias, act, y, y_dtype, m, n, k); break;
+    }
 }
 
 }  // namespace lx2v

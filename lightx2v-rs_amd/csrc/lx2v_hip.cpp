@@ -206,6 +206,7 @@ void free_weight(lx2v_hip_weight *w) {
     if (w->raw_e4m3) (void)hipFree(w->raw_e4m3);
     if (w->sscale) (void)hipFree(w->sscale);
     if (w->szero) (void)hipFree(w->szero);
+    if (w->wbf16) (void)hipFree(w->wbf16);
     delete w;
 }
 
@@ -310,6 +311,15 @@ int lx2v_hip_set_act_dtype(lx2v_hip_ctx *ctx, int dtype) {
     if (int rc = not_capturing(ctx, "set_act_dtype")) return rc;
     if (!valid_dtype(dtype)) return fail(LX2V_ERR_BAD_ARG, "unknown dtype %d", dtype);
     ctx->act_dtype = dtype;
+    return ok();
+}
+
+int lx2v_hip_set_native_mode(lx2v_hip_ctx *ctx, int mode) {
+    NEED(ctx, "ctx");
+    if (int rc = not_capturing(ctx, "set_native_mode")) return rc;
+    if (mode != LX2V_NATIVE_BF16 && mode != LX2V_NATIVE_F32)
+        return fail(LX2V_ERR_BAD_ARG, "unknown native weight mode %d", mode);
+    ctx->native_mode = mode;
     return ok();
 }
 
@@ -482,7 +492,23 @@ int lx2v_hip_weight_f32(lx2v_hip_ctx *ctx, const float *data, size_t rows, size_
         return rc;
     }
     w->device_bytes = rows * cols * 4;
-    HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload");
+    // The bf16 copy the bf16 MFMA reads (RNE), for shapes it tiles.
+    if (cols % 64 == 0 && rows * cols * 2 < (1ull << 31)) {
+        if (hipMalloc((void **)&w->wbf16, rows * cols * 2) != hipSuccess) {
+            w->wbf16 = nullptr;
+            free_weight(w);
+            return fail(LX2V_ERR_OOM, "weight_f32: %zu bytes for the bf16 copy", rows * cols * 2);
+        }
+        launch_convert(ctx->stream, w->codes, LX2V_DTYPE_F32, w->wbf16, LX2V_DTYPE_BF16, rows * cols);
+        w->device_bytes += rows * cols * 2;
+    }
+    {
+        const hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            free_weight(w);
+            return hip_fail(e, "weight upload");
+        }
+    }
     *out = w;
     return ok();
 }
@@ -1861,8 +1887,13 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     // or [f32 bias][bf16 activations], each piece 256-byte aligned.
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     const size_t s_bias = bias && bias->dtype != LX2V_DTYPE_F32 ? al(N * 4) : 0;
+    // Native f32 weights on the bf16 MFMA (their bf16 copy, bf16 activations).
+    const bool native_bf16 = w->fmt == LX2V_WFMT_F32 && w->wbf16 && ctx->native_mode == LX2V_NATIVE_BF16 &&
+                             gemm_bf16_supported(rows, N, K);
     const size_t s_act = e4m3_path ? (x->quantized() ? 0 : al(rows * K) + al(rows * 4))
-                                   : (gemm_w16_dma_supported(w, rows) && x->dtype == LX2V_DTYPE_F32 ? al(rows * K * 2) : 0);
+                                   : ((gemm_w16_dma_supported(w, rows) || native_bf16) && x->dtype == LX2V_DTYPE_F32
+                                          ? al(rows * K * 2)
+                                          : 0);
     if (scr && s_bias + s_act > scr->bytes)
         return fail(LX2V_ERR_UNSUPPORTED,
                     "linear_noalloc: this call needs %zu bytes of scratch (rows %zu x cols %zu), the maximum is %zu",
@@ -1942,6 +1973,32 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
                 }))
                 return rc;
         }
+        return ok();
+    }
+    // bf16 activations for the direct-to-LDS kernels: f32 ones rounded (RNE,
+    // as the register-staged loader would) into the workspace.
+    auto bf16_x = [&](const uint16_t **xb) -> int {
+        *xb = (const uint16_t *)xp;
+        if (x->dtype != LX2V_DTYPE_F32) return LX2V_OK;
+        void *dst = scr ? (void *)(scr->ptr + s_bias) : nullptr;
+        if (!scr) {
+            if (int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, rows * K * 2, "workspace alloc")) return rc;
+            dst = ctx->ws;
+        }
+        if (int rc = run(ctx, "convert", [&] {
+                launch_convert(ctx->stream, xp, LX2V_DTYPE_F32, dst, LX2V_DTYPE_BF16, rows * K);
+            }))
+            return rc;
+        *xb = (const uint16_t *)dst;
+        return LX2V_OK;
+    };
+    if (native_bf16) {
+        const uint16_t *xb;
+        if (int rc = bf16_x(&xb)) return rc;
+        if (int rc = run(ctx, "gemm_bf16_native", [&] {
+                launch_gemm_bf16(ctx->stream, ctx->num_cu, xb, w->wbf16, bp, act, yp, y->dtype, rows, N, K);
+            }))
+            return rc;
         return ok();
     }
     const char *name = w->fmt == LX2V_WFMT_Q8 ? "gemm_w16_q8" : w->fmt == LX2V_WFMT_Q4 ? "gemm_w16_q4" : "gemm_w16_fp8";

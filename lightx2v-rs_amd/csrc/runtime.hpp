@@ -56,6 +56,9 @@ struct lx2v_hip_weight {
     // does not apply (F32, cols % 64 != 0, group % 16 != 0).
     float *sscale = nullptr, *szero = nullptr;
     int spr = 0;
+    // F32 weights with cols % 64 == 0: the bf16 copy (RNE) the bf16 MFMA
+    // reads, [rows, cols].
+    uint16_t *wbf16 = nullptr;
 };
 
 namespace lx2v {
@@ -107,6 +110,7 @@ struct lx2v_hip_ctx {
     std::string name;
     int act_dtype = LX2V_DTYPE_F32;
     int fp8_act = LX2V_FP8_ACT_E4M3;
+    int native_mode = LX2V_NATIVE_BF16;
     int num_cu = 256;
     // Workspace: per-token e4m3 activations + row scales (grown on demand).
     void *ws = nullptr;
@@ -293,5 +297,10 @@ bool gemm_w16_dma_supported(const lx2v_hip_weight *w, size_t M);
 int plan_gemm_w16_dma(int num_cu, size_t M, size_t N);
 void launch_gemm_w16_dma(hipStream_t s, int cfg, const uint16_t *x, const lx2v_hip_weight *w, const float *bias,
                          int act, void *y, int y_dtype, size_t M);
+// bf16 x bf16 (native f32 weights through their bf16 copy): X [M, K] and
+// W [N, K] bf16, K % 64 == 0.
+bool gemm_bf16_supported(size_t M, size_t N, size_t K);
+void launch_gemm_bf16(hipStream_t s, int num_cu, const uint16_t *x, const uint16_t *w, const float *bias, int act,
+                      void *y, int y_dtype, size_t M, size_t N, size_t K);
 
 }  // namespace lx2v

@@ -27,11 +27,12 @@ ACT_NONE, ACT_GELU_TANH = 0, 1
 DTYPE_F32, DTYPE_BF16, DTYPE_E4M3, DTYPE_MXE4M3 = 0, 1, 2, 3
 WFMT_F32, WFMT_Q8, WFMT_Q4, WFMT_FP8 = 0, 1, 2, 3
 FP8_ACT_E4M3, FP8_ACT_BF16 = 0, 1
+NATIVE_BF16, NATIVE_F32 = 0, 1
 
 # Every entry point include/lightx2v_hip.h declares (checked by the tests).
 EXPORTS = [
     "lx2v_hip_last_error", "lx2v_hip_device_count", "lx2v_hip_create", "lx2v_hip_destroy",
-    "lx2v_hip_name", "lx2v_hip_set_act_dtype", "lx2v_hip_set_fp8_act", "lx2v_hip_alloc",
+    "lx2v_hip_name", "lx2v_hip_set_act_dtype", "lx2v_hip_set_fp8_act", "lx2v_hip_set_native_mode", "lx2v_hip_alloc",
     "lx2v_hip_alloc_dtype", "lx2v_hip_upload", "lx2v_hip_write", "lx2v_hip_download",
     "lx2v_hip_buf_len", "lx2v_hip_buf_dtype", "lx2v_hip_copy", "lx2v_hip_buf_free",
     "lx2v_hip_weight_f32", "lx2v_hip_weight_q8", "lx2v_hip_weight_q4", "lx2v_hip_weight_fp8",
@@ -121,6 +122,7 @@ def _load():
         "lx2v_hip_name": (ip, [vp, ctypes.c_char_p, sz]),
         "lx2v_hip_set_act_dtype": (ip, [vp, ip]),
         "lx2v_hip_set_fp8_act": (ip, [vp, ip]),
+        "lx2v_hip_set_native_mode": (ip, [vp, ip]),
         "lx2v_hip_alloc": (ip, [vp, sz, pp]),
         "lx2v_hip_alloc_dtype": (ip, [vp, sz, ip, pp]),
         "lx2v_hip_upload": (ip, [vp, vp, sz, pp]),
@@ -411,6 +413,11 @@ class HipBackend:
 
     def set_fp8_act(self, mode: int):
         _check(lib.lx2v_hip_set_fp8_act(self.ctx, mode))
+
+    def set_native_mode(self, mode: int):
+        """NATIVE_BF16 (default): native f32 weights through their bf16 copy on
+        the bf16 MFMA; NATIVE_F32: f32 operands (the scalar kernel)."""
+        _check(lib.lx2v_hip_set_native_mode(self.ctx, mode))
 
     def _out(self):
         return ctypes.c_void_p()
