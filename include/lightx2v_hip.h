@@ -274,8 +274,12 @@ int lx2v_hip_head_split(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
  * dtype); out [sq, heads*head_dim] (F32 or BF16), heads merged.  Scores
  * q.k / sqrt(head_dim), softmax over keys; masked pairs are -inf (a query
  * with no allowed key gives NaN, as the reference).  head_dim 64 and 128
- * run on the bf16 MFMA (operands rounded to bf16, f32 accumulation and
- * softmax); other head_dim up to 256 on a per-query kernel. */
+ * run on the bf16 MFMA: q, k, v and the softmax weights P rounded to bf16,
+ * f32 accumulation and softmax -- against the reference's f32 attention
+ * (cpu/src/lib.rs:171-203) on the same f32 inputs, rel-L2 about 3e-3 and
+ * max-abs about 5e-3 of the output's range (measured on gfx950 for sk 64 ..
+ * 2048).  Other head_dim up to 256 run on a per-query kernel in f32
+ * (rel-L2 <= 1e-5). */
 int lx2v_hip_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k,
                        const lx2v_hip_buf *v, size_t heads, size_t sq, size_t sk, size_t head_dim,
                        lx2v_hip_buf *out);

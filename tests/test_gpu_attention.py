@@ -3,9 +3,10 @@ oracle's restatement of the reference (crates/lightx2v-cpu/src/lib.rs:155-203).
 
 Tolerances: head_dim 64 / 128 run on the bf16 MFMA (q, k, v and the softmax
 weights P rounded to bf16, f32 accumulation and softmax): against the oracle
-on the same bf16-rounded q, k, v, rel-L2 <= 1e-2 and max-abs <= 2e-2 * max|y|
-(P's bf16 rounding is the dominant term; measured values are printed by the
-assertion on failure).  Other head sizes run the per-query f32 kernel:
+on the same bf16-rounded q, k, v, rel-L2 <= 5e-3 and max-abs <= 1e-2 *
+max|y| (measured 1.3e-3 .. 1.7e-3 and <= 2.1e-3 * max|y|; P's bf16 rounding
+is the remaining term), and against the reference's f32 attention on the
+unrounded inputs F32REF_TOL below.  Other head sizes run the per-query f32 kernel:
 rel-L2 <= 1e-5 (only the summation order and exp2 differ).  Masks: fully
 masked tiles are skipped, mixed tiles read mask bytes; a query with no
 allowed key is NaN in both, sk = 0 gives zeros in both.
@@ -19,7 +20,7 @@ import oracle as O
 from helpers import assert_close, u32
 
 pytestmark = pytest.mark.gpu
-MFMA_TOL = (1e-2, 2e-2)
+MFMA_TOL = (5e-3, 1e-2)
 ROWS_TOL = (1e-5, 1e-4)
 
 
@@ -74,6 +75,28 @@ def test_attention_mfma(be, heads, sq, sk, d, dtype):
     q, k, v = _qkv(1000 + sq + sk, heads, sq, sk, d)
     got = _run(be, q, k, v, dtype=dtype)
     assert_close(got, _want(q, k, v), *MFMA_TOL, what=f"attention {heads}x{sq}x{sk}x{d}")
+
+
+# The MFMA path against the reference's own f32 attention on the unrounded
+# f32 inputs (cpu/src/lib.rs:171-203): the deviation the bf16 operands and
+# bf16 P add.  Measured on gfx950 (printed by this test): rel-L2 2.95e-3 ..
+# 3.46e-3 and max-abs <= 4.9e-3 * max|y| at these shapes, about twice the
+# deviation from the oracle on bf16-rounded q / k / v (rel-L2 1.3e-3 ..
+# 1.7e-3, max-abs <= 2.1e-3 * max|y|): P's rounding and the inputs'
+# contribute alike.
+F32REF_TOL = (5e-3, 1e-2)
+
+
+@pytest.mark.parametrize("heads,sq,sk,d", [(2, 128, 64, 128), (1, 300, 1000, 64), (4, 256, 512, 128),
+                                           (2, 512, 2048, 128)])
+def test_attention_mfma_vs_f32_reference(be, heads, sq, sk, d):
+    q, k, v = _qkv(7000 + sq + sk, heads, sq, sk, d)
+    got = _run(be, q, k, v, dtype=H.DTYPE_F32)
+    r32, m32 = assert_close(got, _want(q, k, v, bf16=False), *F32REF_TOL, what=f"vs f32 reference {sq}x{sk}x{d}")
+    r16, m16 = assert_close(got, _want(q, k, v), *MFMA_TOL, what=f"vs bf16-operand oracle {sq}x{sk}x{d}")
+    scale = float(np.max(np.abs(got)))
+    print(f"attention {heads}x{sq}x{sk}x{d}: vs f32 reference rel-L2 {r32:.3e} max-abs {m32 / scale:.3e}*max; "
+          f"vs bf16-operand oracle rel-L2 {r16:.3e} max-abs {m16 / scale:.3e}*max")
 
 
 @pytest.mark.parametrize("heads,sq,sk,d", [(2, 40, 33, 80), (1, 5, 7, 16), (3, 17, 100, 256)])
