@@ -5,14 +5,18 @@ Wan2.1-1.3B block-linear set in FP8 for one 3-frame chunk (M = 4680
 tokens), 30 layers x 4 DMD steps, 7 linears per layer-step (self-attn QKV,
 O; cross-attn Q, K/V on 512 text tokens, O; FFN up with GELU, FFN down),
 with 30 distinct layers of random-init FP8 per-output-channel weights
-resident in HBM (1.39 GB) and bf16 activations, which each linear quantizes
+resident in HBM (1.48 GB) and bf16 activations, which each linear quantizes
 per token to e4m3 before its fp8 GEMM -- except the FFN hand-off: FFN up
 writes MX e4m3 (one power-of-two scale per 32 columns of a row, quantized in
-its GEMM epilogue) and FFN down reads it directly.  The same chunk with a
-bf16 FFN hand-off is timed too (ms_per_chunk_bf16_ffn_handoff).  One "step"
-is one chunk: 840 Backend::linear calls
-(crates/lightx2v-model/src/dit.rs:602-759).  Inputs are synthetic and
-resident before timing starts.
+its GEMM epilogue) and FFN down reads it directly.  The cross-attention K/V
+projections of the 30 layers all read the same 512 text tokens, so each
+step runs them as one linear over the layers' concatenated weights
+[30 x 3072, 1536] (the reference computes them per prompt, one linear per
+layer: dit.rs:470-492; head_split reads each layer's slice of the output by
+stride).  The same chunk with a bf16 FFN hand-off is timed too
+(ms_per_chunk_bf16_ffn_handoff).  One "step" is one chunk: 724
+Backend::linear calls (6 per layer-step, dit.rs:602-759, plus one K/V call
+per step).  Inputs are synthetic and resident before timing starts.
 
 Timed two ways over the same calls: eagerly (one C-ABI call per linear from
 Python) and as one replayed HIP graph of the whole chunk; `value` is the
@@ -304,16 +308,23 @@ def main():
         be.fill_normal(acts[nm], 1001 + 7 * i, 1.0)
     acts["x_text"] = be.alloc(TEXT * DIM)
     be.fill_normal(acts["x_text"], 1099, 1.0)
-    outs = {name: be.alloc(rows * n) for name, rows, n, _, _, _ in GEMMS}
+    outs = {name: be.alloc(rows * n * (LAYERS if name == "kv2" else 1)) for name, rows, n, _, _, _ in GEMMS}
+    KVW = LAYERS * 2 * DIM  # columns of the concatenated cross-attention K/V output
     ffn_mx = be.alloc_mx(M, FFN)  # FFN up -> FFN down in MX e4m3
     acts["y_ffn1"] = outs["ffn1"]
     tmp = be.alloc(FFN * DIM, H.DTYPE_F32)
+    tmp_kv = be.alloc(KVW * DIM, H.DTYPE_F32)
 
     def make_layers(group):
+        """Per layer: the weights of the six per-layer linears; then the
+        layers' cross-attention K/V weights as one [30 x 3072, 1536] weight
+        (scales and bias concatenated the same way)."""
         out = []
         for l in range(LAYERS):
             lw = {}
             for j, (name, rows, n, k, act, _) in enumerate(GEMMS):
+                if name == "kv2":
+                    continue
                 seed = 10_000 * (l + 1) + 10 * j
                 be.fill_normal(tmp, seed, 0.02)
                 w = be.quantize_fp8(tmp, n, k, group or k)
@@ -321,18 +332,26 @@ def main():
                 be.fill_normal(b, seed + 1, 0.01)
                 lw[name] = (w, b)
             out.append(lw)
-        return out
+        be.fill_normal(tmp_kv, 9_999, 0.02)
+        kvw = be.quantize_fp8(tmp_kv, KVW, DIM, group or DIM)
+        kvb = be.alloc(KVW, H.DTYPE_F32)
+        be.fill_normal(kvb, 9_998, 0.01)
+        return out, (kvw, kvb)
 
-    layers = make_layers(None)
+    layers, kv_all = make_layers(None)
     be.sync()
-    wbytes = sum(w.info()["device_bytes"] for lw in layers for w, _ in lw.values())
+    wbytes = (sum(w.info()["device_bytes"] for lw in layers for w, _ in lw.values()) +
+              kv_all[0].info()["device_bytes"])
     log(f"bench: setup {time.perf_counter() - t0:.1f} s, {wbytes / 1e9:.2f} GB FP8 weights resident")
 
     def chunk(mx_handoff):
         def run():
             for _ in range(DMD):
+                be.linear(acts["x_text"], 0, TEXT, *kv_all, 0, outs["kv2"], 0)
                 for lw in layers:
                     for name, rows, n, k, act, src in GEMMS:
+                        if name == "kv2":
+                            continue
                         w, b = lw[name]
                         x, y = acts[src], outs[name]
                         if mx_handoff and name == "ffn1":
@@ -345,7 +364,7 @@ def main():
     step = chunk(True)
 
     step_flops = flops_of(GEMMS) * LAYERS * DMD
-    n_linear = len(GEMMS) * LAYERS * DMD
+    n_linear = ((len(GEMMS) - 1) * LAYERS + 1) * DMD
 
     def timed(fn, steps, warmup):
         for _ in range(warmup):
@@ -373,12 +392,15 @@ def main():
     log(f"bench: bf16 FFN hand-off (eager) {ms_bf16_handoff:.2f} ms/chunk")
     # the chunk with group-128 weights (the reference's FP8 format, quant.rs:21;
     # FFN up -> down in bf16: MX input takes per-channel weights only), eager
-    g128 = make_layers(128)
+    g128, kv_g128 = make_layers(128)
 
     def chunk_g128():
         for _ in range(DMD):
+            be.linear(acts["x_text"], 0, TEXT, *kv_g128, 0, outs["kv2"], 0)
             for lw in g128:
                 for name, rows, n, k, act, src in GEMMS:
+                    if name == "kv2":
+                        continue
                     w, b = lw[name]
                     be.linear(acts[src], 0, rows, w, b, act, outs[name], 0)
 
@@ -388,8 +410,11 @@ def main():
         for w, b in lw.values():
             w.free()
             b.free()
+    kv_g128[0].free()
+    kv_g128[1].free()
     del g128
     tmp.free()
+    tmp_kv.free()
     value = step_flops / ms / 1e9
 
     # ---- the block's linear path with its producers and consumers ---------------
@@ -433,6 +458,8 @@ def main():
         def run():
             xin = xq_blk if fused else normed
             for _ in range(DMD):
+                # every layer's text K / V in one call; each layer's slices by stride
+                be.linear(acts["x_text"], 0, TEXT, *kv_all, 0, outs["kv2"], 0)
                 for l, lw in enumerate(layers):
                     md, (nw, nb) = lmods[l], lnw[l]
                     nq1, nk1, nq2, nk2 = lrms[l]
@@ -445,9 +472,8 @@ def main():
                     be.residual_norm(h, outs["o"], M, DIM, md, 2, NK.affine(nw, nb), 1e-6, xin)
                     be.linear(xin, 0, M, *lw["q2"], 0, outs["q2"], 0)
                     be.head_split(outs["q2"], M, DIM, 0, DIM // HD, HD, nq2, None, 1e-6, hq)
-                    be.linear(acts["x_text"], 0, TEXT, *lw["kv2"], 0, outs["kv2"], 0)
-                    be.head_split(outs["kv2"], TEXT, 2 * DIM, 0, DIM // HD, HD, nk2, None, 1e-6, hk2)
-                    be.head_split(outs["kv2"], TEXT, 2 * DIM, DIM, DIM // HD, HD, None, None, 1e-6, hv2)
+                    be.head_split(outs["kv2"], TEXT, KVW, 2 * DIM * l, DIM // HD, HD, nk2, None, 1e-6, hk2)
+                    be.head_split(outs["kv2"], TEXT, KVW, 2 * DIM * l + DIM, DIM // HD, HD, None, None, 1e-6, hv2)
                     be.linear(acts["x_o2"], 0, M, *lw["o2"], 0, outs["o2"], 0)
                     be.residual_norm(h, outs["o2"], M, DIM, md, None, NK.mod(4, 3), 1e-6, xin)
                     be.linear(xin, 0, M, *lw["ffn1"], 1, ffn_mx, 0)
@@ -486,16 +512,21 @@ def main():
 
     def gemm_step():
         for _ in range(DMD):
+            be.linear(gx["kv2"], 0, TEXT, *kv_all, 0, gy["kv2"], 0)
             for lw in layers:
                 for name, rows, n, k, act, src in GEMMS:
+                    if name == "kv2":
+                        continue
                     w, b = lw[name]
                     be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
 
     def act_quant_step():
         for _ in range(DMD):
+            be.quantize_act(acts["x_text"], 0, TEXT, xq["x_text"])
             for _ in range(LAYERS):
-                for _, rows, _, k, _, src in per_token:
-                    be.quantize_act(acts[src], 0, rows, xq[src])
+                for name, rows, _, k, _, src in per_token:
+                    if name != "kv2":
+                        be.quantize_act(acts[src], 0, rows, xq[src])
 
     reps = max(1, min(args.steps, 3))
     region = {}
@@ -511,9 +542,10 @@ def main():
     # algorithmic bytes of the chunk's GEMMs as run here: e4m3 X (MX for FFN
     # down, + its scale bytes), e4m3 W + f32 channel scales, f32 bias, bf16 Y
     # (MX e4m3 + scales for FFN up), averaged per launch
-    alg_per_launch = sum(r * k + (r * k // 32 if nm == "ffn2" else r * 4) + n * k + n * 8 +
-                         (r * n + r * n // 32 if nm == "ffn1" else 2 * r * n)
-                         for nm, r, n, k, _, _ in GEMMS) / len(GEMMS)
+    alg_step = sum((r * k + (r * k // 32 if nm == "ffn2" else r * 4)) * (1 if nm == "kv2" else LAYERS) +
+                   (n * k + n * 8 + (r * n + r * n // 32 if nm == "ffn1" else 2 * r * n)) * LAYERS
+                   for nm, r, n, k, _, _ in GEMMS)
+    alg_per_launch = alg_step / ((len(GEMMS) - 1) * LAYERS + 1)
     achieved = step_flops / gemm_ms / 1e9
     log(f"bench: GEMM-only {gemm_ms:.2f} ms/chunk ({gemm_ms * 1e3 / n_linear:.2f} us/launch, "
         f"{achieved:.1f} TFLOP/s); act quant {region['act_quant_chunk']:.2f} ms/chunk")
@@ -521,21 +553,24 @@ def main():
     # per-shape GEMM time (layer 0 weights, 50 back-to-back launches in a region)
     per = {}
     for name, rows, n, k, act, src in GEMMS:
-        w, b = layers[0][name]
+        # the K / V call covers all the layers: its per-layer share is reported
+        w, b = kv_all if name == "kv2" else layers[0][name]
         be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
         be.profile_region("g_" + name, True)
         for _ in range(50):
             be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
         be.profile_region("g_" + name, False)
-        us = be.profile_kernel("g_" + name)[1] * 1e3 / 50
+        us = be.profile_kernel("g_" + name)[1] * 1e3 / 50 / (LAYERS if name == "kv2" else 1)
         uq = 0.0  # FFN down's input is quantized in FFN up's epilogue
         if name != "ffn2":
             be.profile_region("q_" + name, True)
             for _ in range(50):
                 be.quantize_act(acts[src], 0, rows, xq[src])
             be.profile_region("q_" + name, False)
-            uq = be.profile_kernel("q_" + name)[1] * 1e3 / 50
-        per[name] = {"shape": f"{rows}x{k}->{n}", "gemm_us": round(us, 2), "act_quant_us": round(uq, 2),
+            uq = be.profile_kernel("q_" + name)[1] * 1e3 / 50 / (LAYERS if name == "kv2" else 1)
+        per[name] = {"shape": f"{rows}x{k}->{n}" + (f", the {LAYERS} layers in one call (per layer)"
+                                                   if name == "kv2" else ""),
+                     "gemm_us": round(us, 2), "act_quant_us": round(uq, 2),
                      "tflops": round(2.0 * rows * n * k / (us * 1e-6) / 1e12, 1),
                      "pct_fp8_peak": round(2.0 * rows * n * k / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS * 100, 1)}
 
@@ -690,10 +725,12 @@ def main():
         "config": {
             "workload": "cfg4: Wan2.1-1.3B 30-layer x 4-step FP8 block-linear set, one 3-frame chunk",
             "tokens": M, "text_tokens": TEXT, "layers": LAYERS, "dmd_steps": DMD,
-            "gemms_per_layer_step": len(GEMMS), "tflop_per_step": round(step_flops / 1e12, 3),
+            "gemms_per_layer_step": len(GEMMS), "linear_calls_per_step": n_linear, "tflop_per_step": round(step_flops / 1e12, 3),
             "activations": "bf16 in/out, per-token dynamic e4m3 inside linear; FFN up -> FFN down in MX e4m3 "
                            "(per-32-column power-of-two scales, quantized in FFN up's epilogue)",
             "weights_gb": round(wbytes / 1e9, 3),
+            "cross_kv": "the 30 layers' K/V projections (512 text tokens) as one linear per step over their "
+                        "concatenated weights",
         },
         "pct_fp8_peak": round(value / PEAK_FP8_TFLOPS * 100, 2),
         "ms_per_chunk": round(ms, 3),
@@ -722,7 +759,8 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
             "traffic": traffic,
-            "kernel": "fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma: 256x128, 128x256 and 128x128 tiles)",
+            "kernel": ("fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma 256x128 / 128x128 tiles, the persistent "
+                       "k_gemm_fp8_ov 256x128 with the epilogue overlapped for QKV and FFN up)"),
             "avg_launch_us": round(gemm_ms * 1e3 / n_linear, 2),
             "hbm_gbs": round(traffic / (gemm_ms * 1e-3 / n_linear) / 1e9, 1) if traffic else None,
             "alg_bytes_per_launch": round(alg_per_launch),
