@@ -288,6 +288,9 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config linears")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eagerly only (rocprofv3 cannot trace hipGraphLaunch here)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="run the chunk's GEMMs --steps times on pre-quantized activations and the counter "
+                         "calibration kernel, then exit (the workload of the rocprofv3 summaries in profiles/)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the linear path shards over token rows with no exchange, "
@@ -365,6 +368,44 @@ def main():
 
     step_flops = flops_of(GEMMS) * LAYERS * DMD
     n_linear = ((len(GEMMS) - 1) * LAYERS + 1) * DMD
+
+    # The chunk's GEMMs alone, on pre-quantized activations (FFN up writes
+    # the MX buffer FFN down reads; the other inputs per-token e4m3).
+    per_token = [g for g in GEMMS if g[0] != "ffn2"]
+    xq = {src: be.alloc_e4m3(rows, k) for _, rows, _, k, _, src in per_token}
+    for _, rows, _, k, _, src in per_token:
+        be.quantize_act(acts[src], 0, rows, xq[src])
+    gx = {name: (ffn_mx if name == "ffn2" else xq[src]) for name, _, _, _, _, src in GEMMS}
+    gy = {name: (ffn_mx if name == "ffn1" else outs[name]) for name, _, _, _, _, _ in GEMMS}
+
+    def gemm_step():
+        for _ in range(DMD):
+            be.linear(gx["kv2"], 0, TEXT, *kv_all, 0, gy["kv2"], 0)
+            for lw in layers:
+                for name, rows, n, k, act, src in GEMMS:
+                    if name == "kv2":
+                        continue
+                    w, b = lw[name]
+                    be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
+
+    def calibrate():
+        """The rocprofv3 FETCH_SIZE / WRITE_SIZE calibration: one plain
+        streaming kernel of known bytes (k_convert, f32 -> bf16: 1 GiB read,
+        512 MiB written, both past the 256 MB Infinity Cache)."""
+        cal_n = 256 << 20
+        ca, cb = be.alloc(cal_n, H.DTYPE_F32), be.alloc(cal_n, H.DTYPE_BF16)
+        be.copy(ca, 0, cb, 0, cal_n)
+        be.sync()
+        ca.free()
+        cb.free()
+
+    if args.gemm_only:
+        for _ in range(max(1, args.steps)):
+            gemm_step()
+        be.sync()
+        calibrate()
+        log(f"bench: --gemm-only: {n_linear} GEMM launches and the calibration kernel")
+        return
 
     def timed(fn, steps, warmup):
         for _ in range(warmup):
@@ -503,23 +544,6 @@ def main():
     # (the chunk's GEMMs exactly: FFN up writes the MX buffer FFN down reads;
     # the other inputs come per-token quantized; act_quant_step is the
     # chunk's remaining per-token quantization)
-    per_token = [g for g in GEMMS if g[0] != "ffn2"]
-    xq = {src: be.alloc_e4m3(rows, k) for _, rows, _, k, _, src in per_token}
-    for _, rows, _, k, _, src in per_token:
-        be.quantize_act(acts[src], 0, rows, xq[src])
-    gx = {name: (ffn_mx if name == "ffn2" else xq[src]) for name, _, _, _, _, src in GEMMS}
-    gy = {name: (ffn_mx if name == "ffn1" else outs[name]) for name, _, _, _, _, _ in GEMMS}
-
-    def gemm_step():
-        for _ in range(DMD):
-            be.linear(gx["kv2"], 0, TEXT, *kv_all, 0, gy["kv2"], 0)
-            for lw in layers:
-                for name, rows, n, k, act, src in GEMMS:
-                    if name == "kv2":
-                        continue
-                    w, b = lw[name]
-                    be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
-
     def act_quant_step():
         for _ in range(DMD):
             be.quantize_act(acts["x_text"], 0, TEXT, xq["x_text"])
@@ -685,13 +709,7 @@ def main():
     for bb in (kb_, vb_, qb_, ob_):
         bb.free()
 
-    # plain-copy calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-    cal_n = 64 << 20
-    ca, cb = be.alloc(cal_n, H.DTYPE_F32), be.alloc(cal_n, H.DTYPE_F32)
-    be.copy(ca, 0, cb, 0, cal_n)
-    be.sync()
-    ca.free()
-    cb.free()
+    calibrate()
 
     configs = None
     if not args.no_configs:
