@@ -215,6 +215,68 @@ def per_config(be, H):
     return out
 
 
+def yardstick(be, H):
+    """hipBLASLt's fp8 GEMM through torch._scaled_mm (e4m3 x e4m3, per-tensor
+    scales, bf16 output) beside this build's GEMM on pre-quantized per-token
+    e4m3 activations (per-channel weight scales, bias; FFN up with GELU), at
+    the chunk's shapes: 100 launches each after a warm-up, CUDA / HIP events.
+    A reference point for the GEMM alone, not part of the metric."""
+    import torch
+
+    dev = torch.device("cuda:0")
+
+    def ev_time(fn, it=100):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(it):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / it * 1e3
+
+    shapes = [(nm, r, n, k, act) for nm, r, n, k, act, _ in GEMMS]
+    shapes.append(("kv2_all_layers", TEXT, LAYERS * 2 * DIM, DIM, 0))
+    res = {}
+    for nm, rows, n, k, act in shapes:
+        a8 = torch.randn(rows, k, device=dev).to(torch.float8_e4m3fn)
+        w8 = (0.02 * torch.randn(n, k, device=dev)).to(torch.float8_e4m3fn)
+        one = torch.ones((), device=dev)
+        t_blas = ev_time(lambda: torch._scaled_mm(a8, w8.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16))
+        del a8, w8
+        torch.cuda.empty_cache()
+        be.set_act_dtype(H.DTYPE_F32)
+        xf = be.alloc(rows * k)
+        be.fill_normal(xf, 11, 1.0)
+        xq = be.alloc_e4m3(rows, k)
+        be.quantize_act(xf, 0, rows, xq)
+        tmp = be.alloc(n * k)
+        be.fill_normal(tmp, 12, 0.02)
+        w = be.quantize_fp8(tmp, n, k, k)
+        bias = be.alloc(n)
+        be.fill_normal(bias, 13, 0.01)
+        be.set_act_dtype(H.DTYPE_BF16)
+        y = be.alloc(rows * n)
+        for _ in range(10):
+            be.linear(xq, 0, rows, w, bias, act, y, 0)
+        be.profile_region("y_" + nm, True)
+        for _ in range(100):
+            be.linear(xq, 0, rows, w, bias, act, y, 0)
+        be.profile_region("y_" + nm, False)
+        t_ours = be.profile_kernel("y_" + nm)[1] * 1e3 / 100
+        for h in (xf, xq, tmp, bias, y):
+            h.free()
+        w.free()
+        res[nm] = {"shape": f"{rows}x{k}->{n}", "hipblaslt_us": round(t_blas, 2), "this_build_us": round(t_ours, 2),
+                   "hipblaslt_tflops": round(2.0 * rows * n * k / t_blas / 1e6, 1),
+                   "this_build_tflops": round(2.0 * rows * n * k / t_ours / 1e6, 1)}
+        log(f"yardstick {nm} {rows}x{k}->{n}: hipBLASLt {t_blas:.2f} us, this build {t_ours:.2f} us")
+    print(json.dumps({"yardstick": "hipBLASLt fp8 GEMM (torch._scaled_mm) vs this build, chunk shapes",
+                      "torch": torch.__version__, "shapes": res}), flush=True)
+
+
 def cpu_baseline(seconds_target=12.0):
     """The CPU oracle (crates/lightx2v-cpu/src/lib.rs:296-326 restated: a
     sequential f32 acc += x*w per output, then bias, then GELU) on a row
@@ -288,6 +350,9 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config linears")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eagerly only (rocprofv3 cannot trace hipGraphLaunch here)")
+    ap.add_argument("--yardstick", action="store_true",
+                    help="time hipBLASLt's fp8 GEMM (torch._scaled_mm, per-tensor scales, bf16 out) against "
+                         "this build's GEMM at the chunk's shapes, print one JSON line, exit")
     ap.add_argument("--gemm-only", action="store_true",
                     help="run the chunk's GEMMs --steps times on pre-quantized activations and the counter "
                          "calibration kernel, then exit (the workload of the rocprofv3 summaries in profiles/)")
@@ -297,10 +362,18 @@ def main():
               f"so a multi-GPU figure is not run here (--gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
 
+    if args.yardstick:
+        import torch
+
+        torch.cuda.init()  # before the library's context: torch must see the device first
+
     import lightx2v_hip as H
 
     be = H.HipBackend(0)
     log(f"bench: {be.name()}")
+    if args.yardstick:
+        yardstick(be, H)
+        return
     be.set_act_dtype(H.DTYPE_BF16)
 
     # ---- resident synthetic inputs and weights --------------------------------
