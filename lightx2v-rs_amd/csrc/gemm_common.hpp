@@ -45,6 +45,13 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// The same wait that also retires every LDS read of this wave (lgkmcnt 0).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lds0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
 // LDS-staged epilogue, used where the main loop leaves a large LDS ring
 // free.  Stage 1 (acc_to_lds): each wave applies the token scale, channel
 // scale, bias and GELU (in that order, in f32) and writes the results,

@@ -27,6 +27,11 @@
 // consecutive output channels n.
 #include "gemm_common.hpp"
 
+// The skewed K loop of k_gemm_fp8_dma (on unless built with -DLX2V_FP8_SKEW=0).
+#ifndef LX2V_FP8_SKEW
+#define LX2V_FP8_SKEW 1
+#endif
+
 namespace lx2v {
 
 namespace {
@@ -384,89 +389,104 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         for (int i = 0; i < TM; i++) acc[j][i] = (f32x16){};
 
     const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
-    // compute(buf, stage, dkt, dbuf): the MFMAs of `stage` from slot buf,
-    // with the A / B loads of stage dkt (slot dbuf) issued one after each of
-    // its first MFMAs -- issued back to back right after the barrier, the
-    // loads held both waves of a SIMD off the MFMA pipe (7-9% at one
-    // workgroup per CU).  dkt < 0: no loads.
-    f32x16 part[GS ? TN : 1][GS ? TM : 1];  // grouped scales: this stage's partial sums
-    auto compute = [&](int buf, int stage, int dkt, int dbuf) {
+    constexpr int LPS = ALD + BLD;
+    // The K loop skewed by one slice (below): 128-byte stages, per-stage
+    // scales not folded per stage.
+    constexpr bool SKEW = LX2V_FP8_SKEW && BKB == 128 && !GS;
+    // One 64-byte K slice's fragments: the wave's TM A row blocks and TN B
+    // column blocks.
+    struct Frag {
+        i32x8 a[TM], b[TN];
+    };
+    // read_half(buf, kk, f): slice kk of the stage in slot buf.  16-byte
+    // chunks of the 64-byte K slice each lane supplies: the block-scaled MFMA
+    // reads a lane's bytes 0..15 as K [16 h, 16 h + 16) and bytes 16..31 as
+    // K [32 + 16 h, +16) of the slice (h = lane / 32) and scales K [0, 32)
+    // with the lanes-0..31 scale and K [32, 64) with the lanes-32..63 one
+    // (probed on gfx950), so with MX activations lane half h takes chunks h
+    // and h + 2 and each MX block is one hardware scale block.  Unscaled, any
+    // K order shared by both operands is the same product.
+    auto read_half = [&](int buf, int kk, Frag &f) {
         const uint8_t *s = smem + buf * STAGE;
-        uint32_t sraw[AM ? TM : 1];
-        if constexpr (AM) {
+        const uint32_t c0 = AM ? kk * 4 + (lane >> 5) : kk * 4 + fhalf;
+        const uint32_t c1 = AM ? c0 + 2 : c0 + 1;
 #pragma unroll
-            for (int i = 0; i < TM; i++)
-                sraw[i] = *(const uint32_t *)(asl + buf * ASL + (wm * WM + i * 32 + frow) * 4);
+        for (int i = 0; i < TM; i++) {
+            const uint32_t row = wm * WM + i * 32 + frow;
+            u32x4 lo = *(const u32x4 *)(s + ((row * BKB + (dma_slot<BKB>(row, c0) << 4)) & AMASK));
+            u32x4 hi = *(const u32x4 *)(s + ((row * BKB + (dma_slot<BKB>(row, c1) << 4)) & AMASK));
+            f.a[i] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
         }
 #pragma unroll
-        for (int kk = 0; kk < BKB / 64; kk++) {
-            i32x8 af[TM], bf[TN];
-            // 16-byte chunks of the 64-byte K slice each lane supplies.  The
-            // block-scaled MFMA reads a lane's bytes 0..15 as K [16 h, 16 h
-            // + 16) and bytes 16..31 as K [32 + 16 h, +16) of the slice (h =
-            // lane / 32) and scales K [0, 32) with the lanes-0..31 scale and
-            // K [32, 64) with the lanes-32..63 one (probed on gfx950), so
-            // with MX activations lane half h takes chunks h and h + 2 and
-            // each MX block is one hardware scale block.  Unscaled, any K
-            // order shared by both operands is the same product.
-            const uint32_t c0 = AM ? kk * 4 + (lane >> 5) : kk * 4 + fhalf;
-            const uint32_t c1 = AM ? c0 + 2 : c0 + 1;
+        for (int j = 0; j < TN; j++) {
+            const uint32_t row = BM + wn * WN + j * 32 + frow;
+            const uint32_t rb = row - BM;
+            u32x4 lo = *(const u32x4 *)(s + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c0) << 4)) & BMASK));
+            u32x4 hi = *(const u32x4 *)(s + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c1) << 4)) & BMASK));
+            f.b[j] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+    };
+    // MX activations: each of the wave's rows' 4 scale bytes of the stage in
+    // slot buf, and the scale operand of slice kk (lane l holds block 2 s +
+    // l / 32 of its row's 128-column group, s the 64-column slice: that
+    // block's scale shifted into byte 0).
+    typedef uint32_t SRaw[AM ? TM : 1];
+    typedef int SOp[AM ? TM : 1];
+    auto read_sraw = [&](int buf, SRaw &sr) {
+        if constexpr (AM) {
+#pragma unroll
+            for (int i = 0; i < TM; i++) sr[i] = *(const uint32_t *)(asl + buf * ASL + (wm * WM + i * 32 + frow) * 4);
+        }
+    };
+    auto scale_op = [&](const SRaw &sr, int kk, int stage, SOp &as) {
+        if constexpr (AM) {
+            const int sh = 8 * (int)(lane >> 5) + 16 * (BKB == 128 ? kk : (stage & 1));
+#pragma unroll
+            for (int i = 0; i < TM; i++) as[i] = (int)(sr[i] >> sh);
+        }
+    };
+    // mfma_half(f, as, nbase, dkt, dbuf): the slice's TN x TM MFMAs into acc
+    // (or, grouped, into the stage's partial sums, fresh when kk == 0), with
+    // load nbase + (j TM + i) of stage dkt (slot dbuf) issued after MFMA (j,
+    // i) while it is below LPS -- issued back to back right after the
+    // barrier, the loads held both waves of a SIMD off the MFMA pipe (7-9%
+    // at one workgroup per CU).  dkt < 0: no loads.
+    f32x16 part[GS ? TN : 1][GS ? TM : 1];  // grouped scales: this stage's partial sums
+    auto mfma_half = [&](const Frag &f, const SOp &as, int kk, int nbase, int dkt, int dbuf) {
+#pragma unroll
+        for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                const uint32_t row = wm * WM + i * 32 + frow;
-                u32x4 lo = *(const u32x4 *)(s + ((row * BKB + (dma_slot<BKB>(row, c0) << 4)) & AMASK));
-                u32x4 hi = *(const u32x4 *)(s + ((row * BKB + (dma_slot<BKB>(row, c1) << 4)) & AMASK));
-                af[i] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                                (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+                if constexpr (AM)
+                    acc[j][i] =
+                        __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc[j][i], 0, 0, 0, 127, 0, as[i]);
+                else if constexpr (GS)
+                    part[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        f.b[j], f.a[i], kk == 0 ? (f32x16){} : part[j][i], 0, 0, 0, 0, 0, 0);
+                else
+                    acc[j][i] =
+                        __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc[j][i], 0, 0, 0, 0, 0, 0);
+                const int n = nbase + j * TM + i;
+                if (n < LPS && dkt >= 0) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    piece(n, dkt, dbuf);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
+    };
+    // compute(buf, stage, dkt, dbuf): the MFMAs of `stage` from slot buf,
+    // slice by slice (each slice's reads, then its MFMAs), with the loads of
+    // stage dkt interleaved.
+    auto compute = [&](int buf, int stage, int dkt, int dbuf) {
+        SRaw sraw;
+        read_sraw(buf, sraw);
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const uint32_t row = BM + wn * WN + j * 32 + frow;
-                const uint32_t rb = row - BM;
-                u32x4 lo = *(const u32x4 *)(s + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c0) << 4)) & BMASK));
-                u32x4 hi = *(const u32x4 *)(s + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c1) << 4)) & BMASK));
-                bf[j] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                                (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-            }
-            if constexpr (AM) {
-                // lane l holds block 2 s + l / 32 of its row's 128-column group
-                // (s: the 64-column slice): that block's scale into byte 0
-                const int sh = 8 * (int)(lane >> 5) + 16 * (BKB == 128 ? kk : (stage & 1));
-                int as[TM];
-#pragma unroll
-                for (int i = 0; i < TM; i++) as[i] = (int)(sraw[i] >> sh);
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-#pragma unroll
-                    for (int i = 0; i < TM; i++) {
-                        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                            bf[j], af[i], acc[j][i], 0, 0, 0, 127, 0, as[i]);
-                        const int n = kk * TN * TM + j * TM + i;
-                        if (n < ALD + BLD && dkt >= 0) {
-                            __builtin_amdgcn_sched_barrier(0);
-                            piece(n, dkt, dbuf);
-                            __builtin_amdgcn_sched_barrier(0);
-                        }
-                    }
-            } else {
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-#pragma unroll
-                    for (int i = 0; i < TM; i++) {
-                        if constexpr (GS)
-                            part[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                                bf[j], af[i], kk == 0 ? (f32x16){} : part[j][i], 0, 0, 0, 0, 0, 0);
-                        else
-                            acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                                bf[j], af[i], acc[j][i], 0, 0, 0, 0, 0, 0);
-                        const int n = kk * TN * TM + j * TM + i;
-                        if (n < ALD + BLD && dkt >= 0) {
-                            __builtin_amdgcn_sched_barrier(0);
-                            piece(n, dkt, dbuf);
-                            __builtin_amdgcn_sched_barrier(0);
-                        }
-                    }
-            }
+        for (int kk = 0; kk < BKB / 64; kk++) {
+            Frag f;
+            read_half(buf, kk, f);
+            SOp as;
+            scale_op(sraw, kk, stage, as);
+            mfma_half(f, as, kk, kk * TN * TM, dkt, dbuf);
         }
         if constexpr (GS) {
             // acc += part * s[n, stage]: lane l's register 4 g + q of block j
@@ -494,22 +514,79 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // leaves stage kt complete for this wave; the barrier then publishes
     // every wave's part of it and retires the reads of stage kt - 1, whose
     // buffer the next issue overwrites.
-    constexpr int LPS = ALD + BLD;
 #pragma unroll
     for (int st = 0; st < NS - 1; st++) issue(st, st);
-    for (int kt = 0; kt < KT; kt += NS) {
+    if constexpr (SKEW) {
+        // Skewed by one 64-byte slice: a wave reads stage kt's second slice
+        // at the end of iteration kt and contracts it after the next barrier,
+        // while stage kt + 1's first slice is being read, so the MFMAs that
+        // follow a barrier never wait for LDS.  Each wait before a barrier
+        // also retires the wave's reads (lgkmcnt 0): the loads issued after
+        // the barrier overwrite the slot those reads came from.
+        Frag f0, f1;
+        SRaw sr;
+        SOp as1;
+        auto wait_stage = [&]() {
+            if (XS && wid_u == 0)  // wave 0 also loads each stage's A scales
+                wait_vmcnt_lds0<(NS - 2) * (LPS + 1)>();
+            else
+                wait_vmcnt_lds0<(NS - 2) * LPS>();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // stage 0: its first slice, then the second slice's reads
+        wait_stage();
+        if constexpr (XS) issue_scales(NS - 1, NS - 1);
+        read_sraw(0, sr);
+        read_half(0, 0, f0);
+        {
+            SOp as0;
+            scale_op(sr, 0, 0, as0);
+            mfma_half(f0, as0, 0, 0, NS - 1, NS - 1);
+        }
 #pragma unroll
-        for (int j = 0; j < NS; j++) {
-            if (kt + j < KT) {
-                if (XS && wid_u == 0)  // wave 0 also loads each stage's A or group scales
-                    wait_vmcnt<(NS - 2) * (LPS + 1)>();
-                else
-                    wait_vmcnt<(NS - 2) * LPS>();
-                __builtin_amdgcn_s_barrier();
-                __builtin_amdgcn_sched_barrier(0);
-                if constexpr (XS) issue_scales(kt + j + NS - 1, (j + NS - 1) % NS);
-                compute(j, kt + j, kt + j + NS - 1, (j + NS - 1) % NS);
-                __builtin_amdgcn_sched_barrier(0);
+        for (int n = TN * TM; n < LPS; n++) piece(n, NS - 1, NS - 1);
+        read_half(0, 1, f1);
+        scale_op(sr, 1, 0, as1);
+        __builtin_amdgcn_sched_barrier(0);
+        // stage kt (kt = 1 mod NS at the top): slot (kt + j) % NS, the loads
+        // of stage kt + j + NS - 1 into slot j
+        for (int kt = 1; kt < KT; kt += NS) {
+#pragma unroll
+            for (int j = 0; j < NS; j++) {
+                if (kt + j < KT) {
+                    const int buf = (1 + j) % NS;
+                    wait_stage();
+                    if constexpr (XS) issue_scales(kt + j + NS - 1, j);
+                    read_sraw(buf, sr);
+                    read_half(buf, 0, f0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mfma_half(f1, as1, 1, 0, kt + j + NS - 1, j);  // stage kt + j - 1, second slice
+                    SOp as0;
+                    scale_op(sr, 0, kt + j, as0);
+                    mfma_half(f0, as0, 0, TN * TM, kt + j + NS - 1, j);
+                    read_half(buf, 1, f1);
+                    scale_op(sr, 1, kt + j, as1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        mfma_half(f1, as1, 1, 0, -1, 0);
+    } else {
+        for (int kt = 0; kt < KT; kt += NS) {
+#pragma unroll
+            for (int j = 0; j < NS; j++) {
+                if (kt + j < KT) {
+                    if (XS && wid_u == 0)  // wave 0 also loads each stage's A or group scales
+                        wait_vmcnt<(NS - 2) * (LPS + 1)>();
+                    else
+                        wait_vmcnt<(NS - 2) * LPS>();
+                    __builtin_amdgcn_s_barrier();
+                    __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (XS) issue_scales(kt + j + NS - 1, (j + NS - 1) % NS);
+                    compute(j, kt + j, kt + j + NS - 1, (j + NS - 1) % NS);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     }
