@@ -356,6 +356,9 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="run the chunk's GEMMs --steps times on pre-quantized activations and the counter "
                          "calibration kernel, then exit (the workload of the rocprofv3 summaries in profiles/)")
+    ap.add_argument("--data-probe", action="store_true",
+                    help="time the chunk's GEMMs (as --gemm-only) on the random activations, then on all-zero "
+                         "activations, print one JSON line, exit: the matrix cores' data-dependent power draw")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the linear path shards over token rows with no exchange, "
@@ -489,6 +492,24 @@ def main():
             fn()
         be.sync()
         return (time.perf_counter() - t0) * 1e3 / steps
+
+    if args.data_probe:
+        # The same launches, shapes and weights; only the activation values
+        # differ (zeros quantize to zero codes with scale 1).  FFN down's MX
+        # input is what FFN up writes: GELU(bias) when its input is zero.
+        ms_rand = timed(gemm_step, args.steps, args.warmup)
+        for _, rows, _, k, _, src in per_token:
+            be.fill_normal(acts[src], 1, 0.0)
+            be.quantize_act(acts[src], 0, rows, xq[src])
+        be.sync()
+        ms_zero = timed(gemm_step, args.steps, args.warmup)
+        log(f"bench: --data-probe: random {ms_rand:.2f} ms, zero {ms_zero:.2f} ms per chunk of GEMMs")
+        print(json.dumps({"data_probe": "the chunk's 724 GEMM launches, random vs all-zero activations",
+                          "ms_random": round(ms_rand, 3), "ms_zero": round(ms_zero, 3),
+                          "tflops_random": round(step_flops / ms_rand / 1e9, 1),
+                          "tflops_zero": round(step_flops / ms_zero / 1e9, 1),
+                          "ratio": round(ms_rand / ms_zero, 3), "steps": args.steps}))
+        return
 
     # ---- eager, then one replayed graph per chunk --------------------------------
     ms_eager = timed(step, args.steps, args.warmup)
