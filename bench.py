@@ -706,6 +706,14 @@ def main():
                   "pct_hbm": round(100.0 * hs_bytes / (hs_us * 1e-6) / 1e9 / HBM_GBS, 1)}
     log(f"bench: head_split {hs_us:.1f} us ({head_split['hbm_gbs']} GB/s)")
 
+    def region_us(name, fn, n):
+        be.sync()
+        be.profile_region(name, True)
+        for _ in range(n):
+            fn()
+        be.profile_region(name, False)
+        return be.profile_kernel(name)[1] * 1e3 / n
+
     # ---- causal attention at the chunk's shape (not part of the linear metric) ----
     # 12 heads x 128, the 3-frame chunk's 4680 queries against one cached
     # 1560-token frame plus the chunk (6240 keys), frame-causal MemRoPE-style
@@ -734,8 +742,25 @@ def main():
             "pct_bf16_peak": round(4.0 * hd * pairs / (attn_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS * 100, 1),
             "kernel": "k_attn_mfma (bf16 MFMA, online softmax)"}
     log(f"bench: causal attention {attn_us:.1f} us ({attn['tflops_allowed_pairs']} TFLOP/s over allowed pairs)")
+    # attention -> O linear (layer 0's weights): the bf16 hand-off (the linear
+    # quantizes per token first) against the MX e4m3 hand-off written by the
+    # attention epilogue
+    amx = be.alloc_mx(M, heads * hd)
+    ow, ob = layers[0]["o"]
+
+    def attn_o(dst):
+        def run():
+            be.causal_attention(aq, ak, av, heads, M, sk, hd, am, dst)
+            be.linear(dst, 0, M, ow, ob, 0, outs["o"], 0)
+        return run
+
+    attn_o(amx)()
+    ao16_us = region_us("attn_o16", attn_o(aout), 10)
+    aomx_us = region_us("attn_omx", attn_o(amx), 10)
+    attn["attention_then_o_linear_us"] = {"bf16_handoff": round(ao16_us, 2), "mx_handoff": round(aomx_us, 2)}
+    log(f"bench: attention + O linear: bf16 hand-off {ao16_us:.1f} us, MX hand-off {aomx_us:.1f} us")
     am.free()
-    for bb in (aq, ak, av, aout):
+    for bb in (aq, ak, av, aout, amx):
         bb.free()
 
     # ---- KV cache at steady state (not part of the linear metric) ----
@@ -769,14 +794,6 @@ def main():
     qb_, ob_ = be.alloc(heads * rows * hd), be.alloc(rows * heads * hd)
     be.fill_normal(qb_, 1702, 1.0)
     kvc.attention(qb_, rows, km, ob_)
-
-    def region_us(name, fn, n):
-        be.sync()
-        be.profile_region(name, True)
-        for _ in range(n):
-            fn()
-        be.profile_region(name, False)
-        return be.profile_kernel(name)[1] * 1e3 / n
 
     kv_attn_us = region_us("kv_attn", lambda: kvc.attention(qb_, rows, km, ob_), 10)
     put_us = region_us("kv_put", lambda: (kvc.put(kb_, vb_, rows, temporal[5]), kvc.memrope_update(cfg, frame)), 10)

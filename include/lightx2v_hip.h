@@ -279,7 +279,14 @@ int lx2v_hip_head_split(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
  * (cpu/src/lib.rs:171-203) on the same f32 inputs, rel-L2 about 3e-3 and
  * max-abs about 5e-3 of the output's range (measured on gfx950 for sk 64 ..
  * 2048).  Other head_dim up to 256 run on a per-query kernel in f32
- * (rel-L2 <= 1e-5). */
+ * (rel-L2 <= 1e-5).
+ * out may also be an MXE4M3 buffer (lx2v_hip_alloc_mx, cols == heads *
+ * head_dim, rows >= sq; head_dim 64 or 128): the epilogue then writes the
+ * MX quantization (lx2v_hip_alloc_mx's rule) of the f32 output, the
+ * attention-O linear's input without a quantization pass (no reference
+ * counterpart: the reference's attention writes f32); a query with no
+ * allowed key keeps NaN codes.  Every entry point
+ * below that takes `out` accepts it the same way. */
 int lx2v_hip_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k,
                        const lx2v_hip_buf *v, size_t heads, size_t sq, size_t sk, size_t head_dim,
                        lx2v_hip_buf *out);

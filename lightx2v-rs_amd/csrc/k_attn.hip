@@ -51,7 +51,8 @@ template <int D, int DT, int ODT>
 __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, const void *__restrict__ K,
                                                   const void *__restrict__ V, int heads, int sq, int sk, int kvs,
                                                   const uint8_t *__restrict__ tiles, const uint32_t *__restrict__ mbits,
-                                                  float c, void *__restrict__ out) {
+                                                  float c, void *__restrict__ out, uint8_t *__restrict__ omx,
+                                                  int omx_rows) {
     constexpr int KSTR = D * 2 + 16;   // bytes per K row in LDS (padded: conflict-free fragment reads)
     constexpr int VSTR = AK * 2 + 8;   // bytes per V^T row (one d, 64 keys; 34 words: conflict-free 8-byte reads)
     constexpr int QS = D / 16;         // 16-wide d steps of S^T
@@ -332,6 +333,33 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     // No allowed key: 0 / 0 = NaN, as the reference's softmax of all -inf;
     // no key at all (sk = 0): 0, the reference's empty sum.
     const float inv = sk == 0 ? 0.0f : 1.0f / lsum;
+    if constexpr (ODT == LX2V_DTYPE_MXE4M3) {
+        // MX e4m3 rows of heads * D columns (the input of the O linear): block
+        // b of this head is d 32 b .. 32 b + 31, split between lanes l and l
+        // + 32 (d 32 b + 8 g + 4 hf + 0..3); the pair's amax gives the block's
+        // scale 2^k, codes = RNE e4m3 of v 2^-k (NaN stays NaN: no clamp is
+        // needed once |v| 2^-k <= 448), the scale byte goes to the scale
+        // array (mx_sidx, omx_rows rows per 128-column group).
+        const size_t row0 = (size_t)q * heads * D + (size_t)head * D;
+#pragma unroll
+        for (int b = 0; b < DB; b++) {
+            float v[16];
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                v[i] = o[b][i] * inv;
+                amax = fmaxf(amax, fabsf(v[i]));
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            const int k = mx_exponent(amax);
+            const float minv = mx_inv(k);
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(uint32_t *)((uint8_t *)out + row0 + 32 * b + 8 * g + 4 * hf) = quant4_nc(v + 4 * g, minv);
+            if (hf == 0) omx[mx_sidx(q, (head * D + 32 * b) / 32, omx_rows)] = (uint8_t)(k + 127);
+        }
+        return;
+    }
 #pragma unroll
     for (int b = 0; b < DB; b++)
 #pragma unroll
@@ -507,13 +535,17 @@ __global__ __launch_bounds__(AT) void k_mask_temporal_tiles(const uint64_t *__re
 
 template <int D, int DT>
 void attn_mfma_od(hipStream_t s, dim3 grid, const void *q, const void *k, const void *v, int heads, int sq, int sk,
-                  int kvs, const uint8_t *tiles, const uint32_t *mask, float c, void *out, int odt) {
+                  int kvs, const uint8_t *tiles, const uint32_t *mask, float c, void *out, int odt, uint8_t *omx,
+                  int omx_rows) {
     if (odt == LX2V_DTYPE_BF16)
         hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_BF16>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
-                           tiles, mask, c, out);
+                           tiles, mask, c, out, omx, omx_rows);
+    else if (odt == LX2V_DTYPE_MXE4M3)
+        hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_MXE4M3>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
+                           tiles, mask, c, out, omx, omx_rows);
     else
         hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_F32>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
-                           tiles, mask, c, out);
+                           tiles, mask, c, out, omx, omx_rows);
 }
 
 }  // namespace
@@ -557,7 +589,7 @@ void launch_mask_pack(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, 
 
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
                       size_t sk, size_t kvs, size_t d, const uint8_t *mask, const uint32_t *mbits,
-                      const uint8_t *tiles, void *out, int odt) {
+                      const uint8_t *tiles, void *out, int odt, uint8_t *omx, size_t omx_rows) {
     if (heads == 0 || sq == 0) return;
     const float c = 1.4426950408889634f / sqrtf((float)d);  // log2(e) / sqrt(d): softmax in base 2
     if (attention_mfma_supported(d)) {
@@ -566,14 +598,14 @@ void launch_attention(hipStream_t s, const void *q, const void *k, const void *v
         const int hq = (int)heads, iq = (int)sq, ik = (int)sk, is = (int)kvs;
         if (d == 128) {
             if (dt == LX2V_DTYPE_BF16)
-                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt);
+                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx, (int)omx_rows);
             else
-                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt);
+                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx, (int)omx_rows);
         } else {
             if (dt == LX2V_DTYPE_BF16)
-                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt);
+                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx, (int)omx_rows);
             else
-                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt);
+                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx, (int)omx_rows);
         }
         return;
     }

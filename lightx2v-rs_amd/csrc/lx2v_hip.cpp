@@ -1060,8 +1060,13 @@ static int attn_check(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_b
     NEED(k, "k");
     NEED(v, "v");
     NEED(out, "out");
-    if (q->quantized() || k->quantized() || v->quantized() || out->quantized())
-        return fail(LX2V_ERR_BAD_ARG, "attention reads and writes F32 or BF16 buffers");
+    if (q->quantized() || k->quantized() || v->quantized() || out->dtype == LX2V_DTYPE_E4M3)
+        return fail(LX2V_ERR_BAD_ARG, "attention reads F32 or BF16 buffers and writes F32, BF16 or MXE4M3 ones");
+    if (out->dtype == LX2V_DTYPE_MXE4M3 && (!attention_mfma_supported(d) || out->cols != heads * d || out->rows < sq))
+        return fail(LX2V_ERR_BAD_SHAPE,
+                    "attention: MXE4M3 output needs head_dim 64 or 128 and a [>= sq, heads * head_dim] buffer "
+                    "(head_dim %zu; buffer %zu x %zu; sq %zu, %zu heads)",
+                    d, out->rows, out->cols, sq, heads);
     if (q->dtype != k->dtype || q->dtype != v->dtype) return fail(LX2V_ERR_BAD_ARG, "attention: q, k, v differ in dtype");
     if (d == 0 || d > 256) return fail(LX2V_ERR_UNSUPPORTED, "attention: head_dim %zu (1..256)", d);
     if (sq >= (1u << 30) || sk >= (1u << 30) || heads >= (1u << 16))
@@ -1085,7 +1090,7 @@ static int attn_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf
     return run(ctx, mask ? "causal_attention" : "attention", [&] {
         launch_attention(ctx->stream, q->ptr, k->ptr, v->ptr, q->dtype, heads, sq, sk, sk, d,
                          mask ? mask->bytes : nullptr, mask ? mask->bits : nullptr, mask ? mask->tiles : nullptr,
-                         out->ptr, out->dtype);
+                         out->ptr, out->dtype, out->mxs, out->srows);
     });
 }
 
@@ -1604,7 +1609,8 @@ int lx2v_hip_kv_cache_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const 
     const lx2v_hip_mask *m = mask && sq * sk ? mask : nullptr;
     return run(ctx, m ? "causal_attention" : "attention", [&] {
         launch_attention(ctx->stream, q->ptr, kb.ptr, vb.ptr, q->dtype, heads, sq, sk, kv->cap, head_dim,
-                         m ? m->bytes : nullptr, m ? m->bits : nullptr, m ? m->tiles : nullptr, out->ptr, out->dtype);
+                         m ? m->bytes : nullptr, m ? m->bits : nullptr, m ? m->tiles : nullptr, out->ptr, out->dtype,
+                         out->mxs, out->srows);
     });
 }
 

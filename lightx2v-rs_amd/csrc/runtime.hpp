@@ -211,7 +211,7 @@ void launch_mask_temporal(hipStream_t s, const uint64_t *tq, size_t sq, const ui
                           uint32_t *bits, uint8_t *tiles);
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
                       size_t sk, size_t kvs, size_t d, const uint8_t *mask, const uint32_t *mbits,
-                      const uint8_t *tiles, void *out, int odt);
+                      const uint8_t *tiles, void *out, int odt, uint8_t *omx = nullptr, size_t omx_rows = 0);
 
 // ---- KV cache (k_kv.hip) ---------------------------------------------------------
 // [heads, rows, d] from src (head stride sstride rows, first row srow0) to dst

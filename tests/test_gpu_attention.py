@@ -168,6 +168,68 @@ def test_attention_wan_shape_sampled(be):
     assert_close(got[rows], want, *MFMA_TOL, what="wan shape")
 
 
+@pytest.mark.parametrize("heads,sq,sk,d,frame", [(2, 300, 257, 128, 0), (3, 200, 320, 64, 0), (2, 520, 780, 128, 260),
+                                                (12, 1560, 3120, 128, 1560)])
+def test_attention_mx_out_is_quantized_f32_out(be, heads, sq, sk, d, frame):
+    """out (MXE4M3) == quantize_mx(out (F32)) of the same attention: the
+    epilogue quantizes the values the F32 output holds, so codes and scales
+    agree bit for bit; a fully masked row (NaN, as the reference) keeps NaN
+    codes."""
+    q, k, v = _qkv(8000 + sq, heads, sq, sk, d)
+    mask = _frame_causal(sq, sk, frame) if frame else None
+    if mask is not None:
+        mask[7] = False  # no allowed key: NaN
+    qb, kb, vb = _up(be, q, H.DTYPE_BF16), _up(be, k, H.DTYPE_BF16), _up(be, v, H.DTYPE_BF16)
+    m = be.mask_upload(mask, sq, sk) if mask is not None else None
+
+    def attend(out):
+        if m is None:
+            be.attention(qb, kb, vb, heads, sq, sk, d, out)
+        else:
+            be.causal_attention(qb, kb, vb, heads, sq, sk, d, m, out)
+
+    of = be.alloc(sq * heads * d, H.DTYPE_F32)
+    attend(of)
+    om = be.alloc_mx(sq + 3, heads * d)
+    attend(om)
+    ref = be.alloc_mx(sq, heads * d)
+    be.quantize_mx(of, 0, sq, ref)
+    q1, s1 = be.download_mx(om, sq + 3, heads * d)
+    q2, s2 = be.download_mx(ref, sq, heads * d)
+    ok = np.ones(sq, bool)
+    if m is not None:
+        m.free()
+        assert np.isnan(be.download(of).reshape(sq, heads * d)[7]).all()
+        # NaN stays NaN (quantize_mx clamps it to -448): e4m3 NaN is s.1111.111
+        assert ((q1[7] & 0x7F) == 0x7F).all()
+        ok[7] = False
+    assert np.array_equal(q1[:sq][ok], q2[ok]) and np.array_equal(s1[:, :sq][:, ok], s2[:, ok])
+
+
+def test_attention_mx_out_feeds_o_linear(be):
+    """attention -> MXE4M3 -> FP8 linear against attention -> BF16 -> FP8
+    linear (per-token e4m3 inside the linear), both against the f32 chain
+    of the oracle: the MX hand-off is no less accurate."""
+    heads, sq, sk, d, n = 4, 300, 400, 128, 256
+    q, k, v = _qkv(8100, heads, sq, sk, d)
+    qb, kb, vb = _up(be, q, H.DTYPE_BF16), _up(be, k, H.DTYPE_BF16), _up(be, v, H.DTYPE_BF16)
+    wq, ws = O.fp8_quantize((O.Rng(8101).normal(n * heads * d) * np.float32(0.02)).reshape(n, heads * d), n,
+                            heads * d, heads * d, True)
+    w = be.weight_fp8(wq, ws, n, heads * d, heads * d)
+    a16 = be.alloc(sq * heads * d, H.DTYPE_BF16)
+    be.attention(qb, kb, vb, heads, sq, sk, d, a16)
+    amx = be.alloc_mx(sq, heads * d)
+    be.attention(qb, kb, vb, heads, sq, sk, d, amx)
+    y16, ymx = be.alloc(sq * n), be.alloc(sq * n)
+    be.linear(a16, 0, sq, w, None, H.ACT_NONE, y16, 0)
+    be.linear(amx, 0, sq, w, None, H.ACT_NONE, ymx, 0)
+    a = _want(q, k, v).reshape(sq, heads * d)
+    want = a @ O.fp8_dequantize(wq, ws, n, heads * d, heads * d).reshape(n, heads * d).T
+    err16 = np.linalg.norm(be.download(y16).reshape(sq, n) - want) / np.linalg.norm(want)
+    errmx = np.linalg.norm(be.download(ymx).reshape(sq, n) - want) / np.linalg.norm(want)
+    assert errmx <= max(1.1 * err16, 1e-2), (errmx, err16)
+
+
 def test_attention_errors(be):
     heads, sq, sk, d = 1, 8, 8, 64
     q, k, v = _qkv(7000, heads, sq, sk, d)
@@ -182,6 +244,12 @@ def test_attention_errors(be):
         be.attention(qb, kb, vb, heads, sq, sk, d, qb)
     with pytest.raises(H.HipError):  # head_dim past 256
         be.attention(qb, kb, vb, 1, 1, 1, 300, out)
+    with pytest.raises(H.HipError):  # MX output of another width
+        be.attention(qb, kb, vb, heads, sq, sk, d, be.alloc_mx(sq, 2 * d))
+    with pytest.raises(H.HipError):  # MX output with a head_dim off the MFMA path
+        be.attention(qb, kb, vb, 2, sq, sk // 2, 32, be.alloc_mx(sq, 64))
+    with pytest.raises(H.HipError):  # per-token E4M3 output
+        be.attention(qb, kb, vb, heads, sq, sk, d, be.alloc_e4m3(sq, d))
     m = be.mask_upload(np.ones((sq, sk), bool), sq, sk)
     with pytest.raises(H.HipError):  # resident mask of another shape
         be.causal_attention(qb, kb, vb, heads, sq - 1, sk, d, m, out)
