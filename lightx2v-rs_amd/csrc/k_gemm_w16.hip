@@ -338,6 +338,9 @@ void launch_tile(hipStream_t s, const void *x, int x_dtype, const lx2v_hip_weigh
 //   slot kt - 1 used; MFMAs.
 
 constexpr int BKE = 64;        // K elements per stage
+// Q4 with every zero 8 (lx2v_hip_weight::zero8): the same codes and scales,
+// no zeros loaded (a format id of this file only)
+constexpr int kWfmtQ4Sym = 100;
 constexpr int XRB = BKE * 2;   // bytes per LDS tile row (bf16)
 
 // 16 consecutive K elements of one weight row, as 8 packed bf16 pairs
@@ -361,6 +364,21 @@ __device__ __forceinline__ void unit_dequant(u32x4 c, float s, float z, uint32_t
             o[2 * q] = pack_bf16x2(f0, f1);
             o[2 * q + 1] = pack_bf16x2(f2, f3);
         }
+    } else if constexpr (WF == kWfmtQ4Sym) {
+        // zero 8: (c - 8) s is exact before its one rounding, and so is
+        // fma(c, s, -8 s) (8 s is exact): the same f32 value
+        const float nb = -8.0f * s;
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const uint32_t lo = w[q] & 0x0F0F0F0Fu, hi = (w[q] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float e0 = __builtin_fmaf((float)((lo >> (8 * b)) & 0xFFu), s, nb);
+                const float e1 = __builtin_fmaf((float)((hi >> (8 * b)) & 0xFFu), s, nb);
+                o[4 * q + b] = pack_bf16x2(e0, e1);
+            }
+        }
+        (void)z;
     } else if constexpr (WF == LX2V_WFMT_Q4) {
         // element 2i in the low nibble of byte i (quant.rs:305-311)
 #pragma unroll
@@ -404,15 +422,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
                                                                  int act, int tiles_m, int tiles_n) {
     constexpr int NW = WGM * WGN, NT = 64 * NW;
     constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
-    constexpr bool Q4 = WF == LX2V_WFMT_Q4;
+    constexpr bool Q4 = WF == LX2V_WFMT_Q4 || WF == kWfmtQ4Sym;
+    constexpr bool ZL = WF == LX2V_WFMT_Q4;  // zeros loaded with the scales
     constexpr int DEN = Q4 ? 2 : 1;          // elements per code byte
     constexpr int CBS = BKE / DEN;           // code bytes per weight row per stage
     constexpr int XS = BM * XRB;             // activation slot
     constexpr int CS = BN * CBS;             // code slot
     constexpr int SS = BN * 16;              // scale (zero) slot: up to 4 per row
     constexpr int WSL = BN * XRB;            // bf16 weight slot
-    constexpr int RING = XS + CS + SS * (Q4 ? 2 : 1);  // one stage of every ring
-    constexpr int XJ = XS / 1024, CJ = CS / 1024, SJ = SS / 1024, ZJ = Q4 ? SJ : 0;
+    constexpr int RING = XS + CS + SS * (ZL ? 2 : 1);  // one stage of every ring
+    constexpr int XJ = XS / 1024, CJ = CS / 1024, SJ = SS / 1024, ZJ = ZL ? SJ : 0;
     constexpr int ALD = XJ / NW;             // activation loads per wave per stage
     constexpr int EJ = CJ + SJ + ZJ;         // weight loads per stage, spread over the waves
     constexpr int EPW = (EJ + NW - 1) / NW;  // ... at most this many per wave
@@ -428,7 +447,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
     uint8_t *const xr = smem;                      // NS activation slots
     uint8_t *const cr = smem + NS * XS;            // NS code slots
     uint8_t *const sr = cr + NS * CS;              // NS scale slots
-    uint8_t *const zr = sr + NS * SS;              // NS zero slots (Q4)
+    uint8_t *const zr = sr + NS * SS;              // NS zero slots (Q4 with zeros)
     uint8_t *const wr = smem + NS * RING;          // 2 bf16 weight slots
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -448,7 +467,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
     const auto rx = make_rsrc(X + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K * 2u);
     const auto rw = make_rsrc(Wc + (size_t)n0 * cbrow, (uint32_t)(N - n0) * cbrow);
     const auto rs = make_rsrc(Wss, (uint32_t)KT * sstage);
-    const auto rz = make_rsrc(Q4 ? Wsz : Wss, Q4 ? (uint32_t)KT * sstage : 0u);
+    const auto rz = make_rsrc(ZL ? Wsz : Wss, ZL ? (uint32_t)KT * sstage : 0u);
 
     // Activation load i of this wave: tile rows [(i NW + wid) 8, +8), lane l
     // fills slot l % 8 of row l / 8.
@@ -518,7 +537,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
             }
             const uint32_t si = row * (uint32_t)spr + ((k16 * (uint32_t)spr) >> 2);
             uint32_t o[8];
-            unit_dequant<WF>(c, ss[si], Q4 ? zs[si] : 0.0f, o);
+            unit_dequant<WF>(c, ss[si], ZL ? zs[si] : 0.0f, o);
             const uint32_t cc = k16 * 2u;
             *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc) << 4)) & (WSL - 1))) = (u32x4){o[0], o[1], o[2], o[3]};
             *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc + 1) << 4)) & (WSL - 1))) =
@@ -638,7 +657,10 @@ void launch_dma_cfg(hipStream_t s, const uint16_t *x, const lx2v_hip_weight *w, 
             launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q8>(s, x, w, bias, act, y, y_dtype, M);
             break;
         case LX2V_WFMT_Q4:
-            launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q4>(s, x, w, bias, act, y, y_dtype, M);
+            if (w->zero8)
+                launch_dma_fmt<BM, BN, WGM, WGN, NS, kWfmtQ4Sym>(s, x, w, bias, act, y, y_dtype, M);
+            else
+                launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q4>(s, x, w, bias, act, y, y_dtype, M);
             break;
         default:
             launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_FP8>(s, x, w, bias, act, y, y_dtype, M);

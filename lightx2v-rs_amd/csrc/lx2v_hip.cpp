@@ -582,6 +582,7 @@ int lx2v_hip_weight_q4(lx2v_hip_ctx *ctx, const uint8_t *codes, int packed, cons
         return rc;
     }
     w->device_bytes = np + 2 * ns * 4;
+    w->zero8 = std::all_of(zeros, zeros + ns, [](float z) { return z == 8.0f; });
     if (int rc2 = stage_scales(ctx, w)) {
         free_weight(w);
         return rc2;
@@ -747,6 +748,7 @@ int lx2v_hip_quantize_q4_sym(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t 
         free_weight(w);
         return rc;
     }
+    w->zero8 = true;  // k_quantize_q4_sym's zeros
     if (int rc2 = stage_scales(ctx, w)) {
         free_weight(w);
         return rc2;

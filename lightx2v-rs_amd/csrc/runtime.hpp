@@ -44,6 +44,10 @@ struct lx2v_hip_weight {
     void *codes = nullptr;    // f32 [rows*cols] | i8 [rows*cols] | packed u8 [rows*cols/2] | e4m3 [rows*cols]
     float *scales = nullptr;  // [rows * cols/group]
     float *zeros = nullptr;   // Q4 only
+    // Q4 only: every zero is 8 (the symmetric codes, quant.rs's packing of
+    // q + 8): the bf16 GEMM then dequantizes (c - 8) s as fma(c, s, -8 s),
+    // the same f32 value, and loads no zeros.
+    bool zero8 = false;
     uint8_t *raw_e4m3 = nullptr;  // FP8: codes exactly as passed in (for the dequant hook), only
                                   // kept when canonicalization changed a code
     size_t device_bytes = 0;

@@ -269,6 +269,29 @@ def test_q4_vs_oracle(be, M, K, N, group, hqq, xdt):
     assert_close(y, O.linear(x, wd, b, 0, nthreads=8), 5e-3, 0.05, what="q4 vs f32 oracle")
 
 
+@pytest.mark.parametrize("M,K,N", [(300, 1536, 512), (1000, 8960, 1536)])
+def test_q4_zero8_path_equals_affine_path(be, M, K, N):
+    """Symmetric Q4 (every zero 8) dequantizes as fma(c, s, -8 s) without
+    loading zeros; the same dequantized weights through the affine path
+    (one group re-expressed as codes c - 1 with zero 7, which decode to the
+    same values) give the same output, bit for bit."""
+    x = normal(40 + M, M * K).reshape(M, K)
+    _, c, s, z = q4_sym_weight(41 + N, N, K, 32)
+    assert (z == 8.0).all()
+    g = int(np.flatnonzero((c.reshape(-1, 32) >= 1).all(axis=1))[0])  # a group with no code 0
+    c2, z2 = c.reshape(-1, 32).copy(), z.reshape(-1).copy()
+    c2[g] -= 1
+    z2[g] = 7.0
+    c2 = c2.reshape(c.shape)
+    assert np.array_equal(O.q4_dequantize(c2, s, z2.reshape(z.shape), N, K, 32), O.q4_dequantize(c, s, z, N, K, 32))
+    b = normal(42, N, 0.01)
+    w_sym = be.weight_q4(O.q4_pack(c), s, z, N, K, 32, packed=True)
+    w_aff = be.weight_q4(O.q4_pack(c2), s, z2.reshape(z.shape), N, K, 32, packed=True)
+    y1 = run_linear(be, x, w_sym, b, H.ACT_NONE, x_dtype=H.DTYPE_BF16)
+    y2 = run_linear(be, x, w_aff, b, H.ACT_NONE, x_dtype=H.DTYPE_BF16)
+    assert np.array_equal(u32(y1), u32(y2))
+
+
 # ---- shapes the MFMA kernels do not tile: the generic kernel ----------------------------
 
 @pytest.mark.parametrize("fmt", ["f32", "q8", "q4", "fp8"])
