@@ -520,29 +520,49 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
         for (int n = 0; n < ALD + EPW; n++) piece(n, kt, slot_x, slot_w);
     };
     // Weight stage kt from its code / scale slot into bf16 weight slot `ws`.
-    auto dequant = [&](int slot_w, int ws) {
+    // ... in three parts, so that a stage can spread them between its MFMAs:
+    // the codes and scales into registers, the conversion, the bf16 stores.
+    u32x4 dqc[UPT];
+    float dqs[UPT], dqz[UPT];
+    uint32_t dqo[UPT][8];
+    auto dq_load = [&](int slot_w) {
         const uint8_t *cs = cr + slot_w * CS;
         const float *ss = (const float *)(sr + slot_w * SS);
         const float *zs = (const float *)(zr + slot_w * SS);
+#pragma unroll
+        for (int u = 0; u < UPT; u++) {
+            const uint32_t id = (uint32_t)(u * NT + tid), row = id / 4u, k16 = id % 4u;
+            if constexpr (Q4) {
+                const u32x2 h = *(const u32x2 *)(cs + row * CBS + k16 * 8u);
+                dqc[u] = (u32x4){h.x, h.y, 0u, 0u};
+            } else {
+                dqc[u] = *(const u32x4 *)(cs + row * CBS + k16 * 16u);
+            }
+            const uint32_t si = row * (uint32_t)spr + ((k16 * (uint32_t)spr) >> 2);
+            dqs[u] = ss[si];
+            dqz[u] = ZL ? zs[si] : 0.0f;
+        }
+    };
+    auto dq_math = [&]() {
+#pragma unroll
+        for (int u = 0; u < UPT; u++) unit_dequant<WF>(dqc[u], dqs[u], dqz[u], dqo[u]);
+    };
+    auto dq_store = [&](int ws) {
         uint8_t *d = wr + ws * WSL;
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const uint32_t id = (uint32_t)(u * NT + tid), row = id / 4u, k16 = id % 4u;
-            u32x4 c;
-            if constexpr (Q4) {
-                const u32x2 h = *(const u32x2 *)(cs + row * CBS + k16 * 8u);
-                c = (u32x4){h.x, h.y, 0u, 0u};
-            } else {
-                c = *(const u32x4 *)(cs + row * CBS + k16 * 16u);
-            }
-            const uint32_t si = row * (uint32_t)spr + ((k16 * (uint32_t)spr) >> 2);
-            uint32_t o[8];
-            unit_dequant<WF>(c, ss[si], ZL ? zs[si] : 0.0f, o);
             const uint32_t cc = k16 * 2u;
-            *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc) << 4)) & (WSL - 1))) = (u32x4){o[0], o[1], o[2], o[3]};
+            *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc) << 4)) & (WSL - 1))) =
+                (u32x4){dqo[u][0], dqo[u][1], dqo[u][2], dqo[u][3]};
             *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc + 1) << 4)) & (WSL - 1))) =
-                (u32x4){o[4], o[5], o[6], o[7]};
+                (u32x4){dqo[u][4], dqo[u][5], dqo[u][6], dqo[u][7]};
         }
+    };
+    auto dequant = [&](int slot_w, int ws) {
+        dq_load(slot_w);
+        dq_math();
+        dq_store(ws);
     };
 
     f32x16 acc[TN][TM];
@@ -586,8 +606,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
         // of X(kt + NS - 1) (into the slot X(kt - 1) used) and weight stage
         // kt + NS (into the slot of stage kt, dequantized in stage kt - 1):
         // issued back to back, the loads held both waves of a SIMD off the
-        // MFMA pipe.  Then the dequantization of weight stage kt + 1, whose
-        // VALU work can run under the MFMAs.
+        // MFMA pipe.  The dequantization of weight stage kt + 1 (its codes
+        // landed before this stage's barrier) goes between later MFMAs: the
+        // reads after MFMA DQL, the conversion after DQM (the reads have
+        // had the MFMAs between to return), the stores after DQS.
+        constexpr int NMF = 4 * TN * TM, DQL = NMF / 4, DQM = NMF / 2, DQS = 3 * NMF / 4;
+        static_assert(ALD + EPW <= NMF, "a stage's loads interleave with its MFMAs");
 #pragma unroll
         for (int kk = 0; kk < 4; kk++)
 #pragma unroll
@@ -603,10 +627,23 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
                         piece(n, kt + NS - 1, (j + NS - 1) % NS, j % NS);
                         __builtin_amdgcn_sched_barrier(0);
                     }
+                    if (n == DQL) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        dq_load((j + 1) % NS);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    if (n == DQM) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        dq_math();
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    if (n == DQS) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        dq_store((j + 1) & 1);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
-        dequant((j + 1) % NS, (j + 1) & 1);
     };
-    static_assert(4 * TN * TM >= ALD + EPW, "a stage's loads interleave with its MFMAs");
 
     // Prologue: weight stage 0 alone, then as stages -NS+1 .. -1 would:
     // X(s) and weight stage s + 1 for s = 0 .. NS - 2; wait for weight
