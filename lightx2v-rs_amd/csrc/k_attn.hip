@@ -54,7 +54,9 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                                                   float c, void *__restrict__ out, uint8_t *__restrict__ omx,
                                                   int omx_rows) {
     constexpr int KSTR = D * 2 + 16;   // bytes per K row in LDS (padded: conflict-free fragment reads)
-    constexpr int VSTR = AK * 2 + 8;   // bytes per V^T row (one d, 64 keys; 34 words: conflict-free 8-byte reads)
+    // bytes per V^T row (one d, 64 keys): 9 16-byte chunks, so the 16-byte
+    // fragment reads of 16 consecutive rows fall in distinct bank groups
+    constexpr int VSTR = AK * 2 + 16;
     constexpr int QS = D / 16;         // 16-wide d steps of S^T
     constexpr int DB = D / 32;         // 32-row d blocks of O^T
     constexpr int KN = AK * D / 8, VN = AK * D / 16, KI = (KN + AT - 1) / AT, VI = (VN + AT - 1) / AT;
@@ -158,6 +160,10 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
             if (idx < KN) *(u32x4 *)(ks + key * KSTR + ch * 16) = kr[it];
         }
     };
+    // V^T key order: bits 2 and 3 of the key swapped, so that the 8 keys a
+    // lane feeds one 16-key MFMA step (4 of group g and 4 of group g + 2,
+    // the order the S^T layout leaves them in) are 16 consecutive bytes.
+    auto vpos = [](int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); };
     auto lstore_v = [&](int buf) {
         uint8_t *vt = lds + 2 * KSZ + buf * VSZ;
 #pragma unroll
@@ -170,7 +176,7 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
             for (int e = 0; e < 8; e++) {
                 const uint32_t lo = (e & 1) ? av[e / 2] >> 16 : av[e / 2] & 0xFFFFu;
                 const uint32_t hi = (e & 1) ? bv[e / 2] >> 16 : bv[e / 2] & 0xFFFFu;
-                *(uint32_t *)(vt + (8 * ch + e) * VSTR + key * 2) = lo | (hi << 16);
+                *(uint32_t *)(vt + (8 * ch + e) * VSTR + vpos(key) * 2) = lo | (hi << 16);
             }
         }
     };
@@ -290,28 +296,35 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                 for (int i = 0; i < 16; i++) o[b][i] *= alpha;
         }
 
-        // O^T += V^T P^T, four 16-key steps: step (j, t) takes registers
+        // O^T += V^T P^T, four 16-key steps: step u = 2 j + t takes registers
         // 8 t .. 8 t + 7 of sc[j], i.e. keys 32 j + 16 t + 4 hf + 0..3 and
-        // 32 j + 16 t + 8 + 4 hf + 0..3, and V^T in the same key order.
+        // 32 j + 16 t + 8 + 4 hf + 0..3, which V^T holds as the 16 bytes at
+        // key position 16 u + 8 hf (vpos).  Step u + 1's V fragments are read
+        // while step u's MFMAs run.
         const uint8_t *vt = lds + 2 * KSZ + vbi * VSZ;
+        auto vread = [&](int u, bf16x8 *vf) {
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+            for (int b = 0; b < DB; b++)
+                vf[b] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(vt + (32 * b + l32) * VSTR + (16 * u + 8 * hf) * 2));
+        };
+        bf16x8 vcur[DB], vnxt[DB];
+        vread(0, vcur);
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const f32x16 &sp = sc[j];
-                const u32x4 pw = (u32x4){pack_bf16x2(sp[8 * t + 0], sp[8 * t + 1]), pack_bf16x2(sp[8 * t + 2], sp[8 * t + 3]),
-                                         pack_bf16x2(sp[8 * t + 4], sp[8 * t + 5]), pack_bf16x2(sp[8 * t + 6], sp[8 * t + 7])};
-                const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
-                const int kk = 32 * j + 16 * t + 4 * hf;
+        for (int u = 0; u < 4; u++) {
+            if (u < 3) vread(u + 1, vnxt);
+            __builtin_amdgcn_sched_barrier(0);
+            const f32x16 &sp = sc[u >> 1];
+            const int t = u & 1;
+            const u32x4 pw = (u32x4){pack_bf16x2(sp[8 * t + 0], sp[8 * t + 1]), pack_bf16x2(sp[8 * t + 2], sp[8 * t + 3]),
+                                     pack_bf16x2(sp[8 * t + 4], sp[8 * t + 5]), pack_bf16x2(sp[8 * t + 6], sp[8 * t + 7])};
+            const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
 #pragma unroll
-                for (int b = 0; b < DB; b++) {
-                    const uint8_t *row = vt + (32 * b + l32) * VSTR;
-                    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-                    const u32x2_t lo = *(const u32x2_t *)(row + kk * 2), hi = *(const u32x2_t *)(row + (kk + 8) * 2);
-                    const bf16x8 vf = __builtin_bit_cast(bf16x8, (u32x4){lo.x, lo.y, hi.x, hi.y});
-                    o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[b], 0, 0, 0);
-                }
-            }
+            for (int b = 0; b < DB; b++) o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vcur[b], pf, o[b], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (u < 3)
+#pragma unroll
+                for (int b = 0; b < DB; b++) vcur[b] = vnxt[b];
+        }
         // K(kt) and V of the previous tile were last read before the previous
         // barrier (stores past the last tile write zeros, unused)
         lstore_k(kbi ^ 1);
