@@ -52,7 +52,7 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                                                   const void *__restrict__ V, int heads, int sq, int sk, int kvs,
                                                   const uint8_t *__restrict__ tiles, const uint32_t *__restrict__ mbits,
                                                   float c, void *__restrict__ out, uint8_t *__restrict__ omx,
-                                                  int omx_rows) {
+                                                  int omx_rows, float *__restrict__ part, int nsplit) {
     constexpr int KSTR = D * 2 + 16;   // bytes per K row in LDS (padded: conflict-free fragment reads)
     // bytes per V^T row (one d, 64 keys): 9 16-byte chunks, so the 16-byte
     // fragment reads of 16 consecutive rows fall in distinct bank groups
@@ -68,9 +68,62 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     // XCD-aware order: workgroups b, b + 8, ... run on one XCD, so give each
     // XCD a contiguous range of (head, query tile) items -- the workgroups of
     // a head then share its K / V in one L2.
+    //
+    // Split mode (nsplit = S > 1, part != null): every item is S pieces, each
+    // over about 1/S of its allowed key tiles, writing its unnormalized O^T,
+    // running max and sum to `part` for k_attn_merge -- S times the
+    // workgroups where the items alone would leave CUs idle.  An XCD's pieces
+    // are dispatched from the last query tile down (under a causal mask the
+    // tiles that see the most keys start first), an item's S pieces side by
+    // side.
     const int nqt = (sq + AQ - 1) / AQ, items = nqt * heads, per_xcd = (items + 7) / 8;
-    const int b = blockIdx.x, item = (b % 8) * per_xcd + b / 8;
-    if (item >= items) return;
+    const bool split = nsplit > 1;
+    const int b = blockIdx.x;
+    int item = -1, piece = 0;
+    if (!split) {
+        item = (b % 8) * per_xcd + b / 8;
+    } else {
+        // XCD x owns positions [lo, hi) of the heads' query tiles, position
+        // h nqt + i holding query tile (i st) mod nqt of head h: a stride
+        // near nqt / golden ratio, so that the part of a head one XCD gets
+        // mixes early and late query tiles (light and heavy under a causal
+        // mask) rather than taking a run of them.
+        const int lo = (b % 8) * per_xcd, hi = min(items, lo + per_xcd);
+        int st = (int)(0.618034f * (float)nqt + 0.5f);
+        st = st < 1 ? 1 : st;
+        auto gcd = [](int a, int c) {
+            while (c) {
+                const int t = a % c;
+                a = c;
+                c = t;
+            }
+            return a;
+        };
+        while (gcd(st, nqt) != 1) st++;
+        int r0 = nqt, r1 = st % nqt, t0 = 0, t1 = 1;  // extended Euclid: st * sinv = 1 mod nqt
+        while (r1) {
+            const int qq = r0 / r1, r2 = r0 - qq * r1, t2 = t0 - qq * t1;
+            r0 = r1;
+            r1 = r2;
+            t0 = t1;
+            t1 = t2;
+        }
+        const int sinv = ((t0 % nqt) + nqt) % nqt;
+        int r = (b / 8) / nsplit;
+        piece = (b / 8) % nsplit;
+        for (int t = nqt - 1; t >= 0 && item < 0; t--) {
+            // the heads h whose query tile t sits at a position in [lo, hi)
+            const int i = (int)(((long long)t * sinv) % nqt);
+            const int h0 = lo <= i ? 0 : (lo - i + nqt - 1) / nqt;
+            const int h1 = hi - 1 < i ? -1 : (hi - 1 - i) / nqt;
+            const int cnt = h1 >= h0 ? h1 - h0 + 1 : 0;
+            if (r < cnt)
+                item = (h0 + r) * nqt + t;
+            else
+                r -= cnt;
+        }
+    }
+    if (item < 0 || item >= items) return;
     const int head = item / nqt, qt = item % nqt, nkt = (sk + AK - 1) / AK;
     const int q = qt * AQ + wv * 32 + l32;  // this lane's query
     const bool qin = q < sq;
@@ -101,9 +154,47 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
         for (int i = tid; i < nkt; i += AT) trow[i] = tiles[(size_t)qt * nkt + i];
     __syncthreads();
     auto tstate = [&](int kt) -> int { return !tiles ? 1 : (tlds ? (int)trow[kt] : 2); };
+    // This workgroup's key tiles [klo, khi): all of them, or in split mode,
+    // of the n tiles with an allowed pair, those after the floor(p n / S)-th
+    // up to and including the floor((p + 1) n / S)-th (piece p; the last
+    // piece runs to the end).  Wave 0 counts with ballots.
+    int klo = 0, khi = nkt;
+    if (split) {
+        __shared__ int scut[2];
+        if (wv == 0) {
+            int total = 0;
+            for (int base = 0; base < nkt; base += 64) {
+                const int t = base + lane;
+                total += __popcll(__ballot(t < nkt && tstate(t) != 0));
+            }
+            // cut(c): the tile after the c-th allowed one (cut(0) = 0)
+            const int c0 = (int)((long long)piece * total / nsplit), c1 = (int)((long long)(piece + 1) * total / nsplit);
+            int cut0 = 0, cut1 = 0, acc = 0;
+            for (int base = 0; base < nkt; base += 64) {
+                const int t = base + lane;
+                const bool al = t < nkt && tstate(t) != 0;
+                const uint64_t bal = __ballot(al);
+                const int cnt = __popcll(bal);
+                const uint64_t upto = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+                const int upto_cnt = acc + __popcll(bal & upto);
+                if (c0 > acc && c0 <= acc + cnt)
+                    cut0 = base + __ffsll((long long)__ballot(al && upto_cnt == c0));
+                if (c1 > acc && c1 <= acc + cnt)
+                    cut1 = base + __ffsll((long long)__ballot(al && upto_cnt == c1));
+                acc += cnt;
+            }
+            if (lane == 0) {
+                scut[0] = cut0;
+                scut[1] = piece == nsplit - 1 ? nkt : cut1;
+            }
+        }
+        __syncthreads();
+        klo = scut[0];
+        khi = scut[1];
+    }
     // The next key tile at or after kt with an allowed pair (uniform).
     auto next_tile = [&](int kt) {
-        while (kt < nkt && tstate(kt) == 0) kt++;
+        while (kt < khi && tstate(kt) == 0) kt++;
         return kt;
     };
 
@@ -132,12 +223,12 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
 #pragma unroll
         for (int it = 0; it < KI; it++) {
             const int idx = it * AT + tid, key = idx / (D / 8), ch = idx % (D / 8);
-            kr[it] = ld8(ksrc, (k0 + key) * D + 8 * ch, idx < KN);
+            kr[it] = ld8(ksrc, (k0 + key) * D + 8 * ch, idx < KN && kt < khi);
         }
     };
     auto gload_v = [&](int kt) {
         const uint32_t k0 = (uint32_t)kt * AK;
-        const bool mixed = kt < nkt && tstate(kt) == 2 && qin;
+        const bool mixed = kt < khi && tstate(kt) == 2 && qin;
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
             mwn[kb] = buffer_load_x1(msrc, mixed ? ((uint32_t)q * nw + k0 / 32 + (uint32_t)kb) * 4 : kOob);
@@ -147,8 +238,8 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
 #pragma unroll
         for (int it = 0; it < VI; it++) {
             const int idx = it * AT + tid, key = 2 * (idx % (AK / 2)), ch = idx / (AK / 2);
-            va[it] = ld8(vsrc, (k0 + key) * D + 8 * ch, idx < VN);
-            vb[it] = ld8(vsrc, (k0 + key + 1) * D + 8 * ch, idx < VN);
+            va[it] = ld8(vsrc, (k0 + key) * D + 8 * ch, idx < VN && kt < khi);
+            vb[it] = ld8(vsrc, (k0 + key + 1) * D + 8 * ch, idx < VN && kt < khi);
         }
     };
     // Registers into LDS: K rows; V transposed (one d per row).
@@ -182,17 +273,19 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     };
     // S^T = K Q^T for the 64 keys in K buffer kb: keys 32 j + (8 g + 4 hf + r),
     // r = 0..3, in registers 4 g + r of st[j].
+    // (the two 32-key blocks' MFMA chains alternate, so that no MFMA waits
+    // for the one just before it)
     auto scores = [&](int kbuf, f32x16 *st) {
         const uint8_t *ks = lds + kbuf * KSZ;
+        st[0] = (f32x16){};
+        st[1] = (f32x16){};
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            st[j] = (f32x16){};
+        for (int s = 0; s < QS; s++)
 #pragma unroll
-            for (int s = 0; s < QS; s++) {
+            for (int j = 0; j < 2; j++) {
                 const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const u32x4 *)(ks + (32 * j + l32) * KSTR + (2 * s + hf) * 16));
                 st[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[j], 0, 0, 0);
             }
-        }
     };
 
     // Mask tile kt's scores in place: a full tile with every pair allowed is
@@ -224,11 +317,11 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     // of a SIMD work at once.  Explicit vmcnt(0) after each store: the mask
     // words were loaded before V and are complete once V is, but the
     // compiler cannot see that across the loop's back edge.
-    int kt = next_tile(0);
-    int kn = kt < nkt ? next_tile(kt + 1) : nkt;
+    int kt = next_tile(klo);
+    int kn = kt < khi ? next_tile(kt + 1) : khi;
     f32x16 sc[2];  // scores of tile kt (raw q.k)
     uint32_t mw[2] = {0u, 0u};
-    if (kt < nkt) {
+    if (kt < khi) {
         gload_k(kt);
         gload_v(kt);
         lstore_k(0);
@@ -240,26 +333,34 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    if (kt < nkt) {
+    if (kt < khi) {
         scores(0, sc);
         apply_mask(sc, kt, mw);
     }
     __syncthreads();  // K buffer 0 is rewritten at the end of the first iteration
     int kbi = 1, vbi = 0;  // K buffer holding K(kn); V buffer holding V(kt)
     const float tau = 8.0f;  // rescale O only when a query's max grows by more than 2^8
-    while (kt < nkt) {
-        const int knn = kn < nkt ? next_tile(kn + 1) : nkt;
+    while (kt < khi) {
+        const int knn = kn < khi ? next_tile(kn + 1) : khi;
         // loads for the stores at the end of this iteration (kOob when past the last tile)
         __builtin_amdgcn_sched_barrier(0);
         gload_k(knn);
         gload_v(kn);
-        __builtin_amdgcn_sched_barrier(0);
 
         // S(kn), unconditionally (past the last tile it reads a stale buffer
         // and is not used): a branch here would keep these MFMAs from being
         // interleaved with the softmax below.
         f32x16 sn[2];
         scores(kbi, sn);
+        // The loads go between the first MFMAs of S(kn): issued back to back
+        // by all eight waves they held each wave's issue for hundreds of
+        // cycles at the top of every tile.
+        constexpr int NVM = (KI + 2 * VI) * (DT == LX2V_DTYPE_BF16 ? 1 : 2) + 2;
+#pragma unroll
+        for (int i = 0; i < NVM; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a global load
+        }
 
         // tile kt's scores were masked when they were computed
         float tmax = -INFINITY;
@@ -332,7 +433,7 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         mw[0] = mwn[0];
         mw[1] = mwn[1];
-        if (kn < nkt) apply_mask(sn, kn, mw);
+        if (kn < khi) apply_mask(sn, kn, mw);
         __syncthreads();
         sc[0] = sn[0];
         sc[1] = sn[1];
@@ -343,6 +444,20 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
     }
 
     if (!qin) return;
+    if (split) {
+        // this piece's O^T (unnormalized), running max (log2 domain) and sum
+        const size_t slot = (size_t)item * nsplit + piece, row = slot * AQ + (size_t)(q - qt * AQ);
+        float *po = part + row * D;
+#pragma unroll
+        for (int b = 0; b < DB; b++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(f32x4 *)(po + 32 * b + 8 * g + 4 * hf) =
+                    (f32x4){o[b][4 * g], o[b][4 * g + 1], o[b][4 * g + 2], o[b][4 * g + 3]};
+        typedef float f32x2_t __attribute__((ext_vector_type(2)));
+        if (hf == 0) *(f32x2_t *)(part + (size_t)items * nsplit * AQ * D + row * 2) = (f32x2_t){m, lsum};
+        return;
+    }
     // No allowed key: 0 / 0 = NaN, as the reference's softmax of all -inf;
     // no key at all (sk = 0): 0, the reference's empty sum.
     const float inv = sk == 0 ? 0.0f : 1.0f / lsum;
@@ -388,6 +503,61 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
                 *(f32x4 *)((float *)out + oi) = (f32x4){v0, v1, v2, v3};
             }
         }
+}
+
+// Split mode's second pass: the S pieces of each (query, head) row
+// combined, O = sum_p O_p 2^(m_p - m) / sum_p l_p 2^(m_p - m) with m = max_p
+// m_p, stored as the one-pass kernel stores (F32 / BF16 rows, or MX e4m3 and
+// its scale bytes).  A thread per 4 consecutive d of a row, so a 32-d MX
+// block is 8 consecutive lanes.
+template <int D, int ODT>
+__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ part, int nsplit, int heads, int sq,
+                                                   int sk, void *__restrict__ out, uint8_t *__restrict__ omx,
+                                                   int omx_rows) {
+    constexpr int CH = D / 4;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x, rows = (size_t)sq * heads;
+    const bool live = t < rows * CH;
+    const size_t r = live ? t / CH : 0;  // q * heads + head, the output row
+    const int ch = (int)(t % CH), q = (int)(r / heads), head = (int)(r % heads);
+    const int nqt = (sq + AQ - 1) / AQ, qt = q / AQ, items = nqt * heads;
+    const size_t row0 = (size_t)(head * nqt + qt) * nsplit * AQ + (size_t)(q - qt * AQ);
+    const float *ml = part + (size_t)items * nsplit * AQ * D;
+    float mm = -INFINITY;
+    for (int p = 0; p < nsplit; p++) mm = fmaxf(mm, ml[2 * (row0 + (size_t)p * AQ)]);
+    // an empty piece (m = -inf) weighs 0; no allowed key in any: 0 / 0 = NaN
+    float l = 0.0f, v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p = 0; p < nsplit; p++) {
+        const size_t rp = row0 + (size_t)p * AQ;
+        const float mp = ml[2 * rp];
+        const float w = mp == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp - mm);
+        l = __builtin_fmaf(ml[2 * rp + 1], w, l);
+        const f32x4 a = *(const f32x4 *)(part + rp * D + 4 * ch);
+        v[0] = __builtin_fmaf(a.x, w, v[0]);
+        v[1] = __builtin_fmaf(a.y, w, v[1]);
+        v[2] = __builtin_fmaf(a.z, w, v[2]);
+        v[3] = __builtin_fmaf(a.w, w, v[3]);
+    }
+    const float inv = sk == 0 ? 0.0f : 1.0f / l;
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] *= inv;
+    const size_t oi = r * D + 4 * ch;
+    if constexpr (ODT == LX2V_DTYPE_MXE4M3) {
+        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        const int k = mx_exponent(amax);
+        const float minv = mx_inv(k);
+        if (!live) return;
+        *(uint32_t *)((uint8_t *)out + oi) = quant4_nc(v, minv);
+        if (ch % 8 == 0) omx[mx_sidx(q, (head * D + 4 * ch) / 32, omx_rows)] = (uint8_t)(k + 127);
+    } else if constexpr (ODT == LX2V_DTYPE_BF16) {
+        if (!live) return;
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        *(u32x2_t *)((uint16_t *)out + oi) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    } else {
+        if (!live) return;
+        *(f32x4 *)((float *)out + oi) = (f32x4){v[0], v[1], v[2], v[3]};
+    }
 }
 
 // Any head size d <= 256: one wave per (head, query), lane j owning
@@ -549,21 +719,59 @@ __global__ __launch_bounds__(AT) void k_mask_temporal_tiles(const uint64_t *__re
 template <int D, int DT>
 void attn_mfma_od(hipStream_t s, dim3 grid, const void *q, const void *k, const void *v, int heads, int sq, int sk,
                   int kvs, const uint8_t *tiles, const uint32_t *mask, float c, void *out, int odt, uint8_t *omx,
-                  int omx_rows) {
+                  int omx_rows, float *part, int nsplit) {
+    if (nsplit > 1) {  // pieces into `part` (the output type only matters to the merge)
+        hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_F32>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
+                           tiles, mask, c, nullptr, nullptr, 0, part, nsplit);
+        const size_t n = (size_t)sq * heads * (D / 4);
+        const dim3 mg((unsigned)((n + 255) / 256));
+        if (odt == LX2V_DTYPE_BF16)
+            hipLaunchKernelGGL((k_attn_merge<D, LX2V_DTYPE_BF16>), mg, dim3(256), 0, s, part, nsplit, heads, sq, sk, out,
+                               omx, omx_rows);
+        else if (odt == LX2V_DTYPE_MXE4M3)
+            hipLaunchKernelGGL((k_attn_merge<D, LX2V_DTYPE_MXE4M3>), mg, dim3(256), 0, s, part, nsplit, heads, sq, sk,
+                               out, omx, omx_rows);
+        else
+            hipLaunchKernelGGL((k_attn_merge<D, LX2V_DTYPE_F32>), mg, dim3(256), 0, s, part, nsplit, heads, sq, sk, out,
+                               omx, omx_rows);
+        return;
+    }
     if (odt == LX2V_DTYPE_BF16)
         hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_BF16>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
-                           tiles, mask, c, out, omx, omx_rows);
+                           tiles, mask, c, out, omx, omx_rows, nullptr, 0);
     else if (odt == LX2V_DTYPE_MXE4M3)
         hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_MXE4M3>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
-                           tiles, mask, c, out, omx, omx_rows);
+                           tiles, mask, c, out, omx, omx_rows, nullptr, 0);
     else
         hipLaunchKernelGGL((k_attn_mfma<D, DT, LX2V_DTYPE_F32>), grid, dim3(AT), 0, s, q, k, v, heads, sq, sk, kvs,
-                           tiles, mask, c, out, omx, omx_rows);
+                           tiles, mask, c, out, omx, omx_rows, nullptr, 0);
 }
 
 }  // namespace
 
 bool attention_mfma_supported(size_t d) { return d == 64 || d == 128; }
+
+// Split mode: S = 2, 4 or 8 pieces per (head, query tile), merged in a
+// second pass, where the items alone would leave at least half the CUs idle
+// (the largest S with items * S <= CUs and 8 S key tiles).  At the Wan
+// chunk's 228 items a two-way split balances the causal mask's heavy and
+// light query tiles but measured no faster: the merge pass and the piece
+// boundaries cost what the balance gains.  LIGHTX2V_HIP_ATTN_SPLIT=0 turns
+// it off, =S (2..16) forces S pieces on every MFMA call.
+int attention_split(size_t heads, size_t sq, size_t sk, size_t d, int num_cu, size_t *bytes) {
+    *bytes = 0;
+    if (!attention_mfma_supported(d) || heads == 0 || sq == 0) return 1;
+    const char *e = getenv("LIGHTX2V_HIP_ATTN_SPLIT");
+    const int mode = e ? atoi(e) : -1;
+    const size_t items = ((sq + AQ - 1) / AQ) * heads, nkt = (sk + AK - 1) / AK;
+    int S = 1;
+    if (mode >= 2)
+        S = mode > 16 ? 16 : mode;
+    else if (mode != 0)
+        while (S < 8 && items * (size_t)S * 2 <= (size_t)num_cu && nkt >= (size_t)S * 16) S *= 2;
+    if (S > 1) *bytes = items * (size_t)S * AQ * (d + 2) * 4;
+    return S;
+}
 
 void launch_mask_tiles_bits(hipStream_t s, const uint32_t *bits, size_t sq, size_t sk, uint8_t *tiles) {
     const int nqt = (int)((sq + AQ - 1) / AQ), nkt = (int)((sk + AK - 1) / AK);
@@ -602,23 +810,29 @@ void launch_mask_pack(hipStream_t s, const uint8_t *mask, size_t sq, size_t sk, 
 
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
                       size_t sk, size_t kvs, size_t d, const uint8_t *mask, const uint32_t *mbits,
-                      const uint8_t *tiles, void *out, int odt, uint8_t *omx, size_t omx_rows) {
+                      const uint8_t *tiles, void *out, int odt, uint8_t *omx, size_t omx_rows, float *part,
+                      int nsplit) {
     if (heads == 0 || sq == 0) return;
     const float c = 1.4426950408889634f / sqrtf((float)d);  // log2(e) / sqrt(d): softmax in base 2
     if (attention_mfma_supported(d)) {
         const size_t items = ((sq + AQ - 1) / AQ) * heads;
-        const dim3 grid((unsigned)(8 * ((items + 7) / 8)));
+        nsplit = part && nsplit > 1 ? nsplit : 1;
+        const dim3 grid((unsigned)(8 * nsplit * ((items + 7) / 8)));
         const int hq = (int)heads, iq = (int)sq, ik = (int)sk, is = (int)kvs;
         if (d == 128) {
             if (dt == LX2V_DTYPE_BF16)
-                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx, (int)omx_rows);
+                attn_mfma_od<128, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx,
+                                                   (int)omx_rows, part, nsplit);
             else
-                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx, (int)omx_rows);
+                attn_mfma_od<128, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx,
+                                                  (int)omx_rows, part, nsplit);
         } else {
             if (dt == LX2V_DTYPE_BF16)
-                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx, (int)omx_rows);
+                attn_mfma_od<64, LX2V_DTYPE_BF16>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx,
+                                                  (int)omx_rows, part, nsplit);
             else
-                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx, (int)omx_rows);
+                attn_mfma_od<64, LX2V_DTYPE_F32>(s, grid, q, k, v, hq, iq, ik, is, tiles, mbits, c, out, odt, omx,
+                                                 (int)omx_rows, part, nsplit);
         }
         return;
     }

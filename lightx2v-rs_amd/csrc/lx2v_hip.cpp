@@ -291,7 +291,7 @@ int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
     for (auto e : ctx->prof.pool) (void)hipEventDestroy(e);
     for (auto &r : ctx->prof.open_regions) (void)hipEventDestroy(r.second);
     if (ctx->ws) (void)hipFree(ctx->ws);
-    for (lx2v::Stage *x : {&ctx->stage, &ctx->mask, &ctx->kv_spare, &ctx->resid})
+    for (lx2v::Stage *x : {&ctx->stage, &ctx->mask, &ctx->kv_spare, &ctx->resid, &ctx->attn})
         if (x->ptr) (void)hipFree(x->ptr);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -1086,13 +1086,28 @@ static int attn_check(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_b
     return set_dev(ctx);
 }
 
+// The split mode's piece count and partial-sum workspace for this call
+// (1 and null where the one-pass kernel runs).
+static int attn_part(lx2v_hip_ctx *ctx, size_t heads, size_t sq, size_t sk, size_t d, float **part, int *nsplit) {
+    *part = nullptr;
+    size_t need = 0;
+    *nsplit = attention_split(heads, sq, sk, d, ctx->num_cu, &need);
+    if (*nsplit <= 1) return LX2V_OK;
+    if (int rc = ensure(ctx, &ctx->attn.ptr, &ctx->attn.bytes, need, "attention workspace alloc")) return rc;
+    *part = (float *)ctx->attn.ptr;
+    return LX2V_OK;
+}
+
 static int attn_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k, const lx2v_hip_buf *v,
                     size_t heads, size_t sq, size_t sk, size_t d, const lx2v_hip_mask *mask, lx2v_hip_buf *out) {
     if (!heads || !sq) return ok();
+    float *part = nullptr;
+    int nsplit = 1;
+    if (int rc = attn_part(ctx, heads, sq, sk, d, &part, &nsplit)) return rc;
     return run(ctx, mask ? "causal_attention" : "attention", [&] {
         launch_attention(ctx->stream, q->ptr, k->ptr, v->ptr, q->dtype, heads, sq, sk, sk, d,
                          mask ? mask->bytes : nullptr, mask ? mask->bits : nullptr, mask ? mask->tiles : nullptr,
-                         out->ptr, out->dtype, out->mxs, out->srows);
+                         out->ptr, out->dtype, out->mxs, out->srows, part, nsplit);
     });
 }
 
@@ -1609,10 +1624,13 @@ int lx2v_hip_kv_cache_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const 
                     sq, sk);
     if (!heads || !sq) return ok();
     const lx2v_hip_mask *m = mask && sq * sk ? mask : nullptr;
+    float *part = nullptr;
+    int nsplit = 1;
+    if (int rc = attn_part(ctx, heads, sq, sk, head_dim, &part, &nsplit)) return rc;
     return run(ctx, m ? "causal_attention" : "attention", [&] {
         launch_attention(ctx->stream, q->ptr, kb.ptr, vb.ptr, q->dtype, heads, sq, sk, kv->cap, head_dim,
                          m ? m->bytes : nullptr, m ? m->bits : nullptr, m ? m->tiles : nullptr, out->ptr, out->dtype,
-                         out->mxs, out->srows);
+                         out->mxs, out->srows, part, nsplit);
     });
 }
 

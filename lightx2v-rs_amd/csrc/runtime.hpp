@@ -127,6 +127,7 @@ struct lx2v_hip_ctx {
     lx2v::Stage mask;      // causal_attention's host mask, uploaded per call, and its tile summary
     lx2v::Stage kv_spare;  // the MemRoPE update's output layout, swapped with the cache it updates
     lx2v::Stage resid;     // linear_residual's output where the add cannot ride in the GEMM
+    lx2v::Stage attn;      // split attention's partial sums (attention_split_bytes)
 };
 
 namespace lx2v {
@@ -213,9 +214,15 @@ void launch_mask_tiles_bits(hipStream_t s, const uint32_t *bits, size_t sq, size
 // All three forms of the mask "tk[k] <= tq[q]" from temporal indices.
 void launch_mask_temporal(hipStream_t s, const uint64_t *tq, size_t sq, const uint64_t *tk, size_t sk, uint8_t *mask,
                           uint32_t *bits, uint8_t *tiles);
+// The split mode's piece count S for this call (each (head, query tile) in
+// S pieces over parts of its allowed key tiles, merged in a second pass; 1:
+// the one-pass kernel) and the bytes of f32 partial sums it needs; `part`
+// points to that many bytes when nsplit > 1.
+int attention_split(size_t heads, size_t sq, size_t sk, size_t d, int num_cu, size_t *bytes);
 void launch_attention(hipStream_t s, const void *q, const void *k, const void *v, int dt, size_t heads, size_t sq,
                       size_t sk, size_t kvs, size_t d, const uint8_t *mask, const uint32_t *mbits,
-                      const uint8_t *tiles, void *out, int odt, uint8_t *omx = nullptr, size_t omx_rows = 0);
+                      const uint8_t *tiles, void *out, int odt, uint8_t *omx = nullptr, size_t omx_rows = 0,
+                      float *part = nullptr, int nsplit = 1);
 
 // ---- KV cache (k_kv.hip) ---------------------------------------------------------
 // [heads, rows, d] from src (head stride sstride rows, first row srow0) to dst
