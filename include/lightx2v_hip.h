@@ -286,7 +286,13 @@ int lx2v_hip_head_split(lx2v_hip_ctx *ctx, const lx2v_hip_buf *src, size_t rows,
  * attention-O linear's input without a quantization pass (no reference
  * counterpart: the reference's attention writes f32); a query with no
  * allowed key keeps NaN codes.  Every entry point
- * below that takes `out` accepts it the same way. */
+ * below that takes `out` accepts it the same way.
+ * Where heads * ceil(sq / 256) is at most half the GPU's CUs (head_dim 64 /
+ * 128), each (head, 256-query) item runs as 2, 4 or 8 pieces over parts of
+ * its keys whose partial sums a second pass merges; those pieces live in a
+ * context workspace grown on first use (like linear's), so such a call,
+ * like linear, must run once eagerly before graph capture.
+ * LIGHTX2V_HIP_ATTN_SPLIT=0 in the environment turns this off. */
 int lx2v_hip_attention(lx2v_hip_ctx *ctx, const lx2v_hip_buf *q, const lx2v_hip_buf *k,
                        const lx2v_hip_buf *v, size_t heads, size_t sq, size_t sk, size_t head_dim,
                        lx2v_hip_buf *out);
