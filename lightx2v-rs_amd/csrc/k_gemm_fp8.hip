@@ -311,14 +311,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     int tm, tn;
     xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int KT = K / BKB;
+    // Split K (gridDim.y > 1; per-token / per-channel scales only, which the
+    // host leaves to the reduction): part blockIdx.y of the stages, its sums
+    // to its own M x N slice of Y.
+    const int kts = K / BKB, kt0 = (int)((long long)blockIdx.y * kts / gridDim.y);
+    const int KT = (int)((long long)(blockIdx.y + 1) * kts / gridDim.y) - kt0;
+    Y += (size_t)blockIdx.y * (size_t)M * (size_t)N;
     Ops ops;
     ops.load(tid, m0, n0, M, N, sa, sb, bias);
 
     // Rows past the matrix read zero (or leave LDS as it was): they only
     // feed output rows / channels that are never stored.
-    const auto ra_src = make_rsrc(A + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K);
-    const auto rb_src = make_rsrc(B + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
+    const uint32_t k0b = (uint32_t)kt0 * BKB;
+    const auto ra_src = make_rsrc(A + (size_t)m0 * K + k0b, (uint32_t)(M - m0) * (uint32_t)K - k0b);
+    const auto rb_src = make_rsrc(B + (size_t)n0 * K + k0b, (uint32_t)(N - n0) * (uint32_t)K - k0b);
     // (readfirstlane: the saturating length would otherwise be computed on
     // the VALU and take the descriptor out of SGPRs)
     const auto rs_src = make_rsrc(
@@ -1349,9 +1355,10 @@ void launch_cfg(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
 template <int BM, int BN, int WGM, int WGN, int BKB, int NS, int OCC = 1, bool MXOUT = false, bool MXIN = false,
           bool GSC = false>
 void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
-                const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
+                const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx,
+                int splits = 1) {
     int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
+    dim3 grid(tiles_m * tiles_n, splits), block(64 * WGM * WGN);
     const uint32_t alen = (uint32_t)mx.a_len;
     const int arows = (int)mx.a_rows, yrows = (int)mx.y_rows;
 #define LX2V_DMA_A(AMV, GSV, ACTV, T)                                                                           \
@@ -1487,6 +1494,76 @@ constexpr DmaCfg kDma[] = {
     {256, 128, 4, 2, 128, 3},  // 7
 };
 
+// Split K's second pass: y = act(sum_p part[p] * sa[m] * sb[n] + b[n]) in
+// the direct epilogue's order of operations, stored as F32, BF16 or MX e4m3
+// (a thread per 4 consecutive channels, so a 32-channel MX block is 8
+// consecutive lanes).  N % 32 == 0.
+template <int ACT, typename TY>
+__global__ __launch_bounds__(256) void k_gemm_splitk_reduce(const float *__restrict__ part, int S, int M, int N,
+                                                          const float *__restrict__ sa, const float *__restrict__ sb,
+                                                          const float *__restrict__ bias, TY *__restrict__ Y,
+                                                          uint8_t *__restrict__ ymx, int ymx_rows) {
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x, nq = (size_t)N / 4;
+    const bool live = t < (size_t)M * nq;
+    const size_t tt = live ? t : 0;
+    const int m = (int)(tt / nq), c = (int)(tt % nq) * 4;
+    const size_t off = (size_t)m * N + c;
+    f32x4 acc = *(const f32x4 *)(part + off);
+    for (int p = 1; p < S; p++) {
+        const f32x4 a = *(const f32x4 *)(part + (size_t)p * M * N + off);
+        acc = (f32x4){acc.x + a.x, acc.y + a.y, acc.z + a.z, acc.w + a.w};
+    }
+    const float am = sa ? sa[m] : 1.0f;
+    const f32x4 s4 = sb ? *(const f32x4 *)(sb + c) : (f32x4){1.0f, 1.0f, 1.0f, 1.0f};
+    const f32x4 b4 = bias ? *(const f32x4 *)(bias + c) : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    float v[4] = {acc.x * am * s4.x + b4.x, acc.y * am * s4.y + b4.y, acc.z * am * s4.z + b4.z,
+                  acc.w * am * s4.w + b4.w};
+    if constexpr (ACT == LX2V_ACT_GELU_TANH)
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = gelu_tanh_fast(v[q]);
+    if constexpr (sizeof(TY) == 1) {
+        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        const int k = mx_exponent(amax);
+        const float inv = mx_inv(k);
+        if (!live) return;
+        *(uint32_t *)((uint8_t *)Y + off) = quant4(v, inv);
+        if (c % 32 == 0) ymx[mx_sidx(m, c / 32, ymx_rows)] = (uint8_t)(k + 127);
+    } else if constexpr (sizeof(TY) == 2) {
+        if (!live) return;
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        *(u32x2_t *)((uint16_t *)Y + off) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    } else {
+        if (!live) return;
+        *(f32x4 *)((float *)Y + off) = (f32x4){v[0], v[1], v[2], v[3]};
+    }
+}
+
+void launch_splitk_reduce(hipStream_t s, const float *part, int S, int M, int N, const float *sa, const float *sb,
+                          const float *bias, int act, void *y, int y_dtype, uint8_t *ymx, int ymx_rows) {
+    const size_t n = (size_t)M * (N / 4);
+    const dim3 grid((unsigned)((n + 255) / 256));
+#define LX2V_RED(ACTV, T)                                                                                          \
+    hipLaunchKernelGGL((k_gemm_splitk_reduce<ACTV, T>), grid, dim3(256), 0, s, part, S, M, N, sa, sb, bias, (T *)y, \
+                       ymx, ymx_rows)
+#define LX2V_RED_T(ACTV)                                  \
+    do {                                                  \
+        if (y_dtype == LX2V_DTYPE_BF16)                   \
+            LX2V_RED(ACTV, uint16_t);                     \
+        else if (y_dtype == LX2V_DTYPE_MXE4M3)            \
+            LX2V_RED(ACTV, uint8_t);                      \
+        else                                              \
+            LX2V_RED(ACTV, float);                        \
+    } while (0)
+    if (act == LX2V_ACT_GELU_TANH)
+        LX2V_RED_T(LX2V_ACT_GELU_TANH);
+    else
+        LX2V_RED_T(LX2V_ACT_NONE);
+#undef LX2V_RED_T
+#undef LX2V_RED
+}
+
 void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
                     const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
     switch (idx) {
@@ -1597,9 +1674,31 @@ bool ov_capable(size_t M, size_t N, size_t K, bool mx_in, bool grouped, int y_dt
 }
 
 Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped, int y_dtype,
-                      int act, bool residual) {
+                      int act, bool residual, bool allow_split) {
     Fp8Plan p;
     if (K % 128 != 0) return p;  // the register-staged kernel
+    // Split K where even the 256 x 128 tiles leave at least half the CUs
+    // idle and K is long: S workgroups per tile (S <= CUs / tiles, >= 32
+    // stages each, <= 8), their partial sums reduced by a second pass.  The
+    // partial sums' store and the reduction cost about 10 us, which only a
+    // long K loop repays (880 x 14336 -> 3072: 68.9 -> 51.0 us at S = 2;
+    // 880 x 3072 -> 3072: 19.1 -> 23.3 us).  LIGHTX2V_HIP_FP8_SPLITK=0 turns
+    // it off, =S forces S where it applies.
+    if (allow_split && !mx_in && !grouped && !residual && N % 128 == 0 && forced_cfg() < 0) {
+        const char *e = getenv("LIGHTX2V_HIP_FP8_SPLITK");
+        const int mode = e ? atoi(e) : -1;
+        const size_t tiles = ((M + 255) / 256) * (N / 128), kts = K / 128;
+        size_t S = 1;
+        if (mode >= 2)
+            S = std::min<size_t>((size_t)mode, kts);
+        else if (mode != 0 && tiles * 2 <= (size_t)num_cu)
+            S = std::min<size_t>(std::min<size_t>((size_t)num_cu / tiles, kts / 32), 8);
+        if (S >= 2 && (size_t)M * N * S * 4 < (1ull << 31)) {
+            p.kernel = 0;
+            p.splits = (int)S;
+            return p;
+        }
+    }
     const int nd = (int)(sizeof(kDma) / sizeof(kDma[0]));
     const int forced = forced_cfg();
     auto ok = [&](int idx) {
@@ -1636,6 +1735,14 @@ void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t 
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
                      int y_dtype, size_t M, size_t N, size_t K, const Fp8Mx &mx) {
     int m = (int)M, n = (int)N, k = (int)K;
+    if (p.splits > 1) {
+        // the partial sums without scales or bias, then the reduction
+        launch_dma<256, 128, 4, 2, 128, 3, 1, true, true, true>(s, a, nullptr, b, nullptr, nullptr, LX2V_ACT_NONE,
+                                                                mx.part, LX2V_DTYPE_F32, m, n, k, Fp8Mx{}, p.splits);
+        launch_splitk_reduce(s, mx.part, p.splits, m, n, a_scale, b_scale, bias, act, y, y_dtype, mx.y,
+                             (int)mx.y_rows);
+        return;
+    }
     if (p.kernel == 6) {
         launch_pt(s, num_cu, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k, mx);
         return;

@@ -291,7 +291,7 @@ int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
     for (auto e : ctx->prof.pool) (void)hipEventDestroy(e);
     for (auto &r : ctx->prof.open_regions) (void)hipEventDestroy(r.second);
     if (ctx->ws) (void)hipFree(ctx->ws);
-    for (lx2v::Stage *x : {&ctx->stage, &ctx->mask, &ctx->kv_spare, &ctx->resid, &ctx->attn})
+    for (lx2v::Stage *x : {&ctx->stage, &ctx->mask, &ctx->kv_spare, &ctx->resid, &ctx->attn, &ctx->splitk})
         if (x->ptr) (void)hipFree(x->ptr);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -1977,14 +1977,20 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         if (fp8_mfma) {
             if (fp8_grouped) mx.wgs = w->sscale;
             const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx, fp8_grouped, y->dtype, act,
-                                               gate != nullptr);
+                                               gate != nullptr, scr == nullptr);
+            if (plan.splits > 1) {  // split K: the partial sums' workspace
+                if (int rc = ensure(ctx, &ctx->splitk.ptr, &ctx->splitk.bytes, (size_t)plan.splits * rows * N * 4,
+                                    "split-K workspace alloc"))
+                    return rc;
+                mx.part = (float *)ctx->splitk.ptr;
+            }
             if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1 && plan.kernel != 6)  // built with grouped scales
                 return fail(LX2V_ERR_UNSUPPORTED, "no grouped-scale fp8 kernel for configuration %d", plan.kernel);
             // Profile name: the kernel configuration and the operand forms,
             // e.g. "gemm_fp8_e4m3.c0.g128.mxout".
             char pname[64];
             char cfg[8] = "creg";  // the register-staged kernel (K % 128 != 0)
-            if (plan.kernel >= 0) snprintf(cfg, sizeof cfg, "c%d", plan.kernel);
+            if (plan.kernel >= 0) snprintf(cfg, sizeof cfg, plan.splits > 1 ? "c%dk%d" : "c%d", plan.kernel, plan.splits);
             snprintf(pname, sizeof pname, "gemm_fp8_e4m3.%s%s%s%s%s", cfg, fp8_grouped ? ".g128" : "", x_mx ? ".mxin" : "", y_mx ? ".mxout" : "", gate ? ".res" : "");
             if (int rc = run(ctx, pname, [&] {
                     launch_gemm_fp8(ctx->stream, ctx->num_cu, plan, q, s, (const uint8_t *)w->codes, w->scales, bp,
@@ -2095,7 +2101,9 @@ int lx2v_hip_linear_noalloc(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_r
 
 // The residual add can ride in the GEMM's epilogue: FP8 weight with one scale
 // per channel on the e4m3 path, a bf16 / f32 output, and a direct-to-LDS
-// configuration (K % 128 == 0; not the 256 x 256 ping-pong tile).
+// configuration (K % 128 == 0; not the 256 x 256 ping-pong tile), where
+// linear itself would not split K (its sums would then be added in another
+// order than the fused kernel's; the pair keeps the two equal).
 static bool linear_fusable(const lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t rows, const lx2v_hip_weight *w,
                            const lx2v_hip_buf *h) {
     const size_t N = w->rows, K = w->cols;
@@ -2104,6 +2112,8 @@ static bool linear_fusable(const lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_
     if (w->fmt != LX2V_WFMT_FP8 || h->quantized() || !gemm_fp8_supported(rows, N, K)) return false;
     if (grouped && !(w->sscale && !x_mx && gemm_fp8_grouped_supported(rows, N, K, w->group))) return false;
     if (!(ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized())) return false;
+    if (plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx, grouped, h->dtype, LX2V_ACT_NONE, false, true).splits > 1)
+        return false;
     return gemm_fp8_residual_ok(plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx, grouped, h->dtype, LX2V_ACT_NONE, true));
 }
 

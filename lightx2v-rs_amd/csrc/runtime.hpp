@@ -127,7 +127,8 @@ struct lx2v_hip_ctx {
     lx2v::Stage mask;      // causal_attention's host mask, uploaded per call, and its tile summary
     lx2v::Stage kv_spare;  // the MemRoPE update's output layout, swapped with the cache it updates
     lx2v::Stage resid;     // linear_residual's output where the add cannot ride in the GEMM
-    lx2v::Stage attn;      // split attention's partial sums (attention_split_bytes)
+    lx2v::Stage attn;      // split attention's partial sums (attention_split)
+    lx2v::Stage splitk;    // split-K fp8 GEMM partial sums (Fp8Plan::splits)
 };
 
 namespace lx2v {
@@ -262,6 +263,10 @@ void launch_gemm_generic(hipStream_t s, const void *a, int amode, const float *a
 // plan_gemm_fp8 picks the kernel configuration for a shape.
 struct Fp8Plan {
     int kernel = -1;  // configuration index, or -1: the register-staged kernel (K % 128 != 0)
+    // > 1: K split over this many workgroups per tile (configuration 0),
+    // their f32 partial sums in Fp8Mx::part, summed by a second pass that
+    // applies the scales, bias, activation and output form
+    int splits = 1;
 };
 // MX e4m3 operands of a launch: A's block scales ([K / 128][a_rows][4],
 // a_len bytes readable from a; a_scale is then null) and/or the output's
@@ -281,6 +286,8 @@ struct Fp8Mx {
     // stage-major scale copy (lx2v_hip_weight::sscale, group 128); b_scale
     // is then ignored.
     const float *wgs = nullptr;
+    // Split-K partial sums (plans with splits > 1): splits * M * N floats.
+    float *part = nullptr;
 };
 bool gemm_fp8_supported(size_t M, size_t N, size_t K);
 // Group-128 FP8 weights on the fp8 MFMA (needs the stage-major scale copy).
@@ -289,8 +296,10 @@ bool gemm_fp8_grouped_supported(size_t M, size_t N, size_t K, size_t group);
 bool gemm_fp8_residual_ok(const Fp8Plan &p);
 // y_dtype / act / residual: the launch's output form (some configurations
 // cover only bf16 / MX output, and the residual epilogue only some).
+// allow_split: the caller can give the split-K partial sums a workspace.
 Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped = false,
-                      int y_dtype = LX2V_DTYPE_BF16, int act = LX2V_ACT_NONE, bool residual = false);
+                      int y_dtype = LX2V_DTYPE_BF16, int act = LX2V_ACT_NONE, bool residual = false,
+                      bool allow_split = false);
 void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t *a, const float *a_scale,
                      const uint8_t *b, const float *b_scale, const float *bias, int act, void *y,
                      int y_dtype, size_t M, size_t N, size_t K, const Fp8Mx &mx);

@@ -107,6 +107,44 @@ def test_fp8_bf16_out_is_rounded_f32_out(be, M, K, N):
         assert_close(y32, oracle_w8a8(x, q, s, K, b, act), *FP8_TIGHT, what="fp8 f32 out")
 
 
+@pytest.mark.parametrize("M,K,N,act,ydt", [(300, 1536, 1536, H.ACT_NONE, H.DTYPE_F32),
+                                            (880, 3072, 1024, H.ACT_GELU_TANH, H.DTYPE_BF16),
+                                            (129, 2048, 384, H.ACT_NONE, H.DTYPE_F32),
+                                            (600, 1024, 512, H.ACT_GELU_TANH, H.DTYPE_MXE4M3)])
+def test_fp8_split_k_vs_one_pass(be, monkeypatch, M, K, N, act, ydt):
+    """Split K (Fp8Plan::splits: the 256 x 128 tiles' K range over S
+    workgroups, partial sums reduced with the scales, bias and activation
+    by a second pass), forced to 2 and 4 pieces, against the oracle to
+    FP8_TIGHT and against the one-pass kernel (only the f32 summation order
+    differs); MX output equals quantize_mx of the split path's own f32
+    output."""
+    x = normal(3001 + M, M * K).reshape(M, K)
+    _, q, s = fp8_weight(3002 + N, N, K, K)
+    b = normal(3003, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, K)
+    want = oracle_w8a8(x, q, s, K, b, act)
+    monkeypatch.setenv("LIGHTX2V_HIP_FP8_SPLITK", "0")
+    one = run_linear(be, x, w, b, act)
+    for pieces in ("2", "4"):
+        monkeypatch.setenv("LIGHTX2V_HIP_FP8_SPLITK", pieces)
+        y32 = run_linear(be, x, w, b, act)
+        assert_close(y32, want, *FP8_TIGHT, what=f"split {pieces} vs oracle")
+        assert_close(y32, one, 1e-6, 1e-5, what=f"split {pieces} vs one pass")
+        if ydt == H.DTYPE_BF16:
+            y16 = run_linear(be, x, w, b, act, y_dtype=H.DTYPE_BF16)
+            assert np.array_equal(u32(y16), u32(O.bf16_round(y32)))
+        elif ydt == H.DTYPE_MXE4M3:
+            xb = be.alloc(M * K)
+            be.write(xb, x)
+            yf, ym, ref = be.alloc(M * N), be.alloc_mx(M, N), be.alloc_mx(M, N)
+            be.linear(xb, 0, M, w, be.upload(b), act, yf, 0)
+            be.linear(xb, 0, M, w, be.upload(b), act, ym, 0)
+            be.quantize_mx(yf, 0, M, ref)
+            c1, s1 = be.download_mx(ym, M, N)
+            c2, s2 = be.download_mx(ref, M, N)
+            assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
+
+
 def test_fp8_no_bias(be):
     M, K, N = 96, 640, 320
     x = normal(8, M * K).reshape(M, K)
