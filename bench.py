@@ -120,6 +120,15 @@ def per_config(be, H):
             be.linear(x, 0, rows, w, b, act, y, 0)
         be.profile_region("c_" + name, False)
         us = be.profile_kernel("c_" + name)[1] * 1e3 / 30
+        # the kernel configuration that ran (the profile report's name for it)
+        be.profile_reset()
+        be.profile_enable(True)
+        try:
+            be.linear(x, 0, rows, w, b, act, y, 0)
+            ran = sorted(kk for kk in be.profile_stats() if kk.startswith("gemm"))
+        finally:
+            be.profile_enable(False)
+            be.profile_reset()
         fl = 2.0 * rows * n * k
         tf = fl / (us * 1e-6) / 1e12
         nb = alg_bytes(rows, n, k, xdt, ydt, kind, group or k)
@@ -130,7 +139,7 @@ def per_config(be, H):
                      "alg_bytes": nb, "ai_flop_per_byte": round(ai, 1),
                      "bound": "hbm" if bound < peak else "mfma", "bound_tflops": round(bound, 1),
                      "us_at_bound": round(fl / (bound * 1e12) * 1e6, 2), "pct_bound": round(100.0 * tf / bound, 1),
-                     "hbm_gbs": round(nb / (us * 1e-6) / 1e9, 1), "path": path}
+                     "hbm_gbs": round(nb / (us * 1e-6) / 1e9, 1), "path": path, "kernel": ",".join(ran)}
         y.free()
         b.free()
 
