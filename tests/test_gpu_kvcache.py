@@ -132,10 +132,15 @@ def test_grows_past_capacity_and_reads_other_dtype(be):
     assert np.array_equal(be.download(kf), k.ravel()) and np.array_equal(be.download(vf), v.ravel())
 
 
+@pytest.mark.parametrize("split", [None, "4"])
 @pytest.mark.parametrize("hd", [128, 64, 48])
-def test_attention_reads_the_cache_in_place(be, hd):
+def test_attention_reads_the_cache_in_place(be, monkeypatch, hd, split):
     """kv_cache_attention == causal_attention on kv_cache_kv's copy, bit for
-    bit, with the DiT's mask (key temporal <= query temporal, dit.rs:643-653)."""
+    bit, with the DiT's mask (key temporal <= query temporal, dit.rs:643-653);
+    also with attention's split mode forced to 4 pieces (the cache's head
+    stride is its capacity, the copy's is sk)."""
+    if split:
+        monkeypatch.setenv("LIGHTX2V_HIP_ATTN_SPLIT", split)
     heads, ft = 2, 40
     dtype = H.DTYPE_BF16
     c = _new(be, heads, hd, 5 * ft, dtype)  # small capacity: the head stride moves as it grows

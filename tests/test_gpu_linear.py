@@ -145,6 +145,24 @@ def test_fp8_split_k_vs_one_pass(be, monkeypatch, M, K, N, act, ydt):
             assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
 
 
+def test_fp8_split_k_row_offsets(be, monkeypatch):
+    """Split K with x_row / y_row offsets and a row count short of the
+    buffers (the reduction's token scales, output rows and MX scale rows all
+    start at the offsets): equal to the one-pass kernel up to f32 summation
+    order, and to the oracle to FP8_TIGHT."""
+    M, K, N = 400, 8192, 384
+    x = normal(3101, M * K).reshape(M, K)
+    _, q, s = fp8_weight(3102, N, K, K)
+    b = normal(3103, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, K)
+    monkeypatch.setenv("LIGHTX2V_HIP_FP8_SPLITK", "0")
+    one = run_linear(be, x, w, b, H.ACT_GELU_TANH, x_row=37, y_row=11, rows=300)
+    monkeypatch.setenv("LIGHTX2V_HIP_FP8_SPLITK", "3")
+    two = run_linear(be, x, w, b, H.ACT_GELU_TANH, x_row=37, y_row=11, rows=300)
+    assert_close(two, one, 1e-6, 1e-5, what="split vs one pass, offsets")
+    assert_close(two, oracle_w8a8(x[37:337], q, s, K, b, H.ACT_GELU_TANH), *FP8_TIGHT, what="split, offsets")
+
+
 def test_fp8_no_bias(be):
     M, K, N = 96, 640, 320
     x = normal(8, M * K).reshape(M, K)
