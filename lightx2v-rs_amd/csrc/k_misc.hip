@@ -369,18 +369,37 @@ void act_quant_rows(hipStream_t s, const void *x, size_t rows, size_t cols, uint
     const size_t per = (cols / 8 + 63) / 64;  // chunks per lane with one wave per row
     const dim3 block(kThreads);
     auto grid = [&](int w) { return dim3((unsigned)((rows + (kThreads / 64 / w) - 1) / (kThreads / 64 / w))); };
-    if (per <= 2)
-        hipLaunchKernelGGL((k_act_quant_rows<DT, 2, 1>), grid(1), block, 0, s, x, rows, cols, q, scale);
-    else if (per == 3)  // 1536 columns (Wan2.1-1.3B): no masked fourth chunk (4.38 -> 4.27 us at 4680 rows)
-        hipLaunchKernelGGL((k_act_quant_rows<DT, 3, 1>), grid(1), block, 0, s, x, rows, cols, q, scale);
-    else if (per <= 4)
-        hipLaunchKernelGGL((k_act_quant_rows<DT, 4, 1>), grid(1), block, 0, s, x, rows, cols, q, scale);
-    else if (per <= 8)
-        hipLaunchKernelGGL((k_act_quant_rows<DT, 4, 2>), grid(2), block, 0, s, x, rows, cols, q, scale);
-    else if (per <= 16)
-        hipLaunchKernelGGL((k_act_quant_rows<DT, 4, 4>), grid(4), block, 0, s, x, rows, cols, q, scale);
-    else
-        hipLaunchKernelGGL((k_act_quant_rows<DT, 8, 4>), grid(4), block, 0, s, x, rows, cols, q, scale);
+    // W waves per row (one up to 2048 columns, two up to 4096, four beyond)
+    // and T = the chunks a lane needs, so that no lane loads a chunk past
+    // every row (1536 columns: 4.38 -> 4.27 us at 4680 rows against a
+    // masked fourth chunk).
+    const int w = per <= 4 ? 1 : (per <= 8 ? 2 : 4);
+    const int t = (int)((per + w - 1) / w);
+#define LX2V_AQ(T, W) \
+    hipLaunchKernelGGL((k_act_quant_rows<DT, T, W>), grid(W), block, 0, s, x, rows, cols, q, scale)
+    if (w == 1) {
+        switch (t) {
+            case 1: LX2V_AQ(1, 1); break;
+            case 2: LX2V_AQ(2, 1); break;
+            case 3: LX2V_AQ(3, 1); break;
+            default: LX2V_AQ(4, 1); break;
+        }
+    } else if (w == 2) {
+        if (t <= 3)
+            LX2V_AQ(3, 2);
+        else
+            LX2V_AQ(4, 2);
+    } else {
+        switch (t) {
+            case 3: LX2V_AQ(3, 4); break;
+            case 4: LX2V_AQ(4, 4); break;
+            case 5: LX2V_AQ(5, 4); break;
+            case 6: LX2V_AQ(6, 4); break;
+            case 7: LX2V_AQ(7, 4); break;
+            default: LX2V_AQ(8, 4); break;
+        }
+    }
+#undef LX2V_AQ
 }
 
 void launch_act_quant(hipStream_t s, const void *x, int dtype, size_t rows, size_t cols,
