@@ -334,16 +334,37 @@ void norm_launch(hipStream_t s, const NormArgs &p) {
     auto grid = [&](int w) { return dim3((unsigned)((p.rows + (kNThreads / 64 / w) - 1) / (kNThreads / 64 / w))); };
     if (p.dim % 8 != 0 || per > 32) {
         hipLaunchKernelGGL((k_norm_any<DT, OD, RES>), dim3((unsigned)p.rows), block, 0, s, p);
-    } else if (per <= 2) {
-        hipLaunchKernelGGL((k_norm_rows<DT, OD, 2, 1, RES>), grid(1), block, 0, s, p);
-    } else if (per <= 4) {
-        hipLaunchKernelGGL((k_norm_rows<DT, OD, 4, 1, RES>), grid(1), block, 0, s, p);
-    } else if (per <= 8) {
-        hipLaunchKernelGGL((k_norm_rows<DT, OD, 4, 2, RES>), grid(2), block, 0, s, p);
-    } else if (per <= 16) {
-        hipLaunchKernelGGL((k_norm_rows<DT, OD, 4, 4, RES>), grid(4), block, 0, s, p);
     } else {
-        hipLaunchKernelGGL((k_norm_rows<DT, OD, 8, 4, RES>), grid(4), block, 0, s, p);
+        // W waves per row (one up to 2048 columns, two up to 4096, four
+        // beyond) and T chunks per lane, T the fewest that cover the row
+        // for the common widths (1536: 3, 3072: 3 x 2, 5120: 3 x 4, 8960:
+        // 5 x 4), so lanes load no chunk past every row.
+        const int w = per <= 4 ? 1 : (per <= 8 ? 2 : 4);
+        const int t = (int)((per + w - 1) / w);
+#define LX2V_NR(T, W) hipLaunchKernelGGL((k_norm_rows<DT, OD, T, W, RES>), grid(W), block, 0, s, p)
+        if (w == 1) {
+            if (t <= 2)
+                LX2V_NR(2, 1);
+            else if (t == 3)
+                LX2V_NR(3, 1);
+            else
+                LX2V_NR(4, 1);
+        } else if (w == 2) {
+            if (t <= 3)
+                LX2V_NR(3, 2);
+            else
+                LX2V_NR(4, 2);
+        } else {
+            if (t <= 3)
+                LX2V_NR(3, 4);
+            else if (t == 4)
+                LX2V_NR(4, 4);
+            else if (t == 5)
+                LX2V_NR(5, 4);
+            else
+                LX2V_NR(8, 4);
+        }
+#undef LX2V_NR
     }
 }
 
