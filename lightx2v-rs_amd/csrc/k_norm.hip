@@ -551,6 +551,8 @@ void head_split_launch(hipStream_t s, const HeadSplitArgs &p) {
         hipLaunchKernelGGL((k_head_split_any<DT, OD>), grid, block, 0, s, p);
     else if (per <= 2)
         hipLaunchKernelGGL((k_head_split<DT, OD, 2>), grid, block, 0, s, p);
+    else if (per == 3)  // 1536 columns: no chunk past the row
+        hipLaunchKernelGGL((k_head_split<DT, OD, 3>), grid, block, 0, s, p);
     else if (per <= 4)
         hipLaunchKernelGGL((k_head_split<DT, OD, 4>), grid, block, 0, s, p);
     else if (per <= 8)
