@@ -49,7 +49,10 @@ enum {
     LX2V_ERR_HIP = 4,         /* a HIP runtime call failed                  */
     LX2V_ERR_BAD_ARG = 5,     /* null handle, unknown enum value            */
     LX2V_ERR_OOM = 6,         /* device allocation failed                   */
-    LX2V_ERR_UNSUPPORTED = 7  /* valid request this build does not serve    */
+    LX2V_ERR_UNSUPPORTED = 7, /* valid request this build does not serve    */
+    LX2V_ERR_BUSY = 8         /* the device scratch is held by another context
+                                 (lx2v_hip_linear_noalloc; no reference
+                                 counterpart)                               */
 };
 
 /* Act (backend.rs:38-43) */
@@ -431,16 +434,20 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
 
 /* No counterpart in the reference: lx2v_hip_linear for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc).  Same arguments, kernels and results as
+ * that forbid hipMalloc).  Same arguments, plan, kernels and results as
  * lx2v_hip_linear, bit for bit; its workspaces (the per-token e4m3
  * activations and row scales, a bf16 bias's f32 copy, f32 activations' bf16
- * copy) live in a device array of 48 MiB per device instead of the
- * context's, so it calls no hipMalloc / hipFree and records no profiler
- * events.  A call needing more (roughly rows * cols > 48 MiB with f32 / bf16
- * activations) fails with LX2V_ERR_UNSUPPORTED and a message; pre-quantized
- * E4M3 / MXE4M3 activations need none.  Every call on one device shares the
- * array, which keeps the last call's contents: calls that overlap on one
- * device (two streams, two contexts, two threads) race. */
+ * copy, split K's f32 partial sums) live in a device array of 48 MiB per
+ * device instead of the context's, so it calls no hipMalloc / hipFree and
+ * records no profiler events.  A call needing more (roughly rows * cols >
+ * 48 MiB with f32 / bf16 activations, plus S * rows * w.rows * 4 bytes where
+ * K is split S ways) fails with LX2V_ERR_UNSUPPORTED and a message and
+ * enqueues nothing; pre-quantized E4M3 / MXE4M3 activations need no
+ * activation workspace.  The array keeps the last call's contents.  One
+ * context at a time holds a device's array: a call (or the launch of a graph
+ * that captured such calls) while another context's work on it is still in
+ * flight fails with LX2V_ERR_BUSY and enqueues nothing; calls of one context
+ * are ordered on its stream.  A context is used by one thread at a time. */
 int lx2v_hip_linear_noalloc(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
                             const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act,
                             lx2v_hip_buf *y, size_t y_row);

@@ -43,6 +43,7 @@ pub const ERR_HIP: c_int = 4;
 pub const ERR_BAD_ARG: c_int = 5;
 pub const ERR_OOM: c_int = 6;
 pub const ERR_UNSUPPORTED: c_int = 7;
+pub const ERR_BUSY: c_int = 8;
 
 pub const ACT_NONE: c_int = 0;
 pub const ACT_GELU_TANH: c_int = 1;

@@ -563,7 +563,10 @@ impl HipBackend {
 
     /// `linear` with no allocation (its workspaces in the library's 48 MiB
     /// per-device scratch): for callers under graph capture or in loops that
-    /// must not allocate.  Calls that overlap on one device race.
+    /// must not allocate.  One context at a time holds a device's scratch:
+    /// `Err(status)` with `ffi::ERR_BUSY` while another context's work on it
+    /// is in flight (nothing was enqueued; retry later); any other failure
+    /// panics like `linear`.
     #[allow(clippy::too_many_arguments)]
     pub fn linear_noalloc(
         &self,
@@ -575,8 +578,8 @@ impl HipBackend {
         act: Act,
         y: &HipBuf,
         y_row: usize,
-    ) {
-        check(unsafe {
+    ) -> Result<(), c_int> {
+        let rc = unsafe {
             ffi::lx2v_hip_linear_noalloc(
                 self.c(),
                 x.raw,
@@ -588,7 +591,12 @@ impl HipBackend {
                 y.raw,
                 y_row,
             )
-        });
+        };
+        if rc == ffi::ERR_BUSY {
+            return Err(rc);
+        }
+        check(rc);
+        Ok(())
     }
 
     /// Native f32 weights on the bf16 MFMA through their bf16 copy

@@ -1588,13 +1588,11 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
 }
 
 // Tuning override: LIGHTX2V_HIP_FP8_CFG=<index into kDma> forces one
-// direct-to-LDS configuration (-1 or unset: automatic).
+// direct-to-LDS configuration (-1 or unset: automatic).  Read on every
+// plan, so a process (or a test) can change it between calls.
 int forced_cfg() {
-    static int v = [] {
-        const char *e = getenv("LIGHTX2V_HIP_FP8_CFG");
-        return e ? atoi(e) : -1;
-    }();
-    return v;
+    const char *e = getenv("LIGHTX2V_HIP_FP8_CFG");
+    return e ? atoi(e) : -1;
 }
 
 }  // namespace

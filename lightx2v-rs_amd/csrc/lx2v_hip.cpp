@@ -259,8 +259,8 @@ int lx2v_hip_create(int device, lx2v_hip_ctx **out) {
         return fail(LX2V_ERR_NO_DEVICE, "device %d is %s, this build targets gfx950", device,
                     prop.gcnArchName);
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
-    // The no-alloc entry point's scratch on this device (once per device;
-    // a failure is reported by that entry point, not here).
+    // The no-alloc entry point's scratch on this device (resolved once per
+    // device; a failure is retried and reported by that entry point).
     (void)scratch_setup(device);
     auto *ctx = new lx2v_hip_ctx;
     ctx->device = device;
@@ -270,6 +270,12 @@ int lx2v_hip_create(int device, lx2v_hip_ctx **out) {
     if (e != hipSuccess) {
         delete ctx;
         return hip_fail(e, "hipStreamCreate");
+    }
+    e = hipEventCreateWithFlags(&ctx->scratch_done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_fail(e, "hipEventCreate");
     }
     const char *pv = getenv("LIGHTX2V_PROFILE");
     ctx->prof.on = pv && strcmp(pv, "0") != 0;
@@ -287,6 +293,8 @@ int lx2v_hip_destroy(lx2v_hip_ctx *ctx) {
         ctx->capturing = false;
     }
     (void)hipStreamSynchronize(ctx->stream);
+    scratch_release(ctx->device, ctx);
+    if (ctx->scratch_done) (void)hipEventDestroy(ctx->scratch_done);
     prof_harvest(ctx);
     for (auto e : ctx->prof.pool) (void)hipEventDestroy(e);
     for (auto &r : ctx->prof.open_regions) (void)hipEventDestroy(r.second);
@@ -1785,6 +1793,7 @@ int lx2v_hip_quantize_mx(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row,
 struct lx2v_hip_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    bool uses_scratch = false;  // holds linear_noalloc calls: each launch claims the device scratch
 };
 
 extern "C" {
@@ -1796,6 +1805,7 @@ int lx2v_hip_graph_begin(lx2v_hip_ctx *ctx) {
     prof_harvest(ctx);  // pending profiler events must not straddle the capture
     HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
     ctx->capturing = true;
+    ctx->capture_scratch = false;
     return ok();
 }
 
@@ -1809,6 +1819,7 @@ int lx2v_hip_graph_end(lx2v_hip_ctx *ctx, lx2v_hip_graph **out) {
     HIP_TRY(hipStreamEndCapture(ctx->stream, &g), "hipStreamEndCapture");
     auto *gr = new lx2v_hip_graph;
     gr->graph = g;
+    gr->uses_scratch = ctx->capture_scratch;
     hipError_t e = hipGraphInstantiate(&gr->exec, g, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         (void)hipGraphDestroy(g);
@@ -1824,7 +1835,23 @@ int lx2v_hip_graph_launch(lx2v_hip_ctx *ctx, const lx2v_hip_graph *g) {
     NEED(g, "graph");
     if (int rc = not_capturing(ctx, "graph_launch")) return rc;
     if (int rc = set_dev(ctx)) return rc;
-    HIP_TRY(hipGraphLaunch(g->exec, ctx->stream), "hipGraphLaunch");
+    if (!g->uses_scratch) {
+        HIP_TRY(hipGraphLaunch(g->exec, ctx->stream), "hipGraphLaunch");
+        return ok();
+    }
+    hipError_t e = hipSuccess;
+    void *p = nullptr;
+    switch (scratch_claim(ctx->device, ctx, ctx->scratch_done, &p, &e)) {
+        case ScratchClaim::Busy:
+            return fail(LX2V_ERR_BUSY, "graph_launch: the graph holds linear_noalloc calls and the device scratch is "
+                        "in use by another context's work in flight on device %d", ctx->device);
+        case ScratchClaim::Error: return hip_fail(e, "graph_launch: device scratch");
+        case ScratchClaim::Held: break;
+    }
+    e = hipGraphLaunch(g->exec, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(ctx->scratch_done, ctx->stream);
+    scratch_unlock(ctx->device);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
     return ok();
 }
 
@@ -1909,22 +1936,55 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
                         (gemm_w16_supported(w) && rows * K * x->elem_bytes() < (1ull << 31));
     const bool e4m3_path = w->fmt == LX2V_WFMT_FP8 &&
                            (x->quantized() || y_mx || (ctx->fp8_act == LX2V_FP8_ACT_E4M3 && (fp8_mfma || !w16_ok)));
-    // Scratch layout (no-alloc variant): [f32 bias][e4m3 codes][f32 row scales]
-    // or [f32 bias][bf16 activations], each piece 256-byte aligned.
-    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-    const size_t s_bias = bias && bias->dtype != LX2V_DTYPE_F32 ? al(N * 4) : 0;
     // Native f32 weights on the bf16 MFMA (their bf16 copy, bf16 activations).
     const bool native_bf16 = w->fmt == LX2V_WFMT_F32 && w->wbf16 && ctx->native_mode == LX2V_NATIVE_BF16 &&
                              gemm_bf16_supported(rows, N, K);
+    // The fp8 MFMA's plan, made before anything is enqueued: a call refused
+    // below leaves nothing on the stream.
+    Fp8Plan plan;
+    if (e4m3_path && fp8_mfma) {
+        plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx, fp8_grouped, y->dtype, act, gate != nullptr,
+                             true);
+        if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1 && plan.kernel != 6)  // built with grouped scales
+            return fail(LX2V_ERR_UNSUPPORTED, "no grouped-scale fp8 kernel for configuration %d", plan.kernel);
+    }
+    // Workspaces, each piece 256-byte aligned: a bf16 bias's f32 copy; the
+    // activations' e4m3 codes and row scales, or their bf16 copy; split K's
+    // f32 partial sums.  The no-alloc variant lays them out in that order in
+    // the device scratch; `linear` keeps them in context workspaces, all
+    // grown here, before the first launch.
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t s_bias = bias && bias->dtype != LX2V_DTYPE_F32 ? al(N * 4) : 0;
     const size_t s_act = e4m3_path ? (x->quantized() ? 0 : al(rows * K) + al(rows * 4))
                                    : ((gemm_w16_dma_supported(w, rows) || native_bf16) && x->dtype == LX2V_DTYPE_F32
                                           ? al(rows * K * 2)
                                           : 0);
-    if (scr && s_bias + s_act > scr->bytes)
+    const size_t s_part = plan.splits > 1 ? al((size_t)plan.splits * rows * N * 4) : 0;
+    if (scr && s_bias + s_act + s_part > scr->bytes)
         return fail(LX2V_ERR_UNSUPPORTED,
-                    "linear_noalloc: this call needs %zu bytes of scratch (rows %zu x cols %zu), the maximum is %zu",
-                    s_bias + s_act, rows, K, scr->bytes);
+                    "linear_noalloc: this call needs %zu bytes of scratch (rows %zu x cols %zu -> %zu), the maximum "
+                    "is %zu",
+                    s_bias + s_act + s_part, rows, K, N, scr->bytes);
     if (int rc = set_dev(ctx)) return rc;
+    uint8_t *p_bias = nullptr, *p_act = nullptr;
+    float *p_part = nullptr;
+    if (scr) {
+        p_bias = scr->ptr;
+        p_act = scr->ptr + s_bias;
+        p_part = (float *)(scr->ptr + s_bias + s_act);
+    } else {
+        void *st = nullptr;
+        if (s_bias)  // slot 0 of the staging (linear_residual's gate is in slot 2)
+            if (int rc = stage_for(ctx, N * 4, &st)) return rc;
+        if (s_act)
+            if (int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, s_act, "workspace alloc")) return rc;
+        if (s_part)
+            if (int rc = ensure(ctx, &ctx->splitk.ptr, &ctx->splitk.bytes, s_part, "split-K workspace alloc"))
+                return rc;
+        p_bias = (uint8_t *)st;
+        p_act = (uint8_t *)ctx->ws;
+        p_part = (float *)ctx->splitk.ptr;
+    }
 
     // The epilogue reads an f32 bias.
     const float *bp = nullptr;
@@ -1932,14 +1992,11 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         if (bias->dtype == LX2V_DTYPE_F32) {
             bp = (const float *)bias->ptr;
         } else {
-            void *st = scr ? (void *)scr->ptr : nullptr;
-            if (!scr)
-                if (int rc = stage_for(ctx, N * 4, &st)) return rc;
             if (int rc = run(ctx, "convert", [&] {
-                    launch_convert(ctx->stream, bias->ptr, LX2V_DTYPE_BF16, st, LX2V_DTYPE_F32, N);
+                    launch_convert(ctx->stream, bias->ptr, LX2V_DTYPE_BF16, p_bias, LX2V_DTYPE_F32, N);
                 }))
                 return rc;
-            bp = (const float *)st;
+            bp = (const float *)p_bias;
         }
     }
 
@@ -1955,17 +2012,11 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
             mx.a = x->mxs + 4 * x_row;
             mx.a_rows = x->srows;
             mx.a_len = x->srows * 4 * (K / 128) - 4 * x_row;
-        } else if (scr) {
-            uint8_t *wq = scr->ptr + s_bias;
-            float *ws = (float *)(wq + al(rows * K));
+        } else {
+            uint8_t *wq = p_act;
+            float *ws = (float *)(p_act + al(rows * K));
             if (int rc = run(ctx, "act_quant_e4m3", [&] { launch_act_quant(ctx->stream, xp, x->dtype, rows, K, wq, ws); }))
                 return rc;
-            q = wq;
-            s = ws;
-        } else {
-            uint8_t *wq;
-            float *ws;
-            if (int rc = act_quant_into_ws(ctx, xp, x->dtype, rows, K, &wq, &ws)) return rc;
             q = wq;
             s = ws;
         }
@@ -1976,16 +2027,7 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         mx.gate = gate;
         if (fp8_mfma) {
             if (fp8_grouped) mx.wgs = w->sscale;
-            const Fp8Plan plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx, fp8_grouped, y->dtype, act,
-                                               gate != nullptr, scr == nullptr);
-            if (plan.splits > 1) {  // split K: the partial sums' workspace
-                if (int rc = ensure(ctx, &ctx->splitk.ptr, &ctx->splitk.bytes, (size_t)plan.splits * rows * N * 4,
-                                    "split-K workspace alloc"))
-                    return rc;
-                mx.part = (float *)ctx->splitk.ptr;
-            }
-            if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1 && plan.kernel != 6)  // built with grouped scales
-                return fail(LX2V_ERR_UNSUPPORTED, "no grouped-scale fp8 kernel for configuration %d", plan.kernel);
+            if (plan.splits > 1) mx.part = p_part;
             // Profile name: the kernel configuration and the operand forms,
             // e.g. "gemm_fp8_e4m3.c0.g128.mxout".
             char pname[64];
@@ -2012,16 +2054,11 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     auto bf16_x = [&](const uint16_t **xb) -> int {
         *xb = (const uint16_t *)xp;
         if (x->dtype != LX2V_DTYPE_F32) return LX2V_OK;
-        void *dst = scr ? (void *)(scr->ptr + s_bias) : nullptr;
-        if (!scr) {
-            if (int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, rows * K * 2, "workspace alloc")) return rc;
-            dst = ctx->ws;
-        }
         if (int rc = run(ctx, "convert", [&] {
-                launch_convert(ctx->stream, xp, LX2V_DTYPE_F32, dst, LX2V_DTYPE_BF16, rows * K);
+                launch_convert(ctx->stream, xp, LX2V_DTYPE_F32, p_act, LX2V_DTYPE_BF16, rows * K);
             }))
             return rc;
-        *xb = (const uint16_t *)dst;
+        *xb = (const uint16_t *)p_act;
         return LX2V_OK;
     };
     if (native_bf16) {
@@ -2035,21 +2072,8 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     }
     const char *name = w->fmt == LX2V_WFMT_Q8 ? "gemm_w16_q8" : w->fmt == LX2V_WFMT_Q4 ? "gemm_w16_q4" : "gemm_w16_fp8";
     if (gemm_w16_dma_supported(w, rows)) {
-        // The direct-to-LDS kernel reads bf16 activations; f32 ones are
-        // rounded (RNE, as the register-staged loader would) into the workspace.
-        const uint16_t *xb = (const uint16_t *)xp;
-        if (x->dtype == LX2V_DTYPE_F32) {
-            void *dst = scr ? (void *)(scr->ptr + s_bias) : nullptr;
-            if (!scr) {
-                if (int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, rows * K * 2, "workspace alloc")) return rc;
-                dst = ctx->ws;
-            }
-            if (int rc = run(ctx, "convert", [&] {
-                    launch_convert(ctx->stream, xp, LX2V_DTYPE_F32, dst, LX2V_DTYPE_BF16, rows * K);
-                }))
-                return rc;
-            xb = (const uint16_t *)dst;
-        }
+        const uint16_t *xb;
+        if (int rc = bf16_x(&xb)) return rc;
         const int cfg = plan_gemm_w16_dma(ctx->num_cu, rows, N);
         if (int rc = run(ctx, name, [&] {
                 launch_gemm_w16_dma(ctx->stream, cfg, xb, w, bp, act, yp, y->dtype, rows);
@@ -2082,20 +2106,44 @@ int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size
 
 // No counterpart in the reference: `linear` for callers that cannot
 // allocate.  The workspaces come from the device scratch array of
-// lx2v_scratch.hip (kScratchBytes per device, resolved at create); no
-// hipMalloc / hipFree, no profiler events.
+// lx2v_scratch.hip (kScratchBytes per device); no hipMalloc / hipFree, no
+// profiler events.  The array is held by one context at a time: while
+// another context's work on it is still in flight the call fails with
+// LX2V_ERR_BUSY and enqueues nothing.
 int lx2v_hip_linear_noalloc(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
                             const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act, lx2v_hip_buf *y,
                             size_t y_row) {
     NEED(ctx, "ctx");
+    if (int rc = set_dev(ctx)) return rc;
     hipError_t e = hipSuccess;
-    void *p = scratch_ptr(ctx->device, &e);
-    if (!p) return hip_fail(e == hipSuccess ? hipErrorNotInitialized : e, "linear_noalloc: device scratch");
+    void *p = nullptr;
+    if (ctx->capturing) {
+        // Nothing runs until the graph is launched, and each launch claims
+        // the array (lx2v_hip_graph_launch); no event may be queried here.
+        p = scratch_address(ctx->device, &e);
+        if (!p) return hip_fail(e, "linear_noalloc: device scratch");
+    } else {
+        switch (scratch_claim(ctx->device, ctx, ctx->scratch_done, &p, &e)) {
+            case ScratchClaim::Busy:
+                return fail(LX2V_ERR_BUSY,
+                            "linear_noalloc: the device scratch is in use by another context's work in flight on "
+                            "device %d", ctx->device);
+            case ScratchClaim::Error: return hip_fail(e, "linear_noalloc: device scratch");
+            case ScratchClaim::Held: break;
+        }
+    }
     const lx2v::Scratch scr{(uint8_t *)p, kScratchBytes};
     const bool prof = ctx->prof.on;
     ctx->prof.on = false;  // no event creation inside this call
-    const int rc = linear_run(ctx, x, x_row, rows, w, bias, act, y, y_row, nullptr, &scr);
+    int rc = linear_run(ctx, x, x_row, rows, w, bias, act, y, y_row, nullptr, &scr);
     ctx->prof.on = prof;
+    if (ctx->capturing) {
+        ctx->capture_scratch = true;
+        return rc;
+    }
+    const hipError_t er = hipEventRecord(ctx->scratch_done, ctx->stream);
+    if (er != hipSuccess && rc == LX2V_OK) rc = hip_fail(er, "hipEventRecord(linear_noalloc)");
+    scratch_unlock(ctx->device);
     return rc;
 }
 

@@ -92,22 +92,34 @@ namespace lx2v {
 
 // Device scratch of lx2v_hip_linear_noalloc (lx2v_scratch.hip): a
 // file-scope device array of kScratchBytes per device, its address resolved
-// by scratch_setup (called by lx2v_hip_create with the device current) and
-// read back with scratch_ptr (null + the error if setup failed or never ran).
+// by scratch_setup (with the device current; a failure is retried by the
+// next setup or claim).
 constexpr size_t kScratchBytes = size_t(48) << 20;
 struct Scratch {
     uint8_t *ptr;
     size_t bytes;
 };
 hipError_t scratch_setup(int device);
-void *scratch_ptr(int device, hipError_t *err);
+// The array's address (null + *err if it cannot be resolved), for a call
+// being captured into a graph: the graph's launches claim the array.
+void *scratch_address(int device, hipError_t *err);
+// Claim the device's array for one call of `owner` (a context), whose
+// completion `owner_done` records on its stream.  Held: *ptr is the array,
+// the device lock is held -- enqueue the work, record owner_done, then
+// scratch_unlock.  Busy: another context's work on the array has not
+// completed.  Error: *err says why (no lock held for Busy / Error).
+enum class ScratchClaim { Held, Busy, Error };
+ScratchClaim scratch_claim(int device, const void *owner, hipEvent_t owner_done, void **ptr, hipError_t *err);
+void scratch_unlock(int device);
+// `owner` is going away: it no longer holds the array.
+void scratch_release(int device, const void *owner);
 
 }  // namespace lx2v
 
 // Everything a context mutates lives in it: two contexts driven from two
 // threads share no host state (the only process-wide state is each thread's
-// last-error string and the per-device scratch addresses, resolved once
-// under a lock).
+// last-error string and, per device, the scratch array's address and which
+// context holds it, under that device's lock).
 struct lx2v_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -129,6 +141,11 @@ struct lx2v_hip_ctx {
     lx2v::Stage resid;     // linear_residual's output where the add cannot ride in the GEMM
     lx2v::Stage attn;      // split attention's partial sums (attention_split)
     lx2v::Stage splitk;    // split-K fp8 GEMM partial sums (Fp8Plan::splits)
+    // The no-alloc entry point's hold on the device scratch: recorded after
+    // each of its calls (and each launch of a graph that holds such calls);
+    // capture_scratch: the capture in progress recorded one.
+    hipEvent_t scratch_done = nullptr;
+    bool capture_scratch = false;
 };
 
 namespace lx2v {

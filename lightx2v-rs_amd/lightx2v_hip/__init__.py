@@ -22,7 +22,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblightx2v_hip.so")
 
-OK, ERR_NO_DEVICE, ERR_BAD_SHAPE, ERR_ALIAS, ERR_HIP, ERR_BAD_ARG, ERR_OOM, ERR_UNSUPPORTED = range(8)
+OK, ERR_NO_DEVICE, ERR_BAD_SHAPE, ERR_ALIAS, ERR_HIP, ERR_BAD_ARG, ERR_OOM, ERR_UNSUPPORTED, ERR_BUSY = range(9)
 ACT_NONE, ACT_GELU_TANH = 0, 1
 DTYPE_F32, DTYPE_BF16, DTYPE_E4M3, DTYPE_MXE4M3 = 0, 1, 2, 3
 WFMT_F32, WFMT_Q8, WFMT_Q4, WFMT_FP8 = 0, 1, 2, 3

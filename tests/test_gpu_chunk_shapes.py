@@ -13,7 +13,10 @@ quantizer of its f32 output), FFN down reads it (against the oracle on the
 decoded MX input), and the chain against the plain f32 oracle (4e-2).
 
 The same shapes with group-128 weights (the reference's FP8 default) run
-the grouped tiles.
+the grouped tiles, each asserted by name.  The bench's other timed launches
+run here too: the 30 layers' cross-attention K/V projections as one call
+over their concatenated weights (512 x 1536 -> 92160), and config 5's
+Wan2.2-5B shapes with the bf16 output the bench writes.
 """
 
 import numpy as np
@@ -27,11 +30,14 @@ pytestmark = pytest.mark.gpu
 
 DIM, FFN, TEXT, M = 1536, 8960, 512, 4680
 
-# (name, rows, K, N, act, configuration the planner picks on 256 CUs)
+# (name, rows, K, N, act, the configuration the planner picks on 256 CUs
+# with per-channel / group-128 weights, bf16 output)
 SITES = [
-    ("qkv", M, DIM, 3 * DIM, H.ACT_NONE, "c7"),
-    ("o", M, DIM, DIM, H.ACT_NONE, "c0"),
-    ("kv2", TEXT, DIM, 2 * DIM, H.ACT_NONE, "c3"),
+    ("qkv", M, DIM, 3 * DIM, H.ACT_NONE, "c7", "c6.g128"),
+    ("o", M, DIM, DIM, H.ACT_NONE, "c0", "c0.g128"),
+    ("kv2", TEXT, DIM, 2 * DIM, H.ACT_NONE, "c3", "c0.g128"),
+    ("ffn1", M, DIM, FFN, H.ACT_GELU_TANH, "c7", "c6.g128"),
+    ("ffn2", M, FFN, DIM, H.ACT_NONE, "c0", "c0.g128"),
 ]
 
 
@@ -61,9 +67,9 @@ def _profiled(be, fn):
     return {k for k in st if k.startswith("gemm")}
 
 
-@pytest.mark.parametrize("name,rows,K,N,act,cfg", SITES)
+@pytest.mark.parametrize("name,rows,K,N,act,cfg,cfg_g128", SITES)
 @pytest.mark.parametrize("group", ["channel", 128])
-def test_call_site(be, name, rows, K, N, act, cfg, group):
+def test_call_site(be, name, rows, K, N, act, cfg, cfg_g128, group):
     g = K if group == "channel" else 128
     x = O.bf16_round(normal(1001 + N, rows * K).reshape(rows, K))
     wf = normal(1002 + N, N * K, 0.02).reshape(N, K)
@@ -74,11 +80,7 @@ def test_call_site(be, name, rows, K, N, act, cfg, group):
     y16 = be.alloc(rows * N, H.DTYPE_BF16)
     y32 = be.alloc(rows * N, H.DTYPE_F32)
     ks = _profiled(be, lambda: be.linear(xb, 0, rows, w, bb, act, y16, 0))
-    want_cfg = f"gemm_fp8_e4m3.{cfg}" if group == "channel" else None
-    if want_cfg:
-        assert ks == {want_cfg}, ks
-    else:
-        assert len(ks) == 1 and next(iter(ks)).endswith(".g128"), ks
+    assert ks == {f"gemm_fp8_e4m3.{cfg if group == 'channel' else cfg_g128}"}, ks
     be.linear(xb, 0, rows, w, bb, act, y32, 0)
     got32 = be.download(y32).reshape(rows, N)
     got16 = be.download(y16).reshape(rows, N)
@@ -130,3 +132,58 @@ def test_ffn_pair_mx_handoff(be, group):
     w1d = O.fp8_dequantize(q1, s1, FFN, DIM, g1)
     hf = O.linear(x[p], w1d, b1, 1, nthreads=8)
     assert_close(got, O.linear(hf, w2d, b2, 0, nthreads=8), 4e-2, 0.3, what="FFN chain vs f32 oracle")
+
+
+def test_cross_kv_30_layers_one_call(be):
+    """The bench's per-step cross-attention K/V call: the 30 layers' K/V
+    weights concatenated by rows ([30 x 2 x 1536, 1536], per-channel scales
+    and bias concatenated the same way, as the bench builds them), one
+    linear over the 512 text tokens, 512 x 1536 -> 92160, on the persistent
+    overlapped-epilogue tile.  bf16 output == f32 output rounded over the
+    whole tensor; sampled rows against the oracle over every column."""
+    rows, K, N = TEXT, DIM, 30 * 2 * DIM
+    x = O.bf16_round(normal(1201, rows * K).reshape(rows, K))
+    wf = normal(1202, N * K, 0.02).reshape(N, K)
+    q, s = O.fp8_quantize(wf, N, K, K, True)
+    del wf
+    b = normal(1203, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, K)
+    xb, bb = _bf16_buf(be, x), be.upload(b)
+    y16 = be.alloc(rows * N, H.DTYPE_BF16)
+    y32 = be.alloc(rows * N, H.DTYPE_F32)
+    assert _profiled(be, lambda: be.linear(xb, 0, rows, w, bb, H.ACT_NONE, y16, 0)) == {"gemm_fp8_e4m3.c7"}
+    be.linear(xb, 0, rows, w, bb, H.ACT_NONE, y32, 0)
+    got32 = be.download(y32).reshape(rows, N)
+    assert np.array_equal(u32(be.download(y16)), u32(O.bf16_round(got32).ravel())), "bf16 output = f32 output rounded"
+    p = np.array([0, 1, 2, 31, 32, 255, 256, 300, 480, 510, 511])
+    assert_close(got32[p], oracle_w8a8(x[p], q, s, K, b, 0), *FP8_TIGHT, what="30-layer K/V call vs oracle")
+    # each layer's slice is that layer's own K/V linear
+    for l in (0, 17, 29):
+        sl = slice(l * 2 * DIM, (l + 1) * 2 * DIM)
+        assert_close(got32[p][:, sl], oracle_w8a8(x[p], q[sl], s[sl], K, b[sl], 0), *FP8_TIGHT, what=f"layer {l}")
+
+
+# Config 5 (Wan2.2-TI2V-5B, per-token e4m3 activations) with the bf16 output
+# the bench writes: (rows, K, N, the configuration the planner picks).
+CFG5 = [(2640, 3072, 9216, "c4"), (2640, 3072, 3072, "c4"), (2640, 3072, 14336, "c7"), (2640, 14336, 3072, "c4"),
+        (880, 3072, 9216, "c4"), (880, 3072, 3072, "c3"), (880, 3072, 14336, "c5"), (880, 14336, 3072, "c0k2")]
+
+
+@pytest.mark.parametrize("rows,K,N,cfg", CFG5)
+def test_cfg5_bf16_output(be, rows, K, N, cfg):
+    x = O.bf16_round(normal(1051, rows * K).reshape(rows, K))
+    wf = normal(1052 + N, N * K, 0.015).reshape(N, K)
+    q, s = O.fp8_quantize(wf, N, K, K, True)
+    b = normal(1053, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, K)
+    xb, bb = _bf16_buf(be, x), be.upload(b)
+    y16 = be.alloc(rows * N, H.DTYPE_BF16)
+    y32 = be.alloc(rows * N, H.DTYPE_F32)
+    assert _profiled(be, lambda: be.linear(xb, 0, rows, w, bb, H.ACT_NONE, y16, 0)) == {f"gemm_fp8_e4m3.{cfg}"}
+    be.linear(xb, 0, rows, w, bb, H.ACT_NONE, y32, 0)
+    got32 = be.download(y32).reshape(rows, N)
+    got16 = be.download(y16).reshape(rows, N)
+    assert np.array_equal(u32(got16), u32(O.bf16_round(got32))), "bf16 output = f32 output rounded"
+    p = _pick(rows, N)[:48]
+    assert_close(got16[p], oracle_w8a8(x[p], q, s, K, b, 0), 4e-3, 1e-2, what="cfg5 bf16 out vs oracle(e4m3 acts)")
+    assert_close(got32[p], oracle_w8a8(x[p], q, s, K, b, 0), *FP8_TIGHT, what="cfg5 f32 out vs oracle(e4m3 acts)")

@@ -163,6 +163,40 @@ def test_fp8_split_k_row_offsets(be, monkeypatch):
     assert_close(two, oracle_w8a8(x[37:337], q, s, K, b, H.ACT_GELU_TANH), *FP8_TIGHT, what="split, offsets")
 
 
+@pytest.mark.parametrize("cfg,act,ydt", [(6, H.ACT_GELU_TANH, H.DTYPE_BF16), (6, H.ACT_NONE, H.DTYPE_F32),
+                                         (6, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (7, H.ACT_GELU_TANH, H.DTYPE_BF16),
+                                         (7, H.ACT_NONE, H.DTYPE_BF16), (7, H.ACT_GELU_TANH, H.DTYPE_MXE4M3)])
+def test_fp8_forced_persistent_vs_config0(be, monkeypatch, cfg, act, ydt):
+    """The persistent 256 x 128 tiles forced (LIGHTX2V_HIP_FP8_CFG, read per
+    call) against the one-shot configuration 0, bit for bit over the whole
+    output: 1937 rows (ragged: 7 x 256 + 145) x 4608 channels is 288 tiles,
+    so part of the grid walks two; GELU or none; bf16, f32 (configuration 6;
+    7 stores bf16 or MX only) and MX e4m3 output.  Both share the K order of
+    every sum, so only a fault in the walk or the epilogue could differ."""
+    M, K, N = 1937, 1536, 4608
+    x = normal(3201, M * K).reshape(M, K)
+    _, q, s = fp8_weight(3202, N, K, K)
+    w = be.weight_fp8(q, s, N, K, K)
+    xb, bb = be.upload(x), be.upload(normal(3203, N, 0.01))
+    mx = ydt == H.DTYPE_MXE4M3
+    sfx = ".mxout" if mx else ""
+
+    def run(c):
+        monkeypatch.setenv("LIGHTX2V_HIP_FP8_CFG", str(c))
+        y = be.alloc_mx(M, N) if mx else be.alloc(M * N, ydt)
+        _, names = _kernels(be, lambda: be.linear(xb, 0, M, w, bb, act, y, 0))
+        assert {k for k in names if k.startswith("gemm")} == {f"gemm_fp8_e4m3.c{c}{sfx}"}, names
+        return be.download_mx(y, M, N) if mx else (u32(be.download(y)),)
+
+    want, got = run(0), run(cfg)
+    assert all(np.array_equal(a, b) for a, b in zip(want, got))
+    if not mx:
+        p = np.arange(0, M, 97)
+        y = got[0].view(np.float32).reshape(M, N)[p]
+        tol = FP8_TIGHT if ydt == H.DTYPE_F32 else (4e-3, 1e-2)
+        assert_close(y, oracle_w8a8(x[p], q, s, K, normal(3203, N, 0.01), act), *tol, what=f"c{cfg} vs oracle")
+
+
 def test_fp8_no_bias(be):
     M, K, N = 96, 640, 320
     x = normal(8, M * K).reshape(M, K)

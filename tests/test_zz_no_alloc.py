@@ -1,13 +1,17 @@
 """lx2v_hip_linear_noalloc (no counterpart in the reference; for callers that
-cannot allocate) against lx2v_hip_linear through the C ABI: the same
-kernels run, so outputs are bit-identical.  Two calls in a row, the second
-with a smaller input (the scratch keeps the first call's contents); the
-paths that use scratch (per-token e4m3 activations, a bf16 bias's f32
-copy, f32 activations' bf16 copy for the bf16 GEMM) and the ones that need
-none; capture in a HIP graph on a fresh context, where any workspace
-growth would fail, replayed against the eager result; a call too large for
-the scratch refused with a message.
+cannot allocate) against lx2v_hip_linear through the C ABI: the same plan
+and kernels run, so outputs are bit-identical.  Two calls in a row, the
+second with a smaller input (the scratch keeps the first call's contents);
+the paths that use scratch (per-token e4m3 activations, a bf16 bias's f32
+copy, f32 activations' bf16 copy for the bf16 GEMM, split K's partial sums)
+and the ones that need none; capture in a HIP graph on a fresh context,
+where any workspace growth would fail, replayed against the eager result;
+a call too large for the scratch refused with a message; two contexts on
+one device, the second refused with LX2V_ERR_BUSY while the first one's
+work on the scratch is in flight.
 """
+
+import os
 
 import numpy as np
 import pytest
@@ -125,6 +129,91 @@ def test_graph_capture_on_a_fresh_context():
         fresh.close()
 
 
+def _profiled_names(be, fn):
+    be.profile_reset()
+    be.profile_enable(True)
+    try:
+        fn()
+        st = be.profile_stats()
+    finally:
+        be.profile_enable(False)
+        be.profile_reset()
+    return {k for k in st if k.startswith("gemm")}
+
+
+def _one_pass(fn):
+    os.environ["LIGHTX2V_HIP_FP8_SPLITK"] = "0"
+    try:
+        return fn()
+    finally:
+        os.environ.pop("LIGHTX2V_HIP_FP8_SPLITK")
+
+
+@pytest.mark.parametrize("M,K,N,cfg", [(880, 14336, 3072, "c0k2"), (300, 8192, 1536, "c0k2")])
+def test_split_k_shapes(be, M, K, N, cfg):
+    """Shapes where linear splits K (config 5's FFN down at M = 880 first,
+    then a smaller one: the scratch keeps the first call's partial sums):
+    the no-alloc call plans the same split, its partial sums in the
+    scratch, bit for bit; the one-pass kernel's sums differ, so the split
+    did run."""
+    _, q, s = fp8_weight(21 + M, N, K, K, 0.015)
+    w = be.weight_fp8(q, s, N, K, K)
+    x = _X(be, normal(22 + M, M * K).reshape(M, K), H.DTYPE_BF16)
+    bias = be.upload(normal(23 + M, N, 0.01))
+    y = be.alloc(M * N, H.DTYPE_BF16)
+    assert _profiled_names(be, lambda: be.linear(x.buf, 0, M, w, bias, H.ACT_NONE, y, 0)) == {f"gemm_fp8_e4m3.{cfg}"}
+    a, b = _pair(be, x, w, bias, H.ACT_NONE, N, H.DTYPE_BF16)
+    assert np.array_equal(u32(a), u32(b))
+    a, b = _pair(be, x, w, bias, H.ACT_NONE, N, H.DTYPE_F32)
+    assert np.array_equal(u32(a), u32(b))
+    one = _one_pass(lambda: _pair(be, x, w, bias, H.ACT_NONE, N, H.DTYPE_F32))
+    assert np.array_equal(u32(one[0]), u32(one[1]))
+    assert not np.array_equal(u32(one[0]), u32(a)), "the split and one-pass f32 sums should differ somewhere"
+    # pre-quantized activations with GELU and f32 output: partial sums only
+    xq = be.alloc_e4m3(M, K)
+    be.quantize_act(x.buf, 0, M, xq)
+    y1, y2 = be.alloc(M * N), be.alloc(M * N)
+    be.linear(xq, 0, M, w, bias, H.ACT_GELU_TANH, y1, 0)
+    be.linear_noalloc(xq, 0, M, w, bias, H.ACT_GELU_TANH, y2, 0)
+    assert np.array_equal(u32(be.download(y1)), u32(be.download(y2)))
+
+
+def test_second_context_busy_while_first_in_flight(be):
+    """The device's scratch is held by one context at a time: a second
+    context's call while the first one's scratch work is still running fails
+    with LX2V_ERR_BUSY (and enqueues nothing); once that work is done the
+    second context takes the array over, and then the first is refused until
+    the second's work is done."""
+    M, K, N = 880, 14336, 3072
+    _, q, s = fp8_weight(31, N, K, K, 0.015)
+    other = H.HipBackend(0)
+    try:
+        wa, wb = be.weight_fp8(q, s, N, K, K), other.weight_fp8(q, s, N, K, K)
+        xa = _buf(be, normal(32, M * K).reshape(M, K), H.DTYPE_BF16)
+        xb = _buf(other, normal(32, M * K).reshape(M, K), H.DTYPE_BF16)
+        ya, yb = be.alloc(M * N), other.alloc(M * N)
+        be.sync()
+        for _ in range(40):  # ~2 ms of queued scratch work on the first context
+            be.linear_noalloc(xa, 0, M, wa, None, H.ACT_NONE, ya, 0)
+        with pytest.raises(H.HipError) as e:
+            other.linear_noalloc(xb, 0, M, wb, None, H.ACT_NONE, yb, 0)
+        assert e.value.status == H.ERR_BUSY and "another context" in str(e.value)
+        be.sync()
+        for _ in range(40):
+            other.linear_noalloc(xb, 0, M, wb, None, H.ACT_NONE, yb, 0)
+        with pytest.raises(H.HipError) as e:
+            be.linear_noalloc(xa, 0, M, wa, None, H.ACT_NONE, ya, 0)
+        assert e.value.status == H.ERR_BUSY
+        other.sync()
+        be.linear_noalloc(xa, 0, M, wa, None, H.ACT_NONE, ya, 0)
+        ref = be.alloc(M * N)
+        be.linear(xa, 0, M, wa, None, H.ACT_NONE, ref, 0)
+        assert np.array_equal(u32(be.download(ya)), u32(be.download(ref)))
+        assert np.array_equal(u32(other.download(yb)), u32(be.download(ref)))
+    finally:
+        other.close()
+
+
 def test_too_large_is_refused(be):
     M, K, N = 6000, 8960, 256  # 6000 x 8960 e4m3 codes > 48 MiB
     _, q, s = fp8_weight(15, N, K, K)
@@ -134,4 +223,9 @@ def test_too_large_is_refused(be):
     with pytest.raises(H.HipError) as e:
         be.linear_noalloc(x, 0, M, w, None, H.ACT_NONE, y, 0)
     assert e.value.status == H.ERR_UNSUPPORTED and "scratch" in str(e.value)
-    be.linear_noalloc(x, 0, 5000, w, None, H.ACT_NONE, y, 0)  # 5000 x 8960 fits
+    # 5000 rows: 42.7 MiB of codes, but linear splits K two ways here and the
+    # partial sums (9.8 MiB) do not fit beside them; 4000 rows fit both
+    with pytest.raises(H.HipError) as e:
+        be.linear_noalloc(x, 0, 5000, w, None, H.ACT_NONE, y, 0)
+    assert e.value.status == H.ERR_UNSUPPORTED
+    be.linear_noalloc(x, 0, 4000, w, None, H.ACT_NONE, y, 0)
