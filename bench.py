@@ -5,27 +5,33 @@ Wan2.1-1.3B block-linear set in FP8 for one 3-frame chunk (M = 4680
 tokens), 30 layers x 4 DMD steps, 7 linears per layer-step (self-attn QKV,
 O; cross-attn Q, K/V on 512 text tokens, O; FFN up with GELU, FFN down),
 with 30 distinct layers of random-init FP8 per-output-channel weights
-resident in HBM (1.48 GB) and bf16 activations, which each linear quantizes
-per token to e4m3 before its fp8 GEMM -- except the FFN hand-off: FFN up
-writes MX e4m3 (one power-of-two scale per 32 columns of a row, quantized in
-its GEMM epilogue) and FFN down reads it directly.  The cross-attention K/V
-projections of the 30 layers all read the same 512 text tokens, so each
-step runs them as one linear over the layers' concatenated weights
-[30 x 3072, 1536] (the reference computes them per prompt, one linear per
-layer: dit.rs:470-492; head_split reads each layer's slice of the output by
-stride).  The same chunk with a bf16 FFN hand-off is timed too
-(ms_per_chunk_bf16_ffn_handoff).  One "step" is one chunk: 724
+resident in HBM (1.48 GB).  Activations are ~N(0,1), rounded to bf16, and
+reach each linear in the form its producer writes it in the DiT block of
+this backend: per-token e4m3 (codes + one f32 scale per row) from the fused
+AdaLN norms for QKV, cross-attn Q and FFN up (layer_norm / residual_norm
+quantize in the same pass that writes them) and for the text tokens
+(quantized once per prompt); MX e4m3 (one power-of-two scale per 32
+columns of a row) from attention's epilogue for O and cross-attn O and from
+FFN up's epilogue for FFN down.  So no linear of the chunk runs a separate
+quantization pass.  The same chunk on bf16 inputs, where each linear first
+quantizes its input per token to e4m3, is timed too
+(ms_per_chunk_bf16_input), and so is the one with a bf16 FFN hand-off.
+The cross-attention K/V projections of the 30 layers all read the same 512
+text tokens, so each step runs them as one linear over the layers'
+concatenated weights [30 x 3072, 1536] (the reference computes them per
+prompt, one linear per layer: dit.rs:470-492; head_split reads each layer's
+slice of the output by stride).  One "step" is one chunk: 724
 Backend::linear calls (6 per layer-step, dit.rs:602-759, plus one K/V call
 per step).  Inputs are synthetic and resident before timing starts.
 
 Timed two ways over the same calls: eagerly (one C-ABI call per linear from
 Python) and as one replayed HIP graph of the whole chunk; `value` is the
 faster.  The roofline object covers the dominant kernel, the fp8 GEMM: the
-chunk's 840 GEMMs are run back to back (eagerly) on pre-quantized
-activations inside a HIP-event region on the context stream, so the
-average launch duration is the GEMM's alone (rocprofv3 --kernel-trace of
-this command with --no-graph reports the same kernel's average).  The CPU
-oracle is timed on a bounded row sample of the same GEMMs beside it.
+chunk's 724 GEMM launches run back to back (eagerly) inside a HIP-event
+region on the context stream, so the average launch duration is the GEMM's
+alone (rocprofv3 --kernel-trace of `bench.py --gemm-only` reports the same
+kernels' average).  The CPU oracle is timed on a bounded row sample of the
+same GEMMs beside it.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-graph]
 """
@@ -433,6 +439,8 @@ def main():
     log(f"bench: setup {time.perf_counter() - t0:.1f} s, {wbytes / 1e9:.2f} GB FP8 weights resident")
 
     def chunk(mx_handoff):
+        """The chunk on bf16 inputs: each linear quantizes its input per
+        token first (FFN up -> FFN down in MX e4m3, or in bf16)."""
         def run():
             for _ in range(DMD):
                 be.linear(acts["x_text"], 0, TEXT, *kv_all, 0, outs["kv2"], 0)
@@ -449,21 +457,30 @@ def main():
                         be.linear(x, 0, rows, w, b, act, y, 0)
         return run
 
-    step = chunk(True)
-
     step_flops = flops_of(GEMMS) * LAYERS * DMD
     n_linear = ((len(GEMMS) - 1) * LAYERS + 1) * DMD
 
-    # The chunk's GEMMs alone, on pre-quantized activations (FFN up writes
-    # the MX buffer FFN down reads; the other inputs per-token e4m3).
+    # The linears' inputs in the forms their producers write them in the DiT
+    # block: per-token e4m3 from the fused norms (QKV, cross Q, FFN up) and
+    # for the text (once per prompt); MX e4m3 from attention's epilogue (O,
+    # cross O) and from FFN up's (FFN down).
+    MX_IN = ("x_o", "x_o2")
     per_token = [g for g in GEMMS if g[0] != "ffn2"]
-    xq = {src: be.alloc_e4m3(rows, k) for _, rows, _, k, _, src in per_token}
+    qin = {}
     for _, rows, _, k, _, src in per_token:
-        be.quantize_act(acts[src], 0, rows, xq[src])
-    gx = {name: (ffn_mx if name == "ffn2" else xq[src]) for name, _, _, _, _, src in GEMMS}
+        if src in MX_IN:
+            qin[src] = be.alloc_mx(rows, k)
+            be.quantize_mx(acts[src], 0, rows, qin[src])
+        else:
+            qin[src] = be.alloc_e4m3(rows, k)
+            be.quantize_act(acts[src], 0, rows, qin[src])
+    gx = {name: (ffn_mx if name == "ffn2" else qin[src]) for name, _, _, _, _, src in GEMMS}
     gy = {name: (ffn_mx if name == "ffn1" else outs[name]) for name, _, _, _, _, _ in GEMMS}
+    # the bf16-input chunk's per-token quantization, timed on its own
+    xq = {src: be.alloc_e4m3(rows, k) for _, rows, _, k, _, src in per_token}
 
     def gemm_step():
+        """The headline chunk: every linear on its producer-written input."""
         for _ in range(DMD):
             be.linear(gx["kv2"], 0, TEXT, *kv_all, 0, gy["kv2"], 0)
             for lw in layers:
@@ -472,6 +489,8 @@ def main():
                         continue
                     w, b = lw[name]
                     be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
+
+    step = gemm_step
 
     def calibrate():
         """The rocprofv3 FETCH_SIZE / WRITE_SIZE calibration: one plain
@@ -509,7 +528,10 @@ def main():
         ms_rand = timed(gemm_step, args.steps, args.warmup)
         for _, rows, _, k, _, src in per_token:
             be.fill_normal(acts[src], 1, 0.0)
-            be.quantize_act(acts[src], 0, rows, xq[src])
+            if src in MX_IN:
+                be.quantize_mx(acts[src], 0, rows, qin[src])
+            else:
+                be.quantize_act(acts[src], 0, rows, qin[src])
         be.sync()
         ms_zero = timed(gemm_step, args.steps, args.warmup)
         log(f"bench: --data-probe: random {ms_rand:.2f} ms, zero {ms_zero:.2f} ms per chunk of GEMMs")
@@ -521,32 +543,44 @@ def main():
         return
 
     # ---- eager, then one replayed graph per chunk --------------------------------
-    ms_eager = timed(step, args.steps, args.warmup)
-    log(f"bench: eager {ms_eager:.2f} ms/chunk, {step_flops / ms_eager / 1e9:.1f} TFLOP/s")
-    graph, ms_graph = None, None
-    if not args.no_graph:
-        be.graph_begin()
-        step()
-        graph = be.graph_end()
-        ms_graph = timed(graph.launch, args.steps, args.warmup)
-        log(f"bench: graph {ms_graph:.2f} ms/chunk, {step_flops / ms_graph / 1e9:.1f} TFLOP/s")
+    def eager_and_graph(fn, what):
+        ms_e = timed(fn, args.steps, args.warmup)
+        ms_g = None
+        if not args.no_graph:
+            be.graph_begin()
+            fn()
+            g = be.graph_end()
+            ms_g = timed(g.launch, args.steps, args.warmup)
+            g.free()
+        log(f"bench: {what}: eager {ms_e:.2f} ms/chunk" + (f", graph {ms_g:.2f} ms/chunk" if ms_g else ""))
+        return ms_e, ms_g
+
+    ms_eager, ms_graph = eager_and_graph(step, "chunk (producer-written e4m3 / MX inputs)")
     ms = min(ms_eager, ms_graph) if ms_graph else ms_eager
-    # the same chunk with the FFN hand-off in bf16 (per-token e4m3 inside FFN down)
+    log(f"bench: chunk {ms:.2f} ms, {step_flops / ms / 1e9:.1f} TFLOP/s")
+    # the chunk on bf16 inputs (each linear quantizes per token first)
+    ms_bf16_e, ms_bf16_g = eager_and_graph(chunk(True), "chunk on bf16 inputs")
+    ms_bf16_input = min(ms_bf16_e, ms_bf16_g) if ms_bf16_g else ms_bf16_e
+    # ... and with the FFN hand-off in bf16 too (per-token e4m3 inside FFN down)
     ms_bf16_handoff = timed(chunk(False), args.steps, args.warmup)
-    log(f"bench: bf16 FFN hand-off (eager) {ms_bf16_handoff:.2f} ms/chunk")
-    # the chunk with group-128 weights (the reference's FP8 format, quant.rs:21;
-    # FFN up -> down in bf16: MX input takes per-channel weights only), eager
+    log(f"bench: bf16 inputs and bf16 FFN hand-off (eager) {ms_bf16_handoff:.2f} ms/chunk")
+    # the chunk with group-128 weights (the reference's FP8 format, quant.rs:21),
+    # eager: QKV, cross Q, FFN up and the text K/V on their per-token e4m3
+    # inputs; O, cross O and FFN down on bf16 inputs, which they quantize per
+    # token (an MX input takes per-channel weights only; FFN up writes bf16)
     g128, kv_g128 = make_layers(128)
+    G128_BF16_IN = ("o", "o2", "ffn2")
 
     def chunk_g128():
         for _ in range(DMD):
-            be.linear(acts["x_text"], 0, TEXT, *kv_g128, 0, outs["kv2"], 0)
+            be.linear(qin["x_text"], 0, TEXT, *kv_g128, 0, outs["kv2"], 0)
             for lw in g128:
                 for name, rows, n, k, act, src in GEMMS:
                     if name == "kv2":
                         continue
                     w, b = lw[name]
-                    be.linear(acts[src], 0, rows, w, b, act, outs[name], 0)
+                    x = acts[src] if name in G128_BF16_IN else qin[src]
+                    be.linear(x, 0, rows, w, b, act, outs[name], 0)
 
     ms_g128 = timed(chunk_g128, args.steps, args.warmup)
     log(f"bench: group-128 weights (eager) {ms_g128:.2f} ms/chunk")
@@ -643,10 +677,10 @@ def main():
     log(f"bench: block linear path with norms: unfused {block['unfused']:.2f} ms/chunk, "
         f"fused {block['fused']:.2f} ms/chunk")
 
-    # ---- the dominant kernel alone: GEMMs on pre-quantized activations ----------
-    # (the chunk's GEMMs exactly: FFN up writes the MX buffer FFN down reads;
-    # the other inputs come per-token quantized; act_quant_step is the
-    # chunk's remaining per-token quantization)
+    # ---- the dominant kernel alone: the headline chunk's GEMM launches ----------
+    # (gemm_step: FFN up writes the MX buffer FFN down reads; the other inputs
+    # per-token or MX e4m3 as their producers write them).  act_quant_step is
+    # the per-token quantization the bf16-input chunk adds to its linears.
     def act_quant_step():
         for _ in range(DMD):
             be.quantize_act(acts["x_text"], 0, TEXT, xq["x_text"])
@@ -666,16 +700,20 @@ def main():
         _, t = be.profile_kernel(name)
         region[name] = t / reps
     gemm_ms = region["gemm_fp8_chunk"]
-    # algorithmic bytes of the chunk's GEMMs as run here: e4m3 X (MX for FFN
-    # down, + its scale bytes), e4m3 W + f32 channel scales, f32 bias, bf16 Y
-    # (MX e4m3 + scales for FFN up), averaged per launch
-    alg_step = sum((r * k + (r * k // 32 if nm == "ffn2" else r * 4)) * (1 if nm == "kv2" else LAYERS) +
+    # algorithmic bytes of the chunk's GEMMs as run here: e4m3 X (+ f32 row
+    # scales, or one E8M0 byte per 32 for the MX inputs of O, cross O and FFN
+    # down), e4m3 W + f32 channel scales, f32 bias, bf16 Y (MX e4m3 + scales
+    # for FFN up), averaged per launch
+    def x_bytes(nm, r, k):
+        return r * k + (r * k // 32 if nm in ("o", "o2", "ffn2") else r * 4)
+
+    alg_step = sum(x_bytes(nm, r, k) * (1 if nm == "kv2" else LAYERS) +
                    (n * k + n * 8 + (r * n + r * n // 32 if nm == "ffn1" else 2 * r * n)) * LAYERS
                    for nm, r, n, k, _, _ in GEMMS)
     alg_per_launch = alg_step / ((len(GEMMS) - 1) * LAYERS + 1)
     achieved = step_flops / gemm_ms / 1e9
     log(f"bench: GEMM-only {gemm_ms:.2f} ms/chunk ({gemm_ms * 1e3 / n_linear:.2f} us/launch, "
-        f"{achieved:.1f} TFLOP/s); act quant {region['act_quant_chunk']:.2f} ms/chunk")
+        f"{achieved:.1f} TFLOP/s); bf16 inputs' act quant {region['act_quant_chunk']:.2f} ms/chunk")
 
     # per-shape GEMM time (layer 0 weights, 50 back-to-back launches in a region)
     per = {}
@@ -697,7 +735,8 @@ def main():
             uq = be.profile_kernel("q_" + name)[1] * 1e3 / 50 / (LAYERS if name == "kv2" else 1)
         per[name] = {"shape": f"{rows}x{k}->{n}" + (f", the {LAYERS} layers in one call (per layer)"
                                                    if name == "kv2" else ""),
-                     "gemm_us": round(us, 2), "act_quant_us": round(uq, 2),
+                     "input": "MX e4m3" if name in ("o", "o2", "ffn2") else "per-token e4m3",
+                     "gemm_us": round(us, 2), "bf16_input_act_quant_us": round(uq, 2),
                      "tflops": round(2.0 * rows * n * k / (us * 1e-6) / 1e12, 1),
                      "pct_fp8_peak": round(2.0 * rows * n * k / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS * 100, 1)}
 
@@ -859,13 +898,15 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8",
-        "data": "synthetic (random-init FP8 per-channel weights ~N(0,0.02), bf16 activations ~N(0,1))",
+        "data": "synthetic (random-init FP8 per-channel weights ~N(0,0.02); activations ~N(0,1) rounded to bf16, "
+                "reaching each linear as its producer writes it: per-token or MX e4m3)",
         "config": {
             "workload": "cfg4: Wan2.1-1.3B 30-layer x 4-step FP8 block-linear set, one 3-frame chunk",
             "tokens": M, "text_tokens": TEXT, "layers": LAYERS, "dmd_steps": DMD,
             "gemms_per_layer_step": len(GEMMS), "linear_calls_per_step": n_linear, "tflop_per_step": round(step_flops / 1e12, 3),
-            "activations": "bf16 in/out, per-token dynamic e4m3 inside linear; FFN up -> FFN down in MX e4m3 "
-                           "(per-32-column power-of-two scales, quantized in FFN up's epilogue)",
+            "activations": "bf16 values ~N(0,1) in the form each linear's producer writes: per-token e4m3 "
+                           "(fused norms: QKV, cross Q, FFN up; the text once per prompt), MX e4m3 (attention's "
+                           "epilogue: O, cross O; FFN up's epilogue: FFN down); bf16 out (FFN up: MX e4m3)",
             "weights_gb": round(wbytes / 1e9, 3),
             "cross_kv": "the 30 layers' K/V projections (512 text tokens) as one linear per step over their "
                         "concatenated weights",
@@ -874,7 +915,9 @@ def main():
         "ms_per_chunk": round(ms, 3),
         "ms_per_chunk_eager": round(ms_eager, 3),
         "ms_per_chunk_graph": round(ms_graph, 3) if ms_graph else None,
-        "ms_per_chunk_bf16_ffn_handoff": round(ms_bf16_handoff, 3),
+        "ms_per_chunk_bf16_input": round(ms_bf16_input, 3),
+        "ms_per_chunk_bf16_input_eager_graph": [round(ms_bf16_e, 3), round(ms_bf16_g, 3) if ms_bf16_g else None],
+        "ms_per_chunk_bf16_input_bf16_ffn_handoff": round(ms_bf16_handoff, 3),
         "ms_per_chunk_g128_weights": round(ms_g128, 3),
         "gemm_only_ms_per_chunk": round(gemm_ms, 3),
         "block_path_ms_per_chunk": {
@@ -884,7 +927,8 @@ def main():
                     "attention and the KV cache excluded); fused = the norms write the FP8 linears' e4m3 inputs "
                     "in the same pass and FFN down's epilogue does the gate-residual add",
         },
-        "act_quant_ms_per_chunk": round(region["act_quant_chunk"], 3),
+        "act_quant_ms_per_chunk": 0.0,
+        "act_quant_ms_per_chunk_bf16_input": round(region["act_quant_chunk"], 3),
         "per_gemm": per,
         "head_split": head_split,
         "causal_attention": attn,
@@ -900,15 +944,17 @@ def main():
             "kernel": ("fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma 256x128 / 128x128 tiles, the persistent "
                        "k_gemm_fp8_ov 256x128 with the epilogue overlapped for QKV and FFN up)"),
             "avg_launch_us": round(gemm_ms * 1e3 / n_linear, 2),
-            "hbm_gbs": round(traffic / (gemm_ms * 1e-3 / n_linear) / 1e9, 1) if traffic else None,
+            # traffic (calibrated FETCH_SIZE + WRITE_SIZE) counts the L2's misses,
+            # served by the 256 MB Infinity Cache or by HBM: gfx950's counters
+            # have no HBM-only byte count, so this is L2-miss traffic per second
+            "l2_miss_gbs": round(traffic / (gemm_ms * 1e-3 / n_linear) / 1e9, 1) if traffic else None,
+            "alg_gbs": round(alg_per_launch / (gemm_ms * 1e-3 / n_linear) / 1e9, 1),
             "alg_bytes_per_launch": round(alg_per_launch),
             "launches_per_step": n_linear,
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
-    if graph:
-        graph.free()
     be.close()
 
 

@@ -31,6 +31,11 @@
 #ifndef LX2V_FP8_SKEW
 #define LX2V_FP8_SKEW 1
 #endif
+// ... with the second slice's fragment reads between the first slice's
+// MFMAs (on unless built with -DLX2V_FP8_EARLY=0).
+#ifndef LX2V_FP8_EARLY
+#define LX2V_FP8_EARLY 1
+#endif
 
 namespace lx2v {
 
@@ -412,25 +417,29 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // (probed on gfx950), so with MX activations lane half h takes chunks h
     // and h + 2 and each MX block is one hardware scale block.  Unscaled, any
     // K order shared by both operands is the same product.
-    auto read_half = [&](int buf, int kk, Frag &f) {
+    // read_frag(buf, kk, f, i): fragment i of slice kk (the wave's A row
+    // blocks 0 .. TM - 1, then its B column blocks).
+    auto read_frag = [&](int buf, int kk, Frag &f, int i) {
         const uint8_t *s = smem + buf * STAGE;
         const uint32_t c0 = AM ? kk * 4 + (lane >> 5) : kk * 4 + fhalf;
         const uint32_t c1 = AM ? c0 + 2 : c0 + 1;
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
+        if (i < TM) {
             const uint32_t row = wm * WM + i * 32 + frow;
             u32x4 lo = *(const u32x4 *)(s + ((row * BKB + (dma_slot<BKB>(row, c0) << 4)) & AMASK));
             u32x4 hi = *(const u32x4 *)(s + ((row * BKB + (dma_slot<BKB>(row, c1) << 4)) & AMASK));
             f.a[i] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
+        } else {
+            const int j = i - TM;
             const uint32_t row = BM + wn * WN + j * 32 + frow;
             const uint32_t rb = row - BM;
             u32x4 lo = *(const u32x4 *)(s + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c0) << 4)) & BMASK));
             u32x4 hi = *(const u32x4 *)(s + BM * BKB + ((rb * BKB + (dma_slot<BKB>(row, c1) << 4)) & BMASK));
             f.b[j] = (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
         }
+    };
+    auto read_half = [&](int buf, int kk, Frag &f) {
+#pragma unroll
+        for (int i = 0; i < TM + TN; i++) read_frag(buf, kk, f, i);
     };
     // MX activations: each of the wave's rows' 4 scale bytes of the stage in
     // slot buf, and the scale operand of slice kk (lane l holds block 2 s +
@@ -458,7 +467,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // barrier, the loads held both waves of a SIMD off the MFMA pipe (7-9%
     // at one workgroup per CU).  dkt < 0: no loads.
     f32x16 part[GS ? TN : 1][GS ? TM : 1];  // grouped scales: this stage's partial sums
-    auto mfma_half = [&](const Frag &f, const SOp &as, int kk, int nbase, int dkt, int dbuf) {
+    // after(m): called after the half's MFMA m (0 .. TN TM - 1), behind the
+    // load it may issue -- the skewed loop reads the next slice's fragments
+    // there, so that they land while the half's later MFMAs run.
+    auto mfma_half_then = [&](const Frag &f, const SOp &as, int kk, int nbase, int dkt, int dbuf, auto &&after) {
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
@@ -478,7 +490,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                     piece(n, dkt, dbuf);
                     __builtin_amdgcn_sched_barrier(0);
                 }
+                after(j * TM + i);
             }
+    };
+    auto mfma_half = [&](const Frag &f, const SOp &as, int kk, int nbase, int dkt, int dbuf) {
+        mfma_half_then(f, as, kk, nbase, dkt, dbuf, [](int) {});
     };
     // compute(buf, stage, dkt, dbuf): the MFMAs of `stage` from slot buf,
     // slice by slice (each slice's reads, then its MFMAs), with the loads of
@@ -570,8 +586,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                     mfma_half(f1, as1, 1, 0, kt + j + NS - 1, j);  // stage kt + j - 1, second slice
                     SOp as0;
                     scale_op(sr, 0, kt + j, as0);
+#if LX2V_FP8_EARLY
+                    // the second slice's fragments read between the first
+                    // slice's MFMAs (RPM reads per MFMA), so that they have
+                    // landed when the next barrier's wait retires them
+                    mfma_half_then(f0, as0, 0, TN * TM, kt + j + NS - 1, j, [&](int m) {
+                        constexpr int RPM = (TM + TN + TN * TM - 1) / (TN * TM);
+#pragma unroll
+                        for (int r = 0; r < RPM; r++)
+                            if (m * RPM + r < TM + TN) {
+                                __builtin_amdgcn_sched_barrier(0);
+                                read_frag(buf, 1, f1, m * RPM + r);
+                                __builtin_amdgcn_sched_barrier(0);
+                            }
+                    });
+#else
                     mfma_half(f0, as0, 0, TN * TM, kt + j + NS - 1, j);
                     read_half(buf, 1, f1);
+#endif
                     scale_op(sr, 1, kt + j, as1);
                     __builtin_amdgcn_sched_barrier(0);
                 }

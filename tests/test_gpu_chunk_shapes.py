@@ -187,3 +187,35 @@ def test_cfg5_bf16_output(be, rows, K, N, cfg):
     p = _pick(rows, N)[:48]
     assert_close(got16[p], oracle_w8a8(x[p], q, s, K, b, 0), 4e-3, 1e-2, what="cfg5 bf16 out vs oracle(e4m3 acts)")
     assert_close(got32[p], oracle_w8a8(x[p], q, s, K, b, 0), *FP8_TIGHT, what="cfg5 f32 out vs oracle(e4m3 acts)")
+
+
+@pytest.mark.parametrize("name,seed", [("o", 1301), ("o2", 1302)])
+def test_o_on_mx_input(be, name, seed):
+    """The headline chunk's O and cross-attn O: 4680 x 1536 -> 1536 on the MX
+    e4m3 input attention's epilogue writes (here the standalone MX quantizer
+    of bf16 N(0,1) values), bf16 output, as the bench runs them: the kernel
+    configuration asserted; sampled rows against the oracle on the decoded
+    MX input (FP8_TIGHT, f32 output) and against the plain f32 oracle on the
+    bf16 values (4e-2)."""
+    x = O.bf16_round(normal(seed, M * DIM).reshape(M, DIM))
+    wf = normal(seed + 1, DIM * DIM, 0.02).reshape(DIM, DIM)
+    q, s = O.fp8_quantize(wf, DIM, DIM, DIM, True)
+    b = normal(seed + 2, DIM, 0.01)
+    w = be.weight_fp8(q, s, DIM, DIM, DIM)
+    xb, bb = _bf16_buf(be, x), be.upload(b)
+    xm = be.alloc_mx(M, DIM)
+    be.quantize_mx(xb, 0, M, xm)
+    y16 = be.alloc(M * DIM, H.DTYPE_BF16)
+    y32 = be.alloc(M * DIM, H.DTYPE_F32)
+    assert _profiled(be, lambda: be.linear(xm, 0, M, w, bb, H.ACT_NONE, y16, 0)) == {"gemm_fp8_e4m3.c0.mxin"}
+    be.linear(xm, 0, M, w, bb, H.ACT_NONE, y32, 0)
+    got32 = be.download(y32).reshape(M, DIM)
+    assert np.array_equal(u32(be.download(y16).reshape(M, DIM)), u32(O.bf16_round(got32)))
+    p = _pick(M, seed)
+    xd = be.download(xm).reshape(M, DIM)[p]  # the decoded MX input
+    # the device decoder against the oracle's own MX quantizer of the same values
+    qo, so = O.act_quant_mx(x[p])
+    assert np.array_equal(u32(xd), u32(O.dequant_mx(qo, so)))
+    wd = O.fp8_dequantize(q, s, DIM, DIM, DIM)
+    assert_close(got32[p], O.linear(xd, wd, b, 0, nthreads=8), *FP8_TIGHT, what=f"{name} on MX input vs oracle")
+    assert_close(got32[p], O.linear(x[p], wd, b, 0, nthreads=8), 4e-2, 0.3, what=f"{name} vs f32 oracle")
