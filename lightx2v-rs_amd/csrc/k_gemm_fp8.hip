@@ -1211,6 +1211,343 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
     wait_vmcnt<0>();  // the walk's trailing loads (zeros) land before the workgroup ends
 }
 
+// ---- persistent 256 x 256 kernel, one wave per SIMD ---------------------------------
+//
+// Measured on gfx950: one wave issues independent 32x32x64 fp8 MFMAs at the
+// full rate (3.6 PF/s on random operands with 4 accumulators in a wave per
+// SIMD), but a wave's ds_read_b128 returns at about one per 40 cycles.  So a
+// wave that is alone on its SIMD keeps the matrix core busy only if it
+// needs at most about one 1 KB fragment read per 64-cycle MFMA: a 128 x 128
+// wave tile (16 MFMAs per 64-byte K slice against 16 reads), four of them
+// in a 256 x 256 tile.  Per 64 bytes of K the tile then moves 32 KB into LDS
+// and 64 KB out of it for 2 x 256 x 256 x 64 FLOPs: half the LDS bytes per
+// FLOP of the 8-wave 256 x 128 tile, whose K loop the LDS bounds.
+//
+// Structure: a grid of min(tiles, CUs) workgroups walking a strided tile
+// list (xcd_tile, as k_gemm_fp8_ov); 64-byte K stages in a 4-slot direct-to-
+// LDS ring that runs on across tiles (stage g + 3 is loaded while stage g
+// is contracted).  The K loop is skewed by one stage: after barrier g each
+// wave contracts stage g - 1 from registers while it reads stage g's
+// fragments (one ds_read_b128 after each MFMA) and issues stage g + 3's
+// loads, so no MFMA waits for LDS.  A tile's token scales, channel scales
+// and bias travel by DMA too (waves 0 / 1 / 2 with the tile's first stage;
+// wave 3 loads a dummy into a spare slot so every wave issues the same 9
+// loads per stage).  The epilogue (scales, bias, GELU, bf16 or MX e4m3)
+// runs from registers after the tile's last MFMAs and stores straight to
+// memory, lanes l and l + 32 paired by v_permlane32_swap into 32-byte row
+// pieces, while the next tile's first three stages load.
+//
+// vmcnt accounting: every stage issues LPS = 9 loads and every epilogue
+// ST stores (stores past M or N go to an out-of-range offset, so the count
+// is the same for every lane and tile; a dummy epilogue of ST out-of-range
+// stores follows the prologue loads for the first tile).  At the top of
+// stage g the loads of g + 1 and g + 2 may still be in flight, and, for the
+// first three stages of a tile, the previous tile's stores issued after
+// stage g's loads: the waits allow exactly those.
+//
+// Constraints (host): K % 64 == 0, K / 64 >= 4, N % 256 == 0, M N sizeof(TY)
+// < 2^31; bf16 or MX e4m3 output; per-token activations, per-channel weight
+// scales; no residual mode.
+template <int BKB, int ACT, typename TY>
+__global__ __launch_bounds__(256, 1) void k_gemm_fp8_w4(const uint8_t *__restrict__ A, const float *__restrict__ sa,
+                                                       const uint8_t *__restrict__ B, const float *__restrict__ sb,
+                                                       const float *__restrict__ bias, TY *__restrict__ Y, int M,
+                                                       int N, int K, int tiles_m, int tiles_n,
+                                                       uint8_t *__restrict__ ymx, int ymx_rows) {
+    constexpr int BM = 256, BN = 256, NW = 4, WGN = 2, WM = 128, WN = 128, TM = 4, TN = 4;
+    static_assert(BKB == 64 || BKB == 128, "64- or 128-byte K stages");
+    constexpr int KK = BKB / 64;                                    // 64-byte K slices per stage
+    constexpr int NS = BKB == 64 ? 4 : 2;                           // ring slots (128 KB)
+    constexpr int CPR = BKB / 16, RPI = 64 / CPR;                   // tile rows per 1 KB load
+    constexpr int ALD = BM / RPI / NW, BLD = BN / RPI / NW;        // ring loads per wave per stage
+    constexpr int LPS = ALD + BLD + 1;                              // + the operand / dummy load
+    constexpr int STAGE = (BM + BN) * BKB;                          // 32 or 64 KB
+    constexpr uint32_t AMASK = BM * BKB - 1, BMASK = BN * BKB - 1;
+    constexpr int NV = BM + 2 * BN;  // token scales, channel scales, bias (one set per tile parity)
+    constexpr int EB = sizeof(TY);
+    static_assert(EB == 1 || EB == 2, "bf16 or MX e4m3 output");
+    constexpr bool GELU = ACT == LX2V_ACT_GELU_TANH;
+    // stores per epilogue per lane: bf16 two 16-byte stores per 32 x 32
+    // block; MX one 16-byte code store and one scale byte
+    constexpr int ST = TM * TN * 2;
+    static_assert((NS - 2) * LPS + ST < 64, "vmcnt range");
+    static_assert(NS * STAGE + 2 * NV * 4 + 1024 <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    __shared__ __attribute__((aligned(16))) float sc[2 * NV];
+    __shared__ __attribute__((aligned(16))) uint8_t dummy[1024];
+
+    const uint32_t smem_at = lds_addr(smem), sc_at = lds_addr(sc), dummy_at = lds_addr(dummy);
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int wid_u = __builtin_amdgcn_readfirstlane(wid);
+    const int G = gridDim.x, w = blockIdx.x, ntiles = tiles_m * tiles_n;
+    const int my_n = w < ntiles ? (ntiles - w + G - 1) / G : 0;
+    if (my_n == 0) return;  // (uniform) no tile: no descriptor may be built
+    const int KT = K / BKB;  // (host: K % 128 == 0, so even for 64-byte stages)
+    auto tile_of = [&](int i, int *m0, int *n0) {
+        int tm, tn;
+        xcd_tile(w + i * G, ntiles, tiles_m, tiles_n, &tm, &tn);
+        *m0 = tm * BM;
+        *n0 = tn * BN;
+    };
+
+    // Issue side: the (tile, stage) whose loads go out next.
+    int is_i = 0, is_kt = 0, is_m0 = 0, is_n0 = 0;
+    tile_of(0, &is_m0, &is_n0);
+    __amdgpu_buffer_rsrc_t ra_src, rb_src;
+    auto set_issue_tile = [&]() {
+        ra_src = make_rsrc(A + (size_t)is_m0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(M - is_m0) * (uint32_t)K));
+        rb_src = make_rsrc(B + (size_t)is_n0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(N - is_n0) * (uint32_t)K));
+    };
+    set_issue_tile();
+    const uint32_t lrow = (uint32_t)lane / CPR, lslot = (uint32_t)lane % CPR;
+    uint32_t a_off[ALD], b_off[BLD];
+#pragma unroll
+    for (int i = 0; i < ALD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * RPI + lrow;
+        a_off[i] = row * (uint32_t)K + dma_slot<BKB>(row, lslot) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < BLD; i++) {
+        const uint32_t row = (uint32_t)(i * NW + wid) * RPI + lrow;
+        b_off[i] = row * (uint32_t)K + dma_slot<BKB>(row, lslot) * 16;
+    }
+    // Ring load n (0 .. ALD + BLD - 1) of the issue stage into slot buf.
+    auto piece = [&](int n, int buf) {
+        const bool in = is_i < my_n;
+        const uint32_t k0 = (uint32_t)is_kt * BKB;
+        const uint32_t sbuf = smem_at + (uint32_t)(buf * STAGE);
+        if (n < ALD)
+            dma16_at(ra_src, sbuf + (n * NW + wid_u) * RPI * BKB, in ? a_off[n < ALD ? n : 0] + k0 : kOob);
+        else
+            dma16_at(rb_src, sbuf + BM * BKB + ((n - ALD) * NW + wid_u) * RPI * BKB,
+                     in ? b_off[n >= ALD ? n - ALD : 0] + k0 : kOob);
+    };
+    // The ninth load of a stage: at the issue tile's first stage (three
+    // stages before that tile is contracted), wave 0 / 1 / 2 load its token
+    // scales / channel scales / bias into the sc set of its parity (a null
+    // bias reads zeros); every other ninth load goes to the dummy slot.
+    auto ninth = [&]() {
+        const bool ops = is_kt == 0 && is_i < my_n && wid_u < 3;
+        if (ops) {
+            const uint32_t dst = sc_at + (uint32_t)(is_i & 1) * NV * 4u;
+            if (wid_u == 0)
+                dma16_at(make_rsrc(sa + is_m0, __builtin_amdgcn_readfirstlane((uint32_t)(M - is_m0) * 4u)), dst,
+                         (uint32_t)lane * 16u);
+            else if (wid_u == 1)
+                dma16_at(make_rsrc(sb + is_n0, __builtin_amdgcn_readfirstlane((uint32_t)(N - is_n0) * 4u)),
+                         dst + BM * 4, (uint32_t)lane * 16u);
+            else
+                dma16_at(make_rsrc(bias ? bias + is_n0 : bias,
+                                   bias ? __builtin_amdgcn_readfirstlane((uint32_t)(N - is_n0) * 4u) : 0u),
+                         dst + (BM + BN) * 4, (uint32_t)lane * 16u);
+        } else {
+            dma16_at(ra_src, dummy_at, kOob);
+        }
+    };
+    auto advance_issue = [&]() {
+        if (++is_kt == KT) {
+            is_kt = 0;
+            if (++is_i < my_n) {
+                tile_of(is_i, &is_m0, &is_n0);
+                set_issue_tile();
+            }
+        }
+    };
+
+    // Fragments of one stage: the wave's TM activation row blocks and TN
+    // weight row blocks, each 32 rows x 64 bytes as two 16-byte reads
+    // (lane half h: chunks 2 h and 2 h + 1 of the row).
+    const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
+    struct Frag {
+        u32x4 a[TM][2], b[TN][2];
+    };
+    // read m (0 .. 2 (TM + TN) - 1) of slice kk of the stage in slot buf
+    auto read_one = [&](int buf, int kk, Frag &f, int m) {
+        const uint8_t *st = smem + buf * STAGE;
+        const int fi = m >> 1, h = m & 1;
+        const uint32_t c = (uint32_t)kk * 4 + fhalf + (uint32_t)h;
+        if (fi < TM) {
+            const uint32_t row = wm * WM + fi * 32 + frow;
+            f.a[fi][h] = *(const u32x4 *)(st + ((row * BKB + (dma_slot<BKB>(row, c) << 4)) & AMASK));
+        } else {
+            const uint32_t row = wn * WN + (fi - TM) * 32 + frow;
+            f.b[fi - TM][h] = *(const u32x4 *)(st + BM * BKB + ((row * BKB + (dma_slot<BKB>(row, c) << 4)) & BMASK));
+        }
+    };
+    auto as8 = [](const u32x4 (&p)[2]) {
+        return (i32x8){(int)p[0].x, (int)p[0].y, (int)p[0].z, (int)p[0].w,
+                       (int)p[1].x, (int)p[1].y, (int)p[1].z, (int)p[1].w};
+    };
+
+    f32x16 acc[TN][TM];
+    Frag fr[2];
+    // One slice's MFMAs from fc (zero accumulators first when FIRST); after
+    // MFMA m, load L0 + m of the issue stage while below L1 (slot dbuf) and,
+    // when RD, read m of slice rkk of the stage in slot rbuf into fn.
+    auto load = [&](int n, int dbuf) {
+        if (n < ALD + BLD)
+            piece(n, dbuf);
+        else
+            ninth();
+    };
+    auto step = [&](auto FIRST, auto RD, auto L0, auto L1, const Frag &fc, Frag &fn, int rbuf, int rkk, int dbuf) {
+        static_for<TN * TM>([&](auto JI) {
+            constexpr int m = decltype(JI)::value, j = m / TM, i = m % TM;
+            if constexpr (decltype(FIRST)::value)
+                acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(as8(fc.b[j]), as8(fc.a[i]), (f32x16){}, 0, 0,
+                                                                            0, 0, 0, 0);
+            else
+                acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(as8(fc.b[j]), as8(fc.a[i]), acc[j][i], 0, 0,
+                                                                            0, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            constexpr int n = decltype(L0)::value + m;
+            if constexpr (n < decltype(L1)::value) load(n, dbuf);
+            if constexpr (decltype(RD)::value) read_one(rbuf, rkk, fn, m);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    static_assert(TN * TM == 2 * (TM + TN) && KK * TN * TM >= LPS, "one read after each MFMA; the loads fit");
+    using I0 = std::integral_constant<int, 0>;
+    using T = std::true_type;
+    using F = std::false_type;
+
+    // ---- epilogue of a finished tile, straight from registers ----
+    const auto ry = make_rsrc(Y, (uint32_t)M * (uint32_t)N * EB);
+    const auto rmx = make_rsrc(ymx, EB == 1 ? ((uint32_t)(N / 128 - 1) * (uint32_t)ymx_rows + (uint32_t)M) * 4u : 0u);
+    const int l32 = lane & 31, hf = lane >> 5;
+    auto epilogue = [&](const float *sct, int m0, int n0) {
+        static_for<TN>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const int cb = wn * WN + j * 32;  // the block's first tile column
+            f32x4 cs[4], bs[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int c = cb + 8 * g + 4 * hf;
+                cs[g] = *(const f32x4 *)(sct + BM + c);
+                bs[g] = *(const f32x4 *)(sct + BM + BN + c);
+            }
+            static_for<TM>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                const float tsc = sct[wm * WM + i * 32 + l32];
+                float v[16];
+                float amax = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    float t = acc[j][i][e] * tsc * cs[e / 4][e % 4] + bs[e / 4][e % 4];
+                    if constexpr (GELU) t = gelu_tanh_fast(t);
+                    v[e] = t;
+                    if constexpr (EB == 1) amax = fmaxf(amax, fabsf(t));
+                }
+                const int m = m0 + wm * WM + i * 32 + l32, n = n0 + cb;
+                const bool in = m < M;
+                const uint32_t row = (uint32_t)m * (uint32_t)N + (uint32_t)n;
+                uint32_t ww[8];
+                if constexpr (EB == 2) {
+#pragma unroll
+                    for (int k = 0; k < 8; k++) ww[k] = pack_bf16x2(v[2 * k], v[2 * k + 1]);
+                    // lane l: channels 0..7 (16..23) of the block, lane l + 32: 8..15 (24..31)
+                    swap32(ww[0], ww[2]);
+                    swap32(ww[1], ww[3]);
+                    swap32(ww[4], ww[6]);
+                    swap32(ww[5], ww[7]);
+                    buffer_store_x4((u32x4){ww[0], ww[1], ww[2], ww[3]}, ry, in ? (row + 8u * (uint32_t)hf) * 2u : kOob);
+                    buffer_store_x4((u32x4){ww[4], ww[5], ww[6], ww[7]}, ry,
+                                    in ? (row + 16u + 8u * (uint32_t)hf) * 2u : kOob);
+                } else {
+                    const int kx = mx_exponent(max_pair32(amax));
+                    const float inv = mx_inv(kx);
+#pragma unroll
+                    for (int g = 0; g < 4; g++) ww[g] = quant4_nc(v + 4 * g, inv);
+                    // lane l: channels 0..15 as w0, w2, w1, w3; lane l + 32: 16..31
+                    swap32(ww[0], ww[2]);
+                    swap32(ww[1], ww[3]);
+                    buffer_store_x4((u32x4){ww[0], ww[2], ww[1], ww[3]}, ry, in ? row + 16u * (uint32_t)hf : kOob);
+                    buffer_store_b8((uint8_t)(kx + 127), rmx,
+                                    in && hf == 0 ? (uint32_t)mx_sidx((size_t)m, (size_t)(n / 32), (size_t)ymx_rows)
+                                                  : kOob);
+                }
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    // Prologue: the first NS - 1 stages, then the dummy epilogue's stores.
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++) {
+#pragma unroll
+        for (int n = 0; n < LPS; n++) load(n, st);
+        advance_issue();
+    }
+#pragma unroll
+    for (int q = 0; q < ST; q++) buffer_store_b8(0, ry, kOob);
+
+    int g = 0;  // global stage index of this workgroup's walk
+    // One stage of the K loop.  The loop is skewed by one 64-byte slice:
+    // after barrier g a wave contracts the slice before stage g's first
+    // (none at a tile's first stage) while it reads that first slice, then
+    // each next slice while reading the one after it.  64-byte stages use
+    // the two fragment sets by stage parity P (KT is even), 128-byte stages
+    // by slice.
+    auto iter = [&](auto P, int kt) {
+        constexpr int p = decltype(P)::value;
+        if (kt < NS - 1)
+            wait_vmcnt_lds0<(NS - 2) * LPS + ST>();
+        else
+            wait_vmcnt_lds0<(NS - 2) * LPS>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int buf = g % NS, dbuf = (g + NS - 1) % NS;
+        if constexpr (KK == 1) {
+            if (kt == 0) {
+                // nothing to contract yet: the loads and reads back to back
+#pragma unroll
+                for (int n = 0; n < LPS; n++) load(n, dbuf);
+#pragma unroll
+                for (int m = 0; m < 2 * (TM + TN); m++) read_one(buf, 0, fr[p], m);
+            } else if (kt == 1) {
+                step(T{}, T{}, I0{}, std::integral_constant<int, LPS>{}, fr[p ^ 1], fr[p], buf, 0, dbuf);
+            } else {
+                step(F{}, T{}, I0{}, std::integral_constant<int, LPS>{}, fr[p ^ 1], fr[p], buf, 0, dbuf);
+            }
+        } else {
+            constexpr int H1 = TN * TM;  // loads of the first slice step
+            if (kt == 0) {
+#pragma unroll
+                for (int n = 0; n < H1; n++) load(n, dbuf);
+#pragma unroll
+                for (int m = 0; m < 2 * (TM + TN); m++) read_one(buf, 0, fr[0], m);
+                step(T{}, T{}, std::integral_constant<int, H1>{}, std::integral_constant<int, LPS>{}, fr[0], fr[1],
+                     buf, 1, dbuf);
+            } else {
+                step(F{}, T{}, I0{}, std::integral_constant<int, H1>{}, fr[1], fr[0], buf, 0, dbuf);
+                step(F{}, T{}, std::integral_constant<int, H1>{}, std::integral_constant<int, LPS>{}, fr[0], fr[1],
+                     buf, 1, dbuf);
+            }
+        }
+        advance_issue();
+        g++;
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int t = 0; t < my_n; t++) {
+        int m0, n0;
+        tile_of(t, &m0, &n0);
+        if constexpr (KK == 1) {
+            for (int kt = 0; kt < KT; kt += 2) {
+                iter(std::integral_constant<int, 0>{}, kt);
+                iter(std::integral_constant<int, 1>{}, kt + 1);
+            }
+        } else {
+            for (int kt = 0; kt < KT; kt++) iter(I0{}, kt);
+        }
+        // the tile's last slice (set 1), from registers, then its epilogue
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): its fragments
+        step(F{}, F{}, I0{}, I0{}, fr[1], fr[0], 0, 0, 0);
+        epilogue(sc + (t & 1) * NV, m0, n0);
+    }
+    wait_vmcnt<0>();  // the walk's trailing loads (zeros) land before the workgroup ends
+}
+
 // ---- ping-pong kernel: two wave groups alternate MFMA and LDS phases ---------------
 //
 // Measured on gfx950: a ds_read_b128 costs its own wave ~25 MFMA cycles of
@@ -1506,6 +1843,33 @@ void launch_ov(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, con
 #undef LX2V_OV
 }
 
+// The persistent 256 x 256 kernel with one wave per SIMD: min(tiles, CUs)
+// workgroups (a multiple of 8 whenever the tiles outnumber the CUs).
+template <int BKB>
+void launch_w4(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
+               const float *bias, int act, void *y, int y_dtype, int M, int N, int K, const Fp8Mx &mx) {
+    const int tiles_m = (M + 255) / 256, tiles_n = N / 256, nt = tiles_m * tiles_n;
+    int g = nt < num_cu ? nt : num_cu;
+    if (g < nt && g >= 8) g = g / 8 * 8;
+    const dim3 grid(g), block(256);
+    const int yr = (int)mx.y_rows;
+#define LX2V_W4(ACTV, T)                                                                                      \
+    hipLaunchKernelGGL((k_gemm_fp8_w4<BKB, ACTV, T>), grid, block, 0, s, a, sa, b, sb, bias, (T *)y, M, N, K, tiles_m, \
+                       tiles_n, mx.y, yr)
+    if (y_dtype == LX2V_DTYPE_BF16) {
+        if (act == LX2V_ACT_GELU_TANH)
+            LX2V_W4(LX2V_ACT_GELU_TANH, uint16_t);
+        else
+            LX2V_W4(LX2V_ACT_NONE, uint16_t);
+    } else {
+        if (act == LX2V_ACT_GELU_TANH)
+            LX2V_W4(LX2V_ACT_GELU_TANH, uint8_t);
+        else
+            LX2V_W4(LX2V_ACT_NONE, uint8_t);
+    }
+#undef LX2V_W4
+}
+
 // Direct-to-LDS configurations: tile (activation rows x channels), wave
 // grid, K bytes per stage, stages.
 struct DmaCfg {
@@ -1524,6 +1888,9 @@ constexpr DmaCfg kDma[] = {
     {256, 128, 4, 2, 128, 3},  // 6
     // persistent 256 x 128, epilogue overlapped with the next tile (k_gemm_fp8_ov)
     {256, 128, 4, 2, 128, 3},  // 7
+    // persistent 256 x 256, one wave per SIMD (k_gemm_fp8_w4)
+    {256, 256, 2, 2, 64, 4},   // 8: 64-byte stages, 4 slots
+    {256, 256, 2, 2, 128, 2},  // 9: 128-byte stages, 2 slots
 };
 
 // Split K's second pass: y = act(sum_p part[p] * sa[m] * sb[n] + b[n]) in
@@ -1615,7 +1982,7 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
         case 5: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
-        default: break;  // 6, 7: launch_pt / launch_ov (need the CU count)
+        default: break;  // 6 .. 9: launch_pt / launch_ov / launch_w4 (need the CU count)
     }
 }
 
@@ -1629,7 +1996,9 @@ int forced_cfg() {
 
 }  // namespace
 
-bool gemm_fp8_residual_ok(const Fp8Plan &p) { return p.kernel >= 0 && p.kernel != 5 && p.kernel != 6 && p.kernel != 7; }
+bool gemm_fp8_residual_ok(const Fp8Plan &p) {
+    return p.kernel >= 0 && p.kernel != 5 && p.kernel != 6 && p.kernel != 7 && p.kernel != 8 && p.kernel != 9;
+}
 
 bool gemm_fp8_grouped_supported(size_t M, size_t N, size_t K, size_t group) {
     return group == 128 && K % 128 == 0 && N % 4 == 0 && gemm_fp8_supported(M, N, K) &&
@@ -1703,6 +2072,15 @@ bool ov_capable(size_t M, size_t N, size_t K, bool mx_in, bool grouped, int y_dt
            M * N * eb < (1ull << 31);
 }
 
+// The persistent 256 x 256 kernel (k_gemm_fp8_w4): per-token activations and
+// per-channel weight scales, bf16 or MX e4m3 output, whole 256-channel
+// tiles, K a multiple of 128 with at least four 64-byte stages.
+bool w4_capable(size_t M, size_t N, size_t K, bool mx_in, bool grouped, int y_dtype, bool residual) {
+    const size_t eb = y_dtype == LX2V_DTYPE_BF16 ? 2 : (y_dtype == LX2V_DTYPE_MXE4M3 ? 1 : 0);
+    return eb && !mx_in && !grouped && !residual && N % 256 == 0 && K % 128 == 0 && K / 64 >= 4 &&
+           M * N * eb < (1ull << 31);
+}
+
 Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx_in, bool grouped, int y_dtype,
                       int act, bool residual, bool allow_split) {
     Fp8Plan p;
@@ -1734,6 +2112,7 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
     auto ok = [&](int idx) {
         if (residual && (idx == 5 || idx == 6)) return false;
         if (idx == 7) return ov_capable(M, N, K, mx_in, grouped, y_dtype, act, residual);
+        if (idx == 8 || idx == 9) return w4_capable(M, N, K, mx_in, grouped, y_dtype, residual);
         return grouped ? grouped_capable(idx, mx, mx_in) : (!mx || mx_capable(idx, mx_in));
     };
     if (forced >= 0 && forced < nd && ok(forced) && (forced != 6 || K >= 256)) {
@@ -1741,23 +2120,42 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
         return p;
     }
     double best = 0.0;
+    auto take = [&](int idx, double t) {
+        if (p.kernel < 0 || t < best * 0.9999) {  // ties keep the earlier
+            best = t;
+            p.kernel = idx;
+        }
+    };
+    const bool heavy_epi = y_dtype == LX2V_DTYPE_MXE4M3 || act == LX2V_ACT_GELU_TANH;
     auto consider = [&](const CfgCost &c) {
         if (!ok(c.idx)) return;
         const DmaCfg &d = kDma[c.idx];
         const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
         const size_t rounds = (tiles + num_cu - 1) / num_cu;
         if (c.persistent && (rounds < 2 || K / 128 < 2)) return;
-        const double t = (double)rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us) + c.fixed_us;
-        if (p.kernel < 0 || t < best * 0.9999) {  // ties keep the earlier
-            best = t;
-            p.kernel = c.idx;
-        }
+        // the overlapped epilogue's MX quantization (and GELU) cost per pass
+        const double epi = c.idx == 7 && y_dtype == LX2V_DTYPE_MXE4M3 ? 1.2 : 0.0;
+        take(c.idx, (double)rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us + epi) + c.fixed_us);
+    };
+    // The 256 x 256 tile with one wave per SIMD (9).  Its stages slow down
+    // with the share of CUs loading at once (measured 1.33-1.36 us per
+    // 128-byte stage with every CU busy, 1.07 us with half of them), so a
+    // round costs stages x (0.63 + 0.72 occupancy) + its prologue and
+    // register-direct epilogue (7 us; 9.5 with GELU or MX output).
+    auto consider9 = [&]() {
+        if (!ok(9)) return;
+        const size_t tiles = ((M + 255) / 256) * (N / 256), full = tiles / num_cu, rem = tiles % num_cu;
+        const double st = (double)(K / 128), b = heavy_epi ? 9.5 : 7.0;
+        double t = (double)full * (st * (0.63 + 0.72) + b) + 0.5;
+        if (rem) t += st * (0.63 + 0.72 * (double)rem / num_cu) + b;
+        take(9, t);
     };
     if (grouped) {
         for (const CfgCost &c : kGroupedAuto) consider(c);
         return p;
     }
     for (const CfgCost &c : kAuto) consider(c);
+    consider9();
     return p;
 }
 
@@ -1779,6 +2177,11 @@ void launch_gemm_fp8(hipStream_t s, int num_cu, const Fp8Plan &p, const uint8_t 
     }
     if (p.kernel == 7) {
         launch_ov(s, num_cu, a, a_scale, b, b_scale, bias, act, y, y_dtype, m, n, k, mx);
+        return;
+    }
+    if (p.kernel == 8 || p.kernel == 9) {
+        (p.kernel == 8 ? launch_w4<64> : launch_w4<128>)(s, num_cu, a, a_scale, b, b_scale, bias, act, y, y_dtype, m,
+                                                         n, k, mx);
         return;
     }
     if (p.kernel >= 0) {

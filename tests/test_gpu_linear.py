@@ -165,15 +165,20 @@ def test_fp8_split_k_row_offsets(be, monkeypatch):
 
 @pytest.mark.parametrize("cfg,act,ydt", [(6, H.ACT_GELU_TANH, H.DTYPE_BF16), (6, H.ACT_NONE, H.DTYPE_F32),
                                          (6, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (7, H.ACT_GELU_TANH, H.DTYPE_BF16),
-                                         (7, H.ACT_NONE, H.DTYPE_BF16), (7, H.ACT_GELU_TANH, H.DTYPE_MXE4M3)])
+                                         (7, H.ACT_NONE, H.DTYPE_BF16), (7, H.ACT_GELU_TANH, H.DTYPE_MXE4M3),
+                                         (8, H.ACT_GELU_TANH, H.DTYPE_BF16), (8, H.ACT_NONE, H.DTYPE_BF16),
+                                         (8, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (8, H.ACT_NONE, H.DTYPE_MXE4M3),
+                                         (9, H.ACT_GELU_TANH, H.DTYPE_BF16), (9, H.ACT_NONE, H.DTYPE_BF16),
+                                         (9, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (9, H.ACT_NONE, H.DTYPE_MXE4M3)])
 def test_fp8_forced_persistent_vs_config0(be, monkeypatch, cfg, act, ydt):
-    """The persistent 256 x 128 tiles forced (LIGHTX2V_HIP_FP8_CFG, read per
-    call) against the one-shot configuration 0, bit for bit over the whole
-    output: 1937 rows (ragged: 7 x 256 + 145) x 4608 channels is 288 tiles,
-    so part of the grid walks two; GELU or none; bf16, f32 (configuration 6;
-    7 stores bf16 or MX only) and MX e4m3 output.  Both share the K order of
+    """The persistent tiles forced (LIGHTX2V_HIP_FP8_CFG, read per call)
+    against the one-shot configuration 0, bit for bit over the whole output:
+    1937 rows (ragged: 7 x 256 + 145) x 9216 channels is 576 tiles of 256 x
+    128 or 288 of 256 x 256 (configurations 8, 9), so every workgroup of the
+    grid walks two or more; GELU or none; bf16, f32 (configuration 6; 7 to
+    9 store bf16 or MX only) and MX e4m3 output.  All share the K order of
     every sum, so only a fault in the walk or the epilogue could differ."""
-    M, K, N = 1937, 1536, 4608
+    M, K, N = 1937, 1536, 9216
     x = normal(3201, M * K).reshape(M, K)
     _, q, s = fp8_weight(3202, N, K, K)
     w = be.weight_fp8(q, s, N, K, K)
