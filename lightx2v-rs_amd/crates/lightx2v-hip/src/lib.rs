@@ -8,8 +8,12 @@
 //! channel or per 128 columns), Q8 / Q4 / f32 weights dequantized to bf16 in
 //! the GEMM's tile loader on the bf16 matrix cores.  The norms, head split,
 //! attention and the MemRoPE KV cache around it run on the device too.  The
-//! ops outside that path (sparse attention, patchify, the sampler, the
-//! decoder's conv2d) are not built: they panic, naming the op.
+//! ops outside that path (sparse attention, patchify / unpatchify, the DMD
+//! sampler step, the decoder's conv2d and tanh clamp) have no kernels here:
+//! they run on the reference's own CPU backend (lightx2v-cpu) over host
+//! copies of their buffers, so `lightx2v check`, `bench` and the pipeline
+//! run end to end with `--backend hip` (those ops at CPU speed, plus two
+//! host transfers each).
 //!
 //! Activations are bf16 on the device (the trait leaves activation precision
 //! to the backend, backend.rs:9-11); `LIGHTX2V_HIP_ACT=f32` keeps them f32.
@@ -33,6 +37,7 @@ use lightx2v_core::{
     quant::{Fp8E4M3, Q4, Q8},
     sparse::SparseSpec,
 };
+use lightx2v_cpu::CpuBackend;
 use std::ffi::{CStr, CString};
 use std::os::raw::c_int;
 use std::sync::Arc;
@@ -162,14 +167,33 @@ impl HipBackend {
         }
     }
 
-    fn outside(op: &str) -> ! {
-        panic!("lightx2v-hip: `{op}` is outside this backend's path (quantized linear, norms, head split, attention, KV cache)")
+    // ---- host delegation of the ops outside this backend's path ----------
+    // The reference's CPU backend (a unit struct) runs the op on host copies:
+    // each input downloaded, the CPU op, then the op's own output extent
+    // written back over the start of the device buffer (`write` overwrites
+    // a prefix, backend.rs:221-222), the rest of the buffer untouched.
+    fn to_cpu(&self, b: &HipBuf) -> <CpuBackend as Backend>::Buf {
+        CpuBackend.upload(&self.download(b))
+    }
+
+    fn from_cpu(&self, out: &HipBuf, b: &<CpuBackend as Backend>::Buf, n: usize) {
+        let v = CpuBackend.download(b);
+        self.write(out, &v[..n]);
+    }
+
+    /// A weight's dequantized f32 values as a CPU-backend weight.
+    fn weight_to_cpu(&self, w: &HipWeight) -> <CpuBackend as Backend>::Weight {
+        let mut info = ffi::lx2v_hip_weight_info_t::default();
+        check(unsafe { ffi::lx2v_hip_weight_info(w.raw, &mut info) });
+        let mut data = vec![0.0f32; info.rows * info.cols];
+        check(unsafe { ffi::lx2v_hip_weight_dequantize(self.c(), w.raw, data.as_mut_ptr(), data.len()) });
+        CpuBackend.weight(&data, info.rows, info.cols)
     }
 }
 
 impl Backend for HipBackend {
     type Buf = HipBuf;
-    type Sparse = ();
+    type Sparse = SparseSpec;
     type Weight = HipWeight;
     type KvCache = HipKv;
 
@@ -423,24 +447,30 @@ impl Backend for HipBackend {
         });
     }
 
+    // Sparse attention on the CPU backend (host delegation, above); the
+    // dense `attention` is this backend's own.
     fn sparse_supported(&self, _head_dim: usize) -> bool {
-        false
+        true
     }
 
-    fn sparse_prepare(&self, _spec: &SparseSpec) {
-        Self::outside("sparse_prepare")
+    fn sparse_prepare(&self, spec: &SparseSpec) -> SparseSpec {
+        CpuBackend.sparse_prepare(spec)
     }
 
     fn sparse_attention(
         &self,
-        _q: &HipBuf,
-        _k: &HipBuf,
-        _v: &HipBuf,
-        _gate: &HipBuf,
-        _sparse: &(),
-        _out: &HipBuf,
+        q: &HipBuf,
+        k: &HipBuf,
+        v: &HipBuf,
+        gate: &HipBuf,
+        sparse: &SparseSpec,
+        out: &HipBuf,
     ) {
-        Self::outside("sparse_attention")
+        let (qc, kc, vc, gc) = (self.to_cpu(q), self.to_cpu(k), self.to_cpu(v), self.to_cpu(gate));
+        let n = self.buf_len(out);
+        let oc = CpuBackend.alloc(n);
+        CpuBackend.sparse_attention(&qc, &kc, &vc, &gc, sparse, &oc);
+        self.from_cpu(out, &oc, n);
     }
 
     // ---- KV cache / MemRoPE ----------------------------------------------
@@ -488,42 +518,70 @@ impl Backend for HipBackend {
         check(unsafe { ffi::lx2v_hip_kv_cache_memrope_update(self.c(), cache.raw, &c, frame_tokens) });
     }
 
-    // ---- outside this backend's path ---------------------------------------
-    fn patchify(&self, _latent: &HipBuf, _c: usize, _t: usize, _h: usize, _w: usize, _p: usize, _out: &HipBuf) {
-        Self::outside("patchify")
+    // ---- outside this backend's path: host delegation to the CPU backend ----
+    fn patchify(&self, latent: &HipBuf, c: usize, t: usize, h: usize, w: usize, p: usize, out: &HipBuf) {
+        let n = t * (h / p) * (w / p) * c * p * p;
+        let (lc, oc) = (self.to_cpu(latent), CpuBackend.alloc(n));
+        CpuBackend.patchify(&lc, c, t, h, w, p, &oc);
+        self.from_cpu(out, &oc, n);
     }
 
-    fn unpatchify(&self, _x: &HipBuf, _c: usize, _t: usize, _h: usize, _w: usize, _p: usize, _out: &HipBuf) {
-        Self::outside("unpatchify")
+    fn unpatchify(&self, x: &HipBuf, c: usize, t: usize, h: usize, w: usize, p: usize, out: &HipBuf) {
+        let n = c * t * h * w;
+        let (xc, oc) = (self.to_cpu(x), CpuBackend.alloc(n));
+        CpuBackend.unpatchify(&xc, c, t, h, w, p, &oc);
+        self.from_cpu(out, &oc, n);
     }
 
     fn dmd_step(
         &self,
-        _x: &HipBuf,
-        _v: &HipBuf,
-        _noise: Option<&HipBuf>,
-        _sigma_t: f32,
-        _sigma_next: f32,
-        _n: usize,
+        x: &HipBuf,
+        v: &HipBuf,
+        noise: Option<&HipBuf>,
+        sigma_t: f32,
+        sigma_next: f32,
+        n: usize,
     ) {
-        Self::outside("dmd_step")
+        let (xc, vc) = (self.to_cpu(x), self.to_cpu(v));
+        let nc = noise.map(|b| self.to_cpu(b));
+        CpuBackend.dmd_step(&xc, &vc, nc.as_ref(), sigma_t, sigma_next, n);
+        self.from_cpu(x, &xc, n);
     }
 
     fn conv2d(
         &self,
-        _a: &HipBuf,
-        _b: Option<&HipBuf>,
-        _shape: &ConvShape,
-        _w: &HipWeight,
-        _bias: Option<&HipBuf>,
-        _epilogue: ConvEpilogue<'_, HipBuf>,
-        _out: &HipBuf,
+        a: &HipBuf,
+        b: Option<&HipBuf>,
+        shape: &ConvShape,
+        w: &HipWeight,
+        bias: Option<&HipBuf>,
+        epilogue: ConvEpilogue<'_, HipBuf>,
+        out: &HipBuf,
     ) {
-        Self::outside("conv2d")
+        let ac = self.to_cpu(a);
+        let bc = b.map(|x| self.to_cpu(x));
+        let wc = self.weight_to_cpu(w);
+        let biasc = bias.map(|x| self.to_cpu(x));
+        let ec = match &epilogue {
+            ConvEpilogue::AddRelu(r) | ConvEpilogue::Prelu(r) => Some(self.to_cpu(r)),
+            _ => None,
+        };
+        let epi = match epilogue {
+            ConvEpilogue::None => ConvEpilogue::None,
+            ConvEpilogue::Relu => ConvEpilogue::Relu,
+            ConvEpilogue::AddRelu(_) => ConvEpilogue::AddRelu(ec.as_ref().unwrap()),
+            ConvEpilogue::Prelu(_) => ConvEpilogue::Prelu(ec.as_ref().unwrap()),
+        };
+        let n = shape.out_len();
+        let oc = CpuBackend.alloc(n);
+        CpuBackend.conv2d(&ac, bc.as_ref(), shape, &wc, biasc.as_ref(), epi, &oc);
+        self.from_cpu(out, &oc, n);
     }
 
-    fn tanh_clamp(&self, _x: &HipBuf, _n: usize, _s: f32) {
-        Self::outside("tanh_clamp")
+    fn tanh_clamp(&self, x: &HipBuf, n: usize, s: f32) {
+        let xc = self.to_cpu(x);
+        CpuBackend.tanh_clamp(&xc, n, s);
+        self.from_cpu(x, &xc, n);
     }
 }
 

@@ -447,7 +447,12 @@ void orc_gate_residual(float *h, const float *a, size_t rows, size_t dim, const 
  * of each of `rows` rows (row stride src_stride) -> out [heads, rows, hd];
  * with rms_w: x * inv * w[j], inv = 1 / sqrt(mean(x^2) + eps), the mean a
  * sequential f32 fold of the squares; with cos / sin ([rows, hd/2]): each
- * head's interleaved pairs (2i, 2i+1) rotated, a*c - b*s and a*s + b*c. */
+ * head's interleaved pairs (2i, 2i+1) rotated, a*c - b*s and a*s + b*c.
+ * The cos / sin index is r * (hd / 2) + i, the [rows, hd/2] layout that the
+ * trait documents (core/src/backend.rs:258) and wgpu indexes
+ * (shaders/head_split.wgsl:33,45). The CPU loop writes r * hd / 2 + i
+ * (cpu/src/lib.rs:447), which is the same for every even hd and differs
+ * for odd hd, where the trait's layout is the one followed. */
 void orc_head_split(const float *src, size_t rows, size_t src_stride, size_t col_off, size_t heads, size_t hd,
                     const float *rms_w, const float *cos_t, const float *sin_t, float eps, float *out) {
     const size_t d = heads * hd;

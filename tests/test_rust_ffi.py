@@ -148,7 +148,7 @@ def test_trait_methods_present():
                 "tanh_clamp"]
     for m in required:
         assert re.search(r"\bfn " + m + r"\s*\(", impl), m
-    for t in ("Buf = HipBuf", "Weight = HipWeight", "KvCache = HipKv", "Sparse = ()"):
+    for t in ("Buf = HipBuf", "Weight = HipWeight", "KvCache = HipKv", "Sparse = SparseSpec"):
         assert "type " + t in impl, t
 
 
