@@ -496,38 +496,73 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     auto mfma_half = [&](const Frag &f, const SOp &as, int kk, int nbase, int dkt, int dbuf) {
         mfma_half_then(f, as, kk, nbase, dkt, dbuf, [](int) {});
     };
+    // Grouped scales: the fold acc += part * s[n, stage] of block b = j TM +
+    // i (lane l's register 4 g + q of block j is channel wn WN + 32 j + 8 g +
+    // 4 (l / 32) + q of the tile) runs behind the second slice's MFMA b + 1
+    // for the blocks of column block 0, and behind the next stage's first
+    // two MFMAs for those of column block 1, so that the folds' VALU work
+    // overlaps the MFMA pipe instead of following the stage's last MFMA
+    // (measured: no faster than all folds after the last MFMA, within 1%;
+    // the grouped tiles' loss against per-channel scales is the unskewed
+    // K loop and the registers, not the folds' VALU time).  g0:
+    // this stage's scales of column block 0; g1: column block 1's, the
+    // previous stage's until its deferred folds are done.  part and g1 start
+    // at zero, so the first stage's deferred folds add +0.
+    static_assert(!GS || (TN == 2 && TM == 2), "grouped scales: 64 x 64 wave tiles");
+    constexpr int NB = TN * TM, GD = 2;  // GD: blocks whose fold runs in the next stage
+    f32x4 g0[4], g1[4];
+    if constexpr (GS) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) g1[g] = (f32x4){};
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int i = 0; i < TM; i++) part[j][i] = (f32x16){};
+    }
+    auto read_gs = [&](int buf, int j, f32x4 (&gs)[4]) {
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            gs[g] = *(const f32x4 *)(asl + buf * ASL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
+    };
+    // fold(b, gs): block b = j TM + i, gs its column block's scales
+    auto fold = [&](int b, const f32x4 *gs) {
+        const int j = b / TM, i = b % TM;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                acc[j][i][4 * g + q] = __builtin_fmaf(part[j][i][4 * g + q], gs[g][q], acc[j][i][4 * g + q]);
+    };
+    // after(kk, m): the folds behind slice kk's MFMA m
+    auto fold_after = [&](int buf, int kk, int m) {
+        if (kk == 0) {
+            if (m < GD) fold(NB - GD + m, g1);  // the previous stage's column block 1
+            if (m == (GD > 0 ? GD - 1 : 0)) read_gs(buf, 1, g1);
+        } else {
+            if (m >= 1 && m - 1 < NB - GD) fold(m - 1, (m - 1) / TM == 0 ? g0 : g1);
+            if (m == NB - 1 && GD == 0) fold(NB - 1, g1);
+        }
+    };
     // compute(buf, stage, dkt, dbuf): the MFMAs of `stage` from slot buf,
     // slice by slice (each slice's reads, then its MFMAs), with the loads of
     // stage dkt interleaved.
     auto compute = [&](int buf, int stage, int dkt, int dbuf) {
         SRaw sraw;
         read_sraw(buf, sraw);
+        if constexpr (GS) read_gs(buf, 0, g0);
 #pragma unroll
         for (int kk = 0; kk < BKB / 64; kk++) {
             Frag f;
             read_half(buf, kk, f);
             SOp as;
             scale_op(sraw, kk, stage, as);
-            mfma_half(f, as, kk, kk * TN * TM, dkt, dbuf);
+            mfma_half_then(f, as, kk, kk * TN * TM, dkt, dbuf, [&](int m) {
+                if constexpr (GS) fold_after(buf, kk, m);
+            });
         }
-        if constexpr (GS) {
-            // acc += part * s[n, stage]: lane l's register 4 g + q of block j
-            // is channel wn WN + 32 j + 8 g + 4 (l / 32) + q of the tile
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                f32x4 g4[4];
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-                    g4[g] = *(const f32x4 *)(asl + buf * ASL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int g = 0; g < 4; g++)
-#pragma unroll
-                        for (int q = 0; q < 4; q++)
-                            acc[j][i][4 * g + q] = __builtin_fmaf(part[j][i][4 * g + q], g4[g][q], acc[j][i][4 * g + q]);
-            }
-        }
+        // g1 is consumed after the next barrier, behind which this slot's
+        // next DMA is issued: the read lands first.
+        if constexpr (GS) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     };
     static_assert((BKB / 64) * TN * TM >= ALD + BLD, "a stage's loads interleave with its MFMAs");
 
@@ -626,6 +661,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
+        }
+        if constexpr (GS) {  // the last stage's deferred folds
+#pragma unroll
+            for (int m = 0; m < GD; m++) fold(NB - GD + m, g1);
         }
     }
     ops.park(sc, tid, m0, n0, M, N, sa, sb);
@@ -777,9 +816,52 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
 
     f32x16 acc[TN][TM];
     f32x16 part[GS ? TN : 1][GS ? TM : 1];
+    // Grouped scales: the folds acc += part * s run behind later MFMAs, as in
+    // k_gemm_fp8_dma (g0 / g1: column block 0's / 1's scales; part and g1
+    // zero before a tile's first stage, whose deferred folds then add +0).
+    // No deferred block (GD = 0: the last two folds follow the stage's last
+    // MFMA): the walk's issue state leaves no registers to carry partial
+    // sums across stages (one deferred block spills).
+    constexpr int NB = TN * TM, GD = 0;
+    f32x4 g0[4], g1[4];
+    auto clear_prev = [&]() {
+        if constexpr (GS) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) g1[g] = (f32x4){};
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int i = 0; i < TM; i++) part[j][i] = (f32x16){};
+        }
+    };
+    auto read_gs = [&](int buf, int j, f32x4 (&gs)[4]) {
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            gs[g] = *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
+    };
+    // fold(b, gs): block b = j TM + i, gs its column block's scales
+    auto fold = [&](int b, const f32x4 *gs) {
+        const int j = b / TM, i = b % TM;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                acc[j][i][4 * g + q] = __builtin_fmaf(part[j][i][4 * g + q], gs[g][q], acc[j][i][4 * g + q]);
+    };
+    // after(kk, m): the folds behind slice kk's MFMA m
+    auto fold_after = [&](int buf, int kk, int m) {
+        if (kk == 0) {
+            if (m < GD) fold(NB - GD + m, g1);  // the previous stage's column block 1
+            if (m == (GD > 0 ? GD - 1 : 0)) read_gs(buf, 1, g1);
+        } else {
+            if (m >= 1 && m - 1 < NB - GD) fold(m - 1, (m - 1) / TM == 0 ? g0 : g1);
+            if (m == NB - 1 && GD == 0) fold(NB - 1, g1);
+        }
+    };
     const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
     auto compute = [&](int buf, bool do_issue, int dbuf) {
         const uint8_t *st = smem + buf * STAGE;
+        if constexpr (GS) read_gs(buf, 0, g0);
 #pragma unroll
         for (int kk = 0; kk < BKB / 64; kk++) {
             i32x8 af[TM], bf[TN];
@@ -815,23 +897,8 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
                         piece(n, dbuf);
                         __builtin_amdgcn_sched_barrier(0);
                     }
+                    if constexpr (GS) fold_after(buf, kk, j * TM + i);
                 }
-        }
-        if constexpr (GS) {
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                f32x4 g4[4];
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-                    g4[g] = *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int g = 0; g < 4; g++)
-#pragma unroll
-                        for (int q = 0; q < 4; q++)
-                            acc[j][i][4 * g + q] = __builtin_fmaf(part[j][i][4 * g + q], g4[g][q], acc[j][i][4 * g + q]);
-            }
         }
     };
     static_assert((BKB / 64) * TN * TM >= LPS, "a stage's loads interleave with its MFMAs");
@@ -852,6 +919,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
         for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int ii = 0; ii < TM; ii++) acc[j][ii] = (f32x16){};
+        clear_prev();
         for (int kt = 0; kt < KT; kt++, s++) {
             // Stage s complete for this wave (stages s + 1 .. s + NS - 2 may
             // still fly); the barrier publishes every wave's part and frees
@@ -868,6 +936,10 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
             compute(buf, true, dbuf);
             advance_issue();
             __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (GS) {  // the tile's last stage's deferred folds
+#pragma unroll
+            for (int m = 0; m < GD; m++) fold(NB - GD + m, g1);
         }
         // The ops DMA went out with stage s - KT, before the ring loads that
         // every later wait covered (KT >= 2).
@@ -1891,6 +1963,8 @@ constexpr DmaCfg kDma[] = {
     // persistent 256 x 256, one wave per SIMD (k_gemm_fp8_w4)
     {256, 256, 2, 2, 64, 4},   // 8: 64-byte stages, 4 slots
     {256, 256, 2, 2, 128, 2},  // 9: 128-byte stages, 2 slots
+    // direct-to-LDS 128 x 128, 128-byte stages, one per CU (grouped scales, few tiles)
+    {128, 128, 2, 2, 128, 3},  // 10
 };
 
 // Split K's second pass: y = act(sum_p part[p] * sa[m] * sb[n] + b[n]) in
@@ -1982,6 +2056,10 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
             launch_dma<128, 256, 2, 4, 64, 3, 2, true, false>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
         case 5: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
+        case 10:
+            launch_dma<128, 128, 2, 2, 128, 3, 1, false, false, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K,
+                                                                      mx);
+            break;
         default: break;  // 6 .. 9: launch_pt / launch_ov / launch_w4 (need the CU count)
     }
 }
@@ -2049,6 +2127,7 @@ constexpr CfgCost kGroupedAuto[] = {
     {0, 0.625, 8.16, 0.21, false},  // 256 x 128
     {1, 0.625, 8.16, 0.21, false},  // 128 x 256
     {6, 0.80, 3.50, 4.00, true},    // 256 x 128 persistent
+    {10, 0.40, 7.00, 0.21, false},  // 128 x 128 (four waves: shapes of few 256 x 128 tiles)
 };
 
 // The configurations with MX-activation / MX-output kernels.  The 128 x 256
@@ -2059,7 +2138,7 @@ bool mx_capable(int idx, bool mx_in) { return idx == 0 || idx == 3 || ((idx == 4
 // workgroup per CU: the partial sums need the registers); MX output on the
 // 256 x 128 tile only, no MX activations.
 bool grouped_capable(int idx, bool mx, bool mx_in) {
-    return !mx_in && (idx == 0 || idx == 6 || (idx == 1 && !mx));
+    return !mx_in && (idx == 0 || idx == 6 || ((idx == 1 || idx == 10) && !mx));
 }
 // The overlapped-epilogue kernel (k_gemm_fp8_ov): per-token activations and
 // per-channel weight scales, bf16 or MX e4m3 output, whole 128-channel

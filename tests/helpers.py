@@ -28,6 +28,19 @@ def u32(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
+def assert_bits_equal(got, want, what=""):
+    """Bit equality of two f32 arrays; on failure, how many elements differ
+    and where (row, column of a 2-D array), with their values."""
+    g, w = u32(got), u32(want)
+    assert g.shape == w.shape, (what, g.shape, w.shape)
+    bad = np.argwhere(g != w)
+    if len(bad):
+        at = [tuple(int(v) for v in b) for b in bad[:8]]
+        gv = np.asarray(got, np.float32)[tuple(bad[:8].T)]
+        wv = np.asarray(want, np.float32)[tuple(bad[:8].T)]
+        raise AssertionError(f"{what}: {len(bad)} of {g.size} differ; first at {at}: got {gv} want {wv}")
+
+
 def rel_l2(got, want):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)

@@ -189,6 +189,8 @@ def test_fp8_forced_persistent_vs_config0(be, monkeypatch, cfg, act, ydt):
     def run(c):
         monkeypatch.setenv("LIGHTX2V_HIP_FP8_CFG", str(c))
         y = be.alloc_mx(M, N) if mx else be.alloc(M * N, ydt)
+        if not mx:  # an element left unwritten stays NaN (a reused allocation cannot mask it)
+            be.write(y, np.full(M * N, np.nan, np.float32))
         _, names = _kernels(be, lambda: be.linear(xb, 0, M, w, bb, act, y, 0))
         assert {k for k in names if k.startswith("gemm")} == {f"gemm_fp8_e4m3.c{c}{sfx}"}, names
         return be.download_mx(y, M, N) if mx else (u32(be.download(y)),)
@@ -200,6 +202,45 @@ def test_fp8_forced_persistent_vs_config0(be, monkeypatch, cfg, act, ydt):
         y = got[0].view(np.float32).reshape(M, N)[p]
         tol = FP8_TIGHT if ydt == H.DTYPE_F32 else (4e-3, 1e-2)
         assert_close(y, oracle_w8a8(x[p], q, s, K, normal(3203, N, 0.01), act), *tol, what=f"c{cfg} vs oracle")
+
+
+@pytest.mark.parametrize("cfg,act,ydt", [(1, H.ACT_GELU_TANH, H.DTYPE_BF16), (1, H.ACT_NONE, H.DTYPE_F32),
+                                         (6, H.ACT_GELU_TANH, H.DTYPE_BF16), (6, H.ACT_NONE, H.DTYPE_F32),
+                                         (6, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (10, H.ACT_GELU_TANH, H.DTYPE_BF16),
+                                         (10, H.ACT_NONE, H.DTYPE_F32)])
+def test_fp8_grouped_forced_vs_config0(be, monkeypatch, cfg, act, ydt):
+    """Group-128 weights (one scale per 128 columns of K per channel) on the
+    grouped configurations forced, against configuration 0, bit for bit over
+    the whole output.  Every configuration folds each 128-column group's
+    partial sum into the accumulator in group order (the fold of a block
+    may run one stage late, behind the next stage's first MFMAs, but never
+    out of order), so the sums are the same f32 operations.  1937 rows
+    (ragged) x 9216 channels x K 1536; GELU or none; bf16, f32 or MX e4m3
+    output; sampled rows against the oracle."""
+    M, K, N = 1937, 1536, 9216
+    x = normal(3211, M * K).reshape(M, K)
+    _, q, s = fp8_weight(3212, N, K, 128)
+    w = be.weight_fp8(q, s, N, K, 128)
+    xb, bb = be.upload(x), be.upload(normal(3213, N, 0.01))
+    mx = ydt == H.DTYPE_MXE4M3
+    sfx = ".g128.mxout" if mx else ".g128"
+
+    def run(c):
+        monkeypatch.setenv("LIGHTX2V_HIP_FP8_CFG", str(c))
+        y = be.alloc_mx(M, N) if mx else be.alloc(M * N, ydt)
+        if not mx:  # an element left unwritten stays NaN (a reused allocation cannot mask it)
+            be.write(y, np.full(M * N, np.nan, np.float32))
+        _, names = _kernels(be, lambda: be.linear(xb, 0, M, w, bb, act, y, 0))
+        assert {k for k in names if k.startswith("gemm")} == {f"gemm_fp8_e4m3.c{c}{sfx}"}, names
+        return be.download_mx(y, M, N) if mx else (u32(be.download(y)),)
+
+    want, got = run(0), run(cfg)
+    assert all(np.array_equal(a, b) for a, b in zip(want, got))
+    if not mx:
+        p = np.arange(0, M, 97)
+        y = got[0].view(np.float32).reshape(M, N)[p]
+        tol = FP8_TIGHT if ydt == H.DTYPE_F32 else (4e-3, 1e-2)
+        assert_close(y, oracle_w8a8(x[p], q, s, 128, normal(3213, N, 0.01), act), *tol, what=f"c{cfg}.g128 vs oracle")
 
 
 def test_fp8_no_bias(be):
