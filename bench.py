@@ -565,22 +565,20 @@ def main():
     ms_bf16_handoff = timed(chunk(False), args.steps, args.warmup)
     log(f"bench: bf16 inputs and bf16 FFN hand-off (eager) {ms_bf16_handoff:.2f} ms/chunk")
     # the chunk with group-128 weights (the reference's FP8 format, quant.rs:21),
-    # eager: QKV, cross Q, FFN up and the text K/V on their per-token e4m3
-    # inputs; O, cross O and FFN down on bf16 inputs, which they quantize per
-    # token (an MX input takes per-channel weights only; FFN up writes bf16)
+    # eager, on the same producer-written inputs as the headline chunk
+    # (per-token e4m3 for QKV, cross Q, FFN up and the text K/V; MX e4m3 for
+    # O, cross O and FFN down, FFN up writing MX)
     g128, kv_g128 = make_layers(128)
-    G128_BF16_IN = ("o", "o2", "ffn2")
 
     def chunk_g128():
         for _ in range(DMD):
-            be.linear(qin["x_text"], 0, TEXT, *kv_g128, 0, outs["kv2"], 0)
+            be.linear(gx["kv2"], 0, TEXT, *kv_g128, 0, gy["kv2"], 0)
             for lw in g128:
                 for name, rows, n, k, act, src in GEMMS:
                     if name == "kv2":
                         continue
                     w, b = lw[name]
-                    x = acts[src] if name in G128_BF16_IN else qin[src]
-                    be.linear(x, 0, rows, w, b, act, outs[name], 0)
+                    be.linear(gx[name], 0, rows, w, b, act, gy[name], 0)
 
     ms_g128 = timed(chunk_g128, args.steps, args.warmup)
     log(f"bench: group-128 weights (eager) {ms_g128:.2f} ms/chunk")

@@ -429,9 +429,9 @@ int lx2v_hip_download_e4m3(lx2v_hip_ctx *ctx, const lx2v_hip_buf *buf, uint8_t *
  * An E4M3 or MXE4M3 x (its cols == w.cols) needs an FP8 weight and skips
  * the activation quantization.  y is F32, BF16 or MXE4M3 (its cols ==
  * w.rows; the result is MX-quantized in the GEMM's epilogue).  MXE4M3 on
- * either side needs an FP8 weight with one scale per output channel,
- * w.cols a multiple of 128 and that buffer's row offset a multiple of 16;
- * otherwise LX2V_ERR_UNSUPPORTED. */
+ * either side needs an FP8 weight with one scale per output channel or per
+ * 128 columns, w.cols a multiple of 128 and that buffer's row offset a
+ * multiple of 16; otherwise LX2V_ERR_UNSUPPORTED. */
 int lx2v_hip_linear(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, size_t rows,
                     const lx2v_hip_weight *w, const lx2v_hip_buf *bias, int act,
                     lx2v_hip_buf *y, size_t y_row);

@@ -301,14 +301,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // per-stage LDS for A's block scales (BM rows x 4 bytes) or the weight's
     // group scales (BN floats): a whole wave's 16-byte DMA (lanes whose
     // offset is out of range still write their zeros)
-    constexpr int ASL = (AM || GS) ? 1024 : 16;
+    constexpr int ASL = AM ? 1024 : 16, GSL = GS ? 1024 : 16;
     static_assert(!AM || BM * 4 <= ASL, "A scale slot");
-    static_assert(!GS || (BKB == 128 && !AM && BN * 4 <= 64 * 16), "grouped scales: one 128-column group per stage");
-    constexpr bool XS = AM || GS;  // wave 0 issues one more load per stage
-    static_assert(NS >= 2 && OCC * (NS * STAGE + Ops::NV * 4 + NS * ASL) <= 160 * 1024, "LDS for OCC workgroups per CU");
+    static_assert(!GS || (BKB == 128 && BN * 4 <= 64 * 16), "grouped scales: one 128-column group per stage");
+    constexpr bool XS = AM || GS;       // wave 0 issues more loads per stage
+    constexpr int XN = (AM ? 1 : 0) + (GS ? 1 : 0);  // ... this many
+    static_assert(NS >= 2 && OCC * (NS * STAGE + Ops::NV * 4 + NS * (ASL + GSL)) <= 160 * 1024,
+                  "LDS for OCC workgroups per CU");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
     __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
     __shared__ __attribute__((aligned(16))) uint8_t asl[NS * ASL];
+    __shared__ __attribute__((aligned(16))) uint8_t gsl[NS * GSL];
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid / WGN, wn = wid % WGN;
@@ -333,10 +336,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // (readfirstlane: the saturating length would otherwise be computed on
     // the VALU and take the descriptor out of SGPRs)
     const auto rs_src = make_rsrc(
-        AM ? amx + 4 * m0 : (GS ? (const uint8_t *)(gsc + n0) : A),
-        __builtin_amdgcn_readfirstlane(
-            AM ? (amx_len > 4u * m0 ? amx_len - 4u * (uint32_t)m0 : 0u)
-               : (GS ? ((uint32_t)(2 * KT) * (uint32_t)N - (uint32_t)n0) * 4u : 0u)));
+        AM ? amx + 4 * m0 : A, __builtin_amdgcn_readfirstlane(AM ? (amx_len > 4u * m0 ? amx_len - 4u * (uint32_t)m0 : 0u)
+                                                                : 0u));
+    const auto rg_src = make_rsrc(
+        GS ? (const uint8_t *)(gsc + n0) : A,
+        __builtin_amdgcn_readfirstlane(GS ? ((uint32_t)(2 * KT) * (uint32_t)N - (uint32_t)n0) * 4u : 0u));
 
     // Load i of this wave covers tile rows [(i NW + wid) RPI, +RPI); lane l
     // fills slot l % CPR of row l / CPR.
@@ -363,7 +367,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             dma16(rb_src, sbuf + (BM + ((n - ALD) * NW + wid_u) * RPI) * BKB,
                   in ? b_off[n >= ALD ? n - ALD : 0] + k0 : kOob);
     };
-    // Wave 0's MX scale load of stage kt (slot buf), or its group-scale load.
+    // Wave 0's MX scale load of stage kt (slot buf) and / or its group-scale load.
     auto issue_scales = [&](int kt, int buf) {
         if constexpr (GS) {
             // lane l: channels n0 + 4 l .. + 3 of stage kt's group; past the
@@ -371,7 +375,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             // channels that are never stored
             if (wid_u == 0) {
                 const bool ok = kt < KT && lane < BN / 4;
-                dma16(rs_src, asl + buf * ASL, ok ? (uint32_t)(2 * kt) * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
+                dma16(rg_src, gsl + buf * GSL, ok ? (uint32_t)(2 * kt) * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
             }
         }
         if constexpr (AM) {
@@ -475,7 +479,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                if constexpr (AM)
+                if constexpr (AM && GS)
+                    part[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        f.b[j], f.a[i], kk == 0 ? (f32x16){} : part[j][i], 0, 0, 0, 127, 0, as[i]);
+                else if constexpr (AM)
                     acc[j][i] =
                         __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc[j][i], 0, 0, 0, 127, 0, as[i]);
                 else if constexpr (GS)
@@ -522,7 +529,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     auto read_gs = [&](int buf, int j, f32x4 (&gs)[4]) {
 #pragma unroll
         for (int g = 0; g < 4; g++)
-            gs[g] = *(const f32x4 *)(asl + buf * ASL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
+            gs[g] = *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
     };
     // fold(b, gs): block b = j TM + i, gs its column block's scales
     auto fold = [&](int b, const f32x4 *gs) {
@@ -585,7 +592,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         SOp as1;
         auto wait_stage = [&]() {
             if (XS && wid_u == 0)  // wave 0 also loads each stage's A scales
-                wait_vmcnt_lds0<(NS - 2) * (LPS + 1)>();
+                wait_vmcnt_lds0<(NS - 2) * (LPS + XN)>();
             else
                 wait_vmcnt_lds0<(NS - 2) * LPS>();
             __builtin_amdgcn_s_barrier();
@@ -650,8 +657,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 #pragma unroll
             for (int j = 0; j < NS; j++) {
                 if (kt + j < KT) {
-                    if (XS && wid_u == 0)  // wave 0 also loads each stage's A or group scales
-                        wait_vmcnt<(NS - 2) * (LPS + 1)>();
+                    if (XS && wid_u == 0)  // wave 0 also loads each stage's A and / or group scales
+                        wait_vmcnt<(NS - 2) * (LPS + XN)>();
                     else
                         wait_vmcnt<(NS - 2) * LPS>();
                     __builtin_amdgcn_s_barrier();
@@ -1814,6 +1821,17 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
             LX2V_DMA_A(AMV, GSV, LX2V_ACT_NONE, T);      \
     } while (0)
 #define LX2V_DMA(AMV, T) LX2V_DMA_G(AMV, 0, T)
+    if constexpr (GSC && MXIN) {
+        if (mx.wgs && mx.a) {
+            if (y_dtype == LX2V_DTYPE_BF16)
+                LX2V_DMA_G(1, 1, uint16_t);
+            else if (y_dtype == LX2V_DTYPE_F32)
+                LX2V_DMA_G(1, 1, float);
+            else
+                LX2V_DMA_G(1, 1, uint8_t);
+            return;
+        }
+    }
     if constexpr (GSC) {
         if (mx.wgs) {
             if (y_dtype == LX2V_DTYPE_BF16)
@@ -2136,9 +2154,9 @@ constexpr CfgCost kGroupedAuto[] = {
 bool mx_capable(int idx, bool mx_in) { return idx == 0 || idx == 3 || ((idx == 4 || idx == 6) && !mx_in); }
 // The configurations built with grouped weight scales (128-byte stages, one
 // workgroup per CU: the partial sums need the registers); MX output on the
-// 256 x 128 tile only, no MX activations.
+// 256 x 128 tiles, MX activations on the one-shot 256 x 128 tile only.
 bool grouped_capable(int idx, bool mx, bool mx_in) {
-    return !mx_in && (idx == 0 || idx == 6 || ((idx == 1 || idx == 10) && !mx));
+    return mx_in ? idx == 0 : (idx == 0 || idx == 6 || ((idx == 1 || idx == 10) && !mx));
 }
 // The overlapped-epilogue kernel (k_gemm_fp8_ov): per-token activations and
 // per-channel weight scales, bf16 or MX e4m3 output, whole 128-channel

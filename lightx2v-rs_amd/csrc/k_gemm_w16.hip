@@ -575,6 +575,40 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
     // share of the weight loads (waves below EJ % NW take one more).
     const bool extra = wid_u < EJ % NW;
     const uint32_t frow = lane & 31, fhalf = lane >> 5;
+    // One 16-element K slice's fragments: the wave's TM activation and TN
+    // weight row blocks.
+    struct Frag {
+        u32x4 x[TM], w[TN];
+    };
+    // read_one(j, kk, f, m): fragment m (activation blocks, then weight
+    // blocks) of slice kk of the stage in ring position j.
+    auto read_one = [&](int j, int kk, Frag &f, int m) {
+        const uint32_t c = (uint32_t)kk * 2u + fhalf;
+        if (m < TM) {
+            const uint8_t *xs = xr + (j % NS) * XS;
+            const uint32_t row = (uint32_t)(wm * WM + m * 32) + frow;
+            f.x[m] = *(const u32x4 *)(xs + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (XS - 1)));
+        } else {
+            const uint8_t *ws = wr + (j & 1) * WSL;
+            const uint32_t row = (uint32_t)(wn * WN + (m - TM) * 32) + frow;
+            f.w[m - TM] = *(const u32x4 *)(ws + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (WSL - 1)));
+        }
+    };
+    // The K loop is skewed by one slice: after barrier kt a wave contracts
+    // the previous stage's last slice (from registers, read before the
+    // barrier) while it reads this stage's first, then each slice while
+    // reading the next, so no MFMA waits for LDS after a barrier (with
+    // every read of a stage issued before its first MFMA, the reads' return
+    // held both waves of a SIMD off the matrix core).  fb holds the slice
+    // carried across the barrier; zero before the first stage, whose
+    // carried MFMAs then add +0.
+    Frag fa, fb;
+#pragma unroll
+    for (int i = 0; i < TM; i++) fb.x[i] = (u32x4){};
+#pragma unroll
+    for (int jj = 0; jj < TN; jj++) fb.w[jj] = (u32x4){};
+    constexpr int MPS = TN * TM;  // MFMAs per slice
+    static_assert(MPS == TM + TN, "one fragment read per MFMA");
     // Stage kt = (multiple of U) + J, U = lcm(NS, 2): ring slots are
     // compile-time offsets.
     auto stage = [&](auto J, int kt) {
@@ -585,64 +619,39 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
         else
             __builtin_amdgcn_s_waitcnt((VM0 & 15) | ((VM0 >> 4) << 14) | (7 << 4));
         asm volatile("s_barrier" ::: "memory");
-        const uint8_t *xs = xr + (j % NS) * XS;
-        const uint8_t *ws = wr + (j & 1) * WSL;
-        u32x4 xf[4][TM], wf[4][TN];
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const uint32_t c = (uint32_t)kk * 2u + fhalf;
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const uint32_t row = (uint32_t)(wm * WM + i * 32) + frow;
-                xf[kk][i] = *(const u32x4 *)(xs + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (XS - 1)));
-            }
-#pragma unroll
-            for (int jj = 0; jj < TN; jj++) {
-                const uint32_t row = (uint32_t)(wn * WN + jj * 32) + frow;
-                wf[kk][jj] = *(const u32x4 *)(ws + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (WSL - 1)));
-            }
-        }
-        // MFMAs; after each of the first ALD + EPW, one load of the batch
-        // of X(kt + NS - 1) (into the slot X(kt - 1) used) and weight stage
-        // kt + NS (into the slot of stage kt, dequantized in stage kt - 1):
+        // MFMAs: slice p - 1 of this stage (p = 0: the previous stage's last
+        // slice) from one fragment set while slice p is read into the other.
+        // After each of the first ALD + EPW MFMAs, one load of the batch of
+        // X(kt + NS - 1) (into the slot X(kt - 1) used) and weight stage kt
+        // + NS (into the slot of stage kt, dequantized in stage kt - 1):
         // issued back to back, the loads held both waves of a SIMD off the
         // MFMA pipe.  The dequantization of weight stage kt + 1 (its codes
         // landed before this stage's barrier) goes between later MFMAs: the
-        // reads after MFMA DQL, the conversion after DQM (the reads have
-        // had the MFMAs between to return), the stores after DQS.
-        constexpr int NMF = 4 * TN * TM, DQL = NMF / 4, DQM = NMF / 2, DQS = 3 * NMF / 4;
+        // reads after MFMA DQL, the conversion after DQM (the reads have had
+        // the MFMAs between to return), the stores after DQS.
+        constexpr int NMF = 4 * MPS, DQL = NMF / 4, DQM = NMF / 2, DQS = 3 * NMF / 4;
         static_assert(ALD + EPW <= NMF, "a stage's loads interleave with its MFMAs");
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++)
+        static_for<4>([&](auto P) {
+            constexpr int p = decltype(P)::value;
+            Frag &fc = p % 2 ? fa : fb;  // contracted (p = 0: carried)
+            Frag &fn = p % 2 ? fb : fa;  // read: slice p of this stage
 #pragma unroll
             for (int jj = 0; jj < TN; jj++)
 #pragma unroll
                 for (int i = 0; i < TM; i++) {
-                    acc[jj][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[kk][jj]),
-                                                                       __builtin_bit_cast(bf16x8, xf[kk][i]),
+                    acc[jj][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fc.w[jj]),
+                                                                       __builtin_bit_cast(bf16x8, fc.x[i]),
                                                                        acc[jj][i], 0, 0, 0);
-                    const int n = (kk * TN + jj) * TM + i;
-                    if (n < ALD + EPW) {
-                        __builtin_amdgcn_sched_barrier(0);
-                        piece(n, kt + NS - 1, (j + NS - 1) % NS, j % NS);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    if (n == DQL) {
-                        __builtin_amdgcn_sched_barrier(0);
-                        dq_load((j + 1) % NS);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    if (n == DQM) {
-                        __builtin_amdgcn_sched_barrier(0);
-                        dq_math();
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    if (n == DQS) {
-                        __builtin_amdgcn_sched_barrier(0);
-                        dq_store((j + 1) & 1);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
+                    const int m = jj * TM + i, n = p * MPS + m;
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (n < ALD + EPW) piece(n, kt + NS - 1, (j + NS - 1) % NS, j % NS);
+                    if (n == DQL) dq_load((j + 1) % NS);
+                    if (n == DQM) dq_math();
+                    if (n == DQS) dq_store((j + 1) & 1);
+                    read_one(j, p, fn, m);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
+        });
     };
 
     // Prologue: weight stage 0 alone, then as stages -NS+1 .. -1 would:
@@ -666,6 +675,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
             if (kt + decltype(J)::value < KT) stage(J, kt + decltype(J)::value);
         });
     }
+    // the last stage's last slice, from registers
+#pragma unroll
+    for (int jj = 0; jj < TN; jj++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+            acc[jj][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fb.w[jj]),
+                                                               __builtin_bit_cast(bf16x8, fb.x[i]), acc[jj][i], 0,
+                                                               0, 0);
     ops.park(sc, tid, m0, n0, M, N, nullptr, nullptr);
     staged_epilogue<BM, BN, NT, NS * RING + 2 * WSL, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0,
                                                               M, N, act, Y);

@@ -1909,14 +1909,13 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3, y_mx = y->dtype == LX2V_DTYPE_MXE4M3;
     if (y_mx && y->cols != N) return fail(LX2V_ERR_BAD_SHAPE, "MXE4M3 y has %zu cols, weight has %zu rows", y->cols, N);
     // FP8 weights the fp8 MFMA takes: one scale per channel, or per 128 columns.
-    const bool fp8_grouped = w->fmt == LX2V_WFMT_FP8 && w->group != K && w->sscale && !x_mx &&
+    const bool fp8_grouped = w->fmt == LX2V_WFMT_FP8 && w->group != K && w->sscale &&
                              gemm_fp8_grouped_supported(rows, N, K, w->group);
     const bool fp8_mfma = w->fmt == LX2V_WFMT_FP8 && (w->group == K ? gemm_fp8_supported(rows, N, K) : fp8_grouped);
-    if ((x_mx || y_mx) && (!fp8_mfma || K % 128 || (x_mx && (w->group != K || x_row % 16))))
+    if ((x_mx || y_mx) && (!fp8_mfma || K % 128 || (x_mx && x_row % 16)))
         return fail(LX2V_ERR_UNSUPPORTED,
-                    "MXE4M3 operands need an FP8 weight with cols %% 128 == 0 and one scale per channel (or, for an "
-                    "MX output only, per 128 columns), and an MX input row offset %% 16 == 0 (weight %zux%zu group "
-                    "%zu, x_row %zu)",
+                    "MXE4M3 operands need an FP8 weight with cols %% 128 == 0 and one scale per channel or per 128 "
+                    "columns, and an MX input row offset %% 16 == 0 (weight %zux%zu group %zu, x_row %zu)",
                     N, K, w->group, x_row);
     const char *xp = (const char *)x->ptr + x_row * K * x->elem_bytes();
     char *yp = (char *)y->ptr + y_row * N * y->elem_bytes();
@@ -2159,7 +2158,7 @@ static bool linear_fusable(const lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_
     const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3;
     const bool grouped = w->group != K;
     if (w->fmt != LX2V_WFMT_FP8 || h->quantized() || !gemm_fp8_supported(rows, N, K)) return false;
-    if (grouped && !(w->sscale && !x_mx && gemm_fp8_grouped_supported(rows, N, K, w->group))) return false;
+    if (grouped && !(w->sscale && gemm_fp8_grouped_supported(rows, N, K, w->group))) return false;
     if (!(ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized())) return false;
     if (plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx, grouped, h->dtype, LX2V_ACT_NONE, false, true).splits > 1)
         return false;

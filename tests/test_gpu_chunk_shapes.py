@@ -93,15 +93,17 @@ def test_call_site(be, name, rows, K, N, act, cfg, cfg_g128, group):
 @pytest.mark.parametrize("group", ["channel", 128])
 def test_ffn_pair_mx_handoff(be, group):
     """FFN up 4680x1536->8960 (GELU, MX output) -> FFN down 4680x8960->1536
-    (MX input), as the bench chains them."""
+    (MX input), as the bench chains them; both weights per-channel or both
+    group 128."""
     g1 = DIM if group == "channel" else 128
+    g2 = FFN if group == "channel" else 128
     x = O.bf16_round(normal(1101, M * DIM).reshape(M, DIM))
     w1f = normal(1102, FFN * DIM, 0.02).reshape(FFN, DIM)
     w2f = normal(1103, DIM * FFN, 0.02).reshape(DIM, FFN)
     q1, s1 = O.fp8_quantize(w1f, FFN, DIM, g1, True)
-    q2, s2 = O.fp8_quantize(w2f, DIM, FFN, FFN, True)  # MX input needs per-channel scales
+    q2, s2 = O.fp8_quantize(w2f, DIM, FFN, g2, True)
     b1, b2 = normal(1104, FFN, 0.01), normal(1105, DIM, 0.01)
-    w1, w2 = be.weight_fp8(q1, s1, FFN, DIM, g1), be.weight_fp8(q2, s2, DIM, FFN, FFN)
+    w1, w2 = be.weight_fp8(q1, s1, FFN, DIM, g1), be.weight_fp8(q2, s2, DIM, FFN, g2)
     xb, bb1, bb2 = _bf16_buf(be, x), be.upload(b1), be.upload(b2)
     h = be.alloc_mx(M, FFN)
     y = be.alloc(M * DIM, H.DTYPE_F32)
@@ -110,7 +112,7 @@ def test_ffn_pair_mx_handoff(be, group):
     if group == "channel":
         assert ks == {"gemm_fp8_e4m3.c9.mxout", "gemm_fp8_e4m3.c0.mxin"}, ks
     else:
-        assert ks == {"gemm_fp8_e4m3.c6.g128.mxout", "gemm_fp8_e4m3.c0.mxin"}, ks
+        assert ks == {"gemm_fp8_e4m3.c6.g128.mxout", "gemm_fp8_e4m3.c0.g128.mxin"}, ks
     # FFN up: MX output == MX quantizer of the same GEMM's f32 output, whole tensor
     h32 = be.alloc(M * FFN, H.DTYPE_F32)
     be.linear(xb, 0, M, w1, bb1, H.ACT_GELU_TANH, h32, 0)
@@ -126,7 +128,7 @@ def test_ffn_pair_mx_handoff(be, group):
     # FFN down on the decoded MX input
     hd = be.download(h).reshape(M, FFN)[p]
     got = be.download(y).reshape(M, DIM)[p]
-    w2d = O.fp8_dequantize(q2, s2, DIM, FFN, FFN)
+    w2d = O.fp8_dequantize(q2, s2, DIM, FFN, g2)
     assert_close(got, O.linear(hd, w2d, b2, 0, nthreads=8), *FP8_TIGHT, what="FFN down on MX input vs oracle")
     # the chain against the plain f32 oracle
     w1d = O.fp8_dequantize(q1, s1, FFN, DIM, g1)
@@ -189,25 +191,28 @@ def test_cfg5_bf16_output(be, rows, K, N, cfg):
     assert_close(got32[p], oracle_w8a8(x[p], q, s, K, b, 0), *FP8_TIGHT, what="cfg5 f32 out vs oracle(e4m3 acts)")
 
 
+@pytest.mark.parametrize("group", ["channel", 128])
 @pytest.mark.parametrize("name,seed", [("o", 1301), ("o2", 1302)])
-def test_o_on_mx_input(be, name, seed):
+def test_o_on_mx_input(be, name, seed, group):
     """The headline chunk's O and cross-attn O: 4680 x 1536 -> 1536 on the MX
     e4m3 input attention's epilogue writes (here the standalone MX quantizer
-    of bf16 N(0,1) values), bf16 output, as the bench runs them: the kernel
-    configuration asserted; sampled rows against the oracle on the decoded
-    MX input (FP8_TIGHT, f32 output) and against the plain f32 oracle on the
-    bf16 values (4e-2)."""
+    of bf16 N(0,1) values), bf16 output, as the bench runs them, per-channel
+    or group-128 weights: the kernel configuration asserted; sampled rows
+    against the oracle on the decoded MX input (FP8_TIGHT, f32 output) and
+    against the plain f32 oracle on the bf16 values (4e-2)."""
+    g = DIM if group == "channel" else 128
     x = O.bf16_round(normal(seed, M * DIM).reshape(M, DIM))
     wf = normal(seed + 1, DIM * DIM, 0.02).reshape(DIM, DIM)
-    q, s = O.fp8_quantize(wf, DIM, DIM, DIM, True)
+    q, s = O.fp8_quantize(wf, DIM, DIM, g, True)
     b = normal(seed + 2, DIM, 0.01)
-    w = be.weight_fp8(q, s, DIM, DIM, DIM)
+    w = be.weight_fp8(q, s, DIM, DIM, g)
     xb, bb = _bf16_buf(be, x), be.upload(b)
     xm = be.alloc_mx(M, DIM)
     be.quantize_mx(xb, 0, M, xm)
     y16 = be.alloc(M * DIM, H.DTYPE_BF16)
     y32 = be.alloc(M * DIM, H.DTYPE_F32)
-    assert _profiled(be, lambda: be.linear(xm, 0, M, w, bb, H.ACT_NONE, y16, 0)) == {"gemm_fp8_e4m3.c0.mxin"}
+    want = "gemm_fp8_e4m3.c0.mxin" if group == "channel" else "gemm_fp8_e4m3.c0.g128.mxin"
+    assert _profiled(be, lambda: be.linear(xm, 0, M, w, bb, H.ACT_NONE, y16, 0)) == {want}
     be.linear(xm, 0, M, w, bb, H.ACT_NONE, y32, 0)
     got32 = be.download(y32).reshape(M, DIM)
     assert np.array_equal(u32(be.download(y16).reshape(M, DIM)), u32(O.bf16_round(got32)))
@@ -216,6 +221,6 @@ def test_o_on_mx_input(be, name, seed):
     # the device decoder against the oracle's own MX quantizer of the same values
     qo, so = O.act_quant_mx(x[p])
     assert np.array_equal(u32(xd), u32(O.dequant_mx(qo, so)))
-    wd = O.fp8_dequantize(q, s, DIM, DIM, DIM)
+    wd = O.fp8_dequantize(q, s, DIM, DIM, g)
     assert_close(got32[p], O.linear(xd, wd, b, 0, nthreads=8), *FP8_TIGHT, what=f"{name} on MX input vs oracle")
     assert_close(got32[p], O.linear(x[p], wd, b, 0, nthreads=8), 4e-2, 0.3, what=f"{name} vs f32 oracle")

@@ -63,12 +63,17 @@ def test_quantize_mx_bit_exact(be, rows, cols, x_row, xdt):
 MX_SHAPES = [(300, 1536, 640), (77, 256, 160), (3000, 512, 2048), (2100, 2048, 2048), (1000, 1536, 8960)]
 
 
+@pytest.mark.parametrize("group", ["channel", 128])
 @pytest.mark.parametrize("M,K,N", MX_SHAPES + [(4680, 8960, 1536)])  # + the chunk's FFN down
-def test_linear_mx_input_vs_oracle(be, M, K, N):
+def test_linear_mx_input_vs_oracle(be, M, K, N, group):
+    """MX e4m3 input, per-channel or group-128 weights (group 128: the
+    256 x 128 grouped tile, the block-scaled MFMA into each group's partial
+    sums): the oracle on the decoded input, FP8_TIGHT."""
+    g = K if group == "channel" else 128
     x = normal(11 + M, M * K).reshape(M, K)
-    _, q, s = fp8_weight(12 + N, N, K, K)
+    _, q, s = fp8_weight(12 + N, N, K, g)
     b = normal(13, N, 0.01)
-    w = be.weight_fp8(q, s, N, K, K)
+    w = be.weight_fp8(q, s, N, K, g)
     bb = be.upload(b)
     xb = _upload(be, x, H.DTYPE_F32)
     xq = be.alloc_mx(M + 16, K)
@@ -84,8 +89,8 @@ def test_linear_mx_input_vs_oracle(be, M, K, N):
                                      np.random.default_rng(M).choice(rows, min(rows, 64), replace=False)]))
     qx, sx = O.act_quant_mx(x)
     xd = O.dequant_mx(qx, sx)[r0:][pick]
-    want = O.linear(xd, O.fp8_dequantize(q, s, N, K, K), b, 0, nthreads=8)
-    assert_close(got[pick], want, *FP8_TIGHT, what="MX-input fp8 GEMM vs oracle")
+    want = O.linear(xd, O.fp8_dequantize(q, s, N, K, g), b, 0, nthreads=8)
+    assert_close(got[pick], want, *FP8_TIGHT, what=f"MX-input fp8 GEMM (group {g}) vs oracle")
 
 
 @pytest.mark.parametrize("M,K,N", MX_SHAPES + [(4680, 1536, 8960)])
@@ -216,15 +221,13 @@ def test_mx_errors(be):
     with pytest.raises(H.HipError) as e:
         be.linear(xq, 0, M, w8, None, H.ACT_NONE, y, 0)
     assert e.value.status == H.ERR_UNSUPPORTED
-    _, qg, sg = fp8_weight(54, N, K, 128)  # grouped scales: no MX input
-    wg = be.weight_fp8(qg, sg, N, K, 128)
-    with pytest.raises(H.HipError) as e:
-        be.linear(xq, 0, M, wg, None, H.ACT_NONE, y, 0)
-    assert e.value.status == H.ERR_UNSUPPORTED
-    _, qg, sg = fp8_weight(55, N, K, 64)  # group 64: no MX output
+    _, qg, sg = fp8_weight(55, N, K, 64)  # group 64: no MX output, no MX input
     wg = be.weight_fp8(qg, sg, N, K, 64)
     with pytest.raises(H.HipError) as e:
         be.linear(xb, 0, M, wg, None, H.ACT_NONE, be.alloc_mx(M, N), 0)
+    assert e.value.status == H.ERR_UNSUPPORTED
+    with pytest.raises(H.HipError) as e:
+        be.linear(xq, 0, M, wg, None, H.ACT_NONE, y, 0)
     assert e.value.status == H.ERR_UNSUPPORTED
     with pytest.raises(H.HipError) as e:
         be.write(xq, np.zeros(4, np.float32))
