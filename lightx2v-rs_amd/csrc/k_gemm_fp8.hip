@@ -2137,6 +2137,11 @@ constexpr CfgCost kAuto[] = {
     {3, 0.606, 0.44, 4.59, false},  // 128 x 128, three per CU
     {5, 1.121, 14.77, 0.0, false},  // 256 x 256 ping-pong
     {7, 0.80, 2.70, 0.80, true},    // 256 x 128 persistent, overlapped epilogue
+    // 128 x 128, 128-byte stages, one per CU (measured 0.365 us per stage
+    // with a third of the CUs busy, 0.443 with all: 880 x 3072 -> 3072 13.3
+    // us against 19.1 on the three-per-CU tile, 880 x 14336 -> 3072 45.4
+    // against 49.9 split in two)
+    {10, 0.43, 4.30, 0.20, false},
 };
 // Grouped weight scales (128-byte stages only): the two one-per-CU tiles,
 // with the per-CU costs of their per-channel versions, and the persistent
@@ -2198,7 +2203,17 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
             S = std::min<size_t>((size_t)mode, kts);
         else if (mode != 0 && tiles * 2 <= (size_t)num_cu)
             S = std::min<size_t>(std::min<size_t>((size_t)num_cu / tiles, kts / 32), 8);
-        if (S >= 2 && (size_t)M * N * S * 4 < (1ull << 31)) {
+        // ... unless the 128 x 128 one-per-CU tile (its 4x the tiles fill the
+        // CUs without a reduction) is cheaper by the model below; a forced
+        // split count always splits
+        bool split = S >= 2 && (size_t)M * N * S * 4 < (1ull << 31);
+        if (split && mode < 2 && y_dtype != LX2V_DTYPE_MXE4M3) {  // (no MX output on that tile)
+            const size_t t10 = ((M + 127) / 128) * (N / 128), r10 = (t10 + num_cu - 1) / num_cu;
+            const double c10 = (double)r10 * ((double)kts * 0.43 + 4.30) + 0.20;
+            const double cs = (double)(kts / S) * 0.625 + 8.37 + 10.0;  // + the partials' store and reduction
+            split = cs <= c10;
+        }
+        if (split) {
             p.kernel = 0;
             p.splits = (int)S;
             return p;

@@ -142,20 +142,27 @@ def _profiled_names(be, fn):
 
 
 def _one_pass(fn):
+    old = os.environ.get("LIGHTX2V_HIP_FP8_SPLITK")
     os.environ["LIGHTX2V_HIP_FP8_SPLITK"] = "0"
     try:
         return fn()
     finally:
-        os.environ.pop("LIGHTX2V_HIP_FP8_SPLITK")
+        if old is None:
+            os.environ.pop("LIGHTX2V_HIP_FP8_SPLITK")
+        else:
+            os.environ["LIGHTX2V_HIP_FP8_SPLITK"] = old
 
 
-@pytest.mark.parametrize("M,K,N,cfg", [(880, 14336, 3072, "c0k2"), (300, 8192, 1536, "c0k2")])
-def test_split_k_shapes(be, M, K, N, cfg):
-    """Shapes where linear splits K (config 5's FFN down at M = 880 first,
-    then a smaller one: the scratch keeps the first call's partial sums):
-    the no-alloc call plans the same split, its partial sums in the
-    scratch, bit for bit; the one-pass kernel's sums differ, so the split
-    did run."""
+@pytest.mark.parametrize("M,K,N", [(880, 14336, 3072), (300, 8192, 1536)])
+def test_split_k_shapes(be, monkeypatch, M, K, N):
+    """Split K in two (LIGHTX2V_HIP_FP8_SPLITK=2, read per call: at these
+    shapes the planner itself prefers the 128 x 128 one-per-CU tile) at
+    config 5's FFN down at M = 880, then a smaller shape (the scratch keeps
+    the first call's partial sums): the no-alloc call plans the same split,
+    its partial sums in the scratch, bit for bit; the one-pass kernel's sums
+    differ, so the split did run."""
+    monkeypatch.setenv("LIGHTX2V_HIP_FP8_SPLITK", "2")
+    cfg = "c0k2"
     _, q, s = fp8_weight(21 + M, N, K, K, 0.015)
     w = be.weight_fp8(q, s, N, K, K)
     x = _X(be, normal(22 + M, M * K).reshape(M, K), H.DTYPE_BF16)
@@ -214,7 +221,7 @@ def test_second_context_busy_while_first_in_flight(be):
         other.close()
 
 
-def test_too_large_is_refused(be):
+def test_too_large_is_refused(be, monkeypatch):
     M, K, N = 6000, 8960, 256  # 6000 x 8960 e4m3 codes > 48 MiB
     _, q, s = fp8_weight(15, N, K, K)
     w = be.weight_fp8(q, s, N, K, K)
@@ -223,8 +230,10 @@ def test_too_large_is_refused(be):
     with pytest.raises(H.HipError) as e:
         be.linear_noalloc(x, 0, M, w, None, H.ACT_NONE, y, 0)
     assert e.value.status == H.ERR_UNSUPPORTED and "scratch" in str(e.value)
-    # 5000 rows: 42.7 MiB of codes, but linear splits K two ways here and the
-    # partial sums (9.8 MiB) do not fit beside them; 4000 rows fit both
+    # 5000 rows: 42.7 MiB of codes fit; with K split two ways the partial
+    # sums (9.8 MiB) do not fit beside them, and 4000 rows fit both
+    be.linear_noalloc(x, 0, 5000, w, None, H.ACT_NONE, y, 0)
+    monkeypatch.setenv("LIGHTX2V_HIP_FP8_SPLITK", "2")
     with pytest.raises(H.HipError) as e:
         be.linear_noalloc(x, 0, 5000, w, None, H.ACT_NONE, y, 0)
     assert e.value.status == H.ERR_UNSUPPORTED
