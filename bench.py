@@ -254,6 +254,10 @@ def yardstick(be, H):
 
     shapes = [(nm, r, n, k, act) for nm, r, n, k, act, _ in GEMMS]
     shapes.append(("kv2_all_layers", TEXT, LAYERS * 2 * DIM, DIM, 0))
+    # two large shapes: what the library reaches where launch, prologue and
+    # epilogue costs vanish against the K loop (a measured fp8 ceiling)
+    shapes.append(("large_4096x4096_14336", 4096, 14336, 4096, 0))
+    shapes.append(("large_8192_cube", 8192, 8192, 8192, 0))
     res = {}
     for nm, rows, n, k, act in shapes:
         a8 = torch.randn(rows, k, device=dev).to(torch.float8_e4m3fn)
@@ -288,7 +292,7 @@ def yardstick(be, H):
                    "hipblaslt_tflops": round(2.0 * rows * n * k / t_blas / 1e6, 1),
                    "this_build_tflops": round(2.0 * rows * n * k / t_ours / 1e6, 1)}
         log(f"yardstick {nm} {rows}x{k}->{n}: hipBLASLt {t_blas:.2f} us, this build {t_ours:.2f} us")
-    print(json.dumps({"yardstick": "hipBLASLt fp8 GEMM (torch._scaled_mm) vs this build, chunk shapes",
+    print(json.dumps({"yardstick": "hipBLASLt fp8 GEMM (torch._scaled_mm) vs this build, chunk shapes and two large ones",
                       "torch": torch.__version__, "shapes": res}), flush=True)
 
 

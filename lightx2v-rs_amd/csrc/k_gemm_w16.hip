@@ -412,7 +412,7 @@ __device__ __forceinline__ void unit_dequant(u32x4 c, float s, float z, uint32_t
     }
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int WF, typename TY>
+template <int BM, int BN, int WGM, int WGN, int NS, int WF, typename TY, int KE>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16_t *__restrict__ X,
                                                                  const uint8_t *__restrict__ Wc,
                                                                  const float *__restrict__ Wss,
@@ -422,25 +422,30 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
                                                                  int act, int tiles_m, int tiles_n) {
     constexpr int NW = WGM * WGN, NT = 64 * NW;
     constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+    // KE K elements per stage (64, or 32 for the 256 x 256 tile, whose
+    // 64-element rings would not fit the LDS); KB bytes per bf16 LDS row
+    constexpr int KB = KE * 2, CPR = KB / 16, RPL = 1024 / KB, SPS = 64 / KE;
+    static_assert(KE == 32 || KE == 64, "32- or 64-element K stages");
     constexpr bool Q4 = WF == LX2V_WFMT_Q4 || WF == kWfmtQ4Sym;
     constexpr bool ZL = WF == LX2V_WFMT_Q4;  // zeros loaded with the scales
     constexpr int DEN = Q4 ? 2 : 1;          // elements per code byte
-    constexpr int CBS = BKE / DEN;           // code bytes per weight row per stage
-    constexpr int XS = BM * XRB;             // activation slot
+    constexpr int CBS = KE / DEN;            // code bytes per weight row per stage
+    constexpr int XS = BM * KB;              // activation slot
     constexpr int CS = BN * CBS;             // code slot
-    constexpr int SS = BN * 16;              // scale (zero) slot: up to 4 per row
-    constexpr int WSL = BN * XRB;            // bf16 weight slot
+    constexpr int SS = BN * 16;              // scale (zero) slot: up to 4 per row (one 64-element stage's)
+    constexpr int WSL = BN * KB;             // bf16 weight slot
     constexpr int RING = XS + CS + SS * (ZL ? 2 : 1);  // one stage of every ring
     constexpr int XJ = XS / 1024, CJ = CS / 1024, SJ = SS / 1024, ZJ = ZL ? SJ : 0;
     constexpr int ALD = XJ / NW;             // activation loads per wave per stage
     constexpr int EJ = CJ + SJ + ZJ;         // weight loads per stage, spread over the waves
     constexpr int EPW = (EJ + NW - 1) / NW;  // ... at most this many per wave
-    constexpr int UPT = BN * (BKE / 16) / NT;  // 16-element units per thread per stage
+    constexpr int UPT = BN * (KE / 16) / NT;  // 16-element units per thread per stage
     using Ops = TileOps<BM, BN, NT>;
-    static_assert(ALD * NW == XJ && CS % 1024 == 0 && SS % 1024 == 0 && UPT * NT == BN * (BKE / 16),
+    static_assert(ALD * NW == XJ && CS % 1024 == 0 && SS % 1024 == 0 && UPT * NT == BN * (KE / 16),
                   "tile loads must split over the waves");
     static_assert(NS >= 2 && (NS - 1) * (ALD + EPW) < 64, "vmcnt range");
     static_assert(NS * RING + 2 * WSL + Ops::NV * 4 <= 160 * 1024, "LDS");
+    static_assert(XJ % NW == 0, "activation loads split over the waves");
     static_assert((XS & (XS - 1)) == 0 && (WSL & (WSL - 1)) == 0, "slot sizes are powers of two");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * RING + 2 * WSL];
     __shared__ __attribute__((aligned(16))) float sc[Ops::NV];
@@ -456,27 +461,29 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
     int tm, tn;
     xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int KT = K / BKE;
+    const int KT = K / KE;
     Ops ops;
     ops.load(tid, m0, n0, M, N, nullptr, nullptr, bias);
 
     // Rows past the matrix read zero (codes) or another row's scales: they
     // only feed outputs that are never stored.
     const uint32_t cbrow = (uint32_t)K / DEN;  // code bytes per weight row
-    const uint32_t sstage = (uint32_t)N * (uint32_t)spr * 4u;  // bytes of one stage of scales
+    // bytes of one 64-element stage of scales (the stage-major copy's rows;
+    // a 32-element stage loads its 64-element stage's)
+    const uint32_t sstage = (uint32_t)N * (uint32_t)spr * 4u;
     const auto rx = make_rsrc(X + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K * 2u);
     const auto rw = make_rsrc(Wc + (size_t)n0 * cbrow, (uint32_t)(N - n0) * cbrow);
-    const auto rs = make_rsrc(Wss, (uint32_t)KT * sstage);
-    const auto rz = make_rsrc(ZL ? Wsz : Wss, ZL ? (uint32_t)KT * sstage : 0u);
+    const auto rs = make_rsrc(Wss, (uint32_t)(KT / SPS) * sstage);
+    const auto rz = make_rsrc(ZL ? Wsz : Wss, ZL ? (uint32_t)(KT / SPS) * sstage : 0u);
 
-    // Activation load i of this wave: tile rows [(i NW + wid) 8, +8), lane l
-    // fills slot l % 8 of row l / 8.
-    const uint32_t lrow = (uint32_t)lane / 8u, lslot = (uint32_t)lane % 8u;
+    // Activation load i of this wave: tile rows [(i NW + wid) RPL, +RPL),
+    // lane l fills slot l % CPR of row l / CPR.
+    const uint32_t lrow = (uint32_t)lane / CPR, lslot = (uint32_t)lane % CPR;
     uint32_t x_off[ALD];
 #pragma unroll
     for (int i = 0; i < ALD; i++) {
-        const uint32_t row = (uint32_t)(i * NW + wid) * 8u + lrow;
-        x_off[i] = row * (uint32_t)K * 2u + dma_slot<XRB>(row, lslot) * 16u;
+        const uint32_t row = (uint32_t)(i * NW + wid) * RPL + lrow;
+        x_off[i] = row * (uint32_t)K * 2u + dma_slot<KB>(row, lslot) * 16u;
     }
     // Weight load x of this wave: job e = x NW + wid of [CJ code KBs, SJ
     // scale KBs, ZJ zero KBs]; its lane offset without the stage term.
@@ -499,7 +506,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
         if (n < ALD) {
             const bool in_x = kt >= 0 && kt < KT;
             dma16(rx, xr + slot_x * XS + (n * NW + wid_u) * 1024,
-                  in_x ? x_off[n < ALD ? n : 0] + (uint32_t)kt * XRB : kOob);
+                  in_x ? x_off[n < ALD ? n : 0] + (uint32_t)kt * KB : kOob);
             return;
         }
         const int x = n - ALD, e = x * NW + wid_u, xe = x < EPW ? x : 0;
@@ -509,36 +516,38 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
             dma16(rw, cr + slot_w * CS + e * 1024, in ? e_off[xe] + (uint32_t)kw * CBS : kOob);
         } else if (e < CJ + SJ) {
             dma16(rs, sr + slot_w * SS + (e - CJ) * 1024,
-                  in && e_off[xe] != kOob ? e_off[xe] + (uint32_t)kw * sstage : kOob);
+                  in && e_off[xe] != kOob ? e_off[xe] + (uint32_t)(kw / SPS) * sstage : kOob);
         } else if (e < EJ) {
             dma16(rz, zr + slot_w * SS + (e - CJ - SJ) * 1024,
-                  in && e_off[xe] != kOob ? e_off[xe] + (uint32_t)kw * sstage : kOob);
+                  in && e_off[xe] != kOob ? e_off[xe] + (uint32_t)(kw / SPS) * sstage : kOob);
         }
     };
     auto issue = [&](int kt, int slot_x, int slot_w) {
 #pragma unroll
         for (int n = 0; n < ALD + EPW; n++) piece(n, kt, slot_x, slot_w);
     };
-    // Weight stage kt from its code / scale slot into bf16 weight slot `ws`.
+    // Weight stage kw from its code / scale slot into bf16 weight slot `ws`.
     // ... in three parts, so that a stage can spread them between its MFMAs:
     // the codes and scales into registers, the conversion, the bf16 stores.
     u32x4 dqc[UPT];
     float dqs[UPT], dqz[UPT];
     uint32_t dqo[UPT][8];
-    auto dq_load = [&](int slot_w) {
+    auto dq_load = [&](int slot_w, int kw) {
         const uint8_t *cs = cr + slot_w * CS;
         const float *ss = (const float *)(sr + slot_w * SS);
         const float *zs = (const float *)(zr + slot_w * SS);
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
-            const uint32_t id = (uint32_t)(u * NT + tid), row = id / 4u, k16 = id % 4u;
+            const uint32_t id = (uint32_t)(u * NT + tid), row = id / (KE / 16), k16 = id % (KE / 16);
             if constexpr (Q4) {
                 const u32x2 h = *(const u32x2 *)(cs + row * CBS + k16 * 8u);
                 dqc[u] = (u32x4){h.x, h.y, 0u, 0u};
             } else {
                 dqc[u] = *(const u32x4 *)(cs + row * CBS + k16 * 16u);
             }
-            const uint32_t si = row * (uint32_t)spr + ((k16 * (uint32_t)spr) >> 2);
+            // the unit's 16 elements within their 64-element scale stage
+            const uint32_t u64 = (uint32_t)(kw % SPS) * (KE / 16) + k16;
+            const uint32_t si = row * (uint32_t)spr + ((u64 * (uint32_t)spr) >> 2);
             dqs[u] = ss[si];
             dqz[u] = ZL ? zs[si] : 0.0f;
         }
@@ -551,16 +560,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
         uint8_t *d = wr + ws * WSL;
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
-            const uint32_t id = (uint32_t)(u * NT + tid), row = id / 4u, k16 = id % 4u;
+            const uint32_t id = (uint32_t)(u * NT + tid), row = id / (KE / 16), k16 = id % (KE / 16);
             const uint32_t cc = k16 * 2u;
-            *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc) << 4)) & (WSL - 1))) =
+            *(u32x4 *)(d + ((row * KB + (dma_slot<KB>(row, cc) << 4)) & (WSL - 1))) =
                 (u32x4){dqo[u][0], dqo[u][1], dqo[u][2], dqo[u][3]};
-            *(u32x4 *)(d + ((row * XRB + (dma_slot<XRB>(row, cc + 1) << 4)) & (WSL - 1))) =
+            *(u32x4 *)(d + ((row * KB + (dma_slot<KB>(row, cc + 1) << 4)) & (WSL - 1))) =
                 (u32x4){dqo[u][4], dqo[u][5], dqo[u][6], dqo[u][7]};
         }
     };
-    auto dequant = [&](int slot_w, int ws) {
-        dq_load(slot_w);
+    auto dequant = [&](int slot_w, int ws, int kw) {
+        dq_load(slot_w, kw);
         dq_math();
         dq_store(ws);
     };
@@ -587,11 +596,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
         if (m < TM) {
             const uint8_t *xs = xr + (j % NS) * XS;
             const uint32_t row = (uint32_t)(wm * WM + m * 32) + frow;
-            f.x[m] = *(const u32x4 *)(xs + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (XS - 1)));
+            f.x[m] = *(const u32x4 *)(xs + ((row * KB + (dma_slot<KB>(row, c) << 4)) & (XS - 1)));
         } else {
             const uint8_t *ws = wr + (j & 1) * WSL;
             const uint32_t row = (uint32_t)(wn * WN + (m - TM) * 32) + frow;
-            f.w[m - TM] = *(const u32x4 *)(ws + ((row * XRB + (dma_slot<XRB>(row, c) << 4)) & (WSL - 1)));
+            f.w[m - TM] = *(const u32x4 *)(ws + ((row * KB + (dma_slot<KB>(row, c) << 4)) & (WSL - 1)));
         }
     };
     // The K loop is skewed by one slice: after barrier kt a wave contracts
@@ -607,8 +616,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
     for (int i = 0; i < TM; i++) fb.x[i] = (u32x4){};
 #pragma unroll
     for (int jj = 0; jj < TN; jj++) fb.w[jj] = (u32x4){};
-    constexpr int MPS = TN * TM;  // MFMAs per slice
-    static_assert(MPS == TM + TN, "one fragment read per MFMA");
+    constexpr int MPS = TN * TM, NSL = KE / 16;  // MFMAs per slice, slices per stage
+    static_assert(MPS >= TM + TN && NSL % 2 == 0, "at most one fragment read per MFMA; the carried set is fb");
     // Stage kt = (multiple of U) + J, U = lcm(NS, 2): ring slots are
     // compile-time offsets.
     auto stage = [&](auto J, int kt) {
@@ -629,9 +638,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
         // landed before this stage's barrier) goes between later MFMAs: the
         // reads after MFMA DQL, the conversion after DQM (the reads have had
         // the MFMAs between to return), the stores after DQS.
-        constexpr int NMF = 4 * MPS, DQL = NMF / 4, DQM = NMF / 2, DQS = 3 * NMF / 4;
+        constexpr int NMF = NSL * MPS, DQL = NMF / 4, DQM = NMF / 2, DQS = 3 * NMF / 4;
         static_assert(ALD + EPW <= NMF, "a stage's loads interleave with its MFMAs");
-        static_for<4>([&](auto P) {
+        static_for<NSL>([&](auto P) {
             constexpr int p = decltype(P)::value;
             Frag &fc = p % 2 ? fa : fb;  // contracted (p = 0: carried)
             Frag &fn = p % 2 ? fb : fa;  // read: slice p of this stage
@@ -645,10 +654,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
                     const int m = jj * TM + i, n = p * MPS + m;
                     __builtin_amdgcn_sched_barrier(0);
                     if (n < ALD + EPW) piece(n, kt + NS - 1, (j + NS - 1) % NS, j % NS);
-                    if (n == DQL) dq_load((j + 1) % NS);
+                    if (n == DQL) dq_load((j + 1) % NS, kt + 1);
                     if (n == DQM) dq_math();
                     if (n == DQS) dq_store((j + 1) & 1);
-                    read_one(j, p, fn, m);
+                    if (m < TM + TN) read_one(j, p, fn, m);
                     __builtin_amdgcn_sched_barrier(0);
                 }
         });
@@ -668,7 +677,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
             __builtin_amdgcn_s_waitcnt((VM0 & 15) | ((VM0 >> 4) << 14) | (7 << 4) | (15 << 8));
     }
     asm volatile("s_barrier" ::: "memory");
-    dequant(0, 0);
+    dequant(0, 0, 0);
     constexpr int U = NS % 2 ? 2 * NS : NS;
     for (int kt = 0; kt < KT; kt += U) {
         static_for<U>([&](auto J) {
@@ -688,7 +697,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
                                                               M, N, act, Y);
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int WF>
+template <int BM, int BN, int WGM, int WGN, int NS, int WF, int KE>
 void launch_dma_fmt(hipStream_t s, const uint16_t *x, const lx2v_hip_weight *w, const float *bias, int act, void *y,
                     int y_dtype, int M) {
     const int N = (int)w->rows, K = (int)w->cols;
@@ -696,28 +705,28 @@ void launch_dma_fmt(hipStream_t s, const uint16_t *x, const lx2v_hip_weight *w, 
     const dim3 grid(tiles_m * tiles_n), block(64 * WGM * WGN);
     const uint8_t *c = (const uint8_t *)w->codes;
     if (y_dtype == LX2V_DTYPE_BF16)
-        hipLaunchKernelGGL((k_gemm_w16_dma<BM, BN, WGM, WGN, NS, WF, uint16_t>), grid, block, 0, s, x, c, w->sscale,
+        hipLaunchKernelGGL((k_gemm_w16_dma<BM, BN, WGM, WGN, NS, WF, uint16_t, KE>), grid, block, 0, s, x, c, w->sscale,
                            w->szero, w->spr, bias, (uint16_t *)y, M, N, K, act, tiles_m, tiles_n);
     else
-        hipLaunchKernelGGL((k_gemm_w16_dma<BM, BN, WGM, WGN, NS, WF, float>), grid, block, 0, s, x, c, w->sscale,
+        hipLaunchKernelGGL((k_gemm_w16_dma<BM, BN, WGM, WGN, NS, WF, float, KE>), grid, block, 0, s, x, c, w->sscale,
                            w->szero, w->spr, bias, (float *)y, M, N, K, act, tiles_m, tiles_n);
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS>
+template <int BM, int BN, int WGM, int WGN, int NS, int KE = 64>
 void launch_dma_cfg(hipStream_t s, const uint16_t *x, const lx2v_hip_weight *w, const float *bias, int act, void *y,
                     int y_dtype, int M) {
     switch (w->fmt) {
         case LX2V_WFMT_Q8:
-            launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q8>(s, x, w, bias, act, y, y_dtype, M);
+            launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q8, KE>(s, x, w, bias, act, y, y_dtype, M);
             break;
         case LX2V_WFMT_Q4:
             if (w->zero8)
-                launch_dma_fmt<BM, BN, WGM, WGN, NS, kWfmtQ4Sym>(s, x, w, bias, act, y, y_dtype, M);
+                launch_dma_fmt<BM, BN, WGM, WGN, NS, kWfmtQ4Sym, KE>(s, x, w, bias, act, y, y_dtype, M);
             else
-                launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q4>(s, x, w, bias, act, y, y_dtype, M);
+                launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_Q4, KE>(s, x, w, bias, act, y, y_dtype, M);
             break;
         default:
-            launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_FP8>(s, x, w, bias, act, y, y_dtype, M);
+            launch_dma_fmt<BM, BN, WGM, WGN, NS, LX2V_WFMT_FP8, KE>(s, x, w, bias, act, y, y_dtype, M);
             break;
     }
 }
@@ -729,6 +738,7 @@ struct DmaCfg {
 constexpr DmaCfg kDmaW16[] = {
     {256, 128, 4, 2, 3},
     {128, 256, 2, 4, 2},
+    {256, 256, 4, 2, 4},  // 32-element K stages: half the activation bytes per MFMA of the 256 x 128 tile
 };
 constexpr int kNumDmaW16 = sizeof(kDmaW16) / sizeof(kDmaW16[0]);
 
@@ -736,19 +746,18 @@ void launch_dma_idx(int idx, hipStream_t s, const uint16_t *x, const lx2v_hip_we
                     void *y, int y_dtype, int M) {
     switch (idx) {
         case 0: launch_dma_cfg<256, 128, 4, 2, 3>(s, x, w, bias, act, y, y_dtype, M); break;
-        default: launch_dma_cfg<128, 256, 2, 4, 2>(s, x, w, bias, act, y, y_dtype, M); break;
+        case 1: launch_dma_cfg<128, 256, 2, 4, 2>(s, x, w, bias, act, y, y_dtype, M); break;
+        default: launch_dma_cfg<256, 256, 4, 2, 4, 32>(s, x, w, bias, act, y, y_dtype, M); break;
     }
 }
 
-// LIGHTX2V_HIP_W16_CFG=<index> forces a configuration (for sweeps).
+// LIGHTX2V_HIP_W16_CFG=<index> forces a configuration (for sweeps and
+// tests; read on every plan).
 int forced_w16_cfg() {
-    static const int v = [] {
-        const char *e = getenv("LIGHTX2V_HIP_W16_CFG");
-        if (!e || !*e) return -1;
-        const int i = atoi(e);
-        return (i >= 0 && i < kNumDmaW16) ? i : -1;
-    }();
-    return v;
+    const char *e = getenv("LIGHTX2V_HIP_W16_CFG");
+    if (!e || !*e) return -1;
+    const int i = atoi(e);
+    return (i >= 0 && i < kNumDmaW16) ? i : -1;
 }
 
 // ---- bf16 x bf16: native f32 weights rounded to bf16 at upload ------------------
@@ -940,7 +949,9 @@ bool gemm_w16_dma_supported(const lx2v_hip_weight *w, size_t M) {
 }
 
 // Fill efficiency of each configuration (useful tiles over tile slots of
-// the rounds the grid takes), the larger workgroup tile on ties.
+// the rounds the grid takes), the larger workgroup tile on ties (it moves
+// fewer activation bytes per MFMA: Q8 4680 x 1536 -> 8960 takes 159 us on
+// the 256 x 256 tile against 184 on 256 x 128, at the same fill).
 int plan_gemm_w16_dma(int num_cu, size_t M, size_t N) {
     if (forced_w16_cfg() >= 0) return forced_w16_cfg();
     double best = -1.0;
@@ -951,7 +962,8 @@ int plan_gemm_w16_dma(int num_cu, size_t M, size_t N) {
         const size_t slots = (size_t)num_cu;
         const size_t rounds = (tiles + slots - 1) / slots;
         const double eff = (double)M * N / ((double)rounds * slots * c.bm * c.bn);
-        if (eff > best * 1.0001) {
+        const bool tie = eff <= best * 1.0001 && eff >= best * 0.9999;
+        if (eff > best * 1.0001 || (tie && c.bm * c.bn > kDmaW16[pick].bm * kDmaW16[pick].bn)) {
             best = eff;
             pick = i;
         }

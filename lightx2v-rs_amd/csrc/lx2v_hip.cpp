@@ -2075,7 +2075,9 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         const uint16_t *xb;
         if (int rc = bf16_x(&xb)) return rc;
         const int cfg = plan_gemm_w16_dma(ctx->num_cu, rows, N);
-        if (int rc = run(ctx, name, [&] {
+        char pname[40];  // e.g. "gemm_w16_q8.c2": the tile configuration
+        snprintf(pname, sizeof pname, "%s.c%d", name, cfg);
+        if (int rc = run(ctx, pname, [&] {
                 launch_gemm_w16_dma(ctx->stream, cfg, xb, w, bp, act, yp, y->dtype, rows);
             }))
             return rc;
