@@ -878,9 +878,13 @@ def main():
         log("bench: configs " + ", ".join(f"{k} {v['us_per_linear']:.1f} us ({v['pct_peak']:.0f}%)"
                                           for k, v in configs.items()))
 
+    # roofline.traffic: the calibrated FETCH_SIZE + WRITE_SIZE bytes per launch
+    # of the chunk's GEMMs (two rocprofv3 --pmc passes of --gemm-only, in the
+    # committed summary)
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
-        traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
+        tj = json.load(open(TRAFFIC_FILE))
+        traffic = tj.get("l2_miss_bytes_per_launch", tj.get("hbm_bytes_per_launch"))
 
     cpu = None
     if not args.no_cpu:

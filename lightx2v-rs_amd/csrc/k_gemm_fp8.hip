@@ -2135,7 +2135,7 @@ constexpr CfgCost kAuto[] = {
     {2, 0.826, 4.21, 2.44, false},  // 256 x 128, two per CU
     {4, 0.926, 2.43, 4.47, false},  // 128 x 256, two per CU
     {3, 0.606, 0.44, 4.59, false},  // 128 x 128, three per CU
-    {5, 1.121, 14.77, 0.0, false},  // 256 x 256 ping-pong
+    {5, 1.40, 14.77, 0.0, false},   // 256 x 256 ping-pong (8192^3: 1.44 us per stage with every CU busy)
     {7, 0.80, 2.70, 0.80, true},    // 256 x 128 persistent, overlapped epilogue
     // 128 x 128, 128-byte stages, one per CU (measured 0.365 us per stage
     // with a third of the CUs busy, 0.443 with all: 880 x 3072 -> 3072 13.3
