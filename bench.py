@@ -104,15 +104,24 @@ def per_config(be, H):
         return w
 
     def alg_bytes(rows, n, k, xdt, ydt, kind, group):
-        """|X| + |W codes| + |scales (+ zeros)| + |bias| + |Y|, each once at its dtype."""
-        eb = {H.DTYPE_F32: 4, H.DTYPE_BF16: 2}
+        """|X| + |W codes| + |scales (+ zeros)| + |bias| + |Y|, each once at its
+        dtype ("e4m3": codes + a row scale; "mx": codes + one scale byte per 32)."""
+        def tensor(r, c, dt):
+            if dt == "e4m3":
+                return r * c + r * 4
+            if dt == "mx":
+                return r * c + r * c // 32
+            return r * c * {H.DTYPE_F32: 4, H.DTYPE_BF16: 2}[dt]
         codes = n * k // 2 if kind == "q4" else (n * k * 2 if kind == "native" else n * k)
         scales = 0 if kind == "native" else n * (k // group) * 4 * (2 if kind == "q4" else 1)
-        return rows * k * eb[xdt] + codes + scales + n * 4 + rows * n * eb[ydt]
+        return tensor(rows, k, xdt) + codes + scales + n * 4 + tensor(rows, n, ydt)
 
     def time_linear(name, x, rows, k, w, n, act, xdt, ydt, peak, path, kind="fp8", group=None):
-        be.set_act_dtype(ydt)
-        y = be.alloc(rows * n)
+        if ydt == "mx":
+            y = be.alloc_mx(rows, n)
+        else:
+            be.set_act_dtype(ydt)
+            y = be.alloc(rows * n)
         b = be.alloc(n, H.DTYPE_F32)
         be.fill_normal(b, 7, 0.01)
         # untimed warm-up for ~50 ms: the clock settles after the allocations and fills
@@ -152,6 +161,9 @@ def per_config(be, H):
     fp8_path = "per-token e4m3 activations (quantized inside linear) x FP8 weight, fp8 MFMA"
     fp8_g128_path = ("per-token e4m3 activations x FP8 weight with one scale per 128 columns, fp8 MFMA (each "
                      "128-column stage's partial sums scaled by the group's scale)")
+    g128_chunk_path = ("the chunk's input as its producer writes it (per-token e4m3: QKV, cross Q, the text K/V, "
+                       "FFN up; MX e4m3: O, cross O, FFN down) x FP8 weight with one scale per 128 columns, fp8 "
+                       "MFMA; bf16 output (FFN up: MX e4m3)")
     # config 1: FP8 self-attn Q projection, f32 activations in and out
     be.set_act_dtype(H.DTYPE_F32)
     x = be.alloc(M * DIM)
@@ -165,14 +177,22 @@ def per_config(be, H):
                 fp8_g128_path, group=128)
     w.free()
     x.free()
-    # config 4's seven GEMMs with group-128 weights, bf16 activations in and out
+    # config 4's seven GEMMs with group-128 weights, each on the input its producer
+    # writes in the chunk and with the chunk's output (as the headline times them)
     for name, rows, n, k, act, _ in GEMMS:
         be.set_act_dtype(H.DTYPE_BF16)
-        x = be.alloc(rows * k)
-        be.fill_normal(x, 1041, 1.0)
+        xb = be.alloc(rows * k)
+        be.fill_normal(xb, 1041, 1.0)
+        if name in ("o", "o2", "ffn2"):
+            x, xdt = be.alloc_mx(rows, k), "mx"
+            be.quantize_mx(xb, 0, rows, x)
+        else:
+            x, xdt = be.alloc_e4m3(rows, k), "e4m3"
+            be.quantize_act(xb, 0, rows, x)
+        xb.free()
         w = weight("fp8", n, k, 0.02, 1042 + n + k, group=128)
-        time_linear(f"cfg4_g128_{name}", x, rows, k, w, n, act, H.DTYPE_BF16, H.DTYPE_BF16, PEAK_FP8_TFLOPS,
-                    fp8_g128_path, group=128)
+        time_linear(f"cfg4_g128_{name}", x, rows, k, w, n, act, xdt, "mx" if name == "ffn1" else H.DTYPE_BF16,
+                    PEAK_FP8_TFLOPS, g128_chunk_path, group=128)
         w.free()
         x.free()
     # config 2: Q8 (per-32 scales) FFN up + GELU, bf16 activations
