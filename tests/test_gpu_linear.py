@@ -169,10 +169,12 @@ def test_fp8_split_k_row_offsets(be, monkeypatch):
                                          (8, H.ACT_GELU_TANH, H.DTYPE_BF16), (8, H.ACT_NONE, H.DTYPE_BF16),
                                          (8, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (8, H.ACT_NONE, H.DTYPE_MXE4M3),
                                          (9, H.ACT_GELU_TANH, H.DTYPE_BF16), (9, H.ACT_NONE, H.DTYPE_BF16),
-                                         (9, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (9, H.ACT_NONE, H.DTYPE_MXE4M3)])
+                                         (9, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (9, H.ACT_NONE, H.DTYPE_MXE4M3),
+                                         (10, H.ACT_GELU_TANH, H.DTYPE_BF16), (10, H.ACT_NONE, H.DTYPE_F32)])
 def test_fp8_forced_persistent_vs_config0(be, monkeypatch, cfg, act, ydt):
-    """The persistent tiles forced (LIGHTX2V_HIP_FP8_CFG, read per call)
-    against the one-shot configuration 0, bit for bit over the whole output:
+    """The persistent tiles (and the 128 x 128 one-per-CU tile, 10) forced
+    (LIGHTX2V_HIP_FP8_CFG, read per call) against the one-shot configuration
+    0, bit for bit over the whole output:
     1937 rows (ragged: 7 x 256 + 145) x 9216 channels is 576 tiles of 256 x
     128 or 288 of 256 x 256 (configurations 8, 9), so every workgroup of the
     grid walks two or more; GELU or none; bf16, f32 (configuration 6; 7 to
