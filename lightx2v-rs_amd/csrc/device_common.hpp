@@ -266,12 +266,16 @@ __device__ __forceinline__ uint32_t buffer_load_x1(__amdgpu_buffer_rsrc_t r, uin
 constexpr uint32_t kOob = 0x80000000u;
 
 // 16-byte vector store through a buffer descriptor: offsets >= num_bytes are
-// dropped by the hardware range check.
+// dropped by the hardware range check.  CP: the instruction's cache-policy
+// bits (gfx950: 1 = sc0, 2 = nt, 16 = sc1), a hint for where the written
+// lines are kept; the values stored are the same for every CP.
+template <int CP = 0>
 __device__ __forceinline__ void buffer_store_x4(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, CP);
 }
+template <int CP = 0>
 __device__ __forceinline__ void buffer_store_b8(uint8_t v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b8(v, r, (int)off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b8(v, r, (int)off, 0, CP);
 }
 
 // v_permlane32_swap: lanes 32..63 of x trade places with lanes 0..31 of y.

@@ -329,8 +329,8 @@ __device__ __forceinline__ void lds_to_global(const uint8_t *stg, int tid, int m
 // sizeof(TY) < 2^31: every LDS read is issued first, then every store, through
 // a descriptor of Y that drops rows past M -- no branches and no waits between
 // the stores.  RES (residual mode): h's chunks and the gate are loaded first
-// and h + y * gate stored.
-template <int R, int BN, int NT, typename TY, bool RES>
+// and h + y * gate stored.  CP: the stores' cache-policy bits (buffer_store_x4).
+template <int R, int BN, int NT, typename TY, bool RES, int CP = 0>
 __device__ __forceinline__ void lds_to_global_fast(const uint8_t *stg, int tid, int m0, int n0, int M, int N,
                                                    TY *__restrict__ Y, const float *__restrict__ gate) {
     constexpr int EB = sizeof(TY), RB = BN * EB, CPR = RB / 16, EPC = 16 / EB, SWZ = stage_swz<BN, TY>();
@@ -372,7 +372,7 @@ __device__ __forceinline__ void lds_to_global_fast(const uint8_t *stg, int tid, 
 #pragma unroll
                 for (int q = 0; q < EPC; q++) e[q] = residual1<TY>(he[q], e[q], gv[q]);
             }
-            buffer_store_x4(v[k], ry, off(b + k));
+            buffer_store_x4<CP>(v[k], ry, off(b + k));
         }
     }
 }
@@ -393,8 +393,10 @@ constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
 // WAIT0 = false: the caller's loads into `smem` are known complete (only a
 // barrier is taken first), so loads still in flight elsewhere -- the next
 // tile's stages of a persistent kernel -- keep flying through the epilogue.
+//
+// CP: the cache-policy bits of the tile's stores (buffer_store_x4).
 template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY, bool RES = true, int ACT = -1,
-          bool WAIT0 = true>
+          bool WAIT0 = true, int CP = 0>
 __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, const float *sc, int wr,
                                                 int wc, int tid, int lane, int m0, int n0, int M, int N, int act,
                                                 TY *__restrict__ Y, MxOut mx = MxOut()) {
@@ -426,17 +428,17 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uin
         __syncthreads();
         if constexpr (sizeof(TY) == 1 || !RES) {
             if (fast)
-                lds_to_global_fast<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y, nullptr);
+                lds_to_global_fast<R, BN, NT, TY, false, CP>(smem, tid, m0 + p * R, n0, M, N, Y, nullptr);
             else
                 lds_to_global<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y);
         } else if (mx.gate) {
             if (fast)
-                lds_to_global_fast<R, BN, NT, TY, true>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
+                lds_to_global_fast<R, BN, NT, TY, true, CP>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
             else
                 lds_to_global<R, BN, NT, TY, true>(smem, tid, m0 + p * R, n0, M, N, Y, mx.gate);
         } else {
             if (fast)
-                lds_to_global_fast<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y, nullptr);
+                lds_to_global_fast<R, BN, NT, TY, false, CP>(smem, tid, m0 + p * R, n0, M, N, Y, nullptr);
             else
                 lds_to_global<R, BN, NT, TY, false>(smem, tid, m0 + p * R, n0, M, N, Y);
         }

@@ -36,12 +36,29 @@
 #ifndef LX2V_FP8_EARLY
 #define LX2V_FP8_EARLY 1
 #endif
+// Cache-policy bits of the output stores (buffer_store: 1 = sc0, 2 = nt,
+// 16 = sc1): of the LDS-staged epilogues (k_gemm_fp8_dma, _pt, _pp) and of
+// k_gemm_fp8_w4's register epilogue with MX e4m3 / bf16 output.  The values
+// written are the same for every policy; the choice is by measured time at
+// the Wan shapes (one-round 4680 x 1536 -> 1536 tiles about 1.3 us faster
+// per launch with sc1, FFN up's MX output about 4.5 us; sc1 made the bf16
+// 256 x 256 stores slower).
+#ifndef LX2V_STAGED_CP
+#define LX2V_STAGED_CP 16
+#endif
+#ifndef LX2V_W4MX_CP
+#define LX2V_W4MX_CP 16
+#endif
+#ifndef LX2V_W4BF_CP
+#define LX2V_W4BF_CP 0
+#endif
 
 namespace lx2v {
 
 namespace {
 
 constexpr int BK = 128;  // bytes (= e4m3 elements) of K per stage
+constexpr int kStagedCP = LX2V_STAGED_CP;
 
 // 16-byte chunk `c` (0..7) of tile row `row` lives at this LDS byte offset.
 __device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t c) {
@@ -679,8 +696,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     mx.scales = ymx;
     mx.rows = ymx_rows;
     mx.gate = gate;
-    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY, true, ACT>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0,
-                                                                     n0, M, N, act, Y, mx);
+    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY, true, ACT, true, kStagedCP>(
+        acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N, act, Y, mx);
 }
 
 // ---- persistent direct-to-LDS kernel ---------------------------------------------
@@ -953,7 +970,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
         MxOut mx;
         mx.scales = ymx;
         mx.rows = ymx_rows;
-        staged_epilogue<BM, BN, 64 * NW, STAGE, TM, TN, TY, false, ACT, false>(
+        staged_epilogue<BM, BN, 64 * NW, STAGE, TM, TN, TY, false, ACT, false, kStagedCP>(
             acc, smem + ((s - 1) % NS) * STAGE, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N, act, Y, mx);
     }
     wait_vmcnt<0>();  // the walk's trailing loads (zeros) land before the workgroup ends
@@ -1349,6 +1366,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8_w4(const uint8_t *__restric
     // stores per epilogue per lane: bf16 two 16-byte stores per 32 x 32
     // block; MX one 16-byte code store and one scale byte
     constexpr int ST = TM * TN * 2;
+    constexpr int W4CP = EB == 1 ? LX2V_W4MX_CP : LX2V_W4BF_CP;  // the stores' cache policy
     static_assert((NS - 2) * LPS + ST < 64, "vmcnt range");
     static_assert(NS * STAGE + 2 * NV * 4 + 1024 <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
@@ -1530,8 +1548,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8_w4(const uint8_t *__restric
                     swap32(ww[1], ww[3]);
                     swap32(ww[4], ww[6]);
                     swap32(ww[5], ww[7]);
-                    buffer_store_x4((u32x4){ww[0], ww[1], ww[2], ww[3]}, ry, in ? (row + 8u * (uint32_t)hf) * 2u : kOob);
-                    buffer_store_x4((u32x4){ww[4], ww[5], ww[6], ww[7]}, ry,
+                    buffer_store_x4<W4CP>((u32x4){ww[0], ww[1], ww[2], ww[3]}, ry, in ? (row + 8u * (uint32_t)hf) * 2u : kOob);
+                    buffer_store_x4<W4CP>((u32x4){ww[4], ww[5], ww[6], ww[7]}, ry,
                                     in ? (row + 16u + 8u * (uint32_t)hf) * 2u : kOob);
                 } else {
                     const int kx = mx_exponent(max_pair32(amax));
@@ -1541,8 +1559,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8_w4(const uint8_t *__restric
                     // lane l: channels 0..15 as w0, w2, w1, w3; lane l + 32: 16..31
                     swap32(ww[0], ww[2]);
                     swap32(ww[1], ww[3]);
-                    buffer_store_x4((u32x4){ww[0], ww[2], ww[1], ww[3]}, ry, in ? row + 16u * (uint32_t)hf : kOob);
-                    buffer_store_b8((uint8_t)(kx + 127), rmx,
+                    buffer_store_x4<W4CP>((u32x4){ww[0], ww[2], ww[1], ww[3]}, ry, in ? row + 16u * (uint32_t)hf : kOob);
+                    buffer_store_b8<W4CP>((uint8_t)(kx + 127), rmx,
                                     in && hf == 0 ? (uint32_t)mx_sidx((size_t)m, (size_t)(n / 32), (size_t)ymx_rows)
                                                   : kOob);
                 }
@@ -1768,8 +1786,8 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pp(const uint8_t *__restric
     if (grp == 0) __builtin_amdgcn_s_barrier();
     ops.park(sc, tid, m0, n0, M, N, sa, sb);
     // no residual mode here: its prefetch registers would spill this tile
-    staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY, false>(acc, smem, sc, grp * (BM / 2) + wm * WM, wn * WN, tid,
-                                                               lane, m0, n0, M, N, act, Y);
+    staged_epilogue<BM, BN, 512, NS * STAGE, TM, TN, TY, false, -1, true, kStagedCP>(
+        acc, smem, sc, grp * (BM / 2) + wm * WM, wn * WN, tid, lane, m0, n0, M, N, act, Y);
 }
 
 template <int BN, int GM, int GN, int BKB, int NS>

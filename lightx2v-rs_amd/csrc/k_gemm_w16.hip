@@ -18,6 +18,14 @@
 
 #include "gemm_common.hpp"
 
+// Cache-policy bits of the LDS-staged epilogue's stores (buffer_store: 1 =
+// sc0, 2 = nt, 16 = sc1; the values written are the same for every policy):
+// sc1, as k_gemm_fp8.hip's staged epilogues (measured: Q4 FFN down and the
+// native 4680 x 64 -> 1536 linear 1-10% faster, Q8 FFN up unchanged).
+#ifndef LX2V_W16_CP
+#define LX2V_W16_CP 16
+#endif
+
 namespace lx2v {
 
 namespace {
@@ -693,8 +701,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_w16_dma(const uint16
                                                                __builtin_bit_cast(bf16x8, fb.x[i]), acc[jj][i], 0,
                                                                0, 0);
     ops.park(sc, tid, m0, n0, M, N, nullptr, nullptr);
-    staged_epilogue<BM, BN, NT, NS * RING + 2 * WSL, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0,
-                                                              M, N, act, Y);
+    staged_epilogue<BM, BN, NT, NS * RING + 2 * WSL, TM, TN, TY, true, -1, true, LX2V_W16_CP>(
+        acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N, act, Y);
 }
 
 template <int BM, int BN, int WGM, int WGN, int NS, int WF, int KE>
@@ -886,8 +894,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_bf16_dma(const uint1
         }
     }
     ops.park(sc, tid, m0, n0, M, N, nullptr, nullptr);
-    staged_epilogue<BM, BN, NT, NS * STAGE, TM, TN, TY>(acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N,
-                                                       act, Y);
+    staged_epilogue<BM, BN, NT, NS * STAGE, TM, TN, TY, true, -1, true, LX2V_W16_CP>(
+        acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N, act, Y);
 }
 
 template <int BM, int BN, int WGM, int WGN, int NS>
