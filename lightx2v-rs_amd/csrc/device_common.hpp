@@ -147,13 +147,19 @@ __device__ __forceinline__ uint32_t e4m3_canon_encode(float v) {
 // the hardware pack conversion, round to nearest even.  An exhaustive sweep
 // of every f32 in [-448, 448] on gfx950 found it bit-identical to
 // e4m3_ocp_encode, the rule the oracle restates.
-// Without the clamp: every finite value scaled by mx_inv(mx_exponent(amax))
-// lies within +-448 already (mx_exponent's bound); infinities and NaNs
-// become NaN codes instead of +-448.
-__device__ __forceinline__ uint32_t quant4_nc(const float *v, float inv) {
-    int r = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, 0, false);
-    r = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, r, true);
-    return (uint32_t)r;
+// Without the clamp (quant4_sc): every finite value of a block scaled by
+// 2^-mx_exponent(amax) lies within +-448 already (mx_exponent's bound);
+// infinities and NaNs become NaN codes instead of +-448.  quant4_sc takes
+// the block's scale 2^k (mx_scale) and divides by it inside gfx950's scaled
+// conversion (v_cvt_scalef32_pk_fp8_f32), which saves the multiply per
+// value; a probe on the GPU found it bit-identical to the unscaled pack of
+// v * 2^-k (lo and hi words, k from -127 to 120, 75 M in-range values plus
+// infinities, NaNs and out-of-range values).
+__device__ __forceinline__ uint32_t quant4_sc(const float *v, float scale) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    v2s r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32((v2s){0, 0}, v[0], v[1], scale, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[2], v[3], scale, true);
+    return __builtin_bit_cast(uint32_t, r);
 }
 
 __device__ __forceinline__ uint32_t quant4(const float *v, float inv) {
@@ -178,6 +184,10 @@ __device__ __forceinline__ int mx_exponent(float amax) {
 
 // 2^-k as an f32 for k in [-127, 126] (every finite amax gives k <= 121).
 __device__ __forceinline__ float mx_inv(int k) { return __uint_as_float((uint32_t)(127 - k) << 23); }
+// The scale operand of quant4_sc: 2^k as an f32 for k in [-126, 127]; k =
+// -127 gives the bit pattern 0, which the conversion reads as the E8M0
+// scale 2^-127 (its exponent field).
+__device__ __forceinline__ float mx_scale(int k) { return __uint_as_float((uint32_t)(127 + k) << 23); }
 
 // ---- GELU (crates/lightx2v-cpu/src/lib.rs:151-153) --------------------------
 

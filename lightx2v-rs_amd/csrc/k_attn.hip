@@ -480,10 +480,10 @@ __global__ __launch_bounds__(AT) void k_attn_mfma(const void *__restrict__ Q, co
             }
             amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
             const int k = mx_exponent(amax);
-            const float minv = mx_inv(k);
+            const float msc = mx_scale(k);
 #pragma unroll
             for (int g = 0; g < 4; g++)
-                *(uint32_t *)((uint8_t *)out + row0 + 32 * b + 8 * g + 4 * hf) = quant4_nc(v + 4 * g, minv);
+                *(uint32_t *)((uint8_t *)out + row0 + 32 * b + 8 * g + 4 * hf) = quant4_sc(v + 4 * g, msc);
             if (hf == 0) omx[mx_sidx(q, (head * D + 32 * b) / 32, omx_rows)] = (uint8_t)(k + 127);
         }
         return;
@@ -546,9 +546,9 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pa
 #pragma unroll
         for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
         const int k = mx_exponent(amax);
-        const float minv = mx_inv(k);
+        const float msc = mx_scale(k);
         if (!live) return;
-        *(uint32_t *)((uint8_t *)out + oi) = quant4_nc(v, minv);
+        *(uint32_t *)((uint8_t *)out + oi) = quant4_sc(v, msc);
         if (ch % 8 == 0) omx[mx_sidx(q, (head * D + 4 * ch) / 32, omx_rows)] = (uint8_t)(k + 127);
     } else if constexpr (ODT == LX2V_DTYPE_BF16) {
         if (!live) return;

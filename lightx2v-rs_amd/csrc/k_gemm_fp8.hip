@@ -1179,9 +1179,9 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
             if constexpr (q == qF23) {
                 const float amax = max_pair32(e.amax);
                 e.kx = mx_exponent(amax);
-                const float inv = mx_inv(e.kx);
+                const float msc = mx_scale(e.kx);
 #pragma unroll
-                for (int g = 0; g < 4; g++) e.w[g] = quant4_nc(e.v + 4 * g, inv);
+                for (int g = 0; g < 4; g++) e.w[g] = quant4_sc(e.v + 4 * g, msc);
                 // lane l: channels 0..15 as w0, w2, w1, w3; lane l + 32: 16..31
                 swap32(e.w[0], e.w[2]);
                 swap32(e.w[1], e.w[3]);
@@ -1553,9 +1553,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8_w4(const uint8_t *__restric
                                     in ? (row + 16u + 8u * (uint32_t)hf) * 2u : kOob);
                 } else {
                     const int kx = mx_exponent(max_pair32(amax));
-                    const float inv = mx_inv(kx);
+                    const float msc = mx_scale(kx);
 #pragma unroll
-                    for (int g = 0; g < 4; g++) ww[g] = quant4_nc(v + 4 * g, inv);
+                    for (int g = 0; g < 4; g++) ww[g] = quant4_sc(v + 4 * g, msc);
                     // lane l: channels 0..15 as w0, w2, w1, w3; lane l + 32: 16..31
                     swap32(ww[0], ww[2]);
                     swap32(ww[1], ww[3]);
