@@ -52,6 +52,9 @@
 #ifndef LX2V_W4BF_CP
 #define LX2V_W4BF_CP 0
 #endif
+#ifndef LX2V_OV_CP
+#define LX2V_OV_CP 0
+#endif
 
 namespace lx2v {
 
@@ -1166,14 +1169,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
                 swap32(e.w[1], e.w[3]);
             }
             if constexpr (q == qS01)
-                buffer_store_x4((u32x4){e.w[0], e.w[1], e.w[2], e.w[3]}, ry,
+                buffer_store_x4<LX2V_OV_CP>((u32x4){e.w[0], e.w[1], e.w[2], e.w[3]}, ry,
                                 in ? (row + 8u * (uint32_t)hf) * 2u : kOob);
             if constexpr (q == qF23) {
                 swap32(e.w[4], e.w[6]);
                 swap32(e.w[5], e.w[7]);
             }
             if constexpr (q == qS23)
-                buffer_store_x4((u32x4){e.w[4], e.w[5], e.w[6], e.w[7]}, ry,
+                buffer_store_x4<LX2V_OV_CP>((u32x4){e.w[4], e.w[5], e.w[6], e.w[7]}, ry,
                                 in ? (row + 16u + 8u * (uint32_t)hf) * 2u : kOob);
         } else {
             if constexpr (q == qF23) {
@@ -1187,8 +1190,8 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
                 swap32(e.w[1], e.w[3]);
             }
             if constexpr (q == qS23) {
-                buffer_store_x4((u32x4){e.w[0], e.w[2], e.w[1], e.w[3]}, ry, in ? row + 16u * (uint32_t)hf : kOob);
-                buffer_store_b8((uint8_t)(e.kx + 127), rmx,
+                buffer_store_x4<LX2V_OV_CP>((u32x4){e.w[0], e.w[2], e.w[1], e.w[3]}, ry, in ? row + 16u * (uint32_t)hf : kOob);
+                buffer_store_b8<LX2V_OV_CP>((uint8_t)(e.kx + 127), rmx,
                                 in && hf == 0 ? (uint32_t)mx_sidx((size_t)m, (size_t)(n / 32), (size_t)ymx_rows)
                                               : kOob);
             }
