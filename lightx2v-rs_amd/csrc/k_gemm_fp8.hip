@@ -37,12 +37,14 @@
 #define LX2V_FP8_EARLY 1
 #endif
 // Cache-policy bits of the output stores (buffer_store: 1 = sc0, 2 = nt,
-// 16 = sc1): of the LDS-staged epilogues (k_gemm_fp8_dma, _pt, _pp) and of
-// k_gemm_fp8_w4's register epilogue with MX e4m3 / bf16 output.  The values
-// written are the same for every policy; the choice is by measured time at
-// the Wan shapes (one-round 4680 x 1536 -> 1536 tiles about 1.3 us faster
-// per launch with sc1, FFN up's MX output about 4.5 us; sc1 made the bf16
-// 256 x 256 stores slower).
+// 16 = sc1): of the LDS-staged epilogues (k_gemm_fp8_dma, _pt, _pp), of
+// k_gemm_fp8_w4's register epilogue with MX e4m3 / bf16 output and of
+// k_gemm_fp8_ov's.  The values written are the same for every policy; the
+// choice is by measured time at the Wan shapes: sc1 made the one-round
+// 4680 x 1536 -> 1536 tiles about 1.3 us faster per launch and FFN up's MX
+// output about 4 us, and made the bf16 256 x 256 stores (the 30-layer K/V
+// call) and the overlapped epilogue's (QKV) slower: 0.1 and 1.3 ms per
+// chunk; nt was slower wherever a tile stores from registers.
 #ifndef LX2V_STAGED_CP
 #define LX2V_STAGED_CP 16
 #endif
