@@ -312,8 +312,52 @@ def yardstick(be, H):
                    "hipblaslt_tflops": round(2.0 * rows * n * k / t_blas / 1e6, 1),
                    "this_build_tflops": round(2.0 * rows * n * k / t_ours / 1e6, 1)}
         log(f"yardstick {nm} {rows}x{k}->{n}: hipBLASLt {t_blas:.2f} us, this build {t_ours:.2f} us")
+    # bf16: hipBLASLt's GEMM (torch.mm, bf16 x bf16 -> bf16) beside this build's
+    # Q8 / Q4 linears (per-32 scales, dequantized to bf16 in the K loop) and its
+    # native bf16-weight linear at configs 2 and 3's shapes, and 8192^3
+    res16 = {}
+    for nm, rows, n, k, act in (("cfg2_ffn_up", M, FFN, DIM, 1), ("cfg3_ffn_down", M, DIM, FFN, 0),
+                                ("large_8192_cube", 8192, 8192, 8192, 0)):
+        xb = torch.randn(rows, k, device=dev, dtype=torch.bfloat16)
+        wb = 0.02 * torch.randn(n, k, device=dev, dtype=torch.bfloat16)
+        t_blas = ev_time(lambda: torch.mm(xb, wb.t()))
+        del xb, wb
+        torch.cuda.empty_cache()
+        be.set_act_dtype(H.DTYPE_BF16)
+        x = be.alloc(rows * k)
+        be.fill_normal(x, 21, 1.0)
+        tmp = be.alloc(n * k, H.DTYPE_F32)
+        be.fill_normal(tmp, 22, 0.02)
+        ws = {"native_bf16": be.weight(be.download(tmp), n, k)}
+        if not nm.startswith("large"):
+            ws["q8_g32"] = be.quantize_q8(tmp, n, k, 32)
+            ws["q4_g32"] = be.quantize_q4_sym(tmp, n, k, 32)
+        tmp.free()
+        bias = be.alloc(n, H.DTYPE_F32)
+        be.fill_normal(bias, 23, 0.01)
+        y = be.alloc(rows * n)
+        entry = {"shape": f"{rows}x{k}->{n}", "hipblaslt_us": round(t_blas, 2),
+                 "hipblaslt_tflops": round(2.0 * rows * n * k / t_blas / 1e6, 1)}
+        for wn, w in ws.items():
+            for _ in range(10):
+                be.linear(x, 0, rows, w, bias, act, y, 0)
+            be.profile_region("y16_" + nm + wn, True)
+            for _ in range(30):
+                be.linear(x, 0, rows, w, bias, act, y, 0)
+            be.profile_region("y16_" + nm + wn, False)
+            t = be.profile_kernel("y16_" + nm + wn)[1] * 1e3 / 30
+            entry[wn + "_us"] = round(t, 2)
+            entry[wn + "_tflops"] = round(2.0 * rows * n * k / t / 1e6, 1)
+            w.free()
+        for h in (x, bias, y):
+            h.free()
+        res16[nm] = entry
+        log(f"yardstick bf16 {nm} {rows}x{k}->{n}: hipBLASLt {t_blas:.2f} us, " +
+            ", ".join(f"{kk[:-3]} {vv} us" for kk, vv in entry.items() if kk.endswith("_us") and kk != "hipblaslt_us"))
     print(json.dumps({"yardstick": "hipBLASLt fp8 GEMM (torch._scaled_mm) vs this build, chunk shapes and two large ones",
-                      "torch": torch.__version__, "shapes": res}), flush=True)
+                      "torch": torch.__version__, "shapes": res,
+                      "bf16": {"what": "hipBLASLt bf16 GEMM (torch.mm) vs this build's Q8 / Q4 / native bf16 linears "
+                                       "(bias; GELU at FFN up)", "shapes": res16}}), flush=True)
 
 
 def cpu_baseline(seconds_target=12.0):
