@@ -2086,8 +2086,8 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
                                                                     mx);
             break;
         case 1:
-            launch_dma<128, 256, 2, 4, 128, 3, 1, false, false, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K,
-                                                                      mx);
+            launch_dma<128, 256, 2, 4, 128, 3, 1, true, true, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K,
+                                                                    mx);
             break;
         case 2: launch_dma<256, 128, 4, 2, 64, 3, 2>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx); break;
         case 3:
@@ -2148,43 +2148,70 @@ bool gemm_fp8_supported(size_t M, size_t N, size_t K) {
 // the Wan shapes: 7 (epilogue folded into the next tile) at 256 x 128 x
 // 1536 tiles -- FFN up 6 passes 75 us, QKV 3 passes 38 us; 6 (grouped
 // scales) at QKV 45 us and FFN up 84 us.
+//
+// The one-per-CU tiles with 128-byte stages (0, 1, 10) have an occupancy
+// term instead: their stages slow down with the share of CUs loading at
+// once, so round r costs stages x (per_stage + occ_stage x busy_r) +
+// per_round, busy_r the share of CUs with a tile in round r.  Fitted to
+// launch times at 4680 x 1536 -> 1536, 4680 x 8960 -> 1536, 512 x 1536 ->
+// 3072 and config 5's 2640- and 880-row shapes (256 x 128 and 128 x 256:
+// 0.40 + 0.38 busy us per stage, 0.53 at a third of the CUs, 0.77 at all;
+// 128 x 128: 0.26 + 0.18 busy): the 128 x 256 tile (1) fits 2640 rows
+// into one round of 252 tiles where 256 x 128 needs two of 264 (2640 x
+// 3072 -> 3072: 24.8 against 40.4 us; 2640 x 14336 -> 3072: 92.8 against
+// 104.8 us on the 128 x 128 tile), and at 4680 rows it runs 222 tiles
+// against 228 (cross-attention Q 13.6 against 14.3 us).
 struct CfgCost {
     int idx;
     double per_stage_us, per_round_us, fixed_us;
     bool persistent;
+    double occ_stage_us = 0.0;
 };
 constexpr CfgCost kAuto[] = {
-    {0, 0.625, 8.16, 0.21, false},  // 256 x 128, one workgroup per CU
-    {2, 0.826, 4.21, 2.44, false},  // 256 x 128, two per CU
-    {4, 0.926, 2.43, 4.47, false},  // 128 x 256, two per CU
-    {3, 0.606, 0.44, 4.59, false},  // 128 x 128, three per CU
-    {5, 1.40, 14.77, 0.0, false},   // 256 x 256 ping-pong (8192^3: 1.44 us per stage with every CU busy)
-    {7, 0.80, 2.70, 0.80, true},    // 256 x 128 persistent, overlapped epilogue
-    // 128 x 128, 128-byte stages, one per CU (measured 0.365 us per stage
-    // with a third of the CUs busy, 0.443 with all: 880 x 3072 -> 3072 13.3
-    // us against 19.1 on the three-per-CU tile, 880 x 14336 -> 3072 45.4
-    // against 49.9 split in two)
-    {10, 0.43, 4.30, 0.20, false},
+    {0, 0.40, 5.30, 0.0, false, 0.38},  // 256 x 128, one workgroup per CU
+    {1, 0.40, 5.00, 0.0, false, 0.38},  // 128 x 256, one per CU
+    {2, 0.826, 4.21, 2.44, false},      // 256 x 128, two per CU
+    {4, 0.926, 2.43, 4.47, false},      // 128 x 256, two per CU
+    {3, 0.606, 0.44, 4.59, false},      // 128 x 128, three per CU
+    {5, 1.40, 14.77, 0.0, false},       // 256 x 256 ping-pong (8192^3: 1.44 us per stage with every CU busy)
+    {7, 0.80, 2.70, 0.80, true},        // 256 x 128 persistent, overlapped epilogue
+    // 128 x 128, 128-byte stages, one per CU: 512 x 1536 -> 3072 7.8 us,
+    // 880 x 14336 -> 3072 45 us (64 on the 256 x 128 or 128 x 256 tile)
+    {10, 0.26, 4.00, 0.0, false, 0.18},
 };
-// Grouped weight scales (128-byte stages only): the two one-per-CU tiles,
-// with the per-CU costs of their per-channel versions, and the persistent
-// 256 x 128 tile.
+// Grouped weight scales (128-byte stages only): the one-per-CU tiles (the
+// folds add about 0.2 us per stage: 0.61 + 0.42 busy for 256 x 128 and 128
+// x 256, 0.53 + 0.16 busy for 128 x 128) and the persistent 256 x 128 tile.
 constexpr CfgCost kGroupedAuto[] = {
-    {0, 0.625, 8.16, 0.21, false},  // 256 x 128
-    {1, 0.625, 8.16, 0.21, false},  // 128 x 256
-    {6, 0.80, 3.50, 4.00, true},    // 256 x 128 persistent
-    {10, 0.40, 7.00, 0.21, false},  // 128 x 128 (four waves: shapes of few 256 x 128 tiles)
+    {0, 0.61, 5.30, 0.0, false, 0.42},  // 256 x 128
+    {1, 0.61, 5.30, 0.0, false, 0.42},  // 128 x 256
+    {6, 0.80, 3.50, 4.00, true},        // 256 x 128 persistent
+    {10, 0.53, 4.50, 0.0, false, 0.16},  // 128 x 128 (four waves: shapes of few 256 x 128 tiles)
 };
+// Modelled time of configuration c at M x N x K (rounds of tiles over num_cu CUs).
+double cfg_cost(const CfgCost &c, size_t tiles, size_t num_cu, size_t K) {
+    const size_t rounds = (tiles + num_cu - 1) / num_cu;
+    const double st = (double)(K / 128);
+    if (c.occ_stage_us <= 0.0) return (double)rounds * (st * c.per_stage_us + c.per_round_us) + c.fixed_us;
+    double t = c.fixed_us;
+    for (size_t r = 0; r < rounds; r++) {
+        const size_t left = tiles - r * num_cu;
+        const double busy = (double)(left < num_cu ? left : num_cu) / (double)num_cu;
+        t += st * (c.per_stage_us + c.occ_stage_us * busy) + c.per_round_us;
+    }
+    return t;
+}
 
 // The configurations with MX-activation / MX-output kernels.  The 128 x 256
 // two-per-CU tile takes no MX activations: their scale handling needs more
-// than the 128 VGPRs two workgroups per CU leave a wave.
-bool mx_capable(int idx, bool mx_in) { return idx == 0 || idx == 3 || ((idx == 4 || idx == 6) && !mx_in); }
+// than the 128 VGPRs two workgroups per CU leave a wave (its one-per-CU
+// version, 1, has 256).
+bool mx_capable(int idx, bool mx_in) { return idx <= 1 || idx == 3 || ((idx == 4 || idx == 6) && !mx_in); }
 // The configurations built with grouped weight scales (128-byte stages, one
 // workgroup per CU: the partial sums need the registers); MX output on the
-// 256 x 128 tiles, MX activations on the one-shot 256 x 128 tile only.
+// 256 x 128 and 128 x 256 tiles, MX activations on the one-shot ones.
 bool grouped_capable(int idx, bool mx, bool mx_in) {
-    return mx_in ? idx == 0 : (idx == 0 || idx == 6 || ((idx == 1 || idx == 10) && !mx));
+    return mx_in ? idx <= 1 : (idx <= 1 || idx == 6 || (idx == 10 && !mx));
 }
 // The overlapped-epilogue kernel (k_gemm_fp8_ov): per-token activations and
 // per-channel weight scales, bf16 or MX e4m3 output, whole 128-channel
@@ -2231,9 +2258,11 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
         // split count always splits
         bool split = S >= 2 && (size_t)M * N * S * 4 < (1ull << 31);
         if (split && mode < 2 && y_dtype != LX2V_DTYPE_MXE4M3) {  // (no MX output on that tile)
-            const size_t t10 = ((M + 127) / 128) * (N / 128), r10 = (t10 + num_cu - 1) / num_cu;
-            const double c10 = (double)r10 * ((double)kts * 0.43 + 4.30) + 0.20;
-            const double cs = (double)(kts / S) * 0.625 + 8.37 + 10.0;  // + the partials' store and reduction
+            const size_t t10 = ((M + 127) / 128) * (N / 128);
+            const double c10 = cfg_cost(kAuto[sizeof(kAuto) / sizeof(kAuto[0]) - 1], t10, (size_t)num_cu, K);
+            // the split's tiles (one round) plus the partials' store and reduction
+            const double busy = (double)std::min<size_t>(tiles * S, (size_t)num_cu) / num_cu;
+            const double cs = (double)(kts / S) * (0.40 + 0.38 * busy) + 5.3 + 10.0;
             split = cs <= c10;
         }
         if (split) {
@@ -2270,7 +2299,7 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
         if (c.persistent && (rounds < 2 || K / 128 < 2)) return;
         // the overlapped epilogue's MX quantization (and GELU) cost per pass
         const double epi = c.idx == 7 && y_dtype == LX2V_DTYPE_MXE4M3 ? 1.2 : 0.0;
-        take(c.idx, (double)rounds * ((double)(K / 128) * c.per_stage_us + c.per_round_us + epi) + c.fixed_us);
+        take(c.idx, cfg_cost(c, tiles, (size_t)num_cu, K) + (double)rounds * epi);
     };
     // The 256 x 256 tile with one wave per SIMD (9).  Its stages slow down
     // with the share of CUs loading at once (measured 1.33-1.36 us per

@@ -34,10 +34,10 @@ DIM, FFN, TEXT, M = 1536, 8960, 512, 4680
 # with per-channel / group-128 weights, bf16 output)
 SITES = [
     ("qkv", M, DIM, 3 * DIM, H.ACT_NONE, "c7", "c6.g128"),
-    ("o", M, DIM, DIM, H.ACT_NONE, "c0", "c0.g128"),
+    ("o", M, DIM, DIM, H.ACT_NONE, "c1", "c1.g128"),
     ("kv2", TEXT, DIM, 2 * DIM, H.ACT_NONE, "c10", "c10.g128"),
     ("ffn1", M, DIM, FFN, H.ACT_GELU_TANH, "c9", "c6.g128"),
-    ("ffn2", M, FFN, DIM, H.ACT_NONE, "c0", "c0.g128"),
+    ("ffn2", M, FFN, DIM, H.ACT_NONE, "c1", "c1.g128"),
 ]
 
 
@@ -110,9 +110,9 @@ def test_ffn_pair_mx_handoff(be, group):
     ks = _profiled(be, lambda: (be.linear(xb, 0, M, w1, bb1, H.ACT_GELU_TANH, h, 0),
                                 be.linear(h, 0, M, w2, bb2, H.ACT_NONE, y, 0)))
     if group == "channel":
-        assert ks == {"gemm_fp8_e4m3.c9.mxout", "gemm_fp8_e4m3.c0.mxin"}, ks
+        assert ks == {"gemm_fp8_e4m3.c9.mxout", "gemm_fp8_e4m3.c1.mxin"}, ks
     else:
-        assert ks == {"gemm_fp8_e4m3.c6.g128.mxout", "gemm_fp8_e4m3.c0.g128.mxin"}, ks
+        assert ks == {"gemm_fp8_e4m3.c6.g128.mxout", "gemm_fp8_e4m3.c1.g128.mxin"}, ks
     # FFN up: MX output == MX quantizer of the same GEMM's f32 output, whole tensor
     h32 = be.alloc(M * FFN, H.DTYPE_F32)
     be.linear(xb, 0, M, w1, bb1, H.ACT_GELU_TANH, h32, 0)
@@ -167,8 +167,8 @@ def test_cross_kv_30_layers_one_call(be):
 
 # Config 5 (Wan2.2-TI2V-5B, per-token e4m3 activations) with the bf16 output
 # the bench writes: (rows, K, N, the configuration the planner picks).
-CFG5 = [(2640, 3072, 9216, "c9"), (2640, 3072, 3072, "c4"), (2640, 3072, 14336, "c9"), (2640, 14336, 3072, "c10"),
-        (880, 3072, 9216, "c4"), (880, 3072, 3072, "c10"), (880, 3072, 14336, "c9"), (880, 14336, 3072, "c10")]
+CFG5 = [(2640, 3072, 9216, "c1"), (2640, 3072, 3072, "c1"), (2640, 3072, 14336, "c9"), (2640, 14336, 3072, "c1"),
+        (880, 3072, 9216, "c1"), (880, 3072, 3072, "c10"), (880, 3072, 14336, "c9"), (880, 14336, 3072, "c10")]
 
 
 @pytest.mark.parametrize("rows,K,N,cfg", CFG5)
@@ -211,7 +211,7 @@ def test_o_on_mx_input(be, name, seed, group):
     be.quantize_mx(xb, 0, M, xm)
     y16 = be.alloc(M * DIM, H.DTYPE_BF16)
     y32 = be.alloc(M * DIM, H.DTYPE_F32)
-    want = "gemm_fp8_e4m3.c0.mxin" if group == "channel" else "gemm_fp8_e4m3.c0.g128.mxin"
+    want = "gemm_fp8_e4m3.c1.mxin" if group == "channel" else "gemm_fp8_e4m3.c1.g128.mxin"
     assert _profiled(be, lambda: be.linear(xm, 0, M, w, bb, H.ACT_NONE, y16, 0)) == {want}
     be.linear(xm, 0, M, w, bb, H.ACT_NONE, y32, 0)
     got32 = be.download(y32).reshape(M, DIM)

@@ -170,9 +170,11 @@ def test_fp8_split_k_row_offsets(be, monkeypatch):
                                          (8, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (8, H.ACT_NONE, H.DTYPE_MXE4M3),
                                          (9, H.ACT_GELU_TANH, H.DTYPE_BF16), (9, H.ACT_NONE, H.DTYPE_BF16),
                                          (9, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (9, H.ACT_NONE, H.DTYPE_MXE4M3),
-                                         (10, H.ACT_GELU_TANH, H.DTYPE_BF16), (10, H.ACT_NONE, H.DTYPE_F32)])
+                                         (10, H.ACT_GELU_TANH, H.DTYPE_BF16), (10, H.ACT_NONE, H.DTYPE_F32),
+                                         (1, H.ACT_GELU_TANH, H.DTYPE_BF16), (1, H.ACT_NONE, H.DTYPE_F32),
+                                         (1, H.ACT_GELU_TANH, H.DTYPE_MXE4M3)])
 def test_fp8_forced_persistent_vs_config0(be, monkeypatch, cfg, act, ydt):
-    """The persistent tiles (and the 128 x 128 one-per-CU tile, 10) forced
+    """The persistent tiles (and the one-per-CU 128 x 128 and 128 x 256 tiles, 10 and 1) forced
     (LIGHTX2V_HIP_FP8_CFG, read per call) against the one-shot configuration
     0, bit for bit over the whole output:
     1937 rows (ragged: 7 x 256 + 145) x 9216 channels is 576 tiles of 256 x
@@ -207,6 +209,7 @@ def test_fp8_forced_persistent_vs_config0(be, monkeypatch, cfg, act, ydt):
 
 
 @pytest.mark.parametrize("cfg,act,ydt", [(1, H.ACT_GELU_TANH, H.DTYPE_BF16), (1, H.ACT_NONE, H.DTYPE_F32),
+                                         (1, H.ACT_GELU_TANH, H.DTYPE_MXE4M3),
                                          (6, H.ACT_GELU_TANH, H.DTYPE_BF16), (6, H.ACT_NONE, H.DTYPE_F32),
                                          (6, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (10, H.ACT_GELU_TANH, H.DTYPE_BF16),
                                          (10, H.ACT_NONE, H.DTYPE_F32)])
@@ -243,6 +246,49 @@ def test_fp8_grouped_forced_vs_config0(be, monkeypatch, cfg, act, ydt):
         y = got[0].view(np.float32).reshape(M, N)[p]
         tol = FP8_TIGHT if ydt == H.DTYPE_F32 else (4e-3, 1e-2)
         assert_close(y, oracle_w8a8(x[p], q, s, 128, normal(3213, N, 0.01), act), *tol, what=f"c{cfg}.g128 vs oracle")
+
+
+@pytest.mark.parametrize("group", ["channel", 128])
+@pytest.mark.parametrize("act,ydt", [(H.ACT_NONE, H.DTYPE_BF16), (H.ACT_GELU_TANH, H.DTYPE_F32),
+                                     (H.ACT_GELU_TANH, H.DTYPE_MXE4M3)])
+def test_fp8_mx_input_forced_vs_config0(be, monkeypatch, group, act, ydt):
+    """MX e4m3 activations (a power-of-two scale per 32 columns of K, applied
+    by the scaled MFMA) on the one-per-CU 128 x 256 tile (configuration 1)
+    forced against the 256 x 128 tile (0), bit for bit over the whole
+    output, per-channel or group-128 weights, bf16, f32 or MX e4m3 output:
+    1937 rows (ragged for both tiles) x 2304 channels x K 1536, an MX input
+    read from row 16 of its buffer; sampled rows against the oracle on the
+    decoded input."""
+    M, K, N, r0 = 1937, 1536, 2304, 16
+    g = K if group == "channel" else 128
+    x = normal(3221, (M + r0) * K).reshape(M + r0, K)
+    _, q, s = fp8_weight(3222, N, K, g)
+    b = normal(3223, N, 0.01)
+    w = be.weight_fp8(q, s, N, K, g)
+    xb, bb = be.upload(x), be.upload(b)
+    xm = be.alloc_mx(M + r0, K)
+    be.quantize_mx(xb, 0, M + r0, xm)
+    mx = ydt == H.DTYPE_MXE4M3
+    sfx = (".g128" if group == 128 else "") + ".mxin" + (".mxout" if mx else "")
+
+    def run(c):
+        monkeypatch.setenv("LIGHTX2V_HIP_FP8_CFG", str(c))
+        y = be.alloc_mx(M, N) if mx else be.alloc(M * N, ydt)
+        if not mx:  # an element left unwritten stays NaN (a reused allocation cannot mask it)
+            be.write(y, np.full(M * N, np.nan, np.float32))
+        _, names = _kernels(be, lambda: be.linear(xm, r0, M, w, bb, act, y, 0))
+        assert {k for k in names if k.startswith("gemm")} == {f"gemm_fp8_e4m3.c{c}{sfx}"}, names
+        return be.download_mx(y, M, N) if mx else (u32(be.download(y)),)
+
+    want, got = run(0), run(1)
+    assert all(np.array_equal(a, b) for a, b in zip(want, got))
+    if ydt == H.DTYPE_F32:
+        p = np.arange(0, M, 97)
+        qx, sx = O.act_quant_mx(x)
+        xd = O.dequant_mx(qx, sx)[r0:][p]
+        yv = got[0].view(np.float32).reshape(M, N)[p]
+        assert_close(yv, O.linear(xd, O.fp8_dequantize(q, s, N, K, g), b, act, nthreads=8), *FP8_TIGHT,
+                     what=f"c1 MX input (group {g}) vs oracle")
 
 
 def test_fp8_no_bias(be):
