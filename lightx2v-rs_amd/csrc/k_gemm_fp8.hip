@@ -285,10 +285,12 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp8(const uint8_t *__restrict__
 // Grouped weight scales (GS = 1): one scale per 128 columns of K per channel
 // (Fp8E4M3 with group 128, quant.rs:21, 425-429), BKB = 128 so that a stage
 // is exactly one scale group.  Wave 0 adds one DMA per stage: the stage's
-// BN channel scales from the stage-major copy (row 2 kt of gsc, N floats a
-// row).  Each stage's two MFMAs per block run into a fresh partial sum,
-// which is then folded in, acc += part * s[n, kt]; sb is then null (1 in the
-// epilogue) and sa still scales each token.
+// BN channel ratios s_{kt-1} / s_kt from the weight's ratio table (row kt
+// of gsc, N floats a row; row 0 all ones).  Before the stage's first MFMA on
+// a block, the block's sums are multiplied by its channels' ratios, so the
+// accumulator always holds the sum in units of the current group's scale;
+// sb holds the last group's scales, which the epilogue applies as a
+// per-channel scale, and sa still scales each token.
 //
 // ACT: the epilogue activation (LX2V_ACT_*), a template parameter so that the
 // epilogue holds one copy of its staging code.
@@ -362,7 +364,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                                                                 : 0u));
     const auto rg_src = make_rsrc(
         GS ? (const uint8_t *)(gsc + n0) : A,
-        __builtin_amdgcn_readfirstlane(GS ? ((uint32_t)(2 * KT) * (uint32_t)N - (uint32_t)n0) * 4u : 0u));
+        __builtin_amdgcn_readfirstlane(GS ? ((uint32_t)KT * (uint32_t)N - (uint32_t)n0) * 4u : 0u));
 
     // Load i of this wave covers tile rows [(i NW + wid) RPI, +RPI); lane l
     // fills slot l % CPR of row l / CPR.
@@ -392,12 +394,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // Wave 0's MX scale load of stage kt (slot buf) and / or its group-scale load.
     auto issue_scales = [&](int kt, int buf) {
         if constexpr (GS) {
-            // lane l: channels n0 + 4 l .. + 3 of stage kt's group; past the
-            // last channel the next row (or zeros at the end) is read, for
+            // lane l: the ratios of channels n0 + 4 l .. + 3 at stage kt; past
+            // the last channel the next row (or zeros at the end) is read, for
             // channels that are never stored
             if (wid_u == 0) {
                 const bool ok = kt < KT && lane < BN / 4;
-                dma16(rg_src, gsl + buf * GSL, ok ? (uint32_t)(2 * kt) * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
+                dma16(rg_src, gsl + buf * GSL, ok ? (uint32_t)kt * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
             }
         }
         if constexpr (AM) {
@@ -429,7 +431,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     constexpr int LPS = ALD + BLD;
     // The K loop skewed by one slice (below): 128-byte stages, per-stage
     // scales not folded per stage.
-    constexpr bool SKEW = LX2V_FP8_SKEW && BKB == 128 && !GS;
+    constexpr bool SKEW = LX2V_FP8_SKEW && BKB == 128;
     // One 64-byte K slice's fragments: the wave's TM A row blocks and TN B
     // column blocks.
     struct Frag {
@@ -486,30 +488,53 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
             for (int i = 0; i < TM; i++) as[i] = (int)(sr[i] >> sh);
         }
     };
-    // mfma_half(f, as, nbase, dkt, dbuf): the slice's TN x TM MFMAs into acc
-    // (or, grouped, into the stage's partial sums, fresh when kk == 0), with
-    // load nbase + (j TM + i) of stage dkt (slot dbuf) issued after MFMA (j,
-    // i) while it is below LPS -- issued back to back right after the
+    // mfma_half(f, as, nbase, dkt, dbuf): the slice's TN x TM MFMAs into acc,
+    // with load nbase + (j TM + i) of stage dkt (slot dbuf) issued after MFMA
+    // (j, i) while it is below LPS -- issued back to back right after the
     // barrier, the loads held both waves of a SIMD off the MFMA pipe (7-9%
-    // at one workgroup per CU).  dkt < 0: no loads.
-    f32x16 part[GS ? TN : 1][GS ? TM : 1];  // grouped scales: this stage's partial sums
+    // at one workgroup per CU).  dkt < 0: no loads.  RS (grouped scales, a
+    // stage's first slice): block m is rescaled (rescale(m)) right before its
+    // MFMA.
     // after(m): called after the half's MFMA m (0 .. TN TM - 1), behind the
     // load it may issue -- the skewed loop reads the next slice's fragments
     // there, so that they land while the half's later MFMAs run.
-    auto mfma_half_then = [&](const Frag &f, const SOp &as, int kk, int nbase, int dkt, int dbuf, auto &&after) {
+    // Grouped scales (GS, one scale per 128 columns of K per channel, a
+    // stage being one group): the accumulator holds the sum so far in units
+    // of the current group's scale.  Before stage g's first MFMA on a block
+    // its sums are multiplied by s_{g-1} / s_g of each of the lane's
+    // channels (the weight's ratio table, row g, loaded by wave 0 with each
+    // stage; row 0 is all ones), and the epilogue's channel scale is the
+    // last group's: every tile shape and kernel applies the same operations
+    // to a block in the same order.
+    f32x4 rg[GS ? TN : 1][4];
+    auto read_r = [&](int buf) {
+        if constexpr (GS) {
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    rg[j][g] = *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
+        }
+    };
+    auto rescale = [&](int m) {
+        if constexpr (GS) {
+            const int j = m / TM, i = m % TM;
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc[j][i][4 * g + q] *= rg[j][g][q];
+        }
+    };
+    auto mfma_half_then = [&](auto RS, const Frag &f, const SOp &as, int kk, int nbase, int dkt, int dbuf,
+                              auto &&after) {
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                if constexpr (AM && GS)
-                    part[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        f.b[j], f.a[i], kk == 0 ? (f32x16){} : part[j][i], 0, 0, 0, 127, 0, as[i]);
-                else if constexpr (AM)
+                if constexpr (decltype(RS)::value) rescale(j * TM + i);
+                if constexpr (AM)
                     acc[j][i] =
                         __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc[j][i], 0, 0, 0, 127, 0, as[i]);
-                else if constexpr (GS)
-                    part[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        f.b[j], f.a[i], kk == 0 ? (f32x16){} : part[j][i], 0, 0, 0, 0, 0, 0);
                 else
                     acc[j][i] =
                         __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc[j][i], 0, 0, 0, 0, 0, 0);
@@ -522,55 +547,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                 after(j * TM + i);
             }
     };
+    using RsNo = std::false_type;
+    using RsYes = std::integral_constant<bool, GS != 0>;
     auto mfma_half = [&](const Frag &f, const SOp &as, int kk, int nbase, int dkt, int dbuf) {
-        mfma_half_then(f, as, kk, nbase, dkt, dbuf, [](int) {});
-    };
-    // Grouped scales: the fold acc += part * s[n, stage] of block b = j TM +
-    // i (lane l's register 4 g + q of block j is channel wn WN + 32 j + 8 g +
-    // 4 (l / 32) + q of the tile) runs behind the second slice's MFMA b + 1
-    // for the blocks of column block 0, and behind the next stage's first
-    // two MFMAs for those of column block 1, so that the folds' VALU work
-    // overlaps the MFMA pipe instead of following the stage's last MFMA
-    // (measured: no faster than all folds after the last MFMA, within 1%;
-    // the grouped tiles' loss against per-channel scales is the unskewed
-    // K loop and the registers, not the folds' VALU time).  g0:
-    // this stage's scales of column block 0; g1: column block 1's, the
-    // previous stage's until its deferred folds are done.  part and g1 start
-    // at zero, so the first stage's deferred folds add +0.
-    static_assert(!GS || (TN == 2 && TM == 2), "grouped scales: 64 x 64 wave tiles");
-    constexpr int NB = TN * TM, GD = 2;  // GD: blocks whose fold runs in the next stage
-    f32x4 g0[4], g1[4];
-    if constexpr (GS) {
-#pragma unroll
-        for (int g = 0; g < 4; g++) g1[g] = (f32x4){};
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int i = 0; i < TM; i++) part[j][i] = (f32x16){};
-    }
-    auto read_gs = [&](int buf, int j, f32x4 (&gs)[4]) {
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            gs[g] = *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
-    };
-    // fold(b, gs): block b = j TM + i, gs its column block's scales
-    auto fold = [&](int b, const f32x4 *gs) {
-        const int j = b / TM, i = b % TM;
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                acc[j][i][4 * g + q] = __builtin_fmaf(part[j][i][4 * g + q], gs[g][q], acc[j][i][4 * g + q]);
-    };
-    // after(kk, m): the folds behind slice kk's MFMA m
-    auto fold_after = [&](int buf, int kk, int m) {
-        if (kk == 0) {
-            if (m < GD) fold(NB - GD + m, g1);  // the previous stage's column block 1
-            if (m == (GD > 0 ? GD - 1 : 0)) read_gs(buf, 1, g1);
-        } else {
-            if (m >= 1 && m - 1 < NB - GD) fold(m - 1, (m - 1) / TM == 0 ? g0 : g1);
-            if (m == NB - 1 && GD == 0) fold(NB - 1, g1);
-        }
+        mfma_half_then(RsNo{}, f, as, kk, nbase, dkt, dbuf, [](int) {});
     };
     // compute(buf, stage, dkt, dbuf): the MFMAs of `stage` from slot buf,
     // slice by slice (each slice's reads, then its MFMAs), with the loads of
@@ -578,20 +558,18 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     auto compute = [&](int buf, int stage, int dkt, int dbuf) {
         SRaw sraw;
         read_sraw(buf, sraw);
-        if constexpr (GS) read_gs(buf, 0, g0);
+        read_r(buf);
 #pragma unroll
         for (int kk = 0; kk < BKB / 64; kk++) {
             Frag f;
             read_half(buf, kk, f);
             SOp as;
             scale_op(sraw, kk, stage, as);
-            mfma_half_then(f, as, kk, kk * TN * TM, dkt, dbuf, [&](int m) {
-                if constexpr (GS) fold_after(buf, kk, m);
-            });
+            if (kk == 0)
+                mfma_half_then(RsYes{}, f, as, kk, kk * TN * TM, dkt, dbuf, [](int) {});
+            else
+                mfma_half(f, as, kk, kk * TN * TM, dkt, dbuf);
         }
-        // g1 is consumed after the next barrier, behind which this slot's
-        // next DMA is issued: the read lands first.
-        if constexpr (GS) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     };
     static_assert((BKB / 64) * TN * TM >= ALD + BLD, "a stage's loads interleave with its MFMAs");
 
@@ -645,6 +623,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                     wait_stage();
                     if constexpr (XS) issue_scales(kt + j + NS - 1, j);
                     read_sraw(buf, sr);
+                    read_r(buf);
                     read_half(buf, 0, f0);
                     __builtin_amdgcn_sched_barrier(0);
                     mfma_half(f1, as1, 1, 0, kt + j + NS - 1, j);  // stage kt + j - 1, second slice
@@ -654,7 +633,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                     // the second slice's fragments read between the first
                     // slice's MFMAs (RPM reads per MFMA), so that they have
                     // landed when the next barrier's wait retires them
-                    mfma_half_then(f0, as0, 0, TN * TM, kt + j + NS - 1, j, [&](int m) {
+                    mfma_half_then(RsYes{}, f0, as0, 0, TN * TM, kt + j + NS - 1, j, [&](int m) {
                         constexpr int RPM = (TM + TN + TN * TM - 1) / (TN * TM);
 #pragma unroll
                         for (int r = 0; r < RPM; r++)
@@ -665,7 +644,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                             }
                     });
 #else
-                    mfma_half(f0, as0, 0, TN * TM, kt + j + NS - 1, j);
+                    mfma_half_then(RsYes{}, f0, as0, 0, TN * TM, kt + j + NS - 1, j, [](int) {});
                     read_half(buf, 1, f1);
 #endif
                     scale_op(sr, 1, kt + j, as1);
@@ -690,10 +669,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-        }
-        if constexpr (GS) {  // the last stage's deferred folds
-#pragma unroll
-            for (int m = 0; m < GD; m++) fold(NB - GD + m, g1);
         }
     }
     ops.park(sc, tid, m0, n0, M, N, sa, sb);
@@ -779,7 +754,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
         rb_src = make_rsrc(B + (size_t)is_n0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(N - is_n0) * (uint32_t)K));
         if constexpr (GS)
             rg_src = make_rsrc(gsc + is_n0, __builtin_amdgcn_readfirstlane(
-                                                ((uint32_t)(2 * KT) * (uint32_t)N - (uint32_t)is_n0) * 4u));
+                                                ((uint32_t)KT * (uint32_t)N - (uint32_t)is_n0) * 4u));
     };
     set_issue_tile();
 
@@ -810,7 +785,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
         if constexpr (GS) {
             if (wid_u == 0) {
                 const bool ok = is_i < my_n && lane < BN / 4;
-                dma16(rg_src, gsl + buf * GSL, ok ? (uint32_t)(2 * is_kt) * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
+                dma16(rg_src, gsl + buf * GSL, ok ? (uint32_t)is_kt * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
             }
         }
     };
@@ -844,53 +819,23 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
     constexpr int LPS = ALD + BLD;
 
     f32x16 acc[TN][TM];
-    f32x16 part[GS ? TN : 1][GS ? TM : 1];
-    // Grouped scales: the folds acc += part * s run behind later MFMAs, as in
-    // k_gemm_fp8_dma (g0 / g1: column block 0's / 1's scales; part and g1
-    // zero before a tile's first stage, whose deferred folds then add +0).
-    // No deferred block (GD = 0: the last two folds follow the stage's last
-    // MFMA): the walk's issue state leaves no registers to carry partial
-    // sums across stages (one deferred block spills).
-    constexpr int NB = TN * TM, GD = 0;
-    f32x4 g0[4], g1[4];
-    auto clear_prev = [&]() {
+    // Grouped scales: as k_gemm_fp8_dma, each block's sums are rescaled by
+    // the stage's ratio s_{g-1} / s_g right before the stage's first MFMA
+    // on the block; the epilogue's channel scale is the last group's.
+    f32x4 rg[GS ? TN : 1][4];
+    auto read_r = [&](int buf) {
         if constexpr (GS) {
-#pragma unroll
-            for (int g = 0; g < 4; g++) g1[g] = (f32x4){};
 #pragma unroll
             for (int j = 0; j < TN; j++)
 #pragma unroll
-                for (int i = 0; i < TM; i++) part[j][i] = (f32x16){};
-        }
-    };
-    auto read_gs = [&](int buf, int j, f32x4 (&gs)[4]) {
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            gs[g] = *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
-    };
-    // fold(b, gs): block b = j TM + i, gs its column block's scales
-    auto fold = [&](int b, const f32x4 *gs) {
-        const int j = b / TM, i = b % TM;
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                acc[j][i][4 * g + q] = __builtin_fmaf(part[j][i][4 * g + q], gs[g][q], acc[j][i][4 * g + q]);
-    };
-    // after(kk, m): the folds behind slice kk's MFMA m
-    auto fold_after = [&](int buf, int kk, int m) {
-        if (kk == 0) {
-            if (m < GD) fold(NB - GD + m, g1);  // the previous stage's column block 1
-            if (m == (GD > 0 ? GD - 1 : 0)) read_gs(buf, 1, g1);
-        } else {
-            if (m >= 1 && m - 1 < NB - GD) fold(m - 1, (m - 1) / TM == 0 ? g0 : g1);
-            if (m == NB - 1 && GD == 0) fold(NB - 1, g1);
+                for (int g = 0; g < 4; g++)
+                    rg[j][g] = *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
         }
     };
     const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
     auto compute = [&](int buf, bool do_issue, int dbuf) {
         const uint8_t *st = smem + buf * STAGE;
-        if constexpr (GS) read_gs(buf, 0, g0);
+        read_r(buf);
 #pragma unroll
         for (int kk = 0; kk < BKB / 64; kk++) {
             i32x8 af[TM], bf[TN];
@@ -914,19 +859,22 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
             for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int i = 0; i < TM; i++) {
-                    if constexpr (GS)
-                        part[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                            bf[j], af[i], kk == 0 ? (f32x16){} : part[j][i], 0, 0, 0, 0, 0, 0);
-                    else
-                        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[j][i], 0, 0, 0,
-                                                                                    0, 0, 0);
+                    if constexpr (GS) {
+                        if (kk == 0) {
+#pragma unroll
+                            for (int g = 0; g < 4; g++)
+#pragma unroll
+                                for (int q = 0; q < 4; q++) acc[j][i][4 * g + q] *= rg[j][g][q];
+                        }
+                    }
+                    acc[j][i] =
+                        __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[j][i], 0, 0, 0, 0, 0, 0);
                     const int n = kk * TN * TM + j * TM + i;
                     if (n < LPS && do_issue) {
                         __builtin_amdgcn_sched_barrier(0);
                         piece(n, dbuf);
                         __builtin_amdgcn_sched_barrier(0);
                     }
-                    if constexpr (GS) fold_after(buf, kk, j * TM + i);
                 }
         }
     };
@@ -948,7 +896,6 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
         for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int ii = 0; ii < TM; ii++) acc[j][ii] = (f32x16){};
-        clear_prev();
         for (int kt = 0; kt < KT; kt++, s++) {
             // Stage s complete for this wave (stages s + 1 .. s + NS - 2 may
             // still fly); the barrier publishes every wave's part and frees
@@ -965,10 +912,6 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
             compute(buf, true, dbuf);
             advance_issue();
             __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (GS) {  // the tile's last stage's deferred folds
-#pragma unroll
-            for (int m = 0; m < GD; m++) fold(NB - GD + m, g1);
         }
         // The ops DMA went out with stage s - KT, before the ring loads that
         // every later wait covered (KT >= 2).
@@ -1834,7 +1777,7 @@ void launch_dma(hipStream_t s, const uint8_t *a, const float *sa, const uint8_t 
     const int arows = (int)mx.a_rows, yrows = (int)mx.y_rows;
 #define LX2V_DMA_A(AMV, GSV, ACTV, T)                                                                           \
     hipLaunchKernelGGL((k_gemm_fp8_dma<BM, BN, WGM, WGN, BKB, NS, OCC, AMV, GSV, ACTV, T>), grid, block, 0, s, a, sa, \
-                       b, GSV ? nullptr : sb, bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y, \
+                       b, sb, bias, (T *)y, M, N, K, act, tiles_m, tiles_n, mx.a, alen, arows, mx.y,             \
                        yrows, mx.gate, mx.wgs)
 #define LX2V_DMA_G(AMV, GSV, T)                       \
     do {                                              \
@@ -1903,7 +1846,7 @@ void launch_pt(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, con
     const dim3 grid(g), block(512);
     const int yr = (int)mx.y_rows;
 #define LX2V_PT(GSV, ACTV, T)                                                                                      \
-    hipLaunchKernelGGL((k_gemm_fp8_pt<GSV, ACTV, T>), grid, block, 0, s, a, sa, b, GSV ? nullptr : sb, bias, (T *)y, \
+    hipLaunchKernelGGL((k_gemm_fp8_pt<GSV, ACTV, T>), grid, block, 0, s, a, sa, b, sb, bias, (T *)y,                 \
                        M, N, K, act, tiles_m, tiles_n, mx.y, yr, mx.wgs)
 #define LX2V_PT_T(GSV, T)                          \
     do {                                           \

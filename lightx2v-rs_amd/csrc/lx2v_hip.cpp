@@ -206,9 +206,13 @@ void free_weight(lx2v_hip_weight *w) {
     if (w->raw_e4m3) (void)hipFree(w->raw_e4m3);
     if (w->sscale) (void)hipFree(w->sscale);
     if (w->szero) (void)hipFree(w->szero);
+    if (w->gratio) (void)hipFree(w->gratio);
+    if (w->glast) (void)hipFree(w->glast);
     if (w->wbf16) (void)hipFree(w->wbf16);
     delete w;
 }
+
+int group_ratios(lx2v_hip_ctx *ctx, lx2v_hip_weight *w);
 
 // The stage-major scale copy (lx2v_hip_weight::sscale) of a weight the
 // direct-to-LDS bf16 GEMM takes, built on the stream after the scales.
@@ -220,7 +224,41 @@ int stage_scales(lx2v_hip_ctx *ctx, lx2v_hip_weight *w) {
     HIP_TRY(hipMalloc((void **)&w->sscale, n * 4), "stage_scales alloc");
     if (w->fmt == LX2V_WFMT_Q4) HIP_TRY(hipMalloc((void **)&w->szero, n * 4), "stage_scales alloc");
     w->device_bytes += n * 4 * (w->szero ? 2 : 1);
-    return run(ctx, "stage_scales", [&] { launch_stage_scales(ctx->stream, w); });
+    if (int rc = run(ctx, "stage_scales", [&] { launch_stage_scales(ctx->stream, w); })) return rc;
+    return group_ratios(ctx, w);
+}
+
+// FP8 group 128: the per-group scale ratios and last-group scales the fp8
+// MFMA kernels take (lx2v_hip_weight::gratio), from the weight's scales
+// (load time: one copy to the host and back).
+int group_ratios(lx2v_hip_ctx *ctx, lx2v_hip_weight *w) {
+    if (w->fmt != LX2V_WFMT_FP8 || w->group != 128 || w->cols % 128) return LX2V_OK;
+    const size_t rows = w->rows, G = w->cols / 128;
+    std::vector<float> s(rows * G), r(rows * G), last(rows);
+    HIP_TRY(hipMemcpyAsync(s.data(), w->scales, s.size() * 4, hipMemcpyDeviceToHost, ctx->stream), "group scales");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "group scales");
+    bool ok = true;
+    for (size_t n = 0; n < rows && ok; n++) {
+        const float *sn = s.data() + n * G;
+        float lo = sn[0], hi = sn[0];
+        for (size_t g = 0; g < G; g++) {
+            if (!(sn[g] > 0.0f && sn[g] <= 3.4e38f)) ok = false;  // finite and positive (NaN fails)
+            lo = std::min(lo, sn[g]);
+            hi = std::max(hi, sn[g]);
+        }
+        if (ok && hi > lo * 0x1p60f) ok = false;
+        for (size_t g = 0; g < G; g++) r[g * rows + n] = g == 0 ? 1.0f : sn[g - 1] / sn[g];
+        last[n] = sn[G - 1];
+    }
+    w->gratio_ok = ok;
+    if (!ok) return LX2V_OK;
+    HIP_TRY(hipMalloc((void **)&w->gratio, r.size() * 4), "group ratios alloc");
+    HIP_TRY(hipMalloc((void **)&w->glast, rows * 4), "group ratios alloc");
+    w->device_bytes += (r.size() + rows) * 4;
+    HIP_TRY(hipMemcpyAsync(w->gratio, r.data(), r.size() * 4, hipMemcpyHostToDevice, ctx->stream), "group ratios");
+    HIP_TRY(hipMemcpyAsync(w->glast, last.data(), rows * 4, hipMemcpyHostToDevice, ctx->stream), "group ratios");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "group ratios");
+    return LX2V_OK;
 }
 
 int check_quant_shape(size_t rows, size_t cols, size_t group) {
@@ -1909,7 +1947,7 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3, y_mx = y->dtype == LX2V_DTYPE_MXE4M3;
     if (y_mx && y->cols != N) return fail(LX2V_ERR_BAD_SHAPE, "MXE4M3 y has %zu cols, weight has %zu rows", y->cols, N);
     // FP8 weights the fp8 MFMA takes: one scale per channel, or per 128 columns.
-    const bool fp8_grouped = w->fmt == LX2V_WFMT_FP8 && w->group != K && w->sscale &&
+    const bool fp8_grouped = w->fmt == LX2V_WFMT_FP8 && w->group != K && w->gratio_ok &&
                              gemm_fp8_grouped_supported(rows, N, K, w->group);
     const bool fp8_mfma = w->fmt == LX2V_WFMT_FP8 && (w->group == K ? gemm_fp8_supported(rows, N, K) : fp8_grouped);
     if ((x_mx || y_mx) && (!fp8_mfma || K % 128 || (x_mx && x_row % 16)))
@@ -2026,7 +2064,7 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
         }
         mx.gate = gate;
         if (fp8_mfma) {
-            if (fp8_grouped) mx.wgs = w->sscale;
+            if (fp8_grouped) mx.wgs = w->gratio;
             if (plan.splits > 1) mx.part = p_part;
             // Profile name: the kernel configuration and the operand forms,
             // e.g. "gemm_fp8_e4m3.c0.g128.mxout".
@@ -2035,8 +2073,8 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
             if (plan.kernel >= 0) snprintf(cfg, sizeof cfg, plan.splits > 1 ? "c%dk%d" : "c%d", plan.kernel, plan.splits);
             snprintf(pname, sizeof pname, "gemm_fp8_e4m3.%s%s%s%s%s", cfg, fp8_grouped ? ".g128" : "", x_mx ? ".mxin" : "", y_mx ? ".mxout" : "", gate ? ".res" : "");
             if (int rc = run(ctx, pname, [&] {
-                    launch_gemm_fp8(ctx->stream, ctx->num_cu, plan, q, s, (const uint8_t *)w->codes, w->scales, bp,
-                                    act, yp, y->dtype, rows, N, K, mx);
+                    launch_gemm_fp8(ctx->stream, ctx->num_cu, plan, q, s, (const uint8_t *)w->codes,
+                                    fp8_grouped ? w->glast : w->scales, bp, act, yp, y->dtype, rows, N, K, mx);
                 }))
                 return rc;
         } else {
@@ -2160,7 +2198,7 @@ static bool linear_fusable(const lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_
     const bool x_mx = x->dtype == LX2V_DTYPE_MXE4M3;
     const bool grouped = w->group != K;
     if (w->fmt != LX2V_WFMT_FP8 || h->quantized() || !gemm_fp8_supported(rows, N, K)) return false;
-    if (grouped && !(w->sscale && gemm_fp8_grouped_supported(rows, N, K, w->group))) return false;
+    if (grouped && !(w->gratio_ok && gemm_fp8_grouped_supported(rows, N, K, w->group))) return false;
     if (!(ctx->fp8_act == LX2V_FP8_ACT_E4M3 || x->quantized())) return false;
     if (plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx, x_mx, grouped, h->dtype, LX2V_ACT_NONE, false, true).splits > 1)
         return false;

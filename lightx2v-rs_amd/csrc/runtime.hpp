@@ -60,6 +60,17 @@ struct lx2v_hip_weight {
     // does not apply (F32, cols % 64 != 0, group % 16 != 0).
     float *sscale = nullptr, *szero = nullptr;
     int spr = 0;
+    // FP8 with group 128 (cols % 128 == 0): what the fp8 MFMA kernels apply
+    // the group scales with.  Their accumulator T holds the sum so far in
+    // units of the current group's scale, T_g = (s_{g-1} / s_g) T_{g-1} + P_g
+    // (P_g the group's raw code products), and the epilogue multiplies by
+    // the last group's scale: gratio [cols / 128][rows] f32 (row g = s_{g-1}
+    // / s_g per channel, row 0 all ones), glast [rows].  gratio_ok: every
+    // scale finite and > 0 and no channel's scales more than 2^60 apart, so
+    // no ratio or partial sum overflows; other grouped weights take the
+    // bf16 MFMA kernel (k_gemm_w16) instead.
+    float *gratio = nullptr, *glast = nullptr;
+    bool gratio_ok = false;
     // F32 weights with cols % 64 == 0: the bf16 copy (RNE) the bf16 MFMA
     // reads, [rows, cols].
     uint16_t *wbf16 = nullptr;
