@@ -953,12 +953,13 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
 // Constraints (host): K % 128 == 0, K / 128 >= EP + 2, N % 128 == 0,
 // M N sizeof(TY) < 2^31; bf16 or MX e4m3 output; per-token activations and
 // per-channel weight scales; no residual mode.
-template <int ACT, typename TY>
+template <int ACT, typename TY, int GS>
 __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restrict__ A, const float *__restrict__ sa,
                                                        const uint8_t *__restrict__ B, const float *__restrict__ sb,
                                                        const float *__restrict__ bias, TY *__restrict__ Y, int M,
                                                        int N, int K, int tiles_m, int tiles_n,
-                                                       uint8_t *__restrict__ ymx, int ymx_rows) {
+                                                       uint8_t *__restrict__ ymx, int ymx_rows,
+                                                       const float *__restrict__ gsc) {
     constexpr int BM = 256, BN = 128, WGN = 2, BKB = 128, NS = 3;
     constexpr int NW = 8, WM = 64, WN = 64, TM = 2, TN = 2;
     constexpr int CPR = BKB / 16, RPI = 64 / CPR;
@@ -983,12 +984,16 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
     static_assert(qS01 % NSLOT >= LPS && qS23 % NSLOT >= LPS, "a block's stores follow its stage's loads");
     // vector-memory stores issued by peeled stage kt
     constexpr auto pst = [](int kt) { return kt < 0 || kt >= EP ? 0 : (EB == 2 ? 1 : (kt % 2 == 1 ? 2 : 0)); };
-    static_assert(NS * STAGE + (2 * NV + 256) * 4 <= 160 * 1024, "LDS");
+    // Grouped weight scales (GS): wave 0 loads each stage's channel ratios
+    // (one more load per stage: XL) into a slot of the stage's ring index
+    constexpr int GSL = 1024, XL = GS ? 1 : 0;
+    static_assert(NS * STAGE + (2 * NV + 256) * 4 + (GS ? NS * GSL : 0) <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
     // Per parity: [BM token scales][BN channel scales][BN bias], then a pad.
     __shared__ __attribute__((aligned(16))) float sc[2 * NV + 256];
+    __shared__ __attribute__((aligned(16))) uint8_t gsl[GS ? NS * GSL : 16];
 
-    const uint32_t smem_at = lds_addr(smem), sc_at = lds_addr(sc);
+    const uint32_t smem_at = lds_addr(smem), sc_at = lds_addr(sc), gsl_at = lds_addr(gsl);
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid / WGN, wn = wid % WGN;
     const int wid_u = __builtin_amdgcn_readfirstlane(wid);
@@ -1006,10 +1011,13 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
     // Issue side: the (pass, stage) whose loads go out next.
     int is_i = 0, is_kt = 0, is_m0 = 0, is_n0 = 0;
     tile_of(0, &is_m0, &is_n0);
-    __amdgpu_buffer_rsrc_t ra_src, rb_src;
+    __amdgpu_buffer_rsrc_t ra_src, rb_src, rg_src;
     auto set_issue_tile = [&]() {
         ra_src = make_rsrc(A + (size_t)is_m0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(M - is_m0) * (uint32_t)K));
         rb_src = make_rsrc(B + (size_t)is_n0 * K, __builtin_amdgcn_readfirstlane((uint32_t)(N - is_n0) * (uint32_t)K));
+        if constexpr (GS)
+            rg_src = make_rsrc(gsc + is_n0, __builtin_amdgcn_readfirstlane(
+                                                ((uint32_t)KT * (uint32_t)N - (uint32_t)is_n0) * 4u));
     };
     set_issue_tile();
     const uint32_t lrow = (uint32_t)lane / CPR, lslot = (uint32_t)lane % CPR;
@@ -1033,6 +1041,26 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
         else
             dma16_at(rb_src, sbuf + (BM + ((n - ALD) * NW + wid_u) * RPI) * BKB,
                      in ? b_off[n >= ALD ? n - ALD : 0] + k0 : kOob);
+    };
+    // Grouped scales: wave 0's load of the issue stage's channel ratios
+    // (lane l: channels 4 l .. 4 l + 3 of the issue tile; lanes past the
+    // tile's BN channels read nothing), first in the stage's issue order.
+    auto ratios = [&](int buf) {
+        if constexpr (GS) {
+            if (wid_u == 0) {
+                const bool ok = is_i < my_n && lane < BN / 4;
+                dma16_at(rg_src, gsl_at + (uint32_t)(buf * GSL),
+                         ok ? (uint32_t)is_kt * (uint32_t)N * 4u + (uint32_t)lane * 16u : kOob);
+            }
+        }
+    };
+    // Wave 0 also waits for each stage's ratio load.
+    auto wait_ring = [&](auto NOUT) {
+        constexpr int nout = decltype(NOUT)::value;
+        if (GS && wid_u == 0)
+            wait_vmcnt<nout + XL>();
+        else
+            wait_vmcnt<nout>();
     };
     auto advance_issue = [&]() {
         if (++is_kt == KT) {
@@ -1148,6 +1176,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
     const uint32_t frow = lane & 31, fhalf = (lane >> 5) * 2;
     auto stage = [&](auto FIRST, f32x16 (&ac)[TN][TM], int buf, int dbuf, auto &&slot) {
         const uint8_t *st = smem + buf * STAGE;
+        ratios(dbuf);
         static_for<BKB / 64>([&](auto KK) {
             constexpr int kk = decltype(KK)::value;
             i32x8 af[TM], bf[TN];
@@ -1170,6 +1199,17 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
             static_for<TN * TM>([&](auto JI) {
                 constexpr int j = decltype(JI)::value / TM, i = decltype(JI)::value % TM;
                 constexpr int n = kk * TN * TM + j * TM + i;
+                if constexpr (GS && kk == 0 && !decltype(FIRST)::value) {
+                    // the block's sums in units of this stage's group scale
+                    // (s_{g-1} / s_g per channel; as k_gemm_fp8_dma)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const f32x4 r4 =
+                            *(const f32x4 *)(gsl + buf * GSL + (wn * WN + j * 32 + 8 * g + 4 * (lane >> 5)) * 4);
+#pragma unroll
+                        for (int q = 0; q < 4; q++) ac[j][i][4 * g + q] *= r4[q];
+                    }
+                }
                 if constexpr (decltype(FIRST)::value && kk == 0)
                     ac[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], (f32x16){}, 0, 0, 0, 0,
                                                                                0, 0);
@@ -1191,6 +1231,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
     // Prologue: the first NS - 1 stages of the walk.
 #pragma unroll
     for (int st = 0; st < NS - 1; st++) {
+        ratios(st);
 #pragma unroll
         for (int n = 0; n < LPS; n++) piece(n, st);
         advance_issue();
@@ -1207,7 +1248,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
             constexpr int kt = decltype(KT_)::value;
             // Stage s complete for this wave; then the barrier publishes
             // every wave's part and frees the slot the issue refills.
-            wait_vmcnt<LPS + pst(kt - 1) + pst(kt - 2)>();
+            wait_ring(std::integral_constant<int, LPS + pst(kt - 1) + pst(kt - 2)>{});
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (kt == 0) issue_ops(m0, n0, sc_at + p * NV * 4);
@@ -1225,7 +1266,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_ov(const uint8_t *__restric
             __builtin_amdgcn_sched_barrier(0);
         });
         for (int kt = EP + 2; kt < KT; kt++, s++) {
-            wait_vmcnt<LPS>();
+            wait_ring(std::integral_constant<int, LPS>{});
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
             const int buf = s % NS, dbuf = (s + NS - 1) % NS;
@@ -1882,9 +1923,16 @@ void launch_ov(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, con
     if (g < nt && g >= 8) g = g / 8 * 8;
     const dim3 grid(g), block(512);
     const int yr = (int)mx.y_rows;
-#define LX2V_OV(ACTV, T)                                                                                      \
-    hipLaunchKernelGGL((k_gemm_fp8_ov<ACTV, T>), grid, block, 0, s, a, sa, b, sb, bias, (T *)y, M, N, K, tiles_m, \
-                       tiles_n, mx.y, yr)
+#define LX2V_OV_G(ACTV, T, GSV)                                                                                  \
+    hipLaunchKernelGGL((k_gemm_fp8_ov<ACTV, T, GSV>), grid, block, 0, s, a, sa, b, sb, bias, (T *)y, M, N, K, tiles_m, \
+                       tiles_n, mx.y, yr, mx.wgs)
+#define LX2V_OV(ACTV, T)              \
+    do {                              \
+        if (mx.wgs)                   \
+            LX2V_OV_G(ACTV, T, 1);    \
+        else                          \
+            LX2V_OV_G(ACTV, T, 0);    \
+    } while (0)
     if (y_dtype == LX2V_DTYPE_BF16) {
         if (act == LX2V_ACT_GELU_TANH)
             LX2V_OV(LX2V_ACT_GELU_TANH, uint16_t);
@@ -1897,6 +1945,7 @@ void launch_ov(hipStream_t s, int num_cu, const uint8_t *a, const float *sa, con
             LX2V_OV(LX2V_ACT_NONE, uint8_t);
     }
 #undef LX2V_OV
+#undef LX2V_OV_G
 }
 
 // The persistent 256 x 256 kernel with one wave per SIMD: min(tiles, CUs)
@@ -2129,6 +2178,7 @@ constexpr CfgCost kGroupedAuto[] = {
     {0, 0.61, 5.30, 0.0, false, 0.42},  // 256 x 128
     {1, 0.61, 5.30, 0.0, false, 0.42},  // 128 x 256
     {6, 0.80, 3.50, 4.00, true},        // 256 x 128 persistent
+    {7, 0.87, 2.70, 0.80, true},        // 256 x 128 persistent, overlapped epilogue (the rescale: ~8% per stage)
     {10, 0.53, 4.50, 0.0, false, 0.16},  // 128 x 128 (four waves: shapes of few 256 x 128 tiles)
 };
 // Modelled time of configuration c at M x N x K (rounds of tiles over num_cu CUs).
@@ -2156,14 +2206,15 @@ bool mx_capable(int idx, bool mx_in) { return idx <= 1 || idx == 3 || ((idx == 4
 bool grouped_capable(int idx, bool mx, bool mx_in) {
     return mx_in ? idx <= 1 : (idx <= 1 || idx == 6 || (idx == 10 && !mx));
 }
-// The overlapped-epilogue kernel (k_gemm_fp8_ov): per-token activations and
-// per-channel weight scales, bf16 or MX e4m3 output, whole 128-channel
+// The overlapped-epilogue kernel (k_gemm_fp8_ov): per-token activations,
+// per-channel or group-128 weight scales, bf16 or MX e4m3 output, whole 128-channel
 // tiles, and enough stages to carry the previous tile's epilogue (4, or 8
 // with GELU) plus the two the ring runs ahead.
 bool ov_capable(size_t M, size_t N, size_t K, bool mx_in, bool grouped, int y_dtype, int act, bool residual) {
     const size_t eb = y_dtype == LX2V_DTYPE_BF16 ? 2 : (y_dtype == LX2V_DTYPE_MXE4M3 ? 1 : 0);
     const size_t ep = act == LX2V_ACT_GELU_TANH ? 8 : 4;
-    return eb && !mx_in && !grouped && !residual && N % 128 == 0 && K % 128 == 0 && K / 128 >= ep + 2 &&
+    (void)grouped;  // group-128 scales by the per-stage rescale (k_gemm_fp8_ov GS)
+    return eb && !mx_in && !residual && N % 128 == 0 && K % 128 == 0 && K / 128 >= ep + 2 &&
            M * N * eb < (1ull << 31);
 }
 
@@ -2240,8 +2291,10 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
         const size_t tiles = ((M + d.bm - 1) / d.bm) * ((N + d.bn - 1) / d.bn);
         const size_t rounds = (tiles + num_cu - 1) / num_cu;
         if (c.persistent && (rounds < 2 || K / 128 < 2)) return;
-        // the overlapped epilogue's MX quantization (and GELU) cost per pass
-        const double epi = c.idx == 7 && y_dtype == LX2V_DTYPE_MXE4M3 ? 1.2 : 0.0;
+        // the overlapped epilogue's MX quantization (and GELU) cost per pass;
+        // the grouped persistent tile's LDS-staged epilogue does its GELU / MX
+        // work after the pass's last stage (measured ~3 us a pass at FFN up)
+        const double epi = c.idx == 7 && y_dtype == LX2V_DTYPE_MXE4M3 ? 1.2 : (c.idx == 6 && heavy_epi ? 3.0 : 0.0);
         take(c.idx, cfg_cost(c, tiles, (size_t)num_cu, K) + (double)rounds * epi);
     };
     // The 256 x 256 tile with one wave per SIMD (9).  Its stages slow down

@@ -1982,7 +1982,7 @@ static int linear_run(lx2v_hip_ctx *ctx, const lx2v_hip_buf *x, size_t x_row, si
     if (e4m3_path && fp8_mfma) {
         plan = plan_gemm_fp8(ctx->num_cu, rows, N, K, x_mx || y_mx, x_mx, fp8_grouped, y->dtype, act, gate != nullptr,
                              true);
-        if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1 && plan.kernel != 6 &&
+        if (fp8_grouped && plan.kernel != 0 && plan.kernel != 1 && plan.kernel != 6 && plan.kernel != 7 &&
             plan.kernel != 10)  // built with grouped scales
             return fail(LX2V_ERR_UNSUPPORTED, "no grouped-scale fp8 kernel for configuration %d", plan.kernel);
     }

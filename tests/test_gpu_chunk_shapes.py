@@ -33,10 +33,10 @@ DIM, FFN, TEXT, M = 1536, 8960, 512, 4680
 # (name, rows, K, N, act, the configuration the planner picks on 256 CUs
 # with per-channel / group-128 weights, bf16 output)
 SITES = [
-    ("qkv", M, DIM, 3 * DIM, H.ACT_NONE, "c7", "c6.g128"),
+    ("qkv", M, DIM, 3 * DIM, H.ACT_NONE, "c7", "c7.g128"),
     ("o", M, DIM, DIM, H.ACT_NONE, "c1", "c1.g128"),
     ("kv2", TEXT, DIM, 2 * DIM, H.ACT_NONE, "c10", "c10.g128"),
-    ("ffn1", M, DIM, FFN, H.ACT_GELU_TANH, "c9", "c6.g128"),
+    ("ffn1", M, DIM, FFN, H.ACT_GELU_TANH, "c9", "c7.g128"),
     ("ffn2", M, FFN, DIM, H.ACT_NONE, "c1", "c1.g128"),
 ]
 
@@ -112,7 +112,7 @@ def test_ffn_pair_mx_handoff(be, group):
     if group == "channel":
         assert ks == {"gemm_fp8_e4m3.c9.mxout", "gemm_fp8_e4m3.c1.mxin"}, ks
     else:
-        assert ks == {"gemm_fp8_e4m3.c6.g128.mxout", "gemm_fp8_e4m3.c1.g128.mxin"}, ks
+        assert ks == {"gemm_fp8_e4m3.c7.g128.mxout", "gemm_fp8_e4m3.c1.g128.mxin"}, ks
     # FFN up: MX output == MX quantizer of the same GEMM's f32 output, whole tensor
     h32 = be.alloc(M * FFN, H.DTYPE_F32)
     be.linear(xb, 0, M, w1, bb1, H.ACT_GELU_TANH, h32, 0)

@@ -210,18 +210,21 @@ def test_fp8_forced_persistent_vs_config0(be, monkeypatch, cfg, act, ydt):
 
 @pytest.mark.parametrize("cfg,act,ydt", [(1, H.ACT_GELU_TANH, H.DTYPE_BF16), (1, H.ACT_NONE, H.DTYPE_F32),
                                          (1, H.ACT_GELU_TANH, H.DTYPE_MXE4M3),
+                                         (7, H.ACT_GELU_TANH, H.DTYPE_BF16), (7, H.ACT_NONE, H.DTYPE_BF16),
+                                         (7, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (7, H.ACT_NONE, H.DTYPE_MXE4M3),
                                          (6, H.ACT_GELU_TANH, H.DTYPE_BF16), (6, H.ACT_NONE, H.DTYPE_F32),
                                          (6, H.ACT_GELU_TANH, H.DTYPE_MXE4M3), (10, H.ACT_GELU_TANH, H.DTYPE_BF16),
                                          (10, H.ACT_NONE, H.DTYPE_F32)])
 def test_fp8_grouped_forced_vs_config0(be, monkeypatch, cfg, act, ydt):
     """Group-128 weights (one scale per 128 columns of K per channel) on the
     grouped configurations forced, against configuration 0, bit for bit over
-    the whole output.  Every configuration folds each 128-column group's
-    partial sum into the accumulator in group order (the fold of a block
-    may run one stage late, behind the next stage's first MFMAs, but never
-    out of order), so the sums are the same f32 operations.  1937 rows
-    (ragged) x 9216 channels x K 1536; GELU or none; bf16, f32 or MX e4m3
-    output; sampled rows against the oracle."""
+    the whole output.  Every configuration rescales a block's sums by the
+    group's s_{g-1} / s_g right before the group's first MFMA on the block
+    and applies the last group's scale in the epilogue, so the sums are the
+    same f32 operations (the overlapped-epilogue tile, 7, included: it
+    walks two or more tiles per workgroup here).  1937 rows (ragged) x 9216
+    channels x K 1536; GELU or none; bf16, f32 or MX e4m3 output; sampled
+    rows against the oracle."""
     M, K, N = 1937, 1536, 9216
     x = normal(3211, M * K).reshape(M, K)
     _, q, s = fp8_weight(3212, N, K, 128)
@@ -394,6 +397,29 @@ def test_fp8_other_groups_bf16_mfma(be, group):
     assert any(k.startswith("gemm_w16_fp8") for k in ks) and "gemm_generic" not in ks, ks
     wd = O.fp8_dequantize(q, s, N, K, group)
     assert_close(y, oracle_w16(x, wd, None, 0), *W16_TIGHT, what=f"fp8 g{group} on the bf16 MFMA")
+
+
+@pytest.mark.parametrize("case", ["zero_group", "wide_range"])
+def test_fp8_g128_ratio_fallback(be, case):
+    """Group-128 FP8 weights whose scales the fp8 MFMA kernels' per-group
+    rescaling cannot carry (a channel with an all-zero group, scale 0; or
+    two groups of a channel more than 2^60 apart) take the bf16 MFMA kernel;
+    its result against the oracle on the dequantized weight (W16_TIGHT)."""
+    M, K, N = 150, 1024, 320
+    x = normal(31, M * K).reshape(M, K)
+    _, q, s = fp8_weight(32, N, K, 128)
+    q, s = q.copy(), s.copy().reshape(N, K // 128)
+    if case == "zero_group":
+        q.reshape(N, K)[7, 256:384] = 0
+        s[7, 2] = 0.0
+    else:
+        s[11, 5] *= 2.0 ** 70
+    s = s.ravel()
+    w = be.weight_fp8(q, s, N, K, 128)
+    y, ks = _kernels(be, lambda: run_linear(be, x, w, None, H.ACT_NONE))
+    assert any(k.startswith("gemm_w16_fp8") for k in ks) and not any(k.startswith("gemm_fp8_e4m3") for k in ks), ks
+    wd = O.fp8_dequantize(q, s, N, K, 128)
+    assert_close(y, oracle_w16(x, wd, None, 0), *W16_TIGHT, what=f"fp8 g128 ({case}) on the bf16 MFMA")
 
 
 def test_fp8_grouped_paths(be):
