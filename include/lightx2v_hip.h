@@ -159,7 +159,12 @@ int lx2v_hip_weight_q4(lx2v_hip_ctx *ctx, const uint8_t *codes, int packed,
  * mantissa (reference value m * 2^-12 * s, at most 3.9e-6 * the group's
  * absmax) are stored as signed zero so the fp8 MFMA, which decodes OCP
  * e4m3fn, sees the reference value of every other code exactly; the count
- * is reported by lx2v_hip_weight_info. */
+ * is reported by lx2v_hip_weight_info.  Group 128 (cols % 128 == 0): the
+ * fp8 MFMA kernels apply the group scales by rescaling their running sums
+ * by s[g-1] / s[g] at each group boundary, from a ratio table built here
+ * (a copy of the scales to the host and back); a weight with a scale that
+ * is zero, negative or not finite, or with two groups of a channel more
+ * than 2^60 apart, runs on the bf16 MFMA kernel instead. */
 int lx2v_hip_weight_fp8(lx2v_hip_ctx *ctx, const uint8_t *q, const float *scales,
                         size_t rows, size_t cols, size_t group, lx2v_hip_weight **out);
 /* Drop of the trait's Weight. */
@@ -168,8 +173,9 @@ int lx2v_hip_weight_free(lx2v_hip_ctx *ctx, lx2v_hip_weight *w);
 typedef struct {
     int fmt;            /* LX2V_WFMT_* */
     size_t rows, cols, group;
-    size_t device_bytes;  /* codes, scales (and zeros), and the bf16 GEMM's
-                             stage-major copy of the scales */
+    size_t device_bytes;  /* codes, scales (and zeros), the bf16 GEMM's
+                             stage-major copy of the scales, and FP8 group
+                             128's ratio table and last-group scales */
     size_t canonicalized; /* FP8 exponent-0 codes stored as zero */
 } lx2v_hip_weight_info_t;
 int lx2v_hip_weight_info(const lx2v_hip_weight *w, lx2v_hip_weight_info_t *info);
