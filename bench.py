@@ -194,6 +194,16 @@ def per_config(be, H):
         time_linear(f"cfg4_g128_{name}", x, rows, k, w, n, act, xdt, "mx" if name == "ffn1" else H.DTYPE_BF16,
                     PEAK_FP8_TFLOPS, g128_chunk_path, group=128)
         w.free()
+        if name == "kv2":
+            # the chunk's form of it: the 30 layers' K/V weights in one call
+            # (the text is the same for every layer); its time per layer
+            kvn = LAYERS * n
+            w = weight("fp8", kvn, k, 0.02, 1043 + n + k, group=128)
+            time_linear("cfg4_g128_kv2_all_layers", x, rows, k, w, kvn, act, xdt, H.DTYPE_BF16, PEAK_FP8_TFLOPS,
+                        g128_chunk_path + "; the 30 layers' weights concatenated, one call", group=128)
+            out["cfg4_g128_kv2_all_layers"]["us_per_layer"] = round(out["cfg4_g128_kv2_all_layers"]["us_per_linear"]
+                                                                    / LAYERS, 2)
+            w.free()
         x.free()
     # config 2: Q8 (per-32 scales) FFN up + GELU, bf16 activations
     be.set_act_dtype(H.DTYPE_BF16)
