@@ -1,9 +1,13 @@
-// k_gemm_fp8.hip -- FP8-e4m3 weight x per-token e4m3 activation GEMM on the
-// gfx950 fp8 MFMA (v_mfma_f32_32x32x64_f8f6f4), for weights with one scale
-// per output channel (Fp8E4M3 with group == cols, quant.rs:364-373,
-// 425-429).
+// k_gemm_fp8.hip -- FP8-e4m3 weight x per-token (or MX) e4m3 activation GEMM
+// on the gfx950 fp8 MFMA (v_mfma_f32_32x32x64_f8f6f4), for weights with one
+// scale per output channel (Fp8E4M3 with group == cols, quant.rs:364-373,
+// 425-429) or one per 128 columns of K (group 128, quant.rs:21).
 //
 //   Y[m, n] = act( (sum_k e4m3(A[m,k]) * e4m3(B[n,k])) * sa[m] * sb[n] + bias[n] )
+//
+// With group 128 the running sums are rescaled by s[n][g-1] / s[n][g] at
+// each group boundary and sb is the last group's scale (k_gemm_fp8_dma's
+// notes on GS).
 //
 // A = per-token quantized activations [M, K], B = the weight's e4m3 codes
 // [N, K] exactly as the reference lays them out (row-major, K contiguous);
