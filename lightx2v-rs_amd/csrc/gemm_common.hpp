@@ -139,13 +139,47 @@ struct MxOut {
 //
 // ACT (compile time, so the per-element code is branch-free): GELU or none.
 // ALLROWS: the pass covers the whole tile (every block of the wave is in it).
-template <int BM, int BN, int TM, int TN, typename TY, int ACT, bool ALLROWS>
+//
+// TR: the blocks are transposed (the MFMA took the activations as its first
+// operand): lane l holds channel l % 32 of block (i, j) and its tile rows
+// 8 g + 4 (l / 32) + q; bf16 / f32 output.  Each element gets the same
+// operations in the same order as in the plain layout.
+template <int BM, int BN, int TM, int TN, typename TY, int ACT, bool ALLROWS, bool TR = false>
 __device__ __forceinline__ void acc_to_lds(const f32x16 (&acc)[TN][TM], const float *sc, uint8_t *stg, int rloc,
                                            int R, int wr, int wc, int lane, MxOut mx, int m0, int n0, int M,
                                            int N) {
     constexpr int EB = sizeof(TY), RB = BN * EB, SWZ = stage_swz<BN, TY>();
     static_assert(RB >= 128 && (RB & (RB - 1)) == 0, "staging row must be a power of two >= 128 bytes");
     const int l32 = lane & 31, hf = lane >> 5;
+    if constexpr (TR) {
+        static_assert(EB != 1, "transposed blocks: bf16 or f32 output");
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int c = wc + j * 32 + l32, cb = c * EB;
+            const float cs = sc[BM + c], bs = sc[BM + BN + c];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                if (!ALLROWS && (rloc + i * 32 < 0 || rloc + i * 32 >= R)) continue;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const f32x4 ts = *(const f32x4 *)(sc + wr + i * 32 + 8 * g + 4 * hf);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        float t = acc[j][i][4 * g + q] * ts[q] * cs + bs;
+                        if constexpr (ACT == LX2V_ACT_GELU_TANH) t = gelu_tanh_fast(t);
+                        const int r = rloc + i * 32 + 8 * g + 4 * hf + q;
+                        uint8_t *p = stg + r * RB + ((((cb >> 4) ^ (r & (SWZ - 1)))) << 4) + (cb & 15);
+                        if constexpr (EB == 4)
+                            *(float *)p = t;
+                        else
+                            *(uint16_t *)p = (uint16_t)pack_bf16x2(t, t);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return;
+    }
     float sam[TM];
 #pragma unroll
     for (int i = 0; i < TM; i++) sam[i] = sc[wr + i * 32 + l32];
@@ -395,8 +429,10 @@ constexpr int pow2_floor(int v) { return v < 2 ? 1 : 2 * pow2_floor(v / 2); }
 // tile's stages of a persistent kernel -- keep flying through the epilogue.
 //
 // CP: the cache-policy bits of the tile's stores (buffer_store_x4).
+//
+// TR: the accumulator blocks are transposed (acc_to_lds).
 template <int BM, int BN, int NT, int SMEM, int TM, int TN, typename TY, bool RES = true, int ACT = -1,
-          bool WAIT0 = true, int CP = 0>
+          bool WAIT0 = true, int CP = 0, bool TR = false>
 __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uint8_t *smem, const float *sc, int wr,
                                                 int wc, int tid, int lane, int m0, int n0, int M, int N, int act,
                                                 TY *__restrict__ Y, MxOut mx = MxOut()) {
@@ -416,14 +452,14 @@ __device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TN][TM], uin
         if (p) __syncthreads();
         if (wr < (p + 1) * R && wr + 32 * TM > p * R) {
             if constexpr (ACT >= 0)
-                acc_to_lds<BM, BN, TM, TN, TY, ACT, R == BM>(acc, sc, smem, wr - p * R, R, wr, wc, lane, mx, m0, n0,
-                                                             M, N);
+                acc_to_lds<BM, BN, TM, TN, TY, ACT, R == BM, TR>(acc, sc, smem, wr - p * R, R, wr, wc, lane, mx, m0,
+                                                                 n0, M, N);
             else if (act == LX2V_ACT_GELU_TANH)
-                acc_to_lds<BM, BN, TM, TN, TY, LX2V_ACT_GELU_TANH, R == BM>(acc, sc, smem, wr - p * R, R, wr, wc,
-                                                                            lane, mx, m0, n0, M, N);
+                acc_to_lds<BM, BN, TM, TN, TY, LX2V_ACT_GELU_TANH, R == BM, TR>(acc, sc, smem, wr - p * R, R, wr, wc,
+                                                                                lane, mx, m0, n0, M, N);
             else
-                acc_to_lds<BM, BN, TM, TN, TY, LX2V_ACT_NONE, R == BM>(acc, sc, smem, wr - p * R, R, wr, wc, lane,
-                                                                       mx, m0, n0, M, N);
+                acc_to_lds<BM, BN, TM, TN, TY, LX2V_ACT_NONE, R == BM, TR>(acc, sc, smem, wr - p * R, R, wr, wc, lane,
+                                                                           mx, m0, n0, M, N);
         }
         __syncthreads();
         if constexpr (sizeof(TY) == 1 || !RES) {

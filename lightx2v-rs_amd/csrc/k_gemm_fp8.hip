@@ -510,9 +510,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     // stage; row 0 is all ones), and the epilogue's channel scale is the
     // last group's: every tile shape and kernel applies the same operations
     // to a block in the same order.
-    f32x4 rg[GS ? TN : 1][4];
+    // TR (grouped scales, bf16 / f32 output): the blocks are transposed --
+    // the MFMA takes the activations as its first operand, so lane l holds
+    // channel l % 32 of a block (and the block's rows 8 g + 4 (l / 32) + q)
+    // and needs one ratio per block, one 4-byte LDS read, where the plain
+    // layout needs 16 channels' ratios, four 16-byte reads: measured, those
+    // reads were most of the grouped kernels' cost over the per-channel
+    // ones.  The swapped MFMA gives exactly the transposed sums (checked bit
+    // for bit on gfx950), so the results are the plain layout's.
+    constexpr bool TR = GS && sizeof(TY) != 1;
+    f32x4 rg[GS && !TR ? TN : 1][4];
+    float rt[TR ? TN : 1];
     auto read_r = [&](int buf) {
-        if constexpr (GS) {
+        if constexpr (TR) {
+#pragma unroll
+            for (int j = 0; j < TN; j++) rt[j] = *(const float *)(gsl + buf * GSL + (wn * WN + j * 32 + (lane & 31)) * 4);
+        } else if constexpr (GS) {
 #pragma unroll
             for (int j = 0; j < TN; j++)
 #pragma unroll
@@ -521,7 +534,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
         }
     };
     auto rescale = [&](int m) {
-        if constexpr (GS) {
+        if constexpr (TR) {
+            const int j = m / TM, i = m % TM;
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[j][i][e] *= rt[j];
+        } else if constexpr (GS) {
             const int j = m / TM, i = m % TM;
 #pragma unroll
             for (int g = 0; g < 4; g++)
@@ -536,9 +553,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 if constexpr (decltype(RS)::value) rescale(j * TM + i);
-                if constexpr (AM)
+                if constexpr (AM && TR)
+                    acc[j][i] =
+                        __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[j][i], 0, 0, 0, as[i], 0, 127);
+                else if constexpr (AM)
                     acc[j][i] =
                         __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc[j][i], 0, 0, 0, 127, 0, as[i]);
+                else if constexpr (TR)
+                    acc[j][i] =
+                        __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[j][i], 0, 0, 0, 0, 0, 0);
                 else
                     acc[j][i] =
                         __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc[j][i], 0, 0, 0, 0, 0, 0);
@@ -680,7 +703,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_fp8_dma(const uint
     mx.scales = ymx;
     mx.rows = ymx_rows;
     mx.gate = gate;
-    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY, true, ACT, true, kStagedCP>(
+    staged_epilogue<BM, BN, 64 * NW, NS * STAGE, TM, TN, TY, true, ACT, true, kStagedCP, TR>(
         acc, smem, sc, wm * WM, wn * WN, tid, lane, m0, n0, M, N, act, Y, mx);
 }
 
@@ -825,7 +848,11 @@ __global__ __launch_bounds__(512, 1) void k_gemm_fp8_pt(const uint8_t *__restric
     f32x16 acc[TN][TM];
     // Grouped scales: as k_gemm_fp8_dma, each block's sums are rescaled by
     // the stage's ratio s_{g-1} / s_g right before the stage's first MFMA
-    // on the block; the epilogue's channel scale is the last group's.
+    // on the block; the epilogue's channel scale is the last group's.  (The
+    // transposed blocks of k_gemm_fp8_dma measured slower here: 45.8 ->
+    // 47.1 us at QKV; a tile's epilogue comes every 12 stages at the Wan
+    // shapes and its 2-byte staging writes cost more than the ratio reads
+    // save.)
     f32x4 rg[GS ? TN : 1][4];
     auto read_r = [&](int buf) {
         if constexpr (GS) {
@@ -2000,7 +2027,8 @@ constexpr DmaCfg kDma[] = {
     // persistent 256 x 256, one wave per SIMD (k_gemm_fp8_w4)
     {256, 256, 2, 2, 64, 4},   // 8: 64-byte stages, 4 slots
     {256, 256, 2, 2, 128, 2},  // 9: 128-byte stages, 2 slots
-    // direct-to-LDS 128 x 128, 128-byte stages, one per CU (grouped scales, few tiles)
+    // direct-to-LDS 128 x 128, 128-byte stages, one per CU (few tiles; with
+    // grouped scales on a 4 x 2 wave grid)
     {128, 128, 2, 2, 128, 3},  // 10
 };
 
@@ -2094,8 +2122,15 @@ void launch_dma_idx(int idx, hipStream_t s, const uint8_t *a, const float *sa, c
             break;
         case 5: launch_pp<256, 1, 4, 64, 4>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K); break;
         case 10:
-            launch_dma<128, 128, 2, 2, 128, 3, 1, false, false, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K,
-                                                                      mx);
+            // grouped scales on eight waves (two per SIMD): with four, the
+            // accumulators sit in AGPRs and each rescale multiply takes a
+            // read and a write besides (kv2 12.4 -> 9.7 us, 880 x 14336 ->
+            // 3072 76 -> 51 us); per-channel, four waves are as fast or faster
+            if (mx.wgs)
+                launch_dma<128, 128, 4, 2, 128, 3, 1, false, false, true>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N,
+                                                                          K, mx);
+            else
+                launch_dma<128, 128, 2, 2, 128, 3, 1>(s, a, sa, b, sb, bias, act, y, y_dtype, M, N, K, mx);
             break;
         default: break;  // 6 .. 9: launch_pt / launch_ov / launch_w4 (need the CU count)
     }
@@ -2175,15 +2210,25 @@ constexpr CfgCost kAuto[] = {
     // 880 x 14336 -> 3072 45 us (64 on the 256 x 128 or 128 x 256 tile)
     {10, 0.26, 4.00, 0.0, false, 0.18},
 };
-// Grouped weight scales (128-byte stages only): the one-per-CU tiles (the
-// folds add about 0.2 us per stage: 0.61 + 0.42 busy for 256 x 128 and 128
-// x 256, 0.53 + 0.16 busy for 128 x 128) and the persistent 256 x 128 tile.
+// Grouped weight scales (128-byte stages only): the one-per-CU tiles and
+// the persistent 256 x 128 tiles, fitted to forced-configuration times at
+// the Wan 2.1 and 2.2 shapes.  The one-per-CU tiles take the transposed
+// layout (one ratio read per block) for bf16 / f32 output -- the 128 x 256
+// tile then runs 4680 x 8960 -> 1536 at 62.8 us and 2640 x 14336 -> 3072 at
+// 104 us, the eight-wave 128 x 128 one 880 x 14336 -> 3072 at 51 us -- and
+// the plain layout for MX output (kGroupedMxOut).
 constexpr CfgCost kGroupedAuto[] = {
+    {0, 0.584, 5.85, 0.0, false, 0.275},  // 256 x 128
+    {1, 0.346, 5.83, 0.0, false, 0.54},   // 128 x 256
+    {6, 0.80, 3.50, 4.00, true},          // 256 x 128 persistent
+    {7, 1.03, 2.70, 0.80, true},          // 256 x 128 persistent, overlapped epilogue (QKV 46 us, the K / V call 90)
+    {10, 0.221, 5.13, 0.0, false, 0.29},  // 128 x 128, eight waves (shapes of few 256 x 128 tiles)
+};
+constexpr CfgCost kGroupedMxOut[] = {
     {0, 0.61, 5.30, 0.0, false, 0.42},  // 256 x 128
     {1, 0.61, 5.30, 0.0, false, 0.42},  // 128 x 256
-    {6, 0.80, 3.50, 4.00, true},        // 256 x 128 persistent
-    {7, 0.87, 2.70, 0.80, true},        // 256 x 128 persistent, overlapped epilogue (the rescale: ~8% per stage)
-    {10, 0.53, 4.50, 0.0, false, 0.16},  // 128 x 128 (four waves: shapes of few 256 x 128 tiles)
+    {6, 0.80, 3.50, 4.00, true},
+    {7, 1.03, 2.70, 0.80, true},
 };
 // Modelled time of configuration c at M x N x K (rounds of tiles over num_cu CUs).
 double cfg_cost(const CfgCost &c, size_t tiles, size_t num_cu, size_t K) {
@@ -2315,7 +2360,10 @@ Fp8Plan plan_gemm_fp8(int num_cu, size_t M, size_t N, size_t K, bool mx, bool mx
         take(9, t);
     };
     if (grouped) {
-        for (const CfgCost &c : kGroupedAuto) consider(c);
+        if (y_dtype == LX2V_DTYPE_MXE4M3)
+            for (const CfgCost &c : kGroupedMxOut) consider(c);
+        else
+            for (const CfgCost &c : kGroupedAuto) consider(c);
         return p;
     }
     for (const CfgCost &c : kAuto) consider(c);

@@ -33,7 +33,7 @@ DIM, FFN, TEXT, M = 1536, 8960, 512, 4680
 # (name, rows, K, N, act, the configuration the planner picks on 256 CUs
 # with per-channel / group-128 weights, bf16 output)
 SITES = [
-    ("qkv", M, DIM, 3 * DIM, H.ACT_NONE, "c7", "c7.g128"),
+    ("qkv", M, DIM, 3 * DIM, H.ACT_NONE, "c7", "c6.g128"),
     ("o", M, DIM, DIM, H.ACT_NONE, "c1", "c1.g128"),
     ("kv2", TEXT, DIM, 2 * DIM, H.ACT_NONE, "c10", "c10.g128"),
     ("ffn1", M, DIM, FFN, H.ACT_GELU_TANH, "c9", "c7.g128"),
@@ -136,33 +136,36 @@ def test_ffn_pair_mx_handoff(be, group):
     assert_close(got, O.linear(hf, w2d, b2, 0, nthreads=8), 4e-2, 0.3, what="FFN chain vs f32 oracle")
 
 
-def test_cross_kv_30_layers_one_call(be):
+@pytest.mark.parametrize("group,cfg", [("channel", "c9"), (128, "c6.g128")])
+def test_cross_kv_30_layers_one_call(be, group, cfg):
     """The bench's per-step cross-attention K/V call: the 30 layers' K/V
-    weights concatenated by rows ([30 x 2 x 1536, 1536], per-channel scales
-    and bias concatenated the same way, as the bench builds them), one
-    linear over the 512 text tokens, 512 x 1536 -> 92160, on the persistent
-    256 x 256 tile.  bf16 output == f32 output rounded over the
-    whole tensor; sampled rows against the oracle over every column."""
+    weights concatenated by rows ([30 x 2 x 1536, 1536], scales and bias
+    concatenated the same way, as the bench builds them), one linear over
+    the 512 text tokens, 512 x 1536 -> 92160: on the persistent 256 x 256
+    tile with per-channel weights, on the persistent 256 x 128 one with
+    group-128 weights.  bf16 output == f32 output rounded over the whole
+    tensor; sampled rows against the oracle over every column."""
     rows, K, N = TEXT, DIM, 30 * 2 * DIM
+    g = K if group == "channel" else group
     x = O.bf16_round(normal(1201, rows * K).reshape(rows, K))
     wf = normal(1202, N * K, 0.02).reshape(N, K)
-    q, s = O.fp8_quantize(wf, N, K, K, True)
+    q, s = O.fp8_quantize(wf, N, K, g, True)
     del wf
     b = normal(1203, N, 0.01)
-    w = be.weight_fp8(q, s, N, K, K)
+    w = be.weight_fp8(q, s, N, K, g)
     xb, bb = _bf16_buf(be, x), be.upload(b)
     y16 = be.alloc(rows * N, H.DTYPE_BF16)
     y32 = be.alloc(rows * N, H.DTYPE_F32)
-    assert _profiled(be, lambda: be.linear(xb, 0, rows, w, bb, H.ACT_NONE, y16, 0)) == {"gemm_fp8_e4m3.c9"}
+    assert _profiled(be, lambda: be.linear(xb, 0, rows, w, bb, H.ACT_NONE, y16, 0)) == {f"gemm_fp8_e4m3.{cfg}"}
     be.linear(xb, 0, rows, w, bb, H.ACT_NONE, y32, 0)
     got32 = be.download(y32).reshape(rows, N)
     assert_bits_equal(be.download(y16), O.bf16_round(got32).ravel(), "bf16 output = f32 output rounded")
     p = np.array([0, 1, 2, 31, 32, 255, 256, 300, 480, 510, 511])
-    assert_close(got32[p], oracle_w8a8(x[p], q, s, K, b, 0), *FP8_TIGHT, what="30-layer K/V call vs oracle")
+    assert_close(got32[p], oracle_w8a8(x[p], q, s, g, b, 0), *FP8_TIGHT, what="30-layer K/V call vs oracle")
     # each layer's slice is that layer's own K/V linear
     for l in (0, 17, 29):
         sl = slice(l * 2 * DIM, (l + 1) * 2 * DIM)
-        assert_close(got32[p][:, sl], oracle_w8a8(x[p], q[sl], s[sl], K, b[sl], 0), *FP8_TIGHT, what=f"layer {l}")
+        assert_close(got32[p][:, sl], oracle_w8a8(x[p], q[sl], s[sl], g, b[sl], 0), *FP8_TIGHT, what=f"layer {l}")
 
 
 # Config 5 (Wan2.2-TI2V-5B, per-token e4m3 activations) with the bf16 output
