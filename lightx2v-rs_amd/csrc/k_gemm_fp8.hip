@@ -2177,8 +2177,9 @@ bool gemm_fp8_supported(size_t M, size_t N, size_t K) {
 // measured no faster than the one-shot tiles there.  Their costs are per
 // pass of a workgroup over its tiles (the same rounds count), measured on
 // the Wan shapes: 7 (epilogue folded into the next tile) at 256 x 128 x
-// 1536 tiles -- FFN up 6 passes 75 us, QKV 3 passes 38 us; 6 (grouped
-// scales) at QKV 45 us and FFN up 84 us.
+// 1536 tiles -- FFN up 6 passes 75 us, QKV 3 passes 38 us; with grouped
+// scales 6 and 7 within 2% of each other at QKV (43-46 us) and the 30-layer
+// K / V call (87-96 us), 7 ahead at FFN up (94 against 102 us).
 //
 // The one-per-CU tiles with 128-byte stages (0, 1, 10) have an occupancy
 // term instead: their stages slow down with the share of CUs loading at
