@@ -1021,7 +1021,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
             "traffic": traffic,
-            "kernel": ("fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma 256x128 for O, cross Q, cross O and "
+            "kernel": ("fp8 GEMM, all 7 shapes of the chunk (k_gemm_fp8_dma 128x256 for O, cross Q, cross O and "
                        "FFN down; the persistent k_gemm_fp8_ov 256x128 with the epilogue overlapped for QKV; the "
                        "persistent k_gemm_fp8_w4 256x256, one wave per SIMD, for FFN up and the 30-layer K/V call)"),
             "avg_launch_us": round(gemm_ms * 1e3 / n_linear, 2),
