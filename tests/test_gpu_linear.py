@@ -251,6 +251,39 @@ def test_fp8_grouped_forced_vs_config0(be, monkeypatch, cfg, act, ydt):
         assert_close(y, oracle_w8a8(x[p], q, s, 128, normal(3213, N, 0.01), act), *tol, what=f"c{cfg}.g128 vs oracle")
 
 
+@pytest.mark.parametrize("cfg,ydt", [(1, H.DTYPE_BF16), (1, H.DTYPE_F32), (10, H.DTYPE_BF16), (10, H.DTYPE_F32)])
+def test_fp8_grouped_ragged_n_vs_config0(be, monkeypatch, cfg, ydt):
+    """Group-128 weights with both edges ragged: 613 rows x 1000 channels
+    (1000 = 3 x 256 + 232 = 7 x 128 + 104, so every tile shape ends on a
+    partial column tile, whose staged epilogue takes the per-element store
+    path) x K 1024 (8 groups), GELU.  The transposed blocks of the one-shot
+    tiles (bf16 / f32 output) store the partial tiles' columns in range and
+    only those: configurations 1 and 10 against 0, bit for bit over the
+    whole output (NaN-filled first), and sampled rows against the oracle."""
+    M, K, N = 613, 1024, 1000
+    x = normal(3311, M * K).reshape(M, K)
+    _, q, s = fp8_weight(3312, N, K, 128)
+    w = be.weight_fp8(q, s, N, K, 128)
+    b = normal(3313, N, 0.01)
+    xb, bb = be.upload(x), be.upload(b)
+
+    def run(c):
+        monkeypatch.setenv("LIGHTX2V_HIP_FP8_CFG", str(c))
+        y = be.alloc(M * N, ydt)
+        be.write(y, np.full(M * N, np.nan, np.float32))
+        _, names = _kernels(be, lambda: be.linear(xb, 0, M, w, bb, H.ACT_GELU_TANH, y, 0))
+        assert {k for k in names if k.startswith("gemm")} == {f"gemm_fp8_e4m3.c{c}.g128"}, names
+        return u32(be.download(y))
+
+    want, got = run(0), run(cfg)
+    assert np.array_equal(want, got)
+    y = got.view(np.float32).reshape(M, N)
+    assert not np.isnan(y).any(), "an output element was left unwritten"
+    p = np.arange(0, M, 41)
+    tol = FP8_TIGHT if ydt == H.DTYPE_F32 else (4e-3, 1e-2)
+    assert_close(y[p], oracle_w8a8(x[p], q, s, 128, b, H.ACT_GELU_TANH), *tol, what=f"c{cfg}.g128 vs oracle")
+
+
 @pytest.mark.parametrize("group", ["channel", 128])
 @pytest.mark.parametrize("act,ydt", [(H.ACT_NONE, H.DTYPE_BF16), (H.ACT_GELU_TANH, H.DTYPE_F32),
                                      (H.ACT_GELU_TANH, H.DTYPE_MXE4M3)])
